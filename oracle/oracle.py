@@ -1,0 +1,284 @@
+"""STEPQuant CPU oracle: Python front end of oracle/stepquant_oracle.c.
+
+TEST INFRASTRUCTURE ONLY.  Only tests/, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may import this module; the product
+package ``stepquant_amd`` never does.  It is the checker, not the thing
+measured or shipped.
+
+Each function restates the reference algorithm it names (paths relative to
+the reference repository):
+
+* ``layout``          stepquant/kernels/pool.py:19-66 (``packed_layout``)
+* ``fit_state``       stepquant/quantization.py:54-98
+* ``encode_page``     fit_state + page stores (kernels/fused.py:62-127, 251-282;
+                      kernels/bitpack.py:6-30)
+* ``decode_page``     kernels/fused.py:18-59 (``_read``), kernels/byte_codec.py:6-28
+* ``prepare``         kernels/fused.py:155-179 (``prepare_inputs_kernel``)
+* ``delta_step``      stepquant/core.py:5-15
+* ``pack``/``unpack`` stepquant/packing.py:6-22
+* ``codec_encode``/``codec_decode``  stepquant/quantization.py:101-152 (``StateCodec``)
+
+Parity status: layout, fit_state, encode_page, decode_page, pack/unpack and
+codec_encode are pinned by golden vectors written from the reference
+(tests/golden) and by the known-answer tests of the reference's own test
+suite.  delta_step and prepare are pinned by closed-form invariants and a
+brute-force sequential check (tests/test_oracle_math.py).
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+import subprocess
+from dataclasses import dataclass
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "_build", "libsqoracle.so")
+_lib = None
+
+
+def build(force: bool = False) -> str:
+    """Compile the C oracle with its Makefile; returns the library path."""
+    if force or not os.path.exists(_LIB_PATH):
+        subprocess.run(["make", "-s", "-C", _HERE, "-B" if force else "all"], check=True)
+    return _LIB_PATH
+
+
+def _load():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        _lib = ctypes.CDLL(_LIB_PATH)
+        P = ctypes.c_void_p
+        I = ctypes.c_int
+        L = ctypes.c_int64
+        F = ctypes.c_float
+        _lib.sqo_layout.argtypes = [P, I, I, I, I, I, I, P, P, P]
+        _lib.sqo_layout.restype = L
+        _lib.sqo_fit_state.argtypes = [P, I, I, I, I, P, P, I, I, P, P, P, P, P]
+        _lib.sqo_fit_state.restype = I
+        _lib.sqo_encode_page.argtypes = [P, I, I, I, I, P, P, I, I, I, P, P, P, P, P, L]
+        _lib.sqo_encode_page.restype = I
+        _lib.sqo_decode_page.argtypes = [P, L, P, I, I, I, I, P, I, I, I, P, P, P, P]
+        _lib.sqo_decode_page.restype = I
+        _lib.sqo_prepare.argtypes = [P, P, L, L, P, P, P, P, I, I, I, I, I, I, F, P, P, P, P]
+        _lib.sqo_prepare.restype = None
+        _lib.sqo_delta_step.argtypes = [P, P, P, P, P, P, I, I, I, I, I, P, P]
+        _lib.sqo_delta_step.restype = None
+        _lib.sqo_torch_inner_sum.argtypes = [P, L]
+        _lib.sqo_torch_inner_sum.restype = F
+        _lib.sqo_torch_outer_sum.argtypes = [P, L, L, L, L]
+        _lib.sqo_torch_outer_sum.restype = F
+        _lib.sqo_f32_to_f16.argtypes = [F]
+        _lib.sqo_f32_to_f16.restype = ctypes.c_uint16
+    return _lib
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _c(a, dtype):
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+@dataclass
+class Plan:
+    """Mirror of QuantizationPlan (quantization.py:7-30), numpy side."""
+    architecture: str
+    bits: np.ndarray  # [H,K] int32, 16 = pivot
+    impact: np.ndarray  # [H,K] float32
+    value_group_size: int = 32
+
+    def __post_init__(self):
+        self.bits = _c(self.bits, np.int32)
+        self.impact = _c(self.impact, np.float32)
+
+    @property
+    def kda(self) -> int:
+        return int(self.architecture == "kda")
+
+
+@dataclass
+class Layout:
+    offsets: np.ndarray
+    rows: np.ndarray
+    columns: np.ndarray
+    page_bytes: int
+
+
+def layout(plan: Plan, value_dim: int, storage: str = "packed") -> Layout:
+    lib = _load()
+    H, K = plan.bits.shape
+    off = np.zeros(H * K + H, np.int32)
+    rows = np.zeros(H * K, np.int32)
+    cols = np.zeros(H, np.int32)
+    total = lib.sqo_layout(_ptr(plan.bits), H, K, value_dim, plan.kda, int(storage == "byte"),
+                           plan.value_group_size, _ptr(off), _ptr(rows), _ptr(cols))
+    return Layout(off, rows, cols, int(total))
+
+
+def _two_heads(plan):
+    if plan.kda:
+        return np.zeros(plan.bits.shape[0], bool)
+    return plan.bits[:, 0] == 2
+
+
+def fit_state(x, plan: Plan):
+    """Returns (z int16, r f16, c f16, r2 f16 or None, reconstructed f32)."""
+    lib = _load()
+    x = _c(x, np.float32)
+    B, H, K, V = x.shape
+    two = _two_heads(plan)
+    G = plan.value_group_size if two.any() else V
+    z = np.zeros(x.shape, np.int16)
+    r = np.zeros((B, H, K), np.uint16)
+    c = np.zeros((B, H, V), np.uint16)
+    r2 = np.zeros((B, H, K, V // G), np.uint16)
+    recon = np.zeros(x.shape, np.float32)
+    rc = lib.sqo_fit_state(_ptr(x), B, H, K, V, _ptr(plan.bits), _ptr(plan.impact), plan.kda,
+                           plan.value_group_size, _ptr(z), _ptr(r), _ptr(c), _ptr(r2), _ptr(recon))
+    if rc:
+        raise ValueError(f"oracle fit_state failed ({rc})")
+    r2o = r2[:, two].view(np.float16) if two.any() else None
+    return z, r.view(np.float16), c.view(np.float16), r2o, recon
+
+
+def encode_page(x, slots, plan: Plan, lay: Layout, data, storage: str = "packed"):
+    """Writes fit_state(x) into data[slots] in place (slot <= 0 skipped)."""
+    lib = _load()
+    x = _c(x, np.float32)
+    B, H, K, V = x.shape
+    slots = _c(slots, np.int64)
+    assert data.dtype == np.uint8 and data.flags.c_contiguous and data.shape[-1] == lay.page_bytes
+    rc = lib.sqo_encode_page(_ptr(x), B, H, K, V, _ptr(plan.bits), _ptr(plan.impact), plan.kda,
+                             plan.value_group_size, int(storage == "byte"), _ptr(lay.offsets),
+                             _ptr(lay.rows), _ptr(lay.columns), _ptr(slots), _ptr(data),
+                             lay.page_bytes)
+    if rc:
+        raise ValueError(f"oracle encode_page failed ({rc})")
+    return data
+
+
+def decode_page(data, slots, plan: Plan, lay: Layout, value_dim: int, storage: str = "packed"):
+    lib = _load()
+    slots = _c(slots, np.int64)
+    H, K = plan.bits.shape
+    B = slots.size
+    out = np.zeros((B, H, K, value_dim), np.float32)
+    lib.sqo_decode_page(_ptr(data), lay.page_bytes, _ptr(slots), B, H, K, value_dim,
+                        _ptr(plan.bits), plan.kda, plan.value_group_size, int(storage == "byte"),
+                        _ptr(lay.offsets), _ptr(lay.rows), _ptr(lay.columns), _ptr(out))
+    return out
+
+
+def prepare(q, k, g, beta, H, K, kda, normalize=False, scale=1.0, a_log=None, dt_bias=None):
+    """q,k: [B, HK*K] (rows may be padded: pass the full 2-D arrays)."""
+    lib = _load()
+    q = _c(q, np.float32).reshape(q.shape[0], -1)
+    k = _c(k, np.float32).reshape(k.shape[0], -1)
+    B = q.shape[0]
+    HK = q.shape[1] // K
+    g = _c(g, np.float32)
+    beta = _c(beta, np.float32)
+    qp = np.zeros((B, H, K), np.float32)
+    kp = np.zeros((B, H, K), np.float32)
+    ld = np.zeros((B, H, K) if kda else (B, H), np.float32)
+    bo = np.zeros((B, H), np.float32)
+    al = None if a_log is None else _c(a_log, np.float32)
+    db = None if dt_bias is None else _c(dt_bias, np.float32)
+    lib.sqo_prepare(_ptr(q), _ptr(k), q.shape[1], k.shape[1], _ptr(g), _ptr(beta), _ptr(al), _ptr(db),
+                    B, H, HK, K, int(kda), int(normalize), float(scale), _ptr(qp), _ptr(kp),
+                    _ptr(ld), _ptr(bo))
+    return qp, kp, ld, bo
+
+
+def delta_step(state, q, k, v, log_decay, beta):
+    """core.py:5-15 on prepared fp32 inputs; returns (output, updated)."""
+    lib = _load()
+    state = _c(state, np.float32)
+    B, H, K, V = state.shape
+    q, k, v = _c(q, np.float32), _c(k, np.float32), _c(v, np.float32)
+    ld = _c(log_decay, np.float32)
+    kda = int(ld.ndim == 3)
+    beta = _c(beta, np.float32)
+    out = np.zeros((B, H, V), np.float32)
+    upd = np.zeros_like(state)
+    lib.sqo_delta_step(_ptr(state), _ptr(q), _ptr(k), _ptr(v), _ptr(ld), _ptr(beta), B, H, K, V,
+                       kda, _ptr(out), _ptr(upd))
+    return out, upd
+
+
+def inner_sum(x):
+    """torch CPU order for x.sum(-1) of one contiguous float32 row."""
+    x = _c(x, np.float32)
+    return np.float32(_load().sqo_torch_inner_sum(_ptr(x), x.size))
+
+
+def outer_sum(x):
+    """torch CPU order for x.sum(-2) of a contiguous [n, ncols] float32 matrix."""
+    x = _c(x, np.float32)
+    n, ncols = x.shape
+    lib = _load()
+    out = np.zeros(ncols, np.float32)
+    base = x.ctypes.data
+    for j in range(ncols):
+        out[j] = lib.sqo_torch_outer_sum(ctypes.c_void_p(base + 4 * j), n, ncols, ncols, j)
+    return out
+
+
+def f32_to_f16_bits(x):
+    lib = _load()
+    x = _c(x, np.float32).ravel()
+    return np.array([lib.sqo_f32_to_f16(float(v)) for v in x], np.uint16)
+
+
+# ---------------------------------------------------------------- packing.py
+
+def pack(codes, bits):
+    """packing.py:6-14: little-endian, n = 8/gcd(bits,8) codes per word."""
+    if bits not in (2, 4, 6, 8):
+        raise ValueError("supported code widths: 2, 4, 6, 8")
+    flat = np.asarray(codes).reshape(-1).astype(np.int64)
+    n = 8 // math.gcd(bits, 8)
+    width = n * bits // 8
+    flat = np.pad(flat, (0, (-flat.size) % n)).reshape(-1, n)
+    word = (flat << (np.arange(n) * bits)).sum(-1)
+    return ((word[:, None] >> (np.arange(width) * 8)) & 255).astype(np.uint8).reshape(-1)
+
+
+def unpack(data, bits, count):
+    """packing.py:17-22."""
+    n = 8 // math.gcd(bits, 8)
+    width = n * bits // 8
+    word = (np.asarray(data).astype(np.int64).reshape(-1, width) << (np.arange(width) * 8)).sum(-1)
+    codes = (word[:, None] >> (np.arange(n) * bits)) & ((1 << bits) - 1)
+    return codes.reshape(-1)[:count].astype(np.int16)
+
+
+# ------------------------------------------------------ StateCodec streams
+
+def codec_encode(x, plan: Plan):
+    """quantization.py:109-126: per-width code streams + scales + pivots."""
+    x = _c(x, np.float32)
+    z, r, c, r2, _ = fit_state(x, plan)
+    B, H, K, V = x.shape
+    flat_bits = plan.bits.reshape(-1)
+    z = z.reshape(B, H * K, V).astype(np.int64)
+    streams = {}
+    for b in (2, 4, 6, 8):
+        idx = np.nonzero(flat_bits == b)[0]
+        codes = z[:, idx]
+        if b == 2 and not plan.kda:
+            codes = np.floor_divide(codes + 3, 2)
+        else:
+            codes = codes + (2 ** (b - 1) - 1)
+        streams[b] = pack(codes, b)
+    integer_rows = np.nonzero(flat_bits != 16)[0]
+    integer_heads = np.nonzero((plan.bits != 16).any(-1))[0]
+    pivots = x.reshape(B, H * K, V)[:, flat_bits == 16].astype(np.float16)
+    return dict(codes=streams, rows=r.reshape(B, -1)[:, integer_rows],
+                columns=c[:, integer_heads], pivots=pivots, two_bit_rows=r2, shape=x.shape)
