@@ -1,0 +1,171 @@
+"""Benchmark of the packed-state GDN decode step on one MI355X.
+
+Workload: STEPQuant@6 GDN decode, one layer,
+B=256 requests, 16 key heads shared GQA-style by 32 value heads, dk=dv=128,
+q/k/v bf16 column views of one mixed_qkv row (as the serving adapter passes
+them), raw gates a ~ N(0,1) with A_log = 0, dt_bias = 0 (g = -softplus(a)),
+beta = sigmoid(N(0,1)), L2-normalised q/k in the kernel.  Per-head widths
+{4, 6, 8} averaging 6 (page = 409,600 B).  Initial state ~ N(0, 0.05^2)
+encoded into slots 1..B.  One step = one decode step of the layer including
+the writeback of the requantised page; steps are replayed from a HIP graph
+and the state evolves from step to step.
+
+Prints one JSON line (metric, value = state-head updates/s, roofline of the
+dominant kernel, CPU baseline from the oracle on a bounded sample).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "state-head updates/sec at B=256 decode; achieved HBM GB/s vs peak"
+PEAK_GBS = 8000.0
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=1024)
+    p.add_argument("--warmup", type=int, default=32)
+    p.add_argument("--batch", type=int, default=256)
+    p.add_argument("--heads", type=int, default=32)
+    p.add_argument("--key-heads", type=int, default=16)
+    p.add_argument("--arch", choices=["gdn", "kda"], default="gdn")
+    p.add_argument("--nominal", type=int, choices=[4, 6], default=6)
+    p.add_argument("--async-writeback", action="store_true",
+                   help="split readout (foreground) and writer (writeback stream)")
+    p.add_argument("--cpu-sample", type=int, default=-1,
+                   help="requests in the CPU-baseline sample (-1: auto, 0: skip)")
+    p.add_argument("--traffic", default=None, help="json with measured HBM bytes per launch")
+    return p.parse_args()
+
+
+def make_plan(torch, arch, H, K, nominal, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    if arch == "gdn":
+        if nominal == 6:
+            widths = torch.tensor([4] * (H // 4) + [6] * (H // 2) + [8] * (H - H // 4 - H // 2))
+        else:
+            widths = torch.tensor([2] * (H // 4) + [4] * (H // 2) + [6] * (H - H // 4 - H // 2))
+        widths = widths[torch.randperm(H, generator=g)]
+        bits = widths[:, None].expand(H, K).contiguous()
+    else:
+        choices = torch.tensor([4, 6, 8] if nominal == 6 else [2, 4, 6])
+        bits = choices[torch.randint(0, 3, (H, K), generator=g)]
+        bits[torch.rand(H, K, generator=g) < .01] = 16
+    impact = torch.rand(H, K, generator=g) + .5
+    return bits, impact
+
+
+def cpu_baseline(bits, impact, arch, B, H, HK, K, V, sample, group=32):
+    """Oracle (C restatement of the reference CPU path) on a bounded sample."""
+    import numpy as np
+    from oracle import oracle as O
+    rng = np.random.default_rng(1)
+    plan = O.Plan(arch, bits.numpy(), impact.numpy(), group)
+    lay = O.layout(plan, V)
+    pages = np.zeros((sample + 1, lay.page_bytes), np.uint8)
+    slots = np.arange(1, sample + 1)
+    x = (rng.standard_normal((sample, H, K, V)) * .05).astype(np.float32)
+    O.encode_page(x, slots, plan, lay, pages)
+    q = rng.standard_normal((sample, HK * K)).astype(np.float32)
+    k = rng.standard_normal((sample, HK * K)).astype(np.float32)
+    v = rng.standard_normal((sample, H, V)).astype(np.float32)
+    a = rng.standard_normal((sample, H, K) if arch == "kda" else (sample, H)).astype(np.float32)
+    b = rng.standard_normal((sample, H)).astype(np.float32)
+    zeros_h = np.zeros(H, np.float32)
+    bias = np.zeros(H * K if arch == "kda" else H, np.float32)
+    t0 = time.perf_counter()
+    state = O.decode_page(pages, slots, plan, lay, V)
+    qp, kp, ld, bt = O.prepare(q, k, a, b, H, K, arch == "kda", True, K ** -.5, zeros_h, bias)
+    out, upd = O.delta_step(state, qp, kp, v, ld, bt)
+    O.encode_page(upd, slots, plan, lay, pages)
+    dt = time.perf_counter() - t0
+    return dict(value=sample * H / dt, unit="updates/s", cores=1, kind="port",
+                sample=f"{sample} requests x {H} heads of the same workload, one step "
+                       f"(decode page, prepare, delta_step, fit_state + page store), 1 thread, {dt:.1f} s")
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {a.gpus} is not supported (the path shards by heads "
+              "with no exchange; see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from stepquant_amd.kernels.pool import PackedStatePool
+    from stepquant_amd.quantization import QuantizationPlan
+
+    dev = torch.device("cuda:0")
+    B, H, HK, K, V = a.batch, a.heads, a.key_heads, 128, 128
+    bits, impact = make_plan(torch, a.arch, H, K, a.nominal)
+    plan = QuantizationPlan(a.arch, bits.to(dev), impact.to(dev))
+    stream = torch.cuda.Stream() if a.async_writeback else None
+    pool = PackedStatePool(plan, B + 1, V, writeback_stream=stream)
+    g = torch.Generator(device=dev).manual_seed(0)
+    slots = torch.arange(1, B + 1, device=dev, dtype=torch.int32)
+    pool.encode(torch.randn(B, H, K, V, device=dev, generator=g) * .05, slots)
+    mixed = torch.randn(B, 2 * HK * K + H * V, device=dev, generator=g).to(torch.bfloat16)
+    q, k, v = mixed.split([HK * K, HK * K, H * V], -1)
+    gate = torch.randn(B, H, K, device=dev, generator=g) if a.arch == "kda" else torch.randn(B, H, device=dev, generator=g)
+    beta = torch.randn(B, H, device=dev, generator=g)
+    a_log = torch.zeros(H, device=dev)
+    dt_bias = torch.zeros(H * K if a.arch == "kda" else H, device=dev)
+
+    def step():
+        out = pool.step(q, k, v, gate, beta, slots, normalize=True, scale=K ** -.5, a_log=a_log, dt_bias=dt_bias)
+        pool.wait()
+        return out
+
+    for _ in range(3):
+        step()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for _ in range(a.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    cur = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(cur)
+    for _ in range(a.steps):
+        graph.replay()
+    end.record(cur)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_total = start.elapsed_time(end)
+    ms_step = ms_total / a.steps
+    page = pool.page_bytes
+    alg_bytes = 2 * B * page
+    achieved = alg_bytes / (ms_step * 1e-3) / 1e9
+    updates = B * H / (ms_step * 1e-3)
+    traffic = None
+    if a.traffic and os.path.exists(a.traffic):
+        traffic = json.load(open(a.traffic)).get("bytes_per_launch")
+    roof = dict(bound="hbm", achieved=round(achieved, 1), peak=PEAK_GBS, unit="GB/s",
+                frac=round(achieved / PEAK_GBS, 4), traffic=traffic,
+                kernel="step_kernel (fused read+update+readout+requant+store)" if stream is None
+                else "readout + writeback kernels", algorithmic_bytes_per_launch=alg_bytes)
+    cpu = None
+    if a.cpu_sample != 0:
+        sample = a.cpu_sample if a.cpu_sample > 0 else B
+        cpu = cpu_baseline(bits, impact, a.arch, B, H, HK, K, V, sample)
+    line = dict(metric=METRIC, value=round(updates, 1), unit="state-head updates/s", n_gpus=1, steps=a.steps,
+                warmup=a.warmup, ms_per_step=round(ms_step, 6), higher_is_better=True, scaling="weak",
+                vs_baseline=None, dtype="f32", data="synthetic",
+                config=dict(workload=f"{a.arch.upper()} decode STEPQuant@{a.nominal}, one layer, B={B}, H={H}, "
+                                     f"HK={HK}, dk=dv={K}, bf16 q/k/v, raw gates, graph-replayed steps"
+                                     + (", async writeback" if stream is not None else ", fused writeback"),
+                            page_bytes=page, global_batch=B, wall_s=round(wall, 3)),
+                roofline=roof, cpu_baseline=cpu)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

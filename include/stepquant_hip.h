@@ -1,0 +1,216 @@
+/*
+ * stepquant_hip.h -- C ABI of the MI355X (gfx950) packed-state recurrent update.
+ *
+ * Plain C: device pointers, sizes and a hipStream_t passed as void*.  No torch
+ * types cross this boundary.  Every entry point is asynchronous on the given
+ * stream, allocates no device memory, and returns 0 on success, a negative
+ * SQ_E* code for invalid arguments, or a positive hipError_t from the launch.
+ * sq_last_error() returns a message for the most recent failure.
+ *
+ * Each entry point replaces one operation of the reference's
+ * stepquant.kernels.pool.PackedStatePool (reference paths below are relative
+ * to the reference repository).
+ */
+#ifndef STEPQUANT_HIP_H
+#define STEPQUANT_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SQ_ABI_VERSION 1
+
+/* dtype codes for q/k/v/g/beta/out and slot indices */
+enum {
+    SQ_F32 = 0,
+    SQ_BF16 = 1,
+    SQ_F16 = 2,
+    SQ_I32 = 3,
+    SQ_I64 = 4
+};
+
+/* error codes (negative; positive values are hipError_t) */
+enum {
+    SQ_OK = 0,
+    SQ_EINVAL = -22,     /* bad argument: null pointer, dtype, shape */
+    SQ_ESHAPE = -23,     /* K/V/group combination outside the supported set */
+    SQ_ESTORAGE = -24    /* storage variant not supported by this entry point */
+};
+
+/*
+ * One layer's page pool.  Mirrors the state of PackedStatePool.__init__
+ * (pool.py:70-119) and the tables of packed_layout (pool.py:19-66):
+ *   data      [num_slots, page_bytes] uint8 pages; the allocation must extend
+ *             at least 16 bytes past the last page (aligned over-reads).
+ *   bits      [H*K]   per key-row width, 16 = FP16 pivot row
+ *   offsets   [H*K+H] packed row byte offsets, then per-head tile strides
+ *             (byte storage: per-head code-plane bases)
+ *   rows      [H*K]   byte offset of each row's fp16 scale(s), -1 for pivots
+ *   columns   [H]     byte offset of each head's fp16 column scales, -1 if none
+ *   impact    [H*K]   fit weights w (float32)
+ *   head_meta [H*4]   per head: code region start, code region bytes,
+ *                     row-scale region start, row-scale region bytes
+ *   max_code_bytes    largest code region of any head (LDS staging size)
+ *   max_row_bytes     largest row-scale region of any head
+ *   flags             sq_pool_flags() of the host copies of the tables
+ */
+typedef struct sq_pool {
+    uint8_t *data;
+    int64_t page_bytes;
+    int64_t num_slots;
+    const int32_t *bits;
+    const int32_t *offsets;
+    const int32_t *rows;
+    const int32_t *columns;
+    const float *impact;
+    const int32_t *head_meta;
+    int32_t heads;        /* H: value heads of this shard */
+    int32_t keys;         /* K */
+    int32_t values;       /* V */
+    int32_t group;        /* value_group_size (GDN 2-bit row scales) */
+    int32_t kda;          /* 0: GDN (per-head widths), 1: KDA (per-row widths) */
+    int32_t storage;      /* 0: packed, 1: byte carriers */
+    int32_t max_code_bytes;
+    int32_t max_row_bytes;   /* largest row-scale region of any head */
+    int32_t flags;           /* SQ_POOL_* bits, from sq_pool_flags() */
+    int32_t reserved;
+} sq_pool;
+
+/* sq_pool.flags: the pool qualifies for the K=V=128 uniform-width GDN kernel */
+#define SQ_POOL_FAST_GDN128 1
+
+/*
+ * Inputs of one decode step (PackedStatePool.step, pool.py:200-282).
+ *   q, k     [B, HK*K] rows with row strides q_stride/k_stride (elements);
+ *            value head h reads key head h / (H/HK) (GQA).
+ *   v        [B, H*V] rows with row stride v_stride.
+ *   g        GDN: [B, H] log-decay (raw gate a when a_log != NULL);
+ *            KDA: [B, H*K] per-channel values.
+ *   beta     [B, H] (raw logits when a_log != NULL: beta = sigmoid(b)).
+ *   a_log    [H] or NULL; dt_bias [H] (GDN) or [H*K] (KDA), with a_log.
+ *   out      [B, H, V] contiguous, dtype out_dtype; slot <= 0 rows are zero.
+ *   slots    [B] page indices, dtype slots_dtype (SQ_I32 or SQ_I64).
+ */
+typedef struct sq_step_args {
+    const void *q;
+    const void *k;
+    const void *v;
+    const void *g;
+    const void *beta;
+    const void *a_log;
+    const void *dt_bias;
+    void *out;
+    const void *slots;
+    int64_t batch;
+    int64_t q_stride;
+    int64_t k_stride;
+    int64_t v_stride;
+    int32_t key_heads;   /* HK */
+    int32_t qkv_dtype;   /* dtype of q, k, v */
+    int32_t gate_dtype;  /* dtype of g, beta, a_log, dt_bias */
+    int32_t out_dtype;
+    int32_t slots_dtype;
+    int32_t normalize;   /* L2-normalise q and k (eps 1e-6) */
+    float scale;         /* query scale */
+    int32_t reserved;
+} sq_step_args;
+
+/*
+ * Writer hand-off of the asynchronous path (the reference keeps the same
+ * four tensors in PackedStatePool.scratch, pool.py:137-158):
+ *   key [B,H,K] f32 prepared keys, decay [B,H,K] f32 per-row retention,
+ *   delta [B,H,V] f32, stable_slots [B] int64 snapshot of the slot indices.
+ */
+typedef struct sq_writeback_scratch {
+    float *key;
+    float *decay;
+    float *delta;
+    int64_t *stable_slots;
+    int64_t capacity;    /* rows available in each buffer (>= batch) */
+} sq_writeback_scratch;
+
+/* ABI version, and the message for the most recent non-zero return. */
+int sq_abi_version(void);
+const char *sq_last_error(void);
+
+/*
+ * Dense fp32 state [B,H,K,V] -> pages of `slots`, requantised exactly as the
+ * reference CPU fit_state (quantization.py:54-98): codes, row/column scales
+ * and FP16 pivots bit-identical.  Replaces PackedStatePool.encode
+ * (pool.py:184-190 -> _writeback, pool.py:319-331).
+ */
+int sq_encode(const sq_pool *pool, const float *state, const void *slots, int32_t slots_dtype,
+              int64_t batch, void *stream);
+
+/*
+ * Pages of `slots` -> dense fp32 state [B,H,K,V] (zeros for slot <= 0).
+ * Replaces PackedStatePool.decode (pool.py:192-198, codec_kernel fused.py:50-59).
+ */
+int sq_decode_dense(const sq_pool *pool, const void *slots, int32_t slots_dtype, int64_t batch,
+                    float *state, void *stream);
+
+/*
+ * Fused decode step: one pass reads each (request, head) page tile, applies
+ * the gated delta update, writes the readout and writes back the requantised
+ * tile.  Replaces PackedStatePool.step without a writeback stream
+ * (pool.py:200-282 with update_kernel fused.py:182-248 and _writeback
+ * pool.py:319-331).
+ */
+int sq_decode_step(const sq_pool *pool, const sq_step_args *args, void *stream);
+
+/*
+ * Asynchronous split of the same step.  sq_decode_readout runs on the
+ * foreground stream: readout `out`, plus the writer hand-off in `scratch`
+ * (replaces the readers readout.py:7-121 / segment_read.py:6-104).
+ * sq_writeback runs on the writeback stream after it: it re-reads the old
+ * tile and stores the requantised one (replaces prepare_rows_kernel
+ * rows.py:52-63 + fit fit.py:152-167 in _finish_update, pool.py:299-316).
+ */
+int sq_decode_readout(const sq_pool *pool, const sq_step_args *args,
+                      const sq_writeback_scratch *scratch, void *stream);
+int sq_writeback(const sq_pool *pool, const sq_writeback_scratch *scratch, int64_t batch,
+                 void *stream);
+
+/*
+ * Slot operations (pool.py:358-365).  sq_clear_slots zeroes whole pages.
+ * sq_copy_slots copies pages src[i] -> dst[i] through `temp`
+ * ([n, page_bytes] bytes) so overlapping index sets behave like the
+ * reference's gather-then-scatter.  Negative indices wrap like Python;
+ * indices outside the pool are skipped.
+ */
+int sq_clear_slots(const sq_pool *pool, const void *slots, int32_t slots_dtype, int64_t n,
+                   void *stream);
+int sq_copy_slots(const sq_pool *pool, const void *src, const void *dst, int32_t slots_dtype,
+                  int64_t n, uint8_t *temp, void *stream);
+
+/*
+ * Flags for sq_pool.flags, computed from host copies of bits [H*K],
+ * head_meta [H*4] and columns [H].  Returns a non-negative flag set, or a
+ * negative SQ_E* code.  Host-only; no device access.
+ */
+int sq_pool_flags(const int32_t *bits, const int32_t *head_meta, const int32_t *columns, int32_t heads,
+                  int32_t keys, int32_t values, int32_t group, int32_t kda, int32_t storage,
+                  int64_t page_bytes);
+
+/*
+ * Capture state of a stream for the writer's event bookkeeping: capturing is
+ * 0 (not capturing), 1 (active) or 2 (invalidated); id identifies the
+ * capture.  Replaces _capture_id (pool.py:11-16, cudaStreamGetCaptureInfo).
+ */
+int sq_stream_capture_id(void *stream, int32_t *capturing, uint64_t *id);
+
+/*
+ * A non-blocking stream restricted to `cus` compute units spread across all
+ * XCDs (hipExtStreamCreateWithCUMask; 0 = unrestricted), at default priority.
+ * Replaces the Green Context SM split of writeback_resources
+ * (kernels/resources.py:19-53).  The stream lives until process exit.
+ */
+int sq_create_cu_stream(int32_t device, int32_t cus, void **stream, int32_t *actual, int32_t *total);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* STEPQUANT_HIP_H */

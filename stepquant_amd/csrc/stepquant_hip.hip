@@ -1,0 +1,1627 @@
+// MI355X (gfx950) kernels for STEPQuant's packed-state recurrent update.
+//
+// One workgroup owns one (request, value-head) tile of K x V state values.
+// The tile's packed code region (contiguous per head in the page layout of
+// stepquant/kernels/pool.py:19-66) is staged through LDS with 16-byte
+// loads, every lane then owns RPT key rows x 4 adjacent value columns, so
+// each lane's codes are one whole byte run of 4*b bits in every row.
+//
+//   sq_encode        dense fp32 -> page, bit-identical to the CPU fit_state
+//                    (quantization.py:54-98): exact IEEE division/sqrt and
+//                    PyTorch's CPU float32 summation order.
+//   sq_decode_dense  page -> dense fp32 (kernels/fused.py:18-59).
+//   sq_decode_step   fused read + gated delta update + readout + requantise +
+//                    store (pool.py:200-331), one HBM pass over the page.
+//   sq_decode_readout / sq_writeback  the same step split over a foreground
+//                    and a writeback stream (pool.py:284-316).
+//
+// Register math of the decode step uses reciprocals of per-row and
+// per-column scales (computed with IEEE division); the encode path uses
+// IEEE division per element.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "stepquant_hip.h"
+
+namespace {
+
+// ------------------------------------------------------------------ fp16
+
+__device__ __forceinline__ float bits_to_f32(uint32_t u) { return __uint_as_float(u); }
+
+// IEEE half -> float, exact for every input (subnormals included).
+__device__ __forceinline__ float h2f(uint32_t h) {
+  uint32_t sign = (h & 0x8000u) << 16;
+  uint32_t e = (h >> 10) & 0x1fu;
+  uint32_t m = h & 0x3ffu;
+  if (e == 0) {
+    // subnormal or zero: m * 2^-24, exact in float
+    float v = (float)m * 5.9604644775390625e-08f;
+    return __uint_as_float(__float_as_uint(v) | sign);
+  }
+  if (e == 31) return __uint_as_float(sign | 0x7f800000u | (m << 13));
+  return __uint_as_float(sign | ((e + 112u) << 23) | (m << 13));
+}
+
+// float -> IEEE half bits, round to nearest even (torch .half()).
+__device__ __forceinline__ uint32_t f2h(float f) {
+  uint32_t x = __float_as_uint(f);
+  uint32_t sign = (x >> 16) & 0x8000u;
+  uint32_t ax = x & 0x7fffffffu;
+  if (ax >= 0x7f800000u) return sign | 0x7c00u | (ax > 0x7f800000u ? 0x200u : 0u);
+  if (ax >= 0x477ff000u) return sign | 0x7c00u;
+  if (ax < 0x38800000u) {
+    if (ax < 0x33000000u) return sign;
+    uint32_t e = ax >> 23;
+    uint32_t m = (ax & 0x7fffffu) | 0x800000u;
+    uint32_t shift = 126u - e;
+    uint32_t q = m >> shift;
+    uint32_t rem = m & ((1u << shift) - 1u);
+    uint32_t half = 1u << (shift - 1u);
+    if (rem > half || (rem == half && (q & 1u))) q++;
+    return sign | q;
+  }
+  uint32_t e = (ax >> 23) - 112u;
+  uint32_t m = ax & 0x7fffffu;
+  uint32_t q = (e << 10) | (m >> 13);
+  uint32_t rem = m & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (q & 1u))) q++;
+  return sign | q;
+}
+
+// quantization.py:49-51: clamp(2^-24, 65504).half().float()
+__device__ __forceinline__ float fp16_scale(float x, uint32_t *hbits) {
+  float c = x < 5.9604644775390625e-08f ? 5.9604644775390625e-08f : x;
+  c = c > 65504.0f ? 65504.0f : c;
+  uint32_t h = f2h(c);
+  if (hbits) *hbits = h;
+  return h2f(h);
+}
+
+__device__ __forceinline__ uint32_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ float load_val(const void *p, int dtype, int64_t idx) {
+  if (dtype == SQ_F32) return ((const float *)p)[idx];
+  if (dtype == SQ_BF16) return __uint_as_float((uint32_t)((const uint16_t *)p)[idx] << 16);
+  return h2f(((const uint16_t *)p)[idx]);
+}
+
+__device__ __forceinline__ void store_val(void *p, int dtype, int64_t idx, float v) {
+  if (dtype == SQ_F32) ((float *)p)[idx] = v;
+  else if (dtype == SQ_BF16) ((uint16_t *)p)[idx] = (uint16_t)f2bf(v);
+  else ((uint16_t *)p)[idx] = (uint16_t)f2h(v);
+}
+
+__device__ __forceinline__ int64_t load_slot(const void *p, int dtype, int64_t idx) {
+  return dtype == SQ_I64 ? ((const int64_t *)p)[idx] : (int64_t)((const int32_t *)p)[idx];
+}
+
+__device__ __forceinline__ uint32_t page_half(const uint8_t *page, int64_t byte) {
+  return (uint32_t)page[byte] | ((uint32_t)page[byte + 1] << 8);
+}
+
+__device__ __forceinline__ void put_page_half(uint8_t *page, int64_t byte, uint32_t h) {
+  *(uint16_t *)(page + byte) = (uint16_t)h;  // byte offsets of scales are even
+}
+
+// ------------------------------------------------ LDS staging of a region
+
+// Stage global bytes [gstart, gend) (2-byte aligned) into LDS.  The LDS copy
+// starts at the enclosing 16-byte boundary: lds byte (a - w16) holds global
+// byte a.  Returns the offset of gstart inside the staged window.
+__device__ __forceinline__ int stage_in(const uint8_t *gstart, int64_t nbytes, uint8_t *lds, int tid,
+                                        int nthreads) {
+  uintptr_t s = (uintptr_t)gstart;
+  uintptr_t w16 = s & ~(uintptr_t)15;
+  uintptr_t e16 = ((uintptr_t)gstart + nbytes + 15) & ~(uintptr_t)15;
+  int n16 = (int)((e16 - w16) >> 4);
+  const uint4 *src = (const uint4 *)w16;
+  uint4 *dst = (uint4 *)lds;
+  for (int c = tid; c < n16; c += nthreads) dst[c] = src[c];
+  return (int)(s - w16);
+}
+
+// Write LDS back to [gstart, gend): whole 16-byte chunks inside the region
+// use 16-byte stores, edge chunks store only the region's 2-byte units.
+// `lds` is the staged window as returned by stage_in (global byte a lives at
+// lds + (a - floor16(gstart))).
+__device__ __forceinline__ void stage_out(uint8_t *gstart, int64_t nbytes, const uint8_t *lds, int tid,
+                                          int nthreads) {
+  uintptr_t s = (uintptr_t)gstart;
+  uintptr_t e = s + (uintptr_t)nbytes;
+  uintptr_t w16 = s & ~(uintptr_t)15;
+  uintptr_t e16 = (e + 15) & ~(uintptr_t)15;
+  int n16 = (int)((e16 - w16) >> 4);
+  for (int c = tid; c < n16; c += nthreads) {
+    uintptr_t a = w16 + ((uintptr_t)c << 4);
+    if (a >= s && a + 16 <= e) {
+      *(uint4 *)a = ((const uint4 *)lds)[c];
+    } else {
+      for (int u = 0; u < 8; u++) {
+        uintptr_t b = a + 2 * u;
+        if (b >= s && b + 2 <= e) *(uint16_t *)b = *(const uint16_t *)(lds + (b - w16));
+      }
+    }
+  }
+}
+
+// 32 bits little-endian starting at an arbitrary LDS byte (4 spare bytes
+// after the staged window keep the second dword in bounds).
+__device__ __forceinline__ uint32_t lds_word(const uint8_t *lds, int p) {
+  const uint32_t *w = (const uint32_t *)(lds + (p & ~3));
+  uint32_t lo = w[0], hi = w[1];
+  return __builtin_amdgcn_alignbit(hi, lo, (uint32_t)(p & 3) * 8u);
+}
+
+__device__ __forceinline__ void lds_put_bytes(uint8_t *lds, int p, uint32_t word, int nbytes) {
+  for (int b = 0; b < nbytes; b++) lds[p + b] = (uint8_t)(word >> (8 * b));
+}
+
+// ---------------------------------------- PyTorch CPU summation order (f32)
+
+// Streaming form of aten SumKernel.cpp multi_row_sum: terms arrive in row-
+// major order (row ii, column k); R accumulators per level; 16-row cascade.
+template <int R>
+struct TorchCascade {
+  float acc[4][R];
+  int64_t size, ii;
+  int k;
+  __device__ void init(int64_t rows) {
+    size = rows;
+    ii = 0;
+    k = 0;
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+      for (int c = 0; c < R; c++) acc[a][c] = 0.0f;
+  }
+  __device__ void push(float t) {
+    // caller guarantees (ii, k) is inside size x R
+#pragma unroll
+    for (int c = 0; c < R; c++)
+      if (c == k) acc[0][c] += t;
+    if (++k == R) {
+      k = 0;
+      ++ii;
+      if ((ii & 15) == 0 && ii <= size) {
+        for (int j = 1; j < 4; j++) {
+#pragma unroll
+          for (int c = 0; c < R; c++) {
+            acc[j][c] += acc[j - 1][c];
+            acc[j - 1][c] = 0.0f;
+          }
+          if (ii & ((int64_t)15 << (4 * j))) break;
+        }
+      }
+    }
+  }
+  __device__ void finish(float *out) {
+#pragma unroll
+    for (int c = 0; c < R; c++) {
+      float a = acc[0][c];
+      a += acc[1][c];
+      a += acc[2][c];
+      a += acc[3][c];
+      out[c] = a;
+    }
+  }
+};
+
+// row_sum with ilp factor 4 over n terms given by f(i), i ascending.
+template <typename F>
+__device__ float torch_row_sum_ilp4(int64_t n, F f) {
+  TorchCascade<4> cas;
+  const int64_t size_ilp = n / 4;
+  cas.init(size_ilp);
+  for (int64_t i = 0; i < size_ilp * 4; i++) cas.push(f(i));
+  float p[4];
+  cas.finish(p);
+  for (int64_t i = size_ilp * 4; i < n; i++) p[0] += f(i);
+  p[0] += p[1];
+  p[0] += p[2];
+  p[0] += p[3];
+  return p[0];
+}
+
+// x.sum(-1) order for n contiguous values f(0..n-1) (8-wide vectors).
+template <typename F>
+__device__ float torch_inner_sum(int64_t n, F f) {
+  if (n < 8) return torch_row_sum_ilp4(n, f);
+  const int64_t nvec = n / 8;
+  float total = 0.0f;
+  for (int64_t t = nvec * 8; t < n; t++) total += f(t);
+  for (int l = 0; l < 8; l++) total += torch_row_sum_ilp4(nvec, [&](int64_t m) { return f(8 * m + l); });
+  return total;
+}
+
+// -------------------------------------------------------- pool metadata
+
+struct PoolDev {
+  uint8_t *data;
+  int64_t page_bytes;
+  int64_t num_slots;
+  const int32_t *bits, *offsets, *rows, *columns, *head_meta;
+  const float *impact;
+  int H, K, V, G, kda;
+  int stage;   // bytes of LDS staging per workgroup (largest head window)
+  int rstage;  // bytes of LDS for one head's row scales (fast path)
+  int fast;    // pool qualifies for the K=V=128 uniform-width GDN kernel
+};
+
+__device__ __forceinline__ int tile_of(const PoolDev &P) { return P.kda ? (P.V < 4 ? P.V : 4) : (P.V < 16 ? P.V : 16); }
+
+// Byte position (relative to the head's code region) of the 4-value group
+// starting at column j0 in row i; pivots use width 16.
+__device__ __forceinline__ int group_pos(int off_rel, int stride, int tile, int j0, int width) {
+  return off_rel + (j0 / tile) * stride + ((j0 % tile) * width) / 8;
+}
+
+// =====================================================================
+// Encode: dense fp32 -> page, bit-exact fit_state.  Thread j owns column j
+// (NT >= V); rows are processed by thread i in the row phase.
+// =====================================================================
+__global__ __launch_bounds__(256) void encode_kernel(PoolDev P, const float *__restrict__ state,
+                                                     const void *slots, int slots_dtype) {
+  // Every product and sum rounds separately, as PyTorch's CPU ops do.
+#pragma clang fp contract(off)
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int H = P.H, K = P.K, V = P.V;
+  const int b = blockIdx.x / H, h = blockIdx.x % H;
+  const int tid = threadIdx.x, NT = blockDim.x;
+  const int64_t slot = load_slot(slots, slots_dtype, b);
+  if (slot <= 0 || slot >= P.num_slots) return;  // masked (or outside the pool)
+  uint8_t *page = P.data + slot * P.page_bytes;
+  const int32_t *hm = P.head_meta + 4 * h;
+  const int code_start = hm[0], code_bytes = hm[1];
+  const int32_t *hbits = P.bits + (int64_t)h * K;
+  const float *hw = P.impact + (int64_t)h * K;
+  const int two = !P.kda && hbits[0] == 2;
+  const int NG = two ? V / P.G : 1;
+  const int Geff = two ? P.G : V;
+  const int tile = tile_of(P);
+  const int stride = P.offsets[(int64_t)H * K + h];
+  const float *X = state + ((int64_t)b * H + h) * K * V;
+
+  // LDS: staging window | row scale per (row, group) f32 [K * NG]
+  uint8_t *stage = smem;
+  float *rsc = (float *)(smem + P.stage);
+
+  int shift = 0;
+  if (code_bytes > 0) shift = stage_in(page + code_start, code_bytes, stage, tid, NT);
+  __syncthreads();
+
+  // ---- row phase: r (and GDN 2-bit group r), pivots
+  for (int i = tid; i < K; i += NT) {
+    const float *xr = X + (int64_t)i * V;
+    const int bi = hbits[i];
+    const float wi = hw[i];
+    if (bi == 16) {
+      const int off_rel = P.offsets[(int64_t)h * K + i] - code_start;
+      for (int j = 0; j < V; j++) {
+        int p = shift + group_pos(off_rel, stride, tile, j, 16);
+        uint32_t hb = f2h(xr[j]);
+        stage[p] = (uint8_t)hb;
+        stage[p + 1] = (uint8_t)(hb >> 8);
+      }
+      rsc[i * NG] = 1.0f;
+      continue;
+    }
+    const int64_t ro = P.rows[(int64_t)h * K + i];
+    if (two) {
+      for (int g = 0; g < NG; g++) {
+        float s = torch_inner_sum(Geff, [&](int64_t t) { return fabsf(xr[g * Geff + t]); });
+        float m = s / (float)Geff;
+        m = m < 1e-20f ? 1e-20f : m;
+        uint32_t hb;
+        float r = fp16_scale(__builtin_sqrtf(m / wi), &hb);
+        rsc[i * NG + g] = r;
+        put_page_half(page, ro + 2 * g, hb);
+      }
+    } else {
+      float s = torch_inner_sum(V, [&](int64_t t) { return fabsf(xr[t]); });
+      float m = s / (float)V;
+      m = m < 1e-20f ? 1e-20f : m;
+      uint32_t hb;
+      float r = fp16_scale(__builtin_sqrtf(m / wi), &hb);
+      rsc[i * NG] = r;
+      put_page_half(page, ro, hb);
+    }
+  }
+  __syncthreads();
+
+  // ---- column phase (thread j <-> column j; lanes of a quad are adjacent columns)
+  const int colbase = P.columns[h];
+  for (int jb = 0; jb < V; jb += NT) {
+    const int j = jb + tid;
+    const bool act = j < V;
+    const int jj = act ? j : V - 1;
+    const int g = two ? jj / P.G : 0;
+    // pass 1: c0 = fp16(max_i where(int, |x/r|/(qmax*norm), 0))
+    float mx = 0.0f;
+    for (int i = 0; i < K; i++) {
+      int bi = hbits[i];
+      if (bi == 16) continue;
+      int bc = bi < 8 ? bi : 8;
+      float qmax = two ? 3.0f : (float)((1 << (bc - 1)) - 1);
+      float norm = P.kda ? (float)(1 << (8 - bc)) : 1.0f;
+      float sc = X[(int64_t)i * V + jj] / rsc[i * NG + g];
+      float t = fabsf(sc) / (qmax * norm);
+      mx = t > mx ? t : mx;
+    }
+    const float c0 = fp16_scale(mx, nullptr);
+    // pass 2: z = encode(c0); weighted sums in torch's key-axis order
+    auto z_of = [&](int i, float cdiv) -> float {
+      int bi = hbits[i];
+      int bc = bi < 8 ? bi : 8;
+      float qmax = (float)((1 << (bc - 1)) - 1);
+      float norm = P.kda ? (float)(1 << (8 - bc)) : 1.0f;
+      float sc = X[(int64_t)i * V + jj] / rsc[i * NG + (bi == 16 ? 0 : g)];
+      float y = sc / cdiv;
+      if (P.kda) y = y / norm;
+      if (two) return (y >= 0.0f ? 1.0f : -1.0f) * (fabsf(y) >= 2.0f ? 3.0f : 1.0f);
+      float z = __builtin_rintf(y);
+      z = z > -qmax ? z : -qmax;
+      z = z < qmax ? z : qmax;
+      return z;
+    };
+    auto term = [&](int64_t i, bool numerator) -> float {
+      int bi = hbits[i];
+      int bc = bi < 8 ? bi : 8;
+      float norm = P.kda ? (float)(1 << (8 - bc)) : 1.0f;
+      float wsq = (hw[i] * hw[i]) * (bi != 16 ? 1.0f : 0.0f);
+      float z = z_of((int)i, c0);
+      float v = (rsc[i * NG + (bi == 16 ? 0 : g)] * norm) * z;
+      return numerator ? (wsq * v) * X[i * V + jj] : wsq * (v * v);
+    };
+    float num, den;
+    if (V >= 32) {
+      TorchCascade<1> cn, cd;
+      cn.init(K);
+      cd.init(K);
+      for (int i = 0; i < K; i++) {
+        cn.push(term(i, true));
+        cd.push(term(i, false));
+      }
+      cn.finish(&num);
+      cd.finish(&den);
+    } else {
+      num = torch_row_sum_ilp4(K, [&](int64_t i) { return term(i, true); });
+      den = torch_row_sum_ilp4(K, [&](int64_t i) { return term(i, false); });
+    }
+    const float denc = den < 1e-30f ? 1e-30f : den;
+    uint32_t chb;
+    const float c = fp16_scale(den > 0.0f ? num / denc : c0, &chb);
+    if (act && colbase >= 0) put_page_half(page, colbase + 2 * (int64_t)j, chb);
+    // pass 3: final codes; quads of lanes assemble each 4-value group
+    for (int i = 0; i < K; i++) {
+      int bi = hbits[i];
+      uint32_t code = 0;
+      if (bi != 16) {
+        int bc = bi < 8 ? bi : 8;
+        float z = z_of(i, c);
+        code = two ? (uint32_t)(((int)z + 3) / 2) : (uint32_t)((int)z + ((1 << (bc - 1)) - 1));
+      }
+      const int lane = tid & 3;
+      uint32_t c1 = __shfl_xor(code, 1);
+      uint32_t c2 = __shfl_xor(code, 2);
+      uint32_t c3 = __shfl_xor(code, 3);
+      if (bi != 16 && act && lane == 0) {
+        uint32_t word = code | (c1 << bi) | (c2 << (2 * bi)) | (c3 << (3 * bi));
+        int off_rel = P.offsets[(int64_t)h * K + i] - code_start;
+        lds_put_bytes(stage, shift + group_pos(off_rel, stride, tile, j, bi), word, bi / 2);
+      }
+    }
+  }
+  __syncthreads();
+  if (code_bytes > 0) stage_out(page + code_start, code_bytes, stage, tid, NT);
+}
+
+// =====================================================================
+// Decode step.  Lane t: column group cg = t / RG (4 columns), row group
+// rg = t % RG; rows rg, rg+RG, ... (RPT of them).
+// =====================================================================
+enum { MODE_FUSED = 0, MODE_READ = 1, MODE_WRITE = 2, MODE_DECODE = 3 };
+
+struct StepDev {
+  const void *q, *k, *v, *g, *beta, *a_log, *dt_bias;
+  void *out;
+  const void *slots;
+  int64_t q_stride, k_stride, v_stride;
+  int HK, qkv_dtype, gate_dtype, out_dtype, slots_dtype, normalize;
+  float scale;
+  float *s_key, *s_decay, *s_delta;
+  int64_t *s_slots;
+  float *dense;  // MODE_DECODE output
+};
+
+template <int RG>
+__device__ __forceinline__ float rg_sum(float x) {
+#pragma unroll
+  for (int m = 1; m < RG; m <<= 1) x += __shfl_xor(x, m);
+  return x;
+}
+
+template <int RG>
+__device__ __forceinline__ float rg_max(float x) {
+#pragma unroll
+  for (int m = 1; m < RG; m <<= 1) x = fmaxf(x, __shfl_xor(x, m));
+  return x;
+}
+
+template <int RPT, int RG, int MODE>
+__global__ __launch_bounds__(512) void step_kernel(PoolDev P, StepDev S) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int H = P.H, K = P.K, V = P.V;
+  const int b = blockIdx.x / H, h = blockIdx.x % H;
+  const int tid = threadIdx.x, NT = blockDim.x;
+  const int CG = V / 4;
+  const int cg = tid / RG, rg = tid % RG;
+  const bool act = cg < CG;
+  const int j0 = (act ? cg : 0) * 4;
+
+  int64_t slot;
+  if (MODE == MODE_WRITE) {
+    slot = S.s_slots[b];
+  } else {
+    slot = load_slot(S.slots, S.slots_dtype, b);
+    if (MODE == MODE_READ && h == 0 && tid == 0) S.s_slots[b] = slot;
+  }
+  if (slot <= 0 || slot >= P.num_slots) {  // masked (or outside the pool): zero readout, no page access
+    if (MODE == MODE_FUSED || MODE == MODE_READ) {
+      for (int j = tid; j < V; j += NT) store_val(S.out, S.out_dtype, ((int64_t)b * H + h) * V + j, 0.0f);
+    }
+    if (MODE == MODE_DECODE) {
+      float *d = S.dense + ((int64_t)b * H + h) * K * V;
+      for (int e = tid; e < K * V; e += NT) d[e] = 0.0f;
+    }
+    return;
+  }
+  uint8_t *page = P.data + slot * P.page_bytes;
+  const int32_t *hm = P.head_meta + 4 * h;
+  const int code_start = hm[0], code_bytes = hm[1];
+  const int32_t *hbits = P.bits + (int64_t)h * K;
+  const int two = !P.kda && hbits[0] == 2;
+  const int tile = tile_of(P);
+  const int stride = P.offsets[(int64_t)H * K + h];
+  const int colbase = P.columns[h];
+
+  // LDS layout: staging window | red [CG][K] f32 (requantising modes) |
+  // prepared q, k, retention per row | 3 scalars
+  uint8_t *stage = smem;
+  float *red = (float *)(smem + P.stage);
+  float *qv = red + ((MODE == MODE_FUSED || MODE == MODE_WRITE) ? CG * K : 0);
+  float *kv = qv + K;
+  float *dv = kv + K;
+  float *misc = dv + K;
+
+  // ---- stage the code region (16-byte loads)
+  int shift = 0;
+  if (code_bytes > 0) shift = stage_in(page + code_start, code_bytes, stage, tid, NT);
+
+  // ---- per-row inputs: prepared q, k, retention
+  float beta = 0.0f;
+  if (MODE == MODE_FUSED || MODE == MODE_READ) {
+    const int hk = h / (H / S.HK);
+    const int64_t qb = (int64_t)b * S.q_stride + (int64_t)hk * K;
+    const int64_t kb = (int64_t)b * S.k_stride + (int64_t)hk * K;
+    // wave 0 computes the norms
+    if (tid < 64) {
+      float sq = 0.0f, sk = 0.0f;
+      for (int i = tid; i < K; i += 64) {
+        float a = load_val(S.q, S.qkv_dtype, qb + i), c = load_val(S.k, S.qkv_dtype, kb + i);
+        sq += a * a;
+        sk += c * c;
+      }
+#pragma unroll
+      for (int m = 1; m < 64; m <<= 1) {
+        sq += __shfl_xor(sq, m);
+        sk += __shfl_xor(sk, m);
+      }
+      if (tid == 0) {
+        misc[0] = S.normalize ? 1.0f / __builtin_sqrtf(sq + 1e-6f) : 1.0f;
+        misc[1] = S.normalize ? 1.0f / __builtin_sqrtf(sk + 1e-6f) : 1.0f;
+        float bt = load_val(S.beta, S.gate_dtype, (int64_t)b * H + h);
+        if (S.a_log) bt = 1.0f / (1.0f + __expf(-bt));
+        misc[2] = bt;
+      }
+    }
+    __syncthreads();
+    const float nq = misc[0], nk = misc[1];
+    beta = misc[2];
+    float alog = S.a_log ? __expf(load_val(S.a_log, S.gate_dtype, h)) : 0.0f;
+    for (int i = tid; i < K; i += NT) {
+      qv[i] = (load_val(S.q, S.qkv_dtype, qb + i) * nq) * S.scale;
+      kv[i] = load_val(S.k, S.qkv_dtype, kb + i) * nk;
+      int64_t gi = P.kda ? ((int64_t)b * H + h) * K + i : (int64_t)b * H + h;
+      float gv = load_val(S.g, S.gate_dtype, gi);
+      if (S.a_log) {
+        float u = gv + load_val(S.dt_bias, S.gate_dtype, P.kda ? (int64_t)h * K + i : (int64_t)h);
+        float sp = u > 20.0f ? u : __logf(1.0f + __expf(u < 20.0f ? u : 20.0f));
+        gv = -alog * sp;
+      }
+      dv[i] = __expf(gv);
+    }
+  } else if (MODE == MODE_WRITE) {
+    const int64_t base = ((int64_t)b * H + h) * K;
+    for (int i = tid; i < K; i += NT) {
+      kv[i] = S.s_key[base + i];
+      dv[i] = S.s_decay[base + i];
+    }
+  }
+  __syncthreads();
+
+  // ---- unpack this lane's RPT x 4 values: x = r*c*z (pivots: fp16)
+  float x[RPT][4];
+  float cj[4] = {0.f, 0.f, 0.f, 0.f};
+  if (act && colbase >= 0) {
+#pragma unroll
+    for (int c = 0; c < 4; c++) cj[c] = h2f(page_half(page, colbase + 2 * (j0 + c)));
+  }
+#pragma unroll
+  for (int r = 0; r < RPT; r++) {
+    const int i = rg + RG * r;
+    const int bi = hbits[i];
+    const int off_rel = P.offsets[(int64_t)h * K + i] - code_start;
+    if (bi == 16) {
+      const int p = shift + group_pos(off_rel, stride, tile, j0, 16);
+      uint32_t w0 = lds_word(stage, p), w1 = lds_word(stage, p + 4);
+      float d = (MODE == MODE_DECODE) ? 1.0f : dv[i];
+      x[r][0] = h2f(w0 & 0xffffu) * d;
+      x[r][1] = h2f(w0 >> 16) * d;
+      x[r][2] = h2f(w1 & 0xffffu) * d;
+      x[r][3] = h2f(w1 >> 16) * d;
+    } else {
+      const int p = shift + group_pos(off_rel, stride, tile, j0, bi);
+      const uint32_t word = lds_word(stage, p);
+      const int bc = bi < 8 ? bi : 8;
+      const int L = (1 << (bc - 1)) - 1;
+      const float norm = P.kda ? (float)(1 << (8 - bc)) : 1.0f;
+      const int64_t ro = P.rows[(int64_t)h * K + i];
+      const float rr = h2f(page_half(page, ro + (two ? 2 * (j0 / P.G) : 0)));
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        uint32_t code = (word >> (c * bi)) & ((1u << bi) - 1u);
+        float z = two ? 2.0f * (float)code - 3.0f : (float)((int)code - L) * norm;
+        if (MODE == MODE_DECODE) x[r][c] = (rr * cj[c]) * z;
+        else x[r][c] = ((rr * dv[i]) * cj[c]) * z;
+      }
+    }
+  }
+
+  if (MODE == MODE_DECODE) {
+    if (act) {
+      float *d = S.dense + ((int64_t)b * H + h) * K * V;
+#pragma unroll
+      for (int r = 0; r < RPT; r++) {
+        const int i = rg + RG * r;
+        *(float4 *)(d + (int64_t)i * V + j0) = make_float4(x[r][0], x[r][1], x[r][2], x[r][3]);
+      }
+    }
+    return;
+  }
+
+  // ---- delta = beta (v - k^T S_retained);  S' = S_retained + k delta^T
+  float delta[4];
+  if (MODE == MODE_WRITE) {
+#pragma unroll
+    for (int c = 0; c < 4; c++) delta[c] = act ? S.s_delta[((int64_t)b * H + h) * V + j0 + c] : 0.0f;
+  } else {
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      float s = 0.0f;
+#pragma unroll
+      for (int r = 0; r < RPT; r++) s += kv[rg + RG * r] * x[r][c];
+      s = rg_sum<RG>(s);
+      float vv = act ? load_val(S.v, S.qkv_dtype, (int64_t)b * S.v_stride + (int64_t)h * V + j0 + c) : 0.0f;
+      delta[c] = beta * (vv - s);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RPT; r++) {
+    const float kk = kv[rg + RG * r];
+#pragma unroll
+    for (int c = 0; c < 4; c++) x[r][c] += kk * delta[c];
+  }
+  if (MODE == MODE_FUSED || MODE == MODE_READ) {
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      float o = 0.0f;
+#pragma unroll
+      for (int r = 0; r < RPT; r++) o += qv[rg + RG * r] * x[r][c];
+      o = rg_sum<RG>(o);
+      if (act && rg == 0) store_val(S.out, S.out_dtype, ((int64_t)b * H + h) * V + j0 + c, o);
+    }
+  }
+  if (MODE == MODE_READ) {
+    if (act && rg == 0) {
+#pragma unroll
+      for (int c = 0; c < 4; c++) S.s_delta[((int64_t)b * H + h) * V + j0 + c] = delta[c];
+    }
+    const int64_t base = ((int64_t)b * H + h) * K;
+    for (int i = tid; i < K; i += NT) {
+      S.s_key[base + i] = kv[i];
+      S.s_decay[base + i] = dv[i];
+    }
+    return;
+  }
+
+  // ================= requantise (FUSED / WRITE) =================
+  // pivot rows: fp16 of the updated values, in place
+#pragma unroll
+  for (int r = 0; r < RPT; r++) {
+    const int i = rg + RG * r;
+    if (hbits[i] == 16 && act) {
+      const int off_rel = P.offsets[(int64_t)h * K + i] - code_start;
+      const int p = shift + group_pos(off_rel, stride, tile, j0, 16);
+      uint16_t *d16 = (uint16_t *)(stage + p);
+#pragma unroll
+      for (int c = 0; c < 4; c++) d16[c] = (uint16_t)f2h(x[r][c]);
+    }
+  }
+  const bool any_int = colbase >= 0;
+  if (any_int) {
+    // row |x| partial sums per lane -> red[cg][i]
+    if (act) {
+#pragma unroll
+      for (int r = 0; r < RPT; r++) {
+        const int i = rg + RG * r;
+        red[cg * K + i] = fabsf(x[r][0]) + fabsf(x[r][1]) + fabsf(x[r][2]) + fabsf(x[r][3]);
+      }
+    }
+    __syncthreads();
+    // r' per (row, group); stored in red[first cg of group][i]
+    const int NG = two ? V / P.G : 1;
+    const int Geff = two ? P.G : V;
+    const int cg_per = Geff / 4;
+    for (int e = tid; e < K * NG; e += NT) {
+      const int i = e / NG, gq = e % NG;
+      const int bi = hbits[i];
+      if (bi == 16) continue;
+      float s = 0.0f;
+      for (int q = 0; q < cg_per; q++) s += red[(gq * cg_per + q) * K + i];
+      float m = s / (float)Geff;
+      m = m < 1e-20f ? 1e-20f : m;
+      uint32_t hb;
+      float rn = fp16_scale(__builtin_sqrtf(m / P.impact[(int64_t)h * K + i]), &hb);
+      put_page_half(page, P.rows[(int64_t)h * K + i] + 2 * gq, hb);
+      red[gq * cg_per * K + i] = rn;
+    }
+    __syncthreads();
+    // scaled values s = x / (r' norm), column statistics
+    const int gq = two ? j0 / P.G : 0;
+    float U[RPT], iL[RPT];
+    float mx[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int r = 0; r < RPT; r++) {
+      const int i = rg + RG * r;
+      const int bi = hbits[i];
+      if (bi == 16) {
+        U[r] = 0.0f;
+        iL[r] = 0.0f;
+        continue;
+      }
+      const int bc = bi < 8 ? bi : 8;
+      const float norm = P.kda ? (float)(1 << (8 - bc)) : 1.0f;
+      const float rn = red[gq * (two ? P.G / 4 : CG) * K + i] * norm;
+      const float inv = 1.0f / rn;
+      const float w = P.impact[(int64_t)h * K + i];
+      U[r] = (w * w) * (rn * rn);
+      iL[r] = two ? (1.0f / 3.0f) : 1.0f / (float)((1 << (bc - 1)) - 1);
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        x[r][c] *= inv;
+        mx[c] = fmaxf(mx[c], fabsf(x[r][c]) * iL[r]);
+      }
+    }
+    float ic0[4], c0[4], num[4], den[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      c0[c] = fp16_scale(rg_max<RG>(mx[c]), nullptr);
+      ic0[c] = 1.0f / c0[c];
+      num[c] = 0.0f;
+      den[c] = 0.0f;
+    }
+#pragma unroll
+    for (int r = 0; r < RPT; r++) {
+      if (iL[r] == 0.0f) continue;
+      const float Lf = two ? 3.0f : 1.0f / iL[r];
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        float y = x[r][c] * ic0[c];
+        float z;
+        if (two) z = (y >= 0.0f ? 1.0f : -1.0f) * (fabsf(y) >= 2.0f ? 3.0f : 1.0f);
+        else z = fminf(fmaxf(__builtin_rintf(y), -Lf), Lf);
+        float t = U[r] * z;
+        num[c] += t * x[r][c];
+        den[c] += t * z;
+      }
+    }
+    float icn[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      float n = rg_sum<RG>(num[c]), d = rg_sum<RG>(den[c]);
+      float dc = d < 1e-30f ? 1e-30f : d;
+      uint32_t hb;
+      float cc = fp16_scale(d > 0.0f ? n / dc : c0[c], &hb);
+      icn[c] = 1.0f / cc;
+      if (act && rg == 0) put_page_half(page, colbase + 2 * (j0 + c), hb);
+    }
+    // final codes -> staging
+#pragma unroll
+    for (int r = 0; r < RPT; r++) {
+      const int i = rg + RG * r;
+      const int bi = hbits[i];
+      if (bi == 16 || !act) continue;
+      const int bc = bi < 8 ? bi : 8;
+      const int L = (1 << (bc - 1)) - 1;
+      uint32_t word = 0;
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        float y = x[r][c] * icn[c];
+        uint32_t code;
+        if (two) {
+          code = y >= 0.0f ? (fabsf(y) >= 2.0f ? 3u : 2u) : (fabsf(y) >= 2.0f ? 0u : 1u);
+        } else {
+          float z = fminf(fmaxf(__builtin_rintf(y), -(float)L), (float)L);
+          code = (uint32_t)((int)z + L);
+        }
+        word |= code << (c * bi);
+      }
+      const int off_rel = P.offsets[(int64_t)h * K + i] - code_start;
+      lds_put_bytes(stage, shift + group_pos(off_rel, stride, tile, j0, bi), word, bi / 2);
+    }
+  }
+  __syncthreads();
+  if (code_bytes > 0) stage_out(page + code_start, code_bytes, stage, tid, NT);
+}
+
+
+// =====================================================================
+// GDN fast path: K = V = 128 and one width per head (2/4/6/8-bit codes or
+// an FP16 pivot head), every region 16-byte aligned.  The width is uniform
+// per workgroup, so it is a scalar branch into a body compiled for that
+// width.  Lane layout: tid = 8*cg + rg, rg = row group in lane bits 0-2, so
+// reductions over the 8 row groups (column statistics) are DPP quad and
+// half-row exchanges; wave w holds column groups 8w..8w+7.
+//
+// Readout algebra: with x_ij = a_i c_j (code_ij - L), a_i = r_i * decay,
+//   k^T x  = c_j (sum_i k_i a_i code_ij - L sum_i k_i a_i)
+//   q^T x' = c_j (sum_i q_i a_i code_ij - L sum_i q_i a_i) + delta_j q^T k
+// so the foreground needs two FMAs per value and no dequantised tile.
+// The writer works on inner_ij = x'_ij / c_j = a_i z_ij + k_i delta_j / c_j.
+// =====================================================================
+namespace fast {
+
+constexpr int FK = 128, FV = 128, FNT = 256, FRPT = 16;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+// sum / max over the 8 row-group lanes (lane bits 0-2)
+__device__ __forceinline__ float rg8_sum(float x) {
+  x += dpp<0xB1>(x);   // quad_perm [1,0,3,2]
+  x += dpp<0x4E>(x);   // quad_perm [2,3,0,1]
+  x += dpp<0x141>(x);  // row_half_mirror
+  return x;
+}
+__device__ __forceinline__ float rg8_max(float x) {
+  x = fmaxf(x, dpp<0xB1>(x));
+  x = fmaxf(x, dpp<0x4E>(x));
+  x = fmaxf(x, dpp<0x141>(x));
+  return x;
+}
+
+__device__ __forceinline__ float hw_h2f(uint32_t h) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+// clamp(2^-24, 65504) then round to half (v_cvt_f16_f32, round to nearest
+// even; f16 denormals are preserved in this kernel's float mode).
+__device__ __forceinline__ float hw_fp16_scale(float x, uint32_t *hbits) {
+  const float c = __builtin_amdgcn_fmed3f(x, 5.9604644775390625e-08f, 65504.0f);
+  const _Float16 h = (_Float16)c;
+  if (hbits) *hbits = __builtin_bit_cast(uint16_t, h);
+  return (float)h;
+}
+
+// hardware reciprocal (1 ulp); the decode step's requantisation only needs
+// quotients accurate to a few ulp
+__device__ __forceinline__ float rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+
+struct Ctx {
+  uint8_t *page;
+  uint8_t *code;   // staged code region
+  uint8_t *rst;    // staged row scales
+  uint8_t *cst;    // staged column scales
+  float *qraw, *kraw, *wv, *misc, *red, *rnew;
+  float *ks, *qs, *as, *ir, *uu;  // per-row prepared k, q, r*retention, 1/r', w^2 r'^2
+  int b, h, tid, rg, cg, wave, j0, blk, sub;
+  int code_start, code_bytes, row_start, row_bytes, colbase;
+};
+
+// Per-row inputs, once per workgroup into LDS (threads 0..127, row i = tid):
+// prepared q (scaled), prepared k, and a_i = r_i * retention per value group.
+template <int MODE>
+__device__ __forceinline__ void row_setup(const StepDev &S, const Ctx &C, int NG) {
+  if (C.tid < FK) {
+    const int i = C.tid;
+    float nq = 1.0f, nk = 1.0f;
+    if (MODE != MODE_WRITE && S.normalize) {
+      nq = 1.0f / __builtin_sqrtf((C.misc[8] + C.misc[10]) + 1e-6f);
+      nk = 1.0f / __builtin_sqrtf((C.misc[9] + C.misc[11]) + 1e-6f);
+    }
+    const float k = MODE == MODE_WRITE ? C.kraw[i] : C.kraw[i] * nk;
+    C.ks[i] = k;
+    C.qs[i] = MODE == MODE_WRITE ? 0.0f : (C.qraw[i] * nq) * S.scale;
+    const uint16_t *r16 = (const uint16_t *)C.rst;
+    for (int g = 0; g < NG; g++) C.as[i * NG + g] = hw_h2f(r16[i * NG + g]) * C.misc[1];
+  }
+}
+
+template <int MODE>
+__device__ __forceinline__ void store_out(const PoolDev &P, const StepDev &S, const Ctx &C, const float *o,
+                                          const float *delta) {
+  const int64_t base = ((int64_t)C.b * P.H + C.h) * FV + C.j0;
+  if (C.rg == 0) {
+    if (MODE == MODE_FUSED || MODE == MODE_READ) {
+#pragma unroll
+      for (int c = 0; c < 4; c++) store_val(S.out, S.out_dtype, base + c, o[c]);
+    }
+    if (MODE == MODE_READ) {
+#pragma unroll
+      for (int c = 0; c < 4; c++) S.s_delta[base + c] = delta[c];
+    }
+  }
+}
+
+// stage out the code region and (integer heads) the row and column scales
+__device__ __forceinline__ void stage_back(const Ctx &C, bool scales) {
+  const int ncode = C.code_bytes >> 4, nrow = scales ? (C.row_bytes >> 4) : 0,
+            ncol = (scales && C.colbase >= 0) ? FV * 2 / 16 : 0;
+  for (int c = C.tid; c < ncode + nrow + ncol; c += FNT) {
+    if (c < ncode)
+      ((uint4 *)(C.page + C.code_start))[c] = ((const uint4 *)C.code)[c];
+    else if (c < ncode + nrow)
+      ((uint4 *)(C.page + C.row_start))[c - ncode] = ((const uint4 *)C.rst)[c - ncode];
+    else
+      ((uint4 *)(C.page + C.colbase))[c - ncode - nrow] = ((const uint4 *)C.cst)[c - ncode - nrow];
+  }
+}
+
+template <int W, int MODE>
+__device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx &C) {
+#pragma clang fp contract(off)
+  constexpr int L = W == 2 ? 3 : (1 << (W - 1)) - 1;
+  constexpr float ZS = W == 2 ? 2.0f : 1.0f;   // z = ZS*code - ZO
+  constexpr float ZO = W == 2 ? 3.0f : (float)L;
+  constexpr int SEG = 2 * W;                   // bytes of one row's 16-value segment
+  constexpr int BLK = FK * SEG;                // bytes of one 16-column block
+  constexpr uint32_t MASK = (1u << W) - 1u;
+  const float beta = C.misc[0];
+  const int NG = W == 2 ? FV / P.G : 1;
+  const int g = W == 2 ? C.j0 / P.G : 0;
+  const uint16_t *c16 = (const uint16_t *)C.cst;
+  row_setup<MODE>(S, C, NG);
+  __syncthreads();
+
+  float cj[4];
+#pragma unroll
+  for (int c = 0; c < 4; c++) cj[c] = hw_h2f(c16[C.j0 + c]);
+
+  // ---- foreground: codes, k^T x and q^T x sums
+  float cf[FRPT][4];
+  float aK[4] = {0.f, 0.f, 0.f, 0.f}, aQ[4] = {0.f, 0.f, 0.f, 0.f};
+  float sKA = 0.f, sQA = 0.f, sQK = 0.f;
+  // rows rg + 8r are 8*SEG bytes apart: one base address, immediate offsets
+  const int pos0 = C.blk * BLK + C.rg * SEG + C.sub * (W / 2);
+  const uint32_t *w32 = (const uint32_t *)(C.code + (pos0 & ~3));
+  const uint32_t sh = (uint32_t)(pos0 & 3) * 8u;
+#pragma unroll
+  for (int r = 0; r < FRPT; r++) {
+    const int i = C.rg + 8 * r;
+    uint32_t word;
+    if (W == 8) word = w32[r * 4 * W];  // 8 rows = 16W bytes = 4W dwords
+    else if (W == 4) word = *(const uint16_t *)(C.code + pos0 + r * 8 * SEG);
+    else if (W == 2) word = C.code[pos0 + r * 8 * SEG];
+    else word = __builtin_amdgcn_alignbit(w32[r * 4 * W + 1], w32[r * 4 * W], sh);
+#pragma unroll
+    for (int c = 0; c < 4; c++) cf[r][c] = (float)((word >> (c * W)) & MASK);
+    const float a = C.as[i * NG + g], k = C.ks[i];
+    const float ka = k * a;
+#pragma unroll
+    for (int c = 0; c < 4; c++) aK[c] = fmaf(ka, cf[r][c], aK[c]);
+    sKA += ka;
+    if (MODE != MODE_WRITE) {
+      const float q = C.qs[i];
+      const float qa = q * a;
+#pragma unroll
+      for (int c = 0; c < 4; c++) aQ[c] = fmaf(qa, cf[r][c], aQ[c]);
+      sQA += qa;
+      sQK = fmaf(q, k, sQK);
+    }
+  }
+  sKA = rg8_sum(sKA);
+  float delta[4], o[4];
+  if (MODE == MODE_WRITE) {
+    const int64_t base = ((int64_t)C.b * P.H + C.h) * FV + C.j0;
+#pragma unroll
+    for (int c = 0; c < 4; c++) delta[c] = S.s_delta[base + c];
+  } else {
+    sQA = rg8_sum(sQA);
+    sQK = rg8_sum(sQK);
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const float kS = cj[c] * fmaf(ZS, rg8_sum(aK[c]), -ZO * sKA);
+      const float vv = load_val(S.v, S.qkv_dtype, (int64_t)C.b * S.v_stride + (int64_t)C.h * FV + C.j0 + c);
+      delta[c] = beta * (vv - kS);
+      o[c] = fmaf(delta[c], sQK, cj[c] * fmaf(ZS, rg8_sum(aQ[c]), -ZO * sQA));
+    }
+    store_out<MODE>(P, S, C, o, delta);
+  }
+  if (MODE == MODE_READ) return;
+
+  // ---- writer: inner = x'/c = a z + k delta/c, row sums of |x'|
+  float dj[4];
+#pragma unroll
+  for (int c = 0; c < 4; c++) dj[c] = delta[c] * rcp(cj[c]);
+  float rowp[FRPT];
+#pragma unroll
+  for (int r = 0; r < FRPT; r++) {
+    const int i = C.rg + 8 * r;
+    const float a = C.as[i * NG + g], k = C.ks[i];
+    const float A = ZS * a, mL = -ZO * a;
+    float acc = 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const float inner = fmaf(A, cf[r][c], fmaf(k, dj[c], mL));
+      cf[r][c] = inner;
+      acc = fmaf(cj[c], fabsf(inner), acc);
+    }
+    rowp[r] = acc;
+  }
+  // reduce-scatter over the wave's 8 column groups (lane bits 3,4,5)
+  const int b3 = (C.tid >> 3) & 1, b4 = (C.tid >> 4) & 1, b5 = (C.tid >> 5) & 1;
+  float p8[8], p4[4], p2[2];
+#pragma unroll
+  for (int r = 0; r < 8; r++) {
+    const float keep = b5 ? rowp[r + 8] : rowp[r], send = b5 ? rowp[r] : rowp[r + 8];
+    p8[r] = keep + __shfl_xor(send, 32);
+  }
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const float keep = b4 ? p8[r + 4] : p8[r], send = b4 ? p8[r] : p8[r + 4];
+    p4[r] = keep + __shfl_xor(send, 16);
+  }
+#pragma unroll
+  for (int r = 0; r < 2; r++) {
+    const float keep = b3 ? p4[r + 2] : p4[r], send = b3 ? p4[r] : p4[r + 2];
+    p2[r] = keep + dpp<0x128>(send);  // row_ror:8 == lane xor 8 within 16
+  }
+#pragma unroll
+  for (int q = 0; q < 2; q++) {
+    const int r = 8 * b5 + 4 * b4 + 2 * b3 + q;
+    C.red[C.wave * FK + C.rg + 8 * r] = p2[q];
+  }
+  __syncthreads();
+  {
+    const int Geff = W == 2 ? P.G : FV;
+    const int wpg = Geff / 32;  // waves per value group
+    for (int e = C.tid; e < FK * NG; e += FNT) {
+      const int i = e / NG, gq = e % NG;
+      float sum = C.red[(gq * wpg) * FK + i];
+      for (int w = 1; w < wpg; w++) sum += C.red[(gq * wpg + w) * FK + i];
+      float m = sum / (float)Geff;
+      m = m < 1e-20f ? 1e-20f : m;
+      uint32_t hb;
+      const float wi = C.wv[i];
+      const float rn = hw_fp16_scale(__builtin_sqrtf(m / wi), &hb);
+      C.ir[e] = rcp(rn);
+      C.uu[e] = (wi * wi) * (rn * rn);
+      ((uint16_t *)C.rst)[e] = (uint16_t)hb;
+    }
+  }
+  __syncthreads();
+  // ---- scaled values s = x'/r', column max
+  float mx[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int r = 0; r < FRPT; r++) {
+    const float ir = C.ir[(C.rg + 8 * r) * NG + g];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const float sv = cf[r][c] * (cj[c] * ir);
+      cf[r][c] = sv;
+      mx[c] = fmaxf(mx[c], fabsf(sv));
+    }
+  }
+  float c0[4], ic0[4], num[4] = {0.f, 0.f, 0.f, 0.f}, den[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    c0[c] = hw_fp16_scale(rg8_max(mx[c]) * (1.0f / (float)L), nullptr);
+    ic0[c] = rcp(c0[c]);
+  }
+#pragma unroll
+  for (int r = 0; r < FRPT; r++) {
+    const float U = C.uu[(C.rg + 8 * r) * NG + g];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const float y = cf[r][c] * ic0[c];
+      float z;
+      if (W == 2) {
+        const float mag = fabsf(y) >= 2.0f ? 3.0f : 1.0f;
+        z = y >= 0.0f ? mag : -mag;
+      } else {
+        z = __builtin_amdgcn_fmed3f(__builtin_rintf(y), -(float)L, (float)L);
+      }
+      const float t = U * z;
+      num[c] = fmaf(t, cf[r][c], num[c]);
+      den[c] = fmaf(t, z, den[c]);
+    }
+  }
+  float ic[4];
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    const float n = rg8_sum(num[c]), d = rg8_sum(den[c]);
+    const float dc = d < 1e-30f ? 1e-30f : d;
+    uint32_t hb;
+    const float cc = hw_fp16_scale(d > 0.0f ? n * rcp(dc) : c0[c], &hb);
+    ic[c] = rcp(cc);
+    if (C.rg == 0) ((uint16_t *)C.cst)[C.j0 + c] = (uint16_t)hb;
+  }
+  // ---- final codes, packed back into the staged region
+#pragma unroll
+  for (int r = 0; r < FRPT; r++) {
+    const int i = C.rg + 8 * r;
+    uint32_t word = 0;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      uint32_t code;
+      if (W == 2) {
+        const float y = cf[r][c] * ic[c];
+        const bool big = fabsf(y) >= 2.0f;
+        code = y >= 0.0f ? (big ? 3u : 2u) : (big ? 0u : 1u);
+      } else {
+        // floor(y + L + 1/2) saturated to [0, 2L]: the level of rint(y) + L
+        code = (uint32_t)__builtin_amdgcn_fmed3f(fmaf(cf[r][c], ic[c], (float)L + 0.5f), 0.0f,
+                                                 (float)(2 * L) + 0.5f);
+      }
+      word |= code << (c * W);
+    }
+    const int pos = pos0 + r * 8 * SEG;
+    (void)i;
+    if (W == 8) *(uint32_t *)(C.code + pos) = word;
+    else if (W == 4) *(uint16_t *)(C.code + pos) = (uint16_t)word;
+    else if (W == 2) C.code[pos] = (uint8_t)word;
+    else {
+      // 3 bytes at an odd or even offset: one aligned half-word and one byte
+      const int odd = C.sub & 1;
+      const uint32_t half = odd ? (word >> 8) : (word & 0xffffu);
+      const uint32_t byte = odd ? (word & 0xffu) : (word >> 16);
+      *(uint16_t *)(C.code + pos + odd) = (uint16_t)half;
+      C.code[pos + 2 - 2 * odd] = (uint8_t)byte;
+    }
+  }
+  __syncthreads();
+  stage_back(C, true);
+}
+
+template <int MODE>
+__device__ __forceinline__ void pivot_body(const PoolDev &P, const StepDev &S, Ctx &C) {
+#pragma clang fp contract(off)
+  constexpr int SEG = 32, BLK = FK * SEG;
+  const float beta = C.misc[0], decay = C.misc[1];
+  row_setup<MODE>(S, C, 0);
+  __syncthreads();
+  float qi[FRPT], ki[FRPT];
+#pragma unroll
+  for (int r = 0; r < FRPT; r++) {
+    qi[r] = C.qs[C.rg + 8 * r];
+    ki[r] = C.ks[C.rg + 8 * r];
+  }
+  float x[FRPT][4];
+  float sk[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int r = 0; r < FRPT; r++) {
+    const int i = C.rg + 8 * r;
+    const uint2 hv = *(const uint2 *)(C.code + C.blk * BLK + i * SEG + C.sub * 8);
+    x[r][0] = hw_h2f(hv.x & 0xffffu) * decay;
+    x[r][1] = hw_h2f(hv.x >> 16) * decay;
+    x[r][2] = hw_h2f(hv.y & 0xffffu) * decay;
+    x[r][3] = hw_h2f(hv.y >> 16) * decay;
+#pragma unroll
+    for (int c = 0; c < 4; c++) sk[c] = fmaf(ki[r], x[r][c], sk[c]);
+  }
+  float delta[4], o[4];
+  const int64_t base = ((int64_t)C.b * P.H + C.h) * FV + C.j0;
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    if (MODE == MODE_WRITE) {
+      delta[c] = S.s_delta[base + c];
+    } else {
+      const float vv = load_val(S.v, S.qkv_dtype, (int64_t)C.b * S.v_stride + (int64_t)C.h * FV + C.j0 + c);
+      delta[c] = beta * (vv - rg8_sum(sk[c]));
+    }
+  }
+  float oq[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int r = 0; r < FRPT; r++)
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      x[r][c] = fmaf(ki[r], delta[c], x[r][c]);
+      oq[c] = fmaf(qi[r], x[r][c], oq[c]);
+    }
+  if (MODE != MODE_WRITE) {
+#pragma unroll
+    for (int c = 0; c < 4; c++) o[c] = rg8_sum(oq[c]);
+    store_out<MODE>(P, S, C, o, delta);
+  }
+  if (MODE == MODE_READ) return;
+#pragma unroll
+  for (int r = 0; r < FRPT; r++) {
+    const int i = C.rg + 8 * r;
+    uint2 hv;
+    hv.x = f2h(x[r][0]) | (f2h(x[r][1]) << 16);
+    hv.y = f2h(x[r][2]) | (f2h(x[r][3]) << 16);
+    *(uint2 *)(C.code + C.blk * BLK + i * SEG + C.sub * 8) = hv;
+  }
+  __syncthreads();
+  stage_back(C, false);
+}
+
+}  // namespace fast
+
+template <int MODE>
+__global__ __launch_bounds__(256) void gdn128_kernel(PoolDev P,
+                                                                                            StepDev S) {
+  using namespace fast;
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int H = P.H;
+  Ctx C;
+  C.b = blockIdx.x / H;
+  C.h = blockIdx.x % H;
+  C.tid = threadIdx.x;
+  C.rg = C.tid & 7;
+  C.cg = C.tid >> 3;
+  C.wave = C.tid >> 6;
+  C.j0 = 4 * C.cg;
+  C.blk = C.cg >> 2;
+  C.sub = C.cg & 3;
+  int64_t slot;
+  if (MODE == MODE_WRITE) {
+    slot = S.s_slots[C.b];
+  } else {
+    slot = load_slot(S.slots, S.slots_dtype, C.b);
+    if (MODE == MODE_READ && C.h == 0 && C.tid == 0) S.s_slots[C.b] = slot;
+  }
+  if (slot <= 0 || slot >= P.num_slots) {
+    if (MODE == MODE_FUSED || MODE == MODE_READ)
+      for (int j = C.tid; j < FV; j += FNT) store_val(S.out, S.out_dtype, ((int64_t)C.b * H + C.h) * FV + j, 0.0f);
+    return;
+  }
+  C.page = P.data + slot * P.page_bytes;
+  const int32_t *hm = P.head_meta + 4 * C.h;
+  C.code_start = hm[0];
+  C.code_bytes = hm[1];
+  C.row_start = hm[2];
+  C.row_bytes = hm[3];
+  C.colbase = P.columns[C.h];
+  const int W = P.bits[(int64_t)C.h * FK];
+  C.code = smem;
+  C.rst = smem + P.stage;
+  C.cst = C.rst + P.rstage;
+  C.qraw = (float *)(C.cst + 2 * FV);
+  C.kraw = C.qraw + FK;
+  C.wv = C.kraw + FK;
+  C.misc = C.wv + FK;
+  C.red = C.misc + 16;
+  C.ks = C.red + 4 * FK;
+  C.qs = C.ks + FK;
+  const int ngm = P.G >= 32 ? FV / P.G : 1;
+  C.as = C.qs + FK;
+  C.ir = C.as + FK * ngm;
+  C.uu = C.ir + FK * ngm;
+  C.rnew = C.uu;
+
+  // stage code, row-scale and column-scale regions (16-byte aligned)
+  {
+    const int ncode = C.code_bytes >> 4, nrow = C.row_bytes >> 4, ncol = C.colbase >= 0 ? 2 * FV / 16 : 0;
+    for (int c = C.tid; c < ncode + nrow + ncol; c += FNT) {
+      if (c < ncode)
+        ((uint4 *)C.code)[c] = ((const uint4 *)(C.page + C.code_start))[c];
+      else if (c < ncode + nrow)
+        ((uint4 *)C.rst)[c - ncode] = ((const uint4 *)(C.page + C.row_start))[c - ncode];
+      else
+        ((uint4 *)C.cst)[c - ncode - nrow] = ((const uint4 *)(C.page + C.colbase))[c - ncode - nrow];
+    }
+  }
+  // inputs: raw q, k rows, norms, beta and the head's retention
+  const int64_t bh = (int64_t)C.b * H + C.h;
+  if (MODE == MODE_WRITE) {
+    if (C.tid < FK) C.kraw[C.tid] = S.s_key[bh * FK + C.tid];
+    if (C.tid == FK) C.misc[1] = S.s_decay[bh * FK];
+  } else {
+    if (C.tid < FK) {
+      const int hk = C.h / (H / S.HK);
+      const float qv = load_val(S.q, S.qkv_dtype, (int64_t)C.b * S.q_stride + (int64_t)hk * FK + C.tid);
+      const float kv = load_val(S.k, S.qkv_dtype, (int64_t)C.b * S.k_stride + (int64_t)hk * FK + C.tid);
+      C.qraw[C.tid] = qv;
+      C.kraw[C.tid] = kv;
+      float sq = qv * qv, sk = kv * kv;
+#pragma unroll
+      for (int m = 1; m < 64; m <<= 1) {
+        sq += __shfl_xor(sq, m);
+        sk += __shfl_xor(sk, m);
+      }
+      if ((C.tid & 63) == 0) {
+        C.misc[8 + 2 * (C.tid >> 6)] = sq;
+        C.misc[9 + 2 * (C.tid >> 6)] = sk;
+      }
+    } else if (C.tid == FK) {
+      float bt = load_val(S.beta, S.gate_dtype, bh);
+      float gv = load_val(S.g, S.gate_dtype, bh);
+      if (S.a_log) {
+        bt = 1.0f / (1.0f + __expf(-bt));
+        const float u = gv + load_val(S.dt_bias, S.gate_dtype, C.h);
+        const float sp = u > 20.0f ? u : __logf(1.0f + __expf(u < 20.0f ? u : 20.0f));
+        gv = -__expf(load_val(S.a_log, S.gate_dtype, C.h)) * sp;
+      }
+      C.misc[0] = bt;
+      C.misc[1] = __expf(gv);
+    }
+  }
+  if (C.tid >= FK && C.tid < 2 * FK) C.wv[C.tid - FK] = P.impact[(int64_t)C.h * FK + C.tid - FK];
+  __syncthreads();
+  if (MODE == MODE_READ && C.tid < FK) {
+    // writer hand-off: prepared key rows and per-row retention
+    float nk = 1.0f;
+    if (S.normalize) nk = 1.0f / __builtin_sqrtf((C.misc[9] + C.misc[11]) + 1e-6f);
+    S.s_key[bh * FK + C.tid] = C.kraw[C.tid] * nk;
+    S.s_decay[bh * FK + C.tid] = C.misc[1];
+  }
+  switch (W) {
+    case 2: int_body<2, MODE>(P, S, C); break;
+    case 4: int_body<4, MODE>(P, S, C); break;
+    case 6: int_body<6, MODE>(P, S, C); break;
+    case 8: int_body<8, MODE>(P, S, C); break;
+    default: pivot_body<MODE>(P, S, C); break;
+  }
+}
+
+__global__ void clear_kernel(uint8_t *data, int64_t page_bytes, int64_t num_slots, const void *slots,
+                             int dtype) {
+  int64_t s = load_slot(slots, dtype, blockIdx.y);
+  if (s < 0) s += num_slots;
+  if (s < 0 || s >= num_slots) return;
+  uint8_t *p = data + s * page_bytes;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < page_bytes;
+       e += (int64_t)gridDim.x * blockDim.x)
+    p[e] = 0;
+}
+
+__global__ void gather_kernel(const uint8_t *data, int64_t page_bytes, int64_t num_slots, const void *slots,
+                              int dtype, uint8_t *temp, int scatter) {
+  int64_t s = load_slot(slots, dtype, blockIdx.y);
+  if (s < 0) s += num_slots;
+  if (s < 0 || s >= num_slots) return;
+  uint8_t *t = temp + (int64_t)blockIdx.y * page_bytes;
+  uint8_t *p = (uint8_t *)data + s * page_bytes;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < page_bytes;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    if (scatter) p[e] = t[e];
+    else t[e] = p[e];
+  }
+}
+
+// ------------------------------------------------------------ host side
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char *msg) {
+  snprintf(g_err, sizeof(g_err), "%s", msg);
+  return code;
+}
+
+int check_launch(const char *what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    snprintf(g_err, sizeof(g_err), "%s: %s", what, hipGetErrorString(e));
+    return (int)e;
+  }
+  return 0;
+}
+
+bool pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
+
+int validate_pool(const sq_pool *p) {
+  if (!p || !p->data || !p->bits || !p->offsets || !p->rows || !p->columns || !p->impact || !p->head_meta)
+    return fail(SQ_EINVAL, "pool: null pointer");
+  if (p->heads < 1 || p->page_bytes <= 0 || p->num_slots < 1) return fail(SQ_EINVAL, "pool: bad sizes");
+  if (!pow2(p->keys) || !pow2(p->values) || p->values < 4 || p->keys < 4)
+    return fail(SQ_ESHAPE, "pool: K and V must be powers of two >= 4");
+  if ((int64_t)p->keys * p->values > 16384 || p->keys > 256 || p->values > 256)
+    return fail(SQ_ESHAPE, "pool: K*V above 16384 (K, V <= 256) is not supported");
+  if (!p->kda && (p->group < 4 || p->values % p->group))
+    return fail(SQ_ESHAPE, "pool: GDN value_group_size must divide V and be >= 4");
+  if (p->storage != 0) return fail(SQ_ESTORAGE, "pool: only packed storage is implemented");
+  return 0;
+}
+
+PoolDev to_dev(const sq_pool *p) {
+  PoolDev d;
+  d.data = p->data;
+  d.page_bytes = p->page_bytes;
+  d.num_slots = p->num_slots;
+  d.bits = p->bits;
+  d.offsets = p->offsets;
+  d.rows = p->rows;
+  d.columns = p->columns;
+  d.head_meta = p->head_meta;
+  d.impact = p->impact;
+  d.H = p->heads;
+  d.K = p->keys;
+  d.V = p->values;
+  d.G = p->group > 0 ? p->group : p->values;
+  d.kda = p->kda;
+  d.stage = (p->max_code_bytes + 47) & ~15;
+  d.rstage = (p->max_row_bytes + 15) & ~15;
+  d.fast = p->flags & SQ_POOL_FAST_GDN128;
+  return d;
+}
+
+int stage_bytes(const sq_pool *p) { return (p->max_code_bytes + 47) & ~15; }
+
+template <int MODE>
+int launch_step_mode(const sq_pool *pool, StepDev sd, int64_t batch, hipStream_t st) {
+  PoolDev pd = to_dev(pool);
+  if (MODE != MODE_DECODE && pd.fast) {
+    const int ng_max = pool->group >= 32 ? 128 / pool->group : 1;
+    // staging | rows | columns | q,k raw + w | misc | red | ks, qs | as, ir, uu per (row, group)
+    size_t lds = (size_t)pd.stage + pd.rstage + 2 * 128 + 3 * 128 * 4 + 16 * 4 + 4 * 128 * 4 + 2 * 128 * 4 +
+                 (size_t)3 * 128 * ng_max * 4;
+    hipLaunchKernelGGL((gdn128_kernel<MODE>), dim3((unsigned)(batch * pool->heads)), dim3(256), lds, st, pd, sd);
+    return check_launch("gdn128_kernel");
+  }
+  const int K = pool->keys, V = pool->values;
+  const int RG = K >= 8 ? 8 : 4;
+  const int RPT = K / RG;
+  int NT = RG * (V / 4);
+  NT = (NT + 63) / 64 * 64;
+  size_t lds = (size_t)stage_bytes(pool);
+  if (MODE == MODE_FUSED || MODE == MODE_WRITE) lds += (size_t)(V / 4) * K * 4;
+  lds += (size_t)3 * K * 4 + 64;
+  dim3 grid((unsigned)(batch * pool->heads));
+#define SQ_LAUNCH(R, G_)                                                                    \
+  hipLaunchKernelGGL((step_kernel<R, G_, MODE>), grid, dim3(NT), lds, st, pd, sd);         \
+  break;
+  switch (RG * 1000 + RPT) {
+    case 4001: SQ_LAUNCH(1, 4)
+    case 8001: SQ_LAUNCH(1, 8)
+    case 8002: SQ_LAUNCH(2, 8)
+    case 8004: SQ_LAUNCH(4, 8)
+    case 8008: SQ_LAUNCH(8, 8)
+    case 8016: SQ_LAUNCH(16, 8)
+    case 8032: SQ_LAUNCH(32, 8)
+    default: return fail(SQ_ESHAPE, "unsupported key dimension");
+  }
+#undef SQ_LAUNCH
+  return check_launch("step_kernel");
+}
+
+int fill_step(const sq_pool *pool, const sq_step_args *a, StepDev &sd) {
+  if (!a || !a->q || !a->k || !a->v || !a->g || !a->beta || !a->out || !a->slots)
+    return fail(SQ_EINVAL, "step: null input pointer");
+  if (a->batch < 0) return fail(SQ_EINVAL, "step: negative batch");
+  if (a->key_heads < 1 || pool->heads % a->key_heads) return fail(SQ_EINVAL, "step: heads not divisible by key heads");
+  if ((a->a_log == nullptr) != (a->dt_bias == nullptr)) return fail(SQ_EINVAL, "step: a_log and dt_bias go together");
+  if (a->qkv_dtype < 0 || a->qkv_dtype > 2 || a->gate_dtype < 0 || a->gate_dtype > 2 || a->out_dtype < 0 ||
+      a->out_dtype > 2 || (a->slots_dtype != SQ_I32 && a->slots_dtype != SQ_I64))
+    return fail(SQ_EINVAL, "step: bad dtype code");
+  memset(&sd, 0, sizeof(sd));
+  sd.q = a->q;
+  sd.k = a->k;
+  sd.v = a->v;
+  sd.g = a->g;
+  sd.beta = a->beta;
+  sd.a_log = a->a_log;
+  sd.dt_bias = a->dt_bias;
+  sd.out = a->out;
+  sd.slots = a->slots;
+  sd.q_stride = a->q_stride;
+  sd.k_stride = a->k_stride;
+  sd.v_stride = a->v_stride;
+  sd.HK = a->key_heads;
+  sd.qkv_dtype = a->qkv_dtype;
+  sd.gate_dtype = a->gate_dtype;
+  sd.out_dtype = a->out_dtype;
+  sd.slots_dtype = a->slots_dtype;
+  sd.normalize = a->normalize;
+  sd.scale = a->scale;
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sq_abi_version(void) { return SQ_ABI_VERSION; }
+
+const char *sq_last_error(void) { return g_err; }
+
+int sq_encode(const sq_pool *pool, const float *state, const void *slots, int32_t slots_dtype, int64_t batch,
+              void *stream) {
+  int rc = validate_pool(pool);
+  if (rc) return rc;
+  if (batch == 0) return 0;
+  if (!state || !slots || batch < 0) return fail(SQ_EINVAL, "encode: null pointer or negative batch");
+  if (slots_dtype != SQ_I32 && slots_dtype != SQ_I64) return fail(SQ_EINVAL, "encode: slots dtype");
+  PoolDev pd = to_dev(pool);
+  const int NG = (!pool->kda) ? pool->values / pd.G : 1;
+  size_t lds = (size_t)stage_bytes(pool) + (size_t)pool->keys * NG * 4 + 16;
+  const int NT = pool->values < 64 ? 64 : pool->values;  // one lane per value column
+  hipLaunchKernelGGL(encode_kernel, dim3((unsigned)(batch * pool->heads)), dim3(NT), lds, (hipStream_t)stream, pd,
+                     state, slots, slots_dtype);
+  return check_launch("encode_kernel");
+}
+
+int sq_decode_dense(const sq_pool *pool, const void *slots, int32_t slots_dtype, int64_t batch, float *state,
+                    void *stream) {
+  int rc = validate_pool(pool);
+  if (rc) return rc;
+  if (batch == 0) return 0;
+  if (!state || !slots || batch < 0) return fail(SQ_EINVAL, "decode: null pointer or negative batch");
+  if (slots_dtype != SQ_I32 && slots_dtype != SQ_I64) return fail(SQ_EINVAL, "decode: slots dtype");
+  StepDev sd;
+  memset(&sd, 0, sizeof(sd));
+  sd.slots = slots;
+  sd.slots_dtype = slots_dtype;
+  sd.dense = state;
+  return launch_step_mode<MODE_DECODE>(pool, sd, batch, (hipStream_t)stream);
+}
+
+int sq_decode_step(const sq_pool *pool, const sq_step_args *args, void *stream) {
+  int rc = validate_pool(pool);
+  if (rc) return rc;
+  StepDev sd;
+  rc = fill_step(pool, args, sd);
+  if (rc) return rc;
+  if (args->batch == 0) return 0;
+  return launch_step_mode<MODE_FUSED>(pool, sd, args->batch, (hipStream_t)stream);
+}
+
+int sq_decode_readout(const sq_pool *pool, const sq_step_args *args, const sq_writeback_scratch *scratch,
+                      void *stream) {
+  int rc = validate_pool(pool);
+  if (rc) return rc;
+  StepDev sd;
+  rc = fill_step(pool, args, sd);
+  if (rc) return rc;
+  if (!scratch || !scratch->key || !scratch->decay || !scratch->delta || !scratch->stable_slots)
+    return fail(SQ_EINVAL, "readout: null scratch");
+  if (args->batch > scratch->capacity) return fail(SQ_EINVAL, "readout: batch exceeds scratch capacity");
+  if (args->batch == 0) return 0;
+  sd.s_key = scratch->key;
+  sd.s_decay = scratch->decay;
+  sd.s_delta = scratch->delta;
+  sd.s_slots = scratch->stable_slots;
+  return launch_step_mode<MODE_READ>(pool, sd, args->batch, (hipStream_t)stream);
+}
+
+int sq_writeback(const sq_pool *pool, const sq_writeback_scratch *scratch, int64_t batch, void *stream) {
+  int rc = validate_pool(pool);
+  if (rc) return rc;
+  if (!scratch || !scratch->key || !scratch->decay || !scratch->delta || !scratch->stable_slots)
+    return fail(SQ_EINVAL, "writeback: null scratch");
+  if (batch < 0 || batch > scratch->capacity) return fail(SQ_EINVAL, "writeback: bad batch");
+  if (batch == 0) return 0;
+  StepDev sd;
+  memset(&sd, 0, sizeof(sd));
+  sd.s_key = scratch->key;
+  sd.s_decay = scratch->decay;
+  sd.s_delta = scratch->delta;
+  sd.s_slots = scratch->stable_slots;
+  return launch_step_mode<MODE_WRITE>(pool, sd, batch, (hipStream_t)stream);
+}
+
+int sq_pool_flags(const int32_t *bits, const int32_t *head_meta, const int32_t *columns, int32_t heads,
+                  int32_t keys, int32_t values, int32_t group, int32_t kda, int32_t storage, int64_t page_bytes) {
+  if (!bits || !head_meta || !columns || heads < 1) return fail(SQ_EINVAL, "pool flags: bad arguments");
+  int flags = 0;
+  bool fast = !kda && keys == 128 && values == 128 && storage == 0 && page_bytes % 16 == 0;
+  for (int h = 0; fast && h < heads; h++) {
+    const int w = bits[(int64_t)h * keys];
+    for (int i = 1; i < keys; i++) fast = fast && bits[(int64_t)h * keys + i] == w;
+    fast = fast && head_meta[4 * h] % 16 == 0 && head_meta[4 * h + 1] % 16 == 0;
+    if (w != 16) fast = fast && head_meta[4 * h + 2] % 16 == 0 && head_meta[4 * h + 3] % 16 == 0 &&
+                        columns[h] >= 0 && columns[h] % 16 == 0;
+    if (w == 2) fast = fast && (group == 32 || group == 64 || group == 128);
+  }
+  if (fast) flags |= SQ_POOL_FAST_GDN128;
+  return flags;
+}
+
+int sq_stream_capture_id(void *stream, int32_t *capturing, uint64_t *id) {
+  if (!capturing || !id) return fail(SQ_EINVAL, "capture id: null output");
+  hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+  unsigned long long ident = 0;
+  hipError_t e = hipStreamGetCaptureInfo((hipStream_t)stream, &status, &ident);
+  if (e != hipSuccess) {
+    snprintf(g_err, sizeof(g_err), "hipStreamGetCaptureInfo: %s", hipGetErrorString(e));
+    return (int)e;
+  }
+  *capturing = status == hipStreamCaptureStatusActive ? 1 : (status == hipStreamCaptureStatusNone ? 0 : 2);
+  *id = (uint64_t)ident;
+  return 0;
+}
+
+int sq_create_cu_stream(int32_t device, int32_t cus, void **stream, int32_t *actual, int32_t *total) {
+  if (!stream || !actual || !total) return fail(SQ_EINVAL, "cu stream: null output");
+  hipError_t e = hipSetDevice(device);
+  if (e != hipSuccess) return fail((int)e, "cu stream: hipSetDevice failed");
+  hipDeviceProp_t prop;
+  e = hipGetDeviceProperties(&prop, device);
+  if (e != hipSuccess) return fail((int)e, "cu stream: hipGetDeviceProperties failed");
+  const int n = prop.multiProcessorCount;
+  *total = n;
+  if (cus < 0 || cus > n) return fail(SQ_EINVAL, "cu stream: budget outside [0, CU count]");
+  hipStream_t s = nullptr;
+  if (cus == 0 || cus == n) {
+    e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+    *actual = n;
+  } else {
+    // Mask bit i selects a CU of XCD i mod 8, so the first `cus` bits give
+    // every XCD the same share of the budget (a mask that leaves an XCD
+    // without CUs is rejected by the runtime).
+    uint32_t mask[32] = {0};
+    const int words = (n + 31) / 32;
+    int chosen = 0;
+    for (int c = 0; c < cus; c++) {
+      mask[c / 32] |= 1u << (c % 32);
+      chosen++;
+    }
+    e = hipExtStreamCreateWithCUMask(&s, (uint32_t)words, mask);
+    *actual = chosen;
+  }
+  if (e != hipSuccess) {
+    snprintf(g_err, sizeof(g_err), "cu stream creation: %s", hipGetErrorString(e));
+    return (int)e;
+  }
+  *stream = (void *)s;
+  return 0;
+}
+
+int sq_clear_slots(const sq_pool *pool, const void *slots, int32_t slots_dtype, int64_t n, void *stream) {
+  if (!pool || !pool->data) return fail(SQ_EINVAL, "clear: null pool");
+  if (n == 0) return 0;
+  if (!slots || n < 0 || n > 65535) return fail(SQ_EINVAL, "clear: bad slot list");
+  if (slots_dtype != SQ_I32 && slots_dtype != SQ_I64) return fail(SQ_EINVAL, "clear: slots dtype");
+  unsigned gx = (unsigned)((pool->page_bytes + 255) / 256);
+  if (gx > 1024) gx = 1024;
+  hipLaunchKernelGGL(clear_kernel, dim3(gx, (unsigned)n), dim3(256), 0, (hipStream_t)stream, pool->data,
+                     pool->page_bytes, pool->num_slots, slots, slots_dtype);
+  return check_launch("clear_kernel");
+}
+
+int sq_copy_slots(const sq_pool *pool, const void *src, const void *dst, int32_t slots_dtype, int64_t n,
+                  uint8_t *temp, void *stream) {
+  if (!pool || !pool->data) return fail(SQ_EINVAL, "copy: null pool");
+  if (n == 0) return 0;
+  if (!src || !dst || !temp || n < 0 || n > 65535) return fail(SQ_EINVAL, "copy: bad arguments");
+  if (slots_dtype != SQ_I32 && slots_dtype != SQ_I64) return fail(SQ_EINVAL, "copy: slots dtype");
+  unsigned gx = (unsigned)((pool->page_bytes + 255) / 256);
+  if (gx > 1024) gx = 1024;
+  hipLaunchKernelGGL(gather_kernel, dim3(gx, (unsigned)n), dim3(256), 0, (hipStream_t)stream, pool->data,
+                     pool->page_bytes, pool->num_slots, src, slots_dtype, temp, 0);
+  int rc = check_launch("gather_kernel");
+  if (rc) return rc;
+  hipLaunchKernelGGL(gather_kernel, dim3(gx, (unsigned)n), dim3(256), 0, (hipStream_t)stream, pool->data,
+                     pool->page_bytes, pool->num_slots, dst, slots_dtype, temp, 1);
+  return check_launch("scatter_kernel");
+}
+
+}  // extern "C"

@@ -1,0 +1,398 @@
+"""Per-layer page pool of packed recurrent states on one MI355X GPU.
+
+Mirrors ``stepquant.kernels.pool`` of the reference (pool.py:19-365): the
+same constructor, methods, attributes and page byte layout, so the serving
+adapter can use it unchanged.  All arithmetic runs in the HIP kernels of
+``libstepquant_hip.so``, reached through the C ABI in include/stepquant_hip.h:
+
+* ``step`` without a writeback stream is one fused kernel per call: read the
+  tile, gated delta update, readout, requantise, store (``sq_decode_step``).
+* ``step`` with a writeback stream splits into a foreground readout
+  (``sq_decode_readout``) and a writer launched on the writeback stream
+  (``sq_writeback``), ordered by events exactly as the reference's
+  ``_schedule_writeback``/``wait`` protocol (pool.py:284-356).
+* ``encode`` requantises dense fp32 states bit-identically to the CPU
+  ``fit_state``; ``decode`` expands pages to fp32.
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _native as N
+
+
+def packed_layout(plan, value_dim, storage="packed"):
+    """Byte layout of one page (reference kernels/pool.py:19-66).
+
+    Returns ``(offsets, rows, columns, page_bytes)``: per key row the byte
+    offset of its first packed value (then one tile stride per head; for byte
+    storage the per-head code-plane base), the byte offset of its fp16 row
+    scale(s) (-1 for pivots), per head the fp16 column-scale offset (-1 when
+    the head has no integer rows), and the page size.  Values are grouped in
+    tiles of 16 (GDN) or 4 (KDA) along the value axis; one tile of every row
+    of a head is stored contiguously, so a head's codes are one contiguous
+    region.  FP16 pivot rows start at even offsets.
+    """
+    if storage not in ("packed", "byte"):
+        raise ValueError("state storage must be packed or byte")
+    widths = plan.bits.cpu().tolist()
+    kda = plan.architecture == "kda"
+    tile = min(4 if kda else 16, value_dim)
+    offsets, rows, columns, heads_base = [], [], [], []
+    cursor = 0
+    for head in widths:
+        if storage == "byte":
+            base = cursor
+            has_codes = any(w != 16 for w in head)
+            if has_codes:
+                cursor += len(head) * value_dim
+            pivot_base = cursor
+            n_pivot = 0
+            for i, w in enumerate(head):
+                if w == 16:
+                    offsets.append(pivot_base + 2 * n_pivot * value_dim)
+                    n_pivot += 1
+                else:
+                    offsets.append(base + i)
+            cursor += 2 * n_pivot * value_dim
+            heads_base.append(base)
+        else:
+            local = 0
+            for w in head:
+                if w == 16:
+                    local += local & 1
+                offsets.append(cursor + local)
+                local += tile * w // 8
+            stride = local + (local & 1)
+            heads_base.append(stride)
+            cursor += stride * (value_dim // tile)
+    offsets.extend(heads_base)
+    cursor += cursor & 1
+    for head in widths:
+        for w in head:
+            if w == 16:
+                rows.append(-1)
+            else:
+                rows.append(cursor)
+                cursor += 2 * (value_dim // plan.value_group_size if (w == 2 and not kda) else 1)
+    for head in widths:
+        if any(w != 16 for w in head):
+            columns.append(cursor)
+            cursor += 2 * value_dim
+        else:
+            columns.append(-1)
+    if storage == "byte":
+        cursor = (cursor + 15) // 16 * 16
+    return offsets, rows, columns, cursor
+
+
+def _head_meta(plan, value_dim, offsets, rows):
+    """Per head: code-region start/bytes and row-scale region start/bytes."""
+    H, K = plan.bits.shape
+    kda = plan.architecture == "kda"
+    tile = min(4 if kda else 16, value_dim)
+    meta = []
+    for h in range(H):
+        start = offsets[h * K]
+        nbytes = offsets[H * K + h] * (value_dim // tile)
+        row_offs = [rows[h * K + i] for i in range(K) if rows[h * K + i] >= 0]
+        if row_offs:
+            rstart = min(row_offs)
+            widths = plan.bits[h].tolist()
+            per = 2 * (value_dim // plan.value_group_size) if (not kda and widths[0] == 2) else 2
+            rbytes = per * len(row_offs)
+        else:
+            rstart, rbytes = -1, 0
+        meta.extend([start, nbytes, rstart, rbytes])
+    return meta
+
+
+def _indices(slots, device):
+    if isinstance(slots, torch.Tensor):
+        t = slots.to(device)
+        if t.dtype not in (torch.int32, torch.int64):
+            t = t.to(torch.int64)
+        return t.reshape(-1).contiguous()
+    return torch.as_tensor(slots, dtype=torch.int64, device=device).reshape(-1).contiguous()
+
+
+class PackedStatePool:
+    def __init__(self, plan, slots, value_dim=128, writeback_stream=None, writeback_workspace=None,
+                 writeback_chunk=64, storage="packed"):
+        if plan.bits.device.type != "cuda":
+            raise ValueError("HIP state pool requires a GPU (cuda) device")
+        if storage not in ("packed", "byte"):
+            raise ValueError("state storage must be packed or byte")
+        if storage == "byte" and writeback_stream is None:
+            raise ValueError("byte storage requires a writeback stream")
+        if storage == "byte":
+            raise NotImplementedError("byte-carrier pages are not implemented by the MI355X kernels yet")
+        self.storage = storage
+        self.early_writeback = True
+        self.plan = plan
+        self.heads, self.keys = plan.bits.shape
+        self.values = value_dim
+        if self.keys & (self.keys - 1) or value_dim & (value_dim - 1) or value_dim % 4:
+            raise ValueError("key/value dimensions must be powers of two, value_dim >= 4")
+        if plan.architecture == "gdn" and value_dim % plan.value_group_size:
+            raise ValueError("value dimension must be divisible by value_group_size")
+        offsets, rows, columns, cursor = packed_layout(plan, value_dim, storage)
+        self.page_bytes = cursor
+        self.device = plan.bits.device
+        dev = self.device
+        self.offsets = torch.tensor(offsets, device=dev, dtype=torch.int32)
+        self.rows = torch.tensor(rows, device=dev, dtype=torch.int32)
+        self.columns = torch.tensor(columns, device=dev, dtype=torch.int32)
+        meta = _head_meta(plan, value_dim, offsets, rows)
+        self.head_meta = torch.tensor(meta, device=dev, dtype=torch.int32)
+        # Kernels over-read up to 15 bytes past a head region with 16-byte loads.
+        self._pages = torch.zeros(slots * cursor + 64, device=dev, dtype=torch.uint8)
+        self.data = self._pages[:slots * cursor].view(slots, cursor)
+        self.bits = plan.bits.to(torch.int32).contiguous()
+        self.head_groups = []
+        if plan.architecture == "gdn":
+            widths = plan.bits[:, 0].cpu().tolist()
+            for width in sorted(set(widths)):
+                ids = [i for i, b in enumerate(widths) if b == width]
+                self.head_groups.append((width, torch.tensor(ids, device=dev, dtype=torch.int32)))
+        self.read_groups = []
+        if self.head_groups:
+            integer_ids = [i for i, b in enumerate(widths) if b != 16]
+            if integer_ids:
+                self.read_groups.append((0, torch.tensor(integer_ids, device=dev, dtype=torch.int32)))
+            self.read_groups.extend((w, ids) for w, ids in self.head_groups if w == 16)
+        self.impact = plan.impact.float().contiguous().to(dev)
+        max_impact = float(self.impact.max().item())
+        self.fast_fit = self.keys * (65504. * 64 * 127 * max_impact) ** 2 < 2. ** 124
+        self.coefficients = None
+        self.row_tile = min(32, value_dim, plan.value_group_size) if plan.architecture == "gdn" else min(8, value_dim)
+        self._desc = N.Pool(
+            data=self._pages.data_ptr(), page_bytes=cursor, num_slots=slots, bits=self.bits.data_ptr(),
+            offsets=self.offsets.data_ptr(), rows=self.rows.data_ptr(), columns=self.columns.data_ptr(),
+            impact=self.impact.data_ptr(), head_meta=self.head_meta.data_ptr(), heads=self.heads,
+            keys=self.keys, values=value_dim, group=plan.value_group_size,
+            kda=int(plan.architecture == "kda"), storage=0,
+            max_code_bytes=max(meta[1::4]) if meta else 0, max_row_bytes=max(meta[3::4]) if meta else 0,
+            flags=N.pool_flags(self.bits.cpu().reshape(-1).tolist(), meta, columns, self.heads, self.keys,
+                               value_dim, plan.value_group_size, int(plan.architecture == "kda"), 0, cursor),
+            reserved=0)
+        self._init_writeback(writeback_stream, writeback_chunk)
+        self._init_workspace(slots, writeback_workspace)
+
+    # ----------------------------------------------------------- writer state
+    def _init_writeback(self, writeback_stream, writeback_chunk):
+        if writeback_chunk < 0:
+            raise ValueError("writeback chunk must be nonnegative")
+        self.writeback_chunk = writeback_chunk
+        self.writeback_stream = writeback_stream
+        self.pending = False
+        self.captured_consumers = False
+        self.consumer_dependencies = set()
+        self.ready_capture = None
+        self.deferred = None
+        # PyTorch-ROCm has no external (cross-graph) events: both events are
+        # ordinary, and ordering across graph replays is carried by the
+        # completion event WritebackGraph.replay records between replays.
+        self.ready = torch.cuda.Event() if writeback_stream is not None else None
+        self.graph_ready = torch.cuda.Event() if writeback_stream is not None else None
+        self.completion = self.ready
+        if self.graph_ready is not None:
+            self.graph_ready.record(torch.cuda.current_stream(self.device))
+
+    def _init_workspace(self, slots, writeback_workspace):
+        self.scratch = None
+        stream = self.writeback_stream
+        if stream is None:
+            return
+        # Writer inputs stay outside any graph's private pool: a captured
+        # graph may otherwise alias them with a later layer's temporaries.
+        dev, H, K, V = self.device, self.heads, self.keys, self.values
+        self.scratch = (torch.empty((slots, H, K), device=dev, dtype=torch.float32),
+                        torch.empty((slots, H, K), device=dev, dtype=torch.float32),
+                        torch.empty((slots, H, V), device=dev, dtype=torch.float32),
+                        torch.empty((slots, 1), device=dev, dtype=torch.float32),
+                        torch.empty(slots, device=dev, dtype=torch.int64))
+        for tensor in self.scratch:
+            tensor.record_stream(stream)
+        # Layers sharing one writer stream share this workspace entry, as in
+        # the reference; the fused writer needs no row-coefficient planes.
+        workspace = {} if writeback_workspace is None else writeback_workspace
+        key = (self.device.index, stream.cuda_stream, slots, H, K)
+        if key not in workspace:
+            workspace[key] = torch.empty(slots, device=dev, dtype=torch.float32)
+        self.coefficients = workspace[key]
+        self.coefficients.record_stream(stream)
+
+    @property
+    def nbytes(self):
+        return self.data.numel()
+
+    def configure_writeback(self, stream, chunk):
+        """Bind a capture's writer stream without replacing pages or scratch."""
+        if self.writeback_stream is None or chunk < 0:
+            raise ValueError("configuring writeback requires an asynchronous pool and nonnegative chunk")
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("select writeback resources before graph capture")
+        self.wait()
+        if stream != self.writeback_stream:
+            for tensor in (*self.scratch, self.coefficients):
+                tensor.record_stream(stream)
+            self.writeback_stream = stream
+        self.writeback_chunk = chunk
+
+    def _args(self):
+        return self.data, self.bits, self.impact, self.offsets, self.rows, self.columns
+
+    # ------------------------------------------------------------- codecs
+    def encode(self, state, slots):
+        self.wait()
+        if state.shape != (slots.numel(), self.heads, self.keys, self.values):
+            raise ValueError("state must be [active slots, heads, key, value]")
+        if slots.numel():
+            self._writeback(state, slots)
+
+    def _writeback(self, state, slots, rows_ready=False, partial=None, row_tile=32):
+        state = state.to(device=self.device, dtype=torch.float32).contiguous()
+        idx = _indices(slots, self.device)
+        N.check(N.lib().sq_encode(self._desc, N.ptr(state), N.ptr(idx), N.dtype_code(idx), idx.numel(),
+                                  N.stream_handle()), "encode")
+
+    def decode(self, slots):
+        self.wait()
+        state = torch.empty((slots.numel(), self.heads, self.keys, self.values), device=self.device,
+                            dtype=torch.float32)
+        if slots.numel():
+            idx = _indices(slots, self.device)
+            N.check(N.lib().sq_decode_dense(self._desc, N.ptr(idx), N.dtype_code(idx), idx.numel(),
+                                            N.ptr(state), N.stream_handle()), "decode")
+        return state
+
+    # ---------------------------------------------------------------- step
+    def _step_args(self, q, k, v, g, beta, slots, out, normalize, scale, a_log, dt_bias, batch, hq):
+        K, H, V = self.keys, self.heads, self.values
+        if q.dtype != k.dtype or q.dtype != v.dtype or q.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+            q, k, v = q.float(), k.float(), v.float()
+        # one request's heads must sit K (V) elements apart for the kernels
+        if q.stride(1) != K:
+            q = q.contiguous()
+        if k.stride(1) != K:
+            k = k.contiguous()
+        if v.stride(1) != V:
+            v = v.contiguous()
+        kda = self.plan.architecture == "kda"
+        gate = [g, beta] + ([a_log, dt_bias] if a_log is not None else [])
+        gdt = g.dtype if all(t.dtype == g.dtype for t in gate) and g.dtype in (
+            torch.float32, torch.bfloat16, torch.float16) else torch.float32
+        gate = [t.to(device=self.device, dtype=gdt).contiguous() for t in gate]
+        g, beta = gate[0], gate[1]
+        if g.numel() != batch * H * (K if kda else 1) or beta.numel() != batch * H:
+            raise ValueError("gate shapes must be [batch, heads] (GDN) or [batch, heads, key] (KDA)")
+        if a_log is not None:
+            a_log, dt_bias = gate[2], gate[3]
+            if a_log.numel() != H or dt_bias.numel() != H * (K if kda else 1):
+                raise ValueError("a_log must be [heads] and dt_bias [heads] (GDN) or [heads*key] (KDA)")
+        idx = _indices(slots, self.device)
+        args = N.StepArgs(q=q.data_ptr(), k=k.data_ptr(), v=v.data_ptr(), g=g.data_ptr(), beta=beta.data_ptr(),
+                          a_log=None if a_log is None else a_log.data_ptr(),
+                          dt_bias=None if dt_bias is None else dt_bias.data_ptr(), out=out.data_ptr(),
+                          slots=idx.data_ptr(), batch=batch, q_stride=q.stride(0), k_stride=k.stride(0),
+                          v_stride=v.stride(0), key_heads=hq, qkv_dtype=N.dtype_code(q),
+                          gate_dtype=N.dtype_code(g), out_dtype=N.dtype_code(out),
+                          slots_dtype=N.dtype_code(idx), normalize=int(bool(normalize)), scale=float(scale),
+                          reserved=0)
+        keep = (q, k, v, g, beta, a_log, dt_bias, idx)
+        return args, keep
+
+    def step(self, q, k, v, g, beta, slots, *, normalize=False, scale=1., a_log=None, dt_bias=None):
+        self.wait()
+        if self.deferred is not None and not self.deferred.attention_windows:
+            self.deferred.release_window()
+        batch = slots.numel()
+        if not batch:
+            return torch.empty((0, self.heads, self.values), device=q.device, dtype=q.dtype)
+        q = q.reshape(batch, -1, self.keys)
+        k = k.reshape(batch, -1, self.keys)
+        v = v.reshape(batch, self.heads, self.values)
+        if q.stride(-1) != 1 or k.stride(-1) != 1 or v.stride(-1) != 1:
+            raise ValueError("head coordinates must be contiguous")
+        hq = q.shape[1]
+        if self.heads % hq or k.shape[1] != hq:
+            raise ValueError("value heads must be divisible by query heads")
+        out = torch.empty((batch, self.heads, self.values), device=q.device, dtype=q.dtype)
+        args, keep = self._step_args(q, k, v, g, beta, slots, out, normalize, scale, a_log, dt_bias, batch, hq)
+        if self.writeback_stream is None:
+            N.check(N.lib().sq_decode_step(self._desc, args, N.stream_handle()), "decode step")
+            return out
+        if batch > self.scratch[0].shape[0]:
+            raise ValueError("active batch exceeds the state pool workspace capacity")
+        update_key, decay, delta, partial, stable_slots = (t[:batch] for t in self.scratch)
+        scratch = self._scratch_desc(update_key, decay, delta, stable_slots)
+        N.check(N.lib().sq_decode_readout(self._desc, args, scratch, N.stream_handle()), "decode readout")
+        self._schedule_writeback(update_key, decay, delta, partial, stable_slots)
+        return out
+
+    @staticmethod
+    def _scratch_desc(update_key, decay, delta, stable_slots):
+        return N.Scratch(key=update_key.data_ptr(), decay=decay.data_ptr(), delta=delta.data_ptr(),
+                         stable_slots=stable_slots.data_ptr(), capacity=stable_slots.shape[0])
+
+    def _schedule_writeback(self, update_key, decay, delta, partial, stable_slots):
+        if self.deferred is not None:
+            self.deferred.append((self, update_key, decay, delta, partial, stable_slots))
+            return
+        current = torch.cuda.current_stream(self.device)
+        self.writeback_stream.wait_stream(current)
+        with torch.cuda.stream(self.writeback_stream):
+            self._finish_update(update_key, decay, delta, partial, stable_slots)
+            self.graph_ready.record()
+            self.ready.record()
+        for tensor in (update_key, decay, delta, partial, stable_slots):
+            tensor.record_stream(self.writeback_stream)
+        self.ready_capture = N.capture_id(current) if torch.cuda.is_current_stream_capturing() else None
+        self.completion = self.ready
+        self.pending = True
+
+    def _finish_update(self, update_key, decay, delta, partial, slots):
+        """Writer for one chunk of requests (runs on the current stream)."""
+        scratch = self._scratch_desc(update_key, decay, delta, slots)
+        N.check(N.lib().sq_writeback(self._desc, scratch, slots.numel(), N.stream_handle()), "writeback")
+
+    def wait(self):
+        """Order the current stream after this pool's pending writer.
+
+        Eagerly this waits on the writer's completion event.  Inside a graph
+        capture only writers recorded in the same capture can be joined (an
+        internal dependency); writers of earlier replays or eager calls are
+        ordered outside the capture: torch synchronises before a capture
+        begins, and WritebackGraph.replay waits on every pool's completion
+        before replaying its forward graph.
+        """
+        if getattr(self, "deferred", None) is not None or not self.pending:
+            return
+        stream = torch.cuda.current_stream(self.device)
+        if torch.cuda.is_current_stream_capturing():
+            if self.ready_capture is not None and self.ready_capture == N.capture_id(stream):
+                stream.wait_event(self.ready)
+            else:
+                self.captured_consumers = True
+            return
+        stream.wait_event(self.completion)
+
+    # ------------------------------------------------------------ slot ops
+    def clear(self, slots):
+        self.wait()
+        idx = _indices(slots, self.device)
+        if idx.numel():
+            N.check(N.lib().sq_clear_slots(self._desc, N.ptr(idx), N.dtype_code(idx), idx.numel(),
+                                           N.stream_handle()), "clear")
+
+    def copy(self, source, destination):
+        self.wait()
+        src = _indices(source, self.device).to(torch.int64)
+        dst = _indices(destination, self.device).to(torch.int64)
+        if src.numel() != dst.numel():
+            raise ValueError("copy needs as many destination slots as source slots")
+        if src.numel():
+            temp = torch.empty((src.numel(), self.page_bytes), device=self.device, dtype=torch.uint8)
+            N.check(N.lib().sq_copy_slots(self._desc, N.ptr(src), N.ptr(dst), N.I64, src.numel(), N.ptr(temp),
+                                          N.stream_handle()), "copy")

@@ -1,0 +1,197 @@
+"""Parity of the HIP pool against the CPU oracle (runs on an MI355X).
+
+Bars (from the build's north star):
+* encode: page bytes bit-identical to the oracle's fit_state + page layout;
+* decode: bit-identical to the oracle's page decode;
+* decode step: readout within rtol 1e-3 / atol 1e-4 of delta_step on the
+  decoded state; requantised codes equal fit_state(updated) except for
+  1-LSB flips on at most 0.1% of elements; scales within one fp16 ulp.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests.helpers import dev, device_plan, make_plan, page_codes
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN_GPU_CASES = ["c_config_gdn", "c_config_gdn_uniform6", "gdn_two_bit_g32", "gdn_mixed_v16_g4",
+                    "kda_mixed_128", "kda_edges_v4", "kda_edges_v32", "gdn_v8_k4", "gdn_v32_k32",
+                    "zero_state", "scale_extremes"]
+
+
+def _pool(oplan, slots, V, **kw):
+    from stepquant_amd.kernels.pool import PackedStatePool
+    return PackedStatePool(device_plan(oplan), slots, V, **kw)
+
+
+@pytest.mark.parametrize("name", GOLDEN_GPU_CASES)
+def test_encode_bit_exact_against_golden(golden, name):
+    data, meta = golden
+    m = meta["cases"][name]
+    oplan = O.Plan(m["arch"], data[f"{name}/bits"], data[f"{name}/impact"], m["group"])
+    x = data[f"{name}/x"]
+    B, H, K, V = x.shape
+    print(f"case {name} shape {x.shape}", flush=True)
+    pool = _pool(oplan, B + 2, V)
+    slots = torch.arange(B, 0, -1, device=dev())
+    pool.encode(torch.from_numpy(x).to(dev()), slots)
+    lay = O.layout(oplan, V)
+    ref = np.zeros((B + 2, lay.page_bytes), np.uint8)
+    O.encode_page(x, slots.cpu().numpy(), oplan, lay, ref)
+    got = pool.data.cpu().numpy()
+    assert (got != ref).sum() == 0, f"{(got != ref).sum()} bytes differ"
+    # and the codes are the reference's fit_state codes
+    z = data[f"{name}/z"].astype(np.int64)
+    codes = page_codes(got, slots.cpu().numpy(), oplan, lay, V)
+    integer = oplan.bits != 16
+    qmax = ((1 << (np.minimum(oplan.bits, 8) - 1)) - 1)[None, :, :, None]
+    two = ((oplan.bits == 2) & (not oplan.kda))[None, :, :, None]
+    expect = np.where(two, (z + 3) // 2, z + qmax)
+    assert np.array_equal(codes[:, integer], expect[:, integer])
+    dec = pool.decode(slots).cpu().numpy()
+    np.testing.assert_array_equal(dec, O.decode_page(ref, slots.cpu().numpy(), oplan, lay, V))
+
+
+@pytest.mark.parametrize("arch,batch", [("gdn", 16), ("kda", 8)])
+def test_encode_bit_exact_full_heads(arch, batch):
+    rng = np.random.default_rng(11)
+    H, K, V = 32, 128, 128
+    if arch == "gdn":
+        bits = np.repeat(rng.choice([4, 6, 8], H)[:, None], K, 1)
+        bits[5] = 16
+        bits[9] = 2
+    else:
+        bits = rng.choice([4, 6, 8], (H, K))
+        bits[rng.random((H, K)) < .01] = 16
+    oplan = make_plan(arch, bits, seed=3)
+    r = np.exp(rng.normal(0, .5, (batch, H, K, 1))).astype(np.float32)
+    c = np.exp(rng.normal(0, .5, (batch, H, 1, V))).astype(np.float32)
+    x = (r * rng.standard_normal((batch, H, K, V)).astype(np.float32) * c * .05).astype(np.float32)
+    pool = _pool(oplan, batch + 1, V)
+    slots = torch.arange(1, batch + 1, device=dev())
+    pool.encode(torch.from_numpy(x).to(dev()), slots)
+    lay = O.layout(oplan, V)
+    ref = np.zeros((batch + 1, lay.page_bytes), np.uint8)
+    O.encode_page(x, slots.cpu().numpy(), oplan, lay, ref)
+    got = pool.data.cpu().numpy()
+    assert (got != ref).sum() == 0, f"{(got != ref).sum()} bytes differ"
+
+
+def _inputs(B, H, K, V, kda, seed, dtype=torch.float32):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, H, K, generator=g)
+    k = torch.nn.functional.normalize(torch.randn(B, H, K, generator=g), dim=-1)
+    v = torch.randn(B, H, V, generator=g)
+    ld = -torch.nn.functional.softplus(torch.randn(B, H, K, generator=g) * (.5 if kda else 1.)) if kda \
+        else -torch.nn.functional.softplus(torch.randn(B, H, generator=g))
+    beta = torch.sigmoid(torch.randn(B, H, generator=g))
+    return q.to(dtype), k.to(dtype), v.to(dtype), ld, beta
+
+
+STEP_CASES = {
+    "gdn6_uniform": ("gdn", lambda H, K: np.full((H, K), 6), 4, 128, 128, 32),
+    "gdn_mixed_pivot": ("gdn", lambda H, K: np.repeat(np.array([6, 4, 8, 16])[:, None], K, 1), 4, 128, 128, 32),
+    "gdn_two_bit_g32": ("gdn", lambda H, K: np.repeat(np.array([2, 6, 2, 8])[:, None], K, 1), 4, 128, 128, 32),
+    "gdn_small_v16": ("gdn", lambda H, K: np.repeat(np.array([2, 4, 6, 8, 16])[:, None], K, 1), 5, 8, 16, 4),
+    "kda_mixed": ("kda", lambda H, K: np.where(np.random.default_rng(2).random((H, K)) < .03, 16,
+                                               np.random.default_rng(3).choice([2, 4, 6, 8], (H, K))), 3, 128, 128, 32),
+    "kda_edges_v4": ("kda", lambda H, K: np.array([[2, 4, 8, 16]]), 1, 4, 4, 32),
+    "kda_edges_v32": ("kda", lambda H, K: np.array([[2, 4, 8, 16]]), 1, 4, 32, 32),
+}
+
+
+def _check_requant(got_pages, slots, oplan, lay, V, updated, flip_budget=1e-3):
+    ref = np.zeros_like(got_pages)
+    O.encode_page(updated, slots, oplan, lay, ref)
+    a = page_codes(got_pages, slots, oplan, lay, V)
+    b = page_codes(ref, slots, oplan, lay, V)
+    integer = np.broadcast_to(oplan.bits[None, :, :, None] != 16, a.shape)
+    live = np.broadcast_to((np.asarray(slots) > 0)[:, None, None, None], a.shape)
+    m = integer & live
+    diff = np.abs(a[m] - b[m])
+    assert diff.max(initial=0) <= 1, f"code differs by {diff.max()}"
+    frac = (diff > 0).mean() if diff.size else 0.0
+    assert frac <= flip_budget, f"{frac:.2e} of codes flipped"
+    pv = (~np.broadcast_to(oplan.bits[None, :, :, None] != 16, a.shape)) & live
+    if pv.any():
+        pa = a[pv].astype(np.uint16).view(np.float16).astype(np.float32)
+        pb = b[pv].astype(np.uint16).view(np.float16).astype(np.float32)
+        np.testing.assert_allclose(pa, pb, rtol=1e-3, atol=1e-5)
+    # row / column scales: equal up to one fp16 ulp
+    for o in list(lay.rows) + list(lay.columns):
+        if o < 0:
+            continue
+    ga = O.decode_page(got_pages, slots, oplan, lay, V)
+    gb = O.decode_page(ref, slots, oplan, lay, V)
+    close = np.isclose(ga, gb, rtol=1e-3, atol=1e-4)
+    assert (~close).mean() <= flip_budget, f"{(~close).mean():.2e} of dequantised values differ"
+    return frac
+
+
+@pytest.mark.parametrize("name", list(STEP_CASES))
+@pytest.mark.parametrize("asynchronous", [False, True])
+def test_decode_step_against_oracle(name, asynchronous):
+    arch, mk, H, K, V, G = STEP_CASES[name]
+    kda = arch == "kda"
+    oplan = make_plan(arch, mk(H, K), group=G, seed=7)
+    B = 6
+    print(f"case {name} async={asynchronous}", flush=True)
+    stream = torch.cuda.Stream() if asynchronous else None
+    pool = _pool(oplan, B + 2, V, writeback_stream=stream)
+    slots_np = np.array([3, 1, 0, 5, 2, 7])
+    slots = torch.from_numpy(slots_np).to(dev())
+    g = torch.Generator().manual_seed(5)
+    x0 = (torch.randn(B, H, K, V, generator=g) * .1).numpy()
+    pool.encode(torch.from_numpy(x0).to(dev()), slots)
+    lay = O.layout(oplan, V)
+    for it in range(3):
+        pages = pool.data.cpu().numpy()
+        state = O.decode_page(pages, slots_np, oplan, lay, V)
+        q, k, v, ld, beta = _inputs(B, H, K, V, kda, 100 + it)
+        out_ref, upd = O.delta_step(state, q.numpy(), k.numpy(), v.numpy(), ld.numpy(), beta.numpy())
+        out = pool.step(q.to(dev()), k.to(dev()), v.to(dev()), ld.to(dev()), beta.to(dev()), slots)
+        pool.wait()
+        torch.cuda.synchronize()
+        o = out.cpu().numpy()
+        live = slots_np > 0
+        np.testing.assert_allclose(o[live], out_ref[live], rtol=1e-3, atol=1e-4)
+        assert not o[~live].any()
+        got = pool.data.cpu().numpy()
+        assert not got[0].any(), "sentinel page 0 was written"
+        _check_requant(got, slots_np, oplan, lay, V, upd)
+
+
+def test_async_and_fused_paths_agree_bitwise():
+    oplan = make_plan("gdn", np.repeat(np.array([6, 4, 8, 16, 2, 6])[:, None], 128, 1), seed=1)
+    B, H, K, V = 8, 6, 128, 128
+    sync = _pool(oplan, B + 1, V)
+    asy = _pool(oplan, B + 1, V, writeback_stream=torch.cuda.Stream())
+    slots = torch.arange(B, 0, -1, device=dev())
+    x = torch.randn(B, H, K, V, device=dev()) * .1
+    sync.encode(x, slots)
+    asy.encode(x, slots)
+    for it in range(4):
+        q, k, v, ld, beta = (t.to(dev()) for t in _inputs(B, H, K, V, False, it))
+        a = sync.step(q, k, v, ld, beta, slots)
+        b = asy.step(q, k, v, ld, beta, slots)
+        slots.fill_(3)  # the scheduler reuses its index tensor while the writer runs
+        slots.copy_(torch.arange(B, 0, -1, device=dev()))
+        asy.wait()
+        torch.testing.assert_close(a, b, rtol=0, atol=0)
+        assert torch.equal(sync.data, asy.data)
+
+
+def test_clear_and_overlapping_copy():
+    oplan = make_plan("kda", np.random.default_rng(0).choice([4, 6, 8, 16], (2, 32)), seed=2)
+    pool = _pool(oplan, 6, 32)
+    slots = torch.tensor([1, 2, 3, 4], device=dev())
+    pool.encode(torch.randn(4, 2, 32, 32, device=dev()), slots)
+    before = pool.data.clone()
+    pool.copy(torch.tensor([1, 2, 3], device=dev()), torch.tensor([2, 3, 4], device=dev()))
+    assert torch.equal(pool.data[2:5], before[1:4])
+    assert torch.equal(pool.data[1], before[1])
+    pool.clear(slots)
+    assert pool.decode(slots).count_nonzero() == 0
+    assert pool.data.count_nonzero() == 0

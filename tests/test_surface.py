@@ -1,0 +1,148 @@
+"""Host-side surface on the CPU: the C ABI exports, layout, plans, schedules."""
+import ctypes
+import re
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+ROOT = __import__("os").path.dirname(__import__("os").path.dirname(__import__("os").path.abspath(__file__)))
+
+
+def _declared_symbols():
+    text = open(f"{ROOT}/include/stepquant_hip.h").read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char \*)\s*(sq_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    from stepquant_amd import _native as N
+    lib = ctypes.CDLL(N.library_path())
+    declared = _declared_symbols()
+    assert len(declared) >= 11
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert set(declared) == set(N.EXPORTS)
+    assert N.lib().sq_abi_version() == N.ABI_VERSION
+
+
+def test_structs_match_header_layout():
+    from stepquant_amd import _native as N
+    # 8-byte pointers/int64 then int32 fields, as in include/stepquant_hip.h
+    assert ctypes.sizeof(N.Pool) == 8 * 9 + 4 * 10
+    assert ctypes.sizeof(N.StepArgs) == 8 * 13 + 4 * 8
+    assert ctypes.sizeof(N.Scratch) == 8 * 5
+
+
+def test_invalid_arguments_are_reported_without_a_device():
+    from stepquant_amd import _native as N
+    lib = N.lib()
+    rc = lib.sq_encode(None, None, None, 4, 1, None)
+    assert rc == -22 and b"pool" in lib.sq_last_error()
+    with pytest.raises(ValueError):
+        N.check(rc, "encode")
+
+
+@pytest.mark.parametrize("arch,bits,V,group", [
+    ("gdn", [[6] * 8, [4] * 8, [16] * 8, [2] * 8], 32, 8),
+    ("kda", [[2, 4, 6, 8, 16, 6, 16, 2]], 8, 32),
+    ("kda", [[2, 4, 8, 16], [16, 16, 16, 16]], 32, 32),
+    ("gdn", [[6] * 128] * 32, 128, 32),
+])
+@pytest.mark.parametrize("storage", ["packed", "byte"])
+def test_product_layout_equals_oracle(arch, bits, V, group, storage):
+    from stepquant_amd.kernels.pool import packed_layout
+    from stepquant_amd.quantization import QuantizationPlan
+    b = torch.tensor(bits)
+    plan = QuantizationPlan(arch, b, torch.ones_like(b, dtype=torch.float32), group)
+    offsets, rows, columns, total = packed_layout(plan, V, storage)
+    lay = O.layout(O.Plan(arch, np.array(bits), np.ones(b.shape), group), V, storage)
+    assert offsets == lay.offsets.tolist() and rows == lay.rows.tolist()
+    assert columns == lay.columns.tolist() and total == lay.page_bytes
+
+
+def test_plan_validation_messages():
+    from stepquant_amd.quantization import QuantizationPlan
+    ones = torch.ones(2, 4)
+    with pytest.raises(ValueError, match="architecture"):
+        QuantizationPlan("mamba", torch.full((2, 4), 6), ones)
+    with pytest.raises(ValueError, match="precision"):
+        QuantizationPlan("kda", torch.full((2, 4), 3), ones)
+    with pytest.raises(ValueError, match="per whole head"):
+        QuantizationPlan("gdn", torch.tensor([[6, 4, 6, 6], [6, 6, 6, 6]]), ones)
+    with pytest.raises(ValueError, match="positive"):
+        QuantizationPlan("kda", torch.full((2, 4), 6), -ones)
+    with pytest.raises(ValueError, match="shape"):
+        QuantizationPlan("kda", torch.full((2, 4), 6), torch.ones(4, 2))
+
+
+def test_pool_requires_a_gpu_plan():
+    from stepquant_amd.kernels.pool import PackedStatePool
+    from stepquant_amd.quantization import QuantizationPlan
+    plan = QuantizationPlan("gdn", torch.full((2, 8), 6), torch.ones(2, 8))
+    with pytest.raises(ValueError):
+        PackedStatePool(plan, 4, 8)
+
+
+def test_profiles_tiers():
+    from stepquant_amd.kernels.profiles import stepquant6_profile
+    for arch in ("gdn", "kda"):
+        for batch in (1, 17, 32, 33, 64, 65, 128, 129, 256, 257, 512):
+            p = stepquant6_profile(arch, batch)
+            assert 0 < p.sms <= 256 and p.chunk % 32 == 0
+        assert stepquant6_profile(arch, 33) == stepquant6_profile(arch, 64)
+    for batch in (0, 513, True, 32.5):
+        with pytest.raises(ValueError):
+            stepquant6_profile("gdn", batch)
+    with pytest.raises(ValueError):
+        stepquant6_profile("mamba", 32)
+
+
+@pytest.mark.parametrize("chunk", [32, 64, 128, 256, 512])
+def test_release_schedule_keeps_tail_bounded(monkeypatch, chunk):
+    """Reference tests/test_writeback_schedule.py:8-23 on the same schedule."""
+    from stepquant_amd.kernels.writeback import CapturedWrites
+    monkeypatch.setattr(torch.cuda, "Event", lambda **kwargs: SimpleNamespace(record=lambda: None))
+    tasks = CapturedWrites(attention_windows=True)
+    slots = torch.arange(512)
+    recurrent = [True, True, True, False] * 6 + [True, True, False]
+    chunks = (len(slots) + chunk - 1) // chunk
+    for is_recurrent in recurrent:
+        tasks.release_window()
+        if is_recurrent:
+            pool = SimpleNamespace(plan=SimpleNamespace(architecture="kda"), storage="byte", writeback_chunk=chunk)
+            tasks.append((pool, slots))
+        assert len(tasks.pending) <= chunks
+    assert not tasks.pending
+    assert len(tasks) == sum(recurrent) * chunks
+    assert sum(task.final for task in tasks) == sum(recurrent)
+
+
+def test_alias_exposes_reference_module_names():
+    import sys
+    import stepquant_amd
+    saved = {k: v for k, v in sys.modules.items() if k == "stepquant" or k.startswith("stepquant.")}
+    try:
+        stepquant_amd.install_alias("stepquant")
+        from stepquant.kernels.pool import PackedStatePool, packed_layout  # noqa: F401
+        from stepquant.kernels.writeback import defer_writeback, WritebackGraph, attention_window  # noqa: F401
+        from stepquant.formats import get_format, FormatPlan  # noqa: F401
+        from stepquant.quantization import QuantizationPlan  # noqa: F401
+        assert get_format("stepquant6").bits == 6
+    finally:
+        for k in [k for k in sys.modules if k == "stepquant" or k.startswith("stepquant.")]:
+            del sys.modules[k]
+        sys.modules.update(saved)
+
+
+@pytest.mark.parametrize("bits", [2, 4, 6, 8])
+@pytest.mark.parametrize("n", [0, 1, 7, 128, 513])
+def test_packing_matches_oracle(bits, n):
+    from stepquant_amd.packing import pack, unpack
+    x = torch.randint(2 ** bits, (n,), generator=torch.Generator().manual_seed(n))
+    p = pack(x, bits)
+    assert p.dtype == torch.uint8
+    np.testing.assert_array_equal(p.numpy(), O.pack(x.numpy(), bits))
+    torch.testing.assert_close(unpack(p, bits, n).long(), x)
