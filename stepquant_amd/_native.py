@@ -11,7 +11,7 @@ import os
 import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libstepquant_hip.so")
+LIB_PATH = os.environ.get("STEPQUANT_HIP_LIB", os.path.join(_HERE, "libstepquant_hip.so"))
 ABI_VERSION = 1
 
 F32, BF16, F16, I32, I64 = 0, 1, 2, 3, 4

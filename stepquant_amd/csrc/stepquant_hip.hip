@@ -796,13 +796,24 @@ __global__ __launch_bounds__(512) void step_kernel(PoolDev P, StepDev S) {
 // so the foreground needs two FMAs per value and no dequantised tile.
 // The writer works on inner_ij = x'_ij / c_j = a_i z_ij + k_i delta_j / c_j.
 // =====================================================================
+#ifndef GDN128_WAVES
+#define GDN128_WAVES 3
+#endif
+#ifndef SCHED_ROWS
+#define SCHED_ROWS 4  // rows between scheduling fences (bounds hoisted LDS loads)
+#endif
+
 namespace fast {
 
 constexpr int FK = 128, FV = 128, FNT = 256, FRPT = 16;
 
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, true));
+}
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, CTRL, 0xF, 0xF, true);
 }
 // sum / max over the 8 row-group lanes (lane bits 0-2)
 __device__ __forceinline__ float rg8_sum(float x) {
@@ -811,11 +822,13 @@ __device__ __forceinline__ float rg8_sum(float x) {
   x += dpp<0x141>(x);  // row_half_mirror
   return x;
 }
-__device__ __forceinline__ float rg8_max(float x) {
-  x = fmaxf(x, dpp<0xB1>(x));
-  x = fmaxf(x, dpp<0x4E>(x));
-  x = fmaxf(x, dpp<0x141>(x));
-  return x;
+// max of non-negative floats, compared as integers (no NaN canonicalisation)
+__device__ __forceinline__ float rg8_max_nonneg(float x) {
+  uint32_t u = __float_as_uint(x);
+  u = max(u, dpp_u<0xB1>(u));
+  u = max(u, dpp_u<0x4E>(u));
+  u = max(u, dpp_u<0x141>(u));
+  return __uint_as_float(u);
 }
 
 __device__ __forceinline__ float hw_h2f(uint32_t h) {
@@ -881,18 +894,37 @@ __device__ __forceinline__ void store_out(const PoolDev &P, const StepDev &S, co
   }
 }
 
-// stage out the code region and (integer heads) the row and column scales
-__device__ __forceinline__ void stage_back(const Ctx &C, bool scales) {
-  const int ncode = C.code_bytes >> 4, nrow = scales ? (C.row_bytes >> 4) : 0,
-            ncol = (scales && C.colbase >= 0) ? FV * 2 / 16 : 0;
-  for (int c = C.tid; c < ncode + nrow + ncol; c += FNT) {
-    if (c < ncode)
-      ((uint4 *)(C.page + C.code_start))[c] = ((const uint4 *)C.code)[c];
-    else if (c < ncode + nrow)
-      ((uint4 *)(C.page + C.row_start))[c - ncode] = ((const uint4 *)C.rst)[c - ncode];
-    else
-      ((uint4 *)(C.page + C.colbase))[c - ncode - nrow] = ((const uint4 *)C.cst)[c - ncode - nrow];
-  }
+// Stage the head's regions into LDS with a compile-time number of 16-byte
+// chunks per lane (the code region of a W-bit head is 128*W chunks, W/2 per
+// lane; FP16 pivot heads: 2048 chunks, 8 per lane).  Row scales use lanes
+// 0..16*NG-1, column scales lanes 240..255.
+template <int CODE_CHUNKS_PER_LANE>
+__device__ __forceinline__ void stage_in_fast(const Ctx &C, int row_chunks, bool cols) {
+  const uint4 *src = (const uint4 *)(C.page + C.code_start);
+  uint4 *dst = (uint4 *)C.code;
+  uint4 v[CODE_CHUNKS_PER_LANE];
+#pragma unroll
+  for (int k = 0; k < CODE_CHUNKS_PER_LANE; k++) v[k] = src[C.tid + FNT * k];
+  uint4 rv = make_uint4(0, 0, 0, 0), cv = make_uint4(0, 0, 0, 0);
+  const bool has_row = C.tid < row_chunks;
+  const bool has_col = cols && C.tid >= FNT - 16;
+  if (has_row) rv = ((const uint4 *)(C.page + C.row_start))[C.tid];
+  if (has_col) cv = ((const uint4 *)(C.page + C.colbase))[C.tid - (FNT - 16)];
+#pragma unroll
+  for (int k = 0; k < CODE_CHUNKS_PER_LANE; k++) dst[C.tid + FNT * k] = v[k];
+  if (has_row) ((uint4 *)C.rst)[C.tid] = rv;
+  if (has_col) ((uint4 *)C.cst)[C.tid - (FNT - 16)] = cv;
+}
+
+template <int CODE_CHUNKS_PER_LANE>
+__device__ __forceinline__ void stage_back_fast(const Ctx &C, int row_chunks, bool cols) {
+  uint4 *dst = (uint4 *)(C.page + C.code_start);
+  const uint4 *src = (const uint4 *)C.code;
+#pragma unroll
+  for (int k = 0; k < CODE_CHUNKS_PER_LANE; k++) dst[C.tid + FNT * k] = src[C.tid + FNT * k];
+  if (C.tid < row_chunks) ((uint4 *)(C.page + C.row_start))[C.tid] = ((const uint4 *)C.rst)[C.tid];
+  if (cols && C.tid >= FNT - 16)
+    ((uint4 *)(C.page + C.colbase))[C.tid - (FNT - 16)] = ((const uint4 *)C.cst)[C.tid - (FNT - 16)];
 }
 
 template <int W, int MODE>
@@ -908,6 +940,8 @@ __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx
   const int NG = W == 2 ? FV / P.G : 1;
   const int g = W == 2 ? C.j0 / P.G : 0;
   const uint16_t *c16 = (const uint16_t *)C.cst;
+  stage_in_fast<W / 2>(C, 16 * NG, true);
+  __syncthreads();
   row_setup<MODE>(S, C, NG);
   __syncthreads();
 
@@ -925,6 +959,7 @@ __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx
   const uint32_t sh = (uint32_t)(pos0 & 3) * 8u;
 #pragma unroll
   for (int r = 0; r < FRPT; r++) {
+    if ((r % SCHED_ROWS) == SCHED_ROWS - 1) __builtin_amdgcn_sched_barrier(0);
     const int i = C.rg + 8 * r;
     uint32_t word;
     if (W == 8) word = w32[r * 4 * W];  // 8 rows = 16W bytes = 4W dwords
@@ -974,6 +1009,7 @@ __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx
   float rowp[FRPT];
 #pragma unroll
   for (int r = 0; r < FRPT; r++) {
+    if ((r % SCHED_ROWS) == SCHED_ROWS - 1) __builtin_amdgcn_sched_barrier(0);
     const int i = C.rg + 8 * r;
     const float a = C.as[i * NG + g], k = C.ks[i];
     const float A = ZS * a, mL = -ZO * a;
@@ -1032,6 +1068,7 @@ __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx
   float mx[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int r = 0; r < FRPT; r++) {
+    if ((r % SCHED_ROWS) == SCHED_ROWS - 1) __builtin_amdgcn_sched_barrier(0);
     const float ir = C.ir[(C.rg + 8 * r) * NG + g];
 #pragma unroll
     for (int c = 0; c < 4; c++) {
@@ -1043,11 +1080,12 @@ __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx
   float c0[4], ic0[4], num[4] = {0.f, 0.f, 0.f, 0.f}, den[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int c = 0; c < 4; c++) {
-    c0[c] = hw_fp16_scale(rg8_max(mx[c]) * (1.0f / (float)L), nullptr);
+    c0[c] = hw_fp16_scale(rg8_max_nonneg(mx[c]) * (1.0f / (float)L), nullptr);
     ic0[c] = rcp(c0[c]);
   }
 #pragma unroll
   for (int r = 0; r < FRPT; r++) {
+    if ((r % SCHED_ROWS) == SCHED_ROWS - 1) __builtin_amdgcn_sched_barrier(0);
     const float U = C.uu[(C.rg + 8 * r) * NG + g];
 #pragma unroll
     for (int c = 0; c < 4; c++) {
@@ -1077,6 +1115,7 @@ __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx
   // ---- final codes, packed back into the staged region
 #pragma unroll
   for (int r = 0; r < FRPT; r++) {
+    if ((r % SCHED_ROWS) == SCHED_ROWS - 1) __builtin_amdgcn_sched_barrier(0);
     const int i = C.rg + 8 * r;
     uint32_t word = 0;
 #pragma unroll
@@ -1108,7 +1147,7 @@ __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx
     }
   }
   __syncthreads();
-  stage_back(C, true);
+  stage_back_fast<W / 2>(C, 16 * NG, true);
 }
 
 template <int MODE>
@@ -1116,6 +1155,8 @@ __device__ __forceinline__ void pivot_body(const PoolDev &P, const StepDev &S, C
 #pragma clang fp contract(off)
   constexpr int SEG = 32, BLK = FK * SEG;
   const float beta = C.misc[0], decay = C.misc[1];
+  stage_in_fast<8>(C, 0, false);
+  __syncthreads();
   row_setup<MODE>(S, C, 0);
   __syncthreads();
   float qi[FRPT], ki[FRPT];
@@ -1171,14 +1212,14 @@ __device__ __forceinline__ void pivot_body(const PoolDev &P, const StepDev &S, C
     *(uint2 *)(C.code + C.blk * BLK + i * SEG + C.sub * 8) = hv;
   }
   __syncthreads();
-  stage_back(C, false);
+  stage_back_fast<8>(C, 0, false);
 }
 
 }  // namespace fast
 
 template <int MODE>
-__global__ __launch_bounds__(256) void gdn128_kernel(PoolDev P,
-                                                                                            StepDev S) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GDN128_WAVES))) void gdn128_kernel(PoolDev P,
+                                                                                                       StepDev S) {
   using namespace fast;
   extern __shared__ __align__(16) uint8_t smem[];
   const int H = P.H;
@@ -1228,18 +1269,6 @@ __global__ __launch_bounds__(256) void gdn128_kernel(PoolDev P,
   C.uu = C.ir + FK * ngm;
   C.rnew = C.uu;
 
-  // stage code, row-scale and column-scale regions (16-byte aligned)
-  {
-    const int ncode = C.code_bytes >> 4, nrow = C.row_bytes >> 4, ncol = C.colbase >= 0 ? 2 * FV / 16 : 0;
-    for (int c = C.tid; c < ncode + nrow + ncol; c += FNT) {
-      if (c < ncode)
-        ((uint4 *)C.code)[c] = ((const uint4 *)(C.page + C.code_start))[c];
-      else if (c < ncode + nrow)
-        ((uint4 *)C.rst)[c - ncode] = ((const uint4 *)(C.page + C.row_start))[c - ncode];
-      else
-        ((uint4 *)C.cst)[c - ncode - nrow] = ((const uint4 *)(C.page + C.colbase))[c - ncode - nrow];
-    }
-  }
   // inputs: raw q, k rows, norms, beta and the head's retention
   const int64_t bh = (int64_t)C.b * H + C.h;
   if (MODE == MODE_WRITE) {

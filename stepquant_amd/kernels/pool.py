@@ -341,6 +341,13 @@ class PackedStatePool:
             self.deferred.append((self, update_key, decay, delta, partial, stable_slots))
             return
         current = torch.cuda.current_stream(self.device)
+        if torch.cuda.is_current_stream_capturing():
+            # Inside a graph the writer follows the readout on the capturing
+            # stream.  A writer branch forked to the writeback stream and
+            # joined through events was observed to overlap the next queued
+            # replay on ROCm, so captures never fork.
+            self._finish_update(update_key, decay, delta, partial, stable_slots)
+            return
         self.writeback_stream.wait_stream(current)
         with torch.cuda.stream(self.writeback_stream):
             self._finish_update(update_key, decay, delta, partial, stable_slots)
@@ -348,7 +355,7 @@ class PackedStatePool:
             self.ready.record()
         for tensor in (update_key, decay, delta, partial, stable_slots):
             tensor.record_stream(self.writeback_stream)
-        self.ready_capture = N.capture_id(current) if torch.cuda.is_current_stream_capturing() else None
+        self.ready_capture = None
         self.completion = self.ready
         self.pending = True
 
@@ -361,20 +368,19 @@ class PackedStatePool:
         """Order the current stream after this pool's pending writer.
 
         Eagerly this waits on the writer's completion event.  Inside a graph
-        capture only writers recorded in the same capture can be joined (an
-        internal dependency); writers of earlier replays or eager calls are
-        ordered outside the capture: torch synchronises before a capture
-        begins, and WritebackGraph.replay waits on every pool's completion
-        before replaying its forward graph.
+        capture the writer of a captured step already ran on the capturing
+        stream; writers of earlier replays or eager calls are ordered outside
+        the capture: torch synchronises before a capture begins, and
+        WritebackGraph.replay waits on every pool's completion before
+        replaying its forward graph.
         """
         if getattr(self, "deferred", None) is not None or not self.pending:
             return
         stream = torch.cuda.current_stream(self.device)
         if torch.cuda.is_current_stream_capturing():
-            if self.ready_capture is not None and self.ready_capture == N.capture_id(stream):
-                stream.wait_event(self.ready)
-            else:
-                self.captured_consumers = True
+            # writers launched inside this capture ran on the capturing
+            # stream already; earlier ones are ordered outside the graph
+            self.captured_consumers = True
             return
         stream.wait_event(self.completion)
 

@@ -59,9 +59,11 @@ class CapturedWrites(list):
             pool, tensors, final = self.pending.popleft()
             super().append(WritebackChunk(pool, ready, tensors, final))
             if self.joined:
-                with torch.cuda.stream(pool.writeback_stream):
-                    ready.wait()
-                    pool._finish_update(*tensors)
+                # Joined writers run on the capturing stream itself: a graph
+                # whose writer branch is forked to another stream and joined
+                # at the end was observed to let queued replays overlap that
+                # branch with the next replay on ROCm.
+                pool._finish_update(*tensors)
 
     def append(self, task):
         pool, *tensors = task
@@ -102,8 +104,6 @@ def defer_writeback(pools, *, attention_windows=False, joined=False):
     finally:
         _captured.reset(token)
         tasks.release_window(len(tasks.pending))
-        if joined and tasks:
-            torch.cuda.current_stream().wait_stream(tasks[0].pool.writeback_stream)
         for pool in pools:
             pool.deferred = None
 

@@ -195,3 +195,54 @@ def test_split_graph_queued_replays_and_batch_switch(arch, attention_windows, jo
     for pool, ref in zip(pools, refs):
         assert torch.equal(pool.decode(all_slots), ref.decode(all_slots))
         assert pool.data[0].count_nonzero() == 0
+
+
+@pytest.mark.parametrize("arch", ["gdn", "kda"])
+def test_queued_replays_of_captured_async_steps(arch):
+    """Graph replays queued back to back (no host sync) match eager twins.
+
+    Regression test: a writer forked to the writeback stream inside a capture
+    overlapped the next queued replay; captured writers now stay on the
+    capturing stream.
+    """
+    bits = np.repeat(np.array([6, 4, 8, 16])[:, None], 128, 1) if arch == "gdn" else \
+        np.where(np.random.default_rng(1).random((4, 128)) < .05, 16, np.random.default_rng(2).choice([4, 6, 8], (4, 128)))
+    oplan = make_plan(arch, bits, seed=12)
+    d = dev()
+    B = 32
+    pools = [_pool(oplan, B + 1, 128, writeback_stream=torch.cuda.Stream()) for _ in range(2)]
+    refs = [_pool(oplan, B + 1, 128) for _ in pools]
+    slots = torch.arange(1, B + 1, device=d)
+    x = torch.randn(B, 4, 128, 128, device=d) * .1
+    for p in pools + refs:
+        p.encode(x, slots)
+    g = torch.Generator(device=d).manual_seed(3)
+    q = torch.randn(B, 4, 128, device=d, generator=g)
+    k = torch.nn.functional.normalize(torch.randn(B, 4, 128, device=d, generator=g), dim=-1)
+    v = torch.randn(B, 4, 128, device=d, generator=g)
+    gate = -torch.rand(B, 4, 128, device=d, generator=g) if arch == "kda" else -torch.rand(B, 4, device=d, generator=g)
+    beta = torch.rand(B, 4, device=d, generator=g)
+
+    def forward():
+        outs = [p.step(q, k, v, gate, beta, slots) for p in pools]
+        for p in pools:
+            p.wait()
+        return outs
+
+    forward()
+    for p, r in zip(pools, refs):
+        r.step(q, k, v, gate, beta, slots)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = forward()
+    got = []
+    for _ in range(6):
+        graph.replay()
+        got.append([o.clone() for o in outs])
+    torch.cuda.synchronize()
+    for step in range(6):
+        for r, o in zip(refs, got[step]):
+            torch.testing.assert_close(o, r.step(q, k, v, gate, beta, slots), atol=0, rtol=0)
+    for p, r in zip(pools, refs):
+        assert torch.equal(p.data, r.data)
