@@ -40,7 +40,12 @@ def parse():
                    help="split readout (foreground) and writer (writeback stream)")
     p.add_argument("--cpu-sample", type=int, default=-1,
                    help="requests in the CPU-baseline sample (-1: auto, 0: skip)")
-    p.add_argument("--traffic", default=None, help="json with measured HBM bytes per launch")
+    p.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "traffic_gdn6_b256.json"),
+                   help="json with HBM bytes per launch measured by rocprofv3 (see profiles/)")
+    p.add_argument("--no-graph", action="store_true",
+                   help="launch steps eagerly (for rocprofv3 --pmc runs, which count per dispatch)")
+    p.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                   help="only run a device-to-device copy of MIB MiB five times (counter calibration)")
     return p.parse_args()
 
 
@@ -97,6 +102,15 @@ def main():
               "with no exchange; see DESIGN.md)", file=sys.stderr)
         sys.exit(2)
     import torch
+    if a.calibrate_copy:
+        n = a.calibrate_copy << 20
+        src = torch.randint(0, 255, (n,), dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps(dict(calibrate_copy_bytes=n, launches=5)), flush=True)
+        return
     from stepquant_amd.kernels.pool import PackedStatePool
     from stepquant_amd.quantization import QuantizationPlan
 
@@ -124,18 +138,22 @@ def main():
     for _ in range(3):
         step()
     torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        step()
+    if a.no_graph:
+        replay = step
+    else:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        replay = graph.replay
     for _ in range(a.warmup):
-        graph.replay()
+        replay()
     torch.cuda.synchronize()
     cur = torch.cuda.current_stream()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     start.record(cur)
     for _ in range(a.steps):
-        graph.replay()
+        replay()
     end.record(cur)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0

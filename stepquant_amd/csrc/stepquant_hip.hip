@@ -902,18 +902,11 @@ template <int CODE_CHUNKS_PER_LANE>
 __device__ __forceinline__ void stage_in_fast(const Ctx &C, int row_chunks, bool cols) {
   const uint4 *src = (const uint4 *)(C.page + C.code_start);
   uint4 *dst = (uint4 *)C.code;
-  uint4 v[CODE_CHUNKS_PER_LANE];
 #pragma unroll
-  for (int k = 0; k < CODE_CHUNKS_PER_LANE; k++) v[k] = src[C.tid + FNT * k];
-  uint4 rv = make_uint4(0, 0, 0, 0), cv = make_uint4(0, 0, 0, 0);
-  const bool has_row = C.tid < row_chunks;
-  const bool has_col = cols && C.tid >= FNT - 16;
-  if (has_row) rv = ((const uint4 *)(C.page + C.row_start))[C.tid];
-  if (has_col) cv = ((const uint4 *)(C.page + C.colbase))[C.tid - (FNT - 16)];
-#pragma unroll
-  for (int k = 0; k < CODE_CHUNKS_PER_LANE; k++) dst[C.tid + FNT * k] = v[k];
-  if (has_row) ((uint4 *)C.rst)[C.tid] = rv;
-  if (has_col) ((uint4 *)C.cst)[C.tid - (FNT - 16)] = cv;
+  for (int k = 0; k < CODE_CHUNKS_PER_LANE; k++) dst[C.tid + FNT * k] = src[C.tid + FNT * k];
+  if (C.tid < row_chunks) ((uint4 *)C.rst)[C.tid] = ((const uint4 *)(C.page + C.row_start))[C.tid];
+  if (cols && C.tid >= FNT - 16)
+    ((uint4 *)C.cst)[C.tid - (FNT - 16)] = ((const uint4 *)(C.page + C.colbase))[C.tid - (FNT - 16)];
 }
 
 template <int CODE_CHUNKS_PER_LANE>
