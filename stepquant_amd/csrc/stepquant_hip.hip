@@ -98,6 +98,39 @@ __device__ __forceinline__ void store_val(void *p, int dtype, int64_t idx, float
   else ((uint16_t *)p)[idx] = (uint16_t)f2h(v);
 }
 
+// four consecutive elements (one dtype test for all four)
+__device__ __forceinline__ void load4(const void *p, int dtype, int64_t idx, float o[4]) {
+  if (dtype == SQ_F32) {
+    const float *f = (const float *)p + idx;
+#pragma unroll
+    for (int c = 0; c < 4; c++) o[c] = f[c];
+  } else if (dtype == SQ_BF16) {
+    const uint16_t *u = (const uint16_t *)p + idx;
+#pragma unroll
+    for (int c = 0; c < 4; c++) o[c] = __uint_as_float((uint32_t)u[c] << 16);
+  } else {
+    const uint16_t *u = (const uint16_t *)p + idx;
+#pragma unroll
+    for (int c = 0; c < 4; c++) o[c] = h2f(u[c]);
+  }
+}
+
+__device__ __forceinline__ void store4(void *p, int dtype, int64_t idx, const float v[4]) {
+  if (dtype == SQ_F32) {
+    float *f = (float *)p + idx;
+#pragma unroll
+    for (int c = 0; c < 4; c++) f[c] = v[c];
+  } else if (dtype == SQ_BF16) {
+    uint16_t *u = (uint16_t *)p + idx;
+#pragma unroll
+    for (int c = 0; c < 4; c++) u[c] = (uint16_t)f2bf(v[c]);
+  } else {
+    uint16_t *u = (uint16_t *)p + idx;
+#pragma unroll
+    for (int c = 0; c < 4; c++) u[c] = (uint16_t)f2h(v[c]);
+  }
+}
+
 __device__ __forceinline__ int64_t load_slot(const void *p, int dtype, int64_t idx) {
   return dtype == SQ_I64 ? ((const int64_t *)p)[idx] : (int64_t)((const int32_t *)p)[idx];
 }
@@ -853,11 +886,75 @@ struct Ctx {
   uint8_t *code;   // staged code region
   uint8_t *rst;    // staged row scales
   uint8_t *cst;    // staged column scales
-  float *qraw, *kraw, *wv, *misc, *red, *rnew;
-  float *ks, *qs, *as, *ir, *uu;  // per-row prepared k, q, r*retention, 1/r', w^2 r'^2
+  float *qraw, *kraw, *wv, *misc, *red;
+  float *ks, *qs;  // per-row prepared k, q
+  float4 *rc;      // per (row, group): k*a, q*a, ZS*a, -ZO*a with a = r * retention
+  float2 *iu;      // per (row, group): 1/r', w^2 r'^2
   int b, h, tid, rg, cg, wave, j0, blk, sub;
   int code_start, code_bytes, row_start, row_bytes, colbase;
 };
+
+// misc[] slots: 0 beta, 1 retention, 8..11 squared norms of q/k halves,
+// 16.. and 32.. per-wave partial sums of k*a (per group), q*a (per group), q*k
+constexpr int MISC_FLOATS = 48;
+constexpr int SUM_KA = 0, SUM_QA = 4, SUM_QK = 8;
+
+// sum over the 64 lanes of a wave, result in every lane: 16-lane rows by
+// DPP, then row pairs and wave halves by lane swaps
+__device__ __forceinline__ float wave_sum(float x) {
+  x = rg8_sum(x);
+  x += dpp<0x140>(x);  // row_mirror
+  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+}
+
+// Per-row constants of the integer bodies (threads 0..127, row i = tid):
+// rc[i, g] and, for the readout, the sums over rows of k*a, q*a and q*k.
+template <int MODE>
+__device__ __forceinline__ void row_setup_int(const StepDev &S, const Ctx &C, int NG, float ZS, float ZO) {
+  if (C.tid < FK) {
+    const int i = C.tid;
+    float nq = 1.0f, nk = 1.0f;
+    if (MODE != MODE_WRITE && S.normalize) {
+      nq = 1.0f / __builtin_sqrtf((C.misc[8] + C.misc[10]) + 1e-6f);
+      nk = 1.0f / __builtin_sqrtf((C.misc[9] + C.misc[11]) + 1e-6f);
+    }
+    const float k = MODE == MODE_WRITE ? C.kraw[i] : C.kraw[i] * nk;
+    const float q = MODE == MODE_WRITE ? 0.0f : (C.qraw[i] * nq) * S.scale;
+    C.ks[i] = k;
+    const uint16_t *r16 = (const uint16_t *)C.rst;
+    const float retention = C.misc[1];
+    float ska[4], sqa[4];
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      ska[g] = 0.0f;
+      sqa[g] = 0.0f;
+      if (g < NG) {
+        const float a = hw_h2f(r16[i * NG + g]) * retention;
+        ska[g] = k * a;
+        sqa[g] = q * a;
+        C.rc[i * NG + g] = make_float4(ska[g], sqa[g], ZS * a, -ZO * a);
+      }
+    }
+    if (MODE != MODE_WRITE) {
+      float* part = C.misc + 16 + 16 * (i >> 6);
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        if (g < NG) {
+          const float s1 = wave_sum(ska[g]), s2 = wave_sum(sqa[g]);
+          if ((i & 63) == 0) {
+            part[SUM_KA + g] = s1;
+            part[SUM_QA + g] = s2;
+          }
+        }
+      }
+      const float s3 = wave_sum(q * k);
+      if ((i & 63) == 0) part[SUM_QK] = s3;
+    }
+  }
+}
 
 // Per-row inputs, once per workgroup into LDS (threads 0..127, row i = tid):
 // prepared q (scaled), prepared k, and a_i = r_i * retention per value group.
@@ -873,8 +970,6 @@ __device__ __forceinline__ void row_setup(const StepDev &S, const Ctx &C, int NG
     const float k = MODE == MODE_WRITE ? C.kraw[i] : C.kraw[i] * nk;
     C.ks[i] = k;
     C.qs[i] = MODE == MODE_WRITE ? 0.0f : (C.qraw[i] * nq) * S.scale;
-    const uint16_t *r16 = (const uint16_t *)C.rst;
-    for (int g = 0; g < NG; g++) C.as[i * NG + g] = hw_h2f(r16[i * NG + g]) * C.misc[1];
   }
 }
 
@@ -883,10 +978,7 @@ __device__ __forceinline__ void store_out(const PoolDev &P, const StepDev &S, co
                                           const float *delta) {
   const int64_t base = ((int64_t)C.b * P.H + C.h) * FV + C.j0;
   if (C.rg == 0) {
-    if (MODE == MODE_FUSED || MODE == MODE_READ) {
-#pragma unroll
-      for (int c = 0; c < 4; c++) store_val(S.out, S.out_dtype, base + c, o[c]);
-    }
+    if (MODE == MODE_FUSED || MODE == MODE_READ) store4(S.out, S.out_dtype, base, o);
     if (MODE == MODE_READ) {
 #pragma unroll
       for (int c = 0; c < 4; c++) S.s_delta[base + c] = delta[c];
@@ -920,6 +1012,35 @@ __device__ __forceinline__ void stage_back_fast(const Ctx &C, int row_chunks, bo
     ((uint4 *)(C.page + C.colbase))[C.tid - (FNT - 16)] = ((const uint4 *)C.cst)[C.tid - (FNT - 16)];
 }
 
+// Final codes of four values from v = y + L: level(y) = rint(y) + L
+// saturated to [0, 2L].  v_cvt_pk_u8_f32 converts with round-to-nearest-even
+// into one byte lane, so the saturated v converts straight into place; the
+// W-bit fields are then gathered with one shift-or and a byte permute or
+// bitfield insert.  Fields: column c at bits [cW, cW + W).
+template <int W>
+__device__ __forceinline__ uint32_t pack_codes(const float v[4]) {
+  constexpr float TOP = (float)(2 * ((1 << (W - 1)) - 1));
+  auto lvl = [](float x) { return __builtin_amdgcn_fmed3f(x, 0.0f, TOP); };
+  if (W == 8) {
+    uint32_t w = __builtin_amdgcn_cvt_pk_u8_f32(lvl(v[0]), 0, 0u);
+    w = __builtin_amdgcn_cvt_pk_u8_f32(lvl(v[1]), 1, w);
+    w = __builtin_amdgcn_cvt_pk_u8_f32(lvl(v[2]), 2, w);
+    return __builtin_amdgcn_cvt_pk_u8_f32(lvl(v[3]), 3, w);
+  }
+  // even columns in bytes 0 and 2, odd columns in bytes 0 and 2 of a second word
+  uint32_t e = __builtin_amdgcn_cvt_pk_u8_f32(lvl(v[0]), 0, 0u);
+  e = __builtin_amdgcn_cvt_pk_u8_f32(lvl(v[2]), 2, e);
+  uint32_t o = __builtin_amdgcn_cvt_pk_u8_f32(lvl(v[1]), 0, 0u);
+  o = __builtin_amdgcn_cvt_pk_u8_f32(lvl(v[3]), 2, o);
+  const uint32_t x = e | (o << W);  // columns 0,1 at bit 0; columns 2,3 at bit 16
+  if (W == 4) return __builtin_amdgcn_perm(0u, x, 0x0c0c0200u);  // bytes 0 and 2
+  // W == 6: bits [0,12) from x, bits [12,24) from x >> 4, as one bitfield
+  // insert (the compiler otherwise rewrites the expression into three ops)
+  uint32_t w;
+  __asm__("v_bfi_b32 %0, %1, %2, %3" : "=v"(w) : "s"(0xfffu), "v"(x), "v"(x >> 4));
+  return w;
+}
+
 template <int W, int MODE>
 __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx &C) {
 #pragma clang fp contract(off)
@@ -935,17 +1056,22 @@ __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx
   const uint16_t *c16 = (const uint16_t *)C.cst;
   stage_in_fast<W / 2>(C, 16 * NG, true);
   __syncthreads();
-  row_setup<MODE>(S, C, NG);
+  row_setup_int<MODE>(S, C, NG, ZS, ZO);
   __syncthreads();
 
   float cj[4];
 #pragma unroll
   for (int c = 0; c < 4; c++) cj[c] = hw_h2f(c16[C.j0 + c]);
 
+  // per-lane row pointers: row rg + 8r of this lane's value group
+  const float4 *rcl = C.rc + C.rg * NG + g;
+  const float2 *iul = C.iu + C.rg * NG + g;
+  const float *ksl = C.ks + C.rg;
+  const int RS8 = 8 * NG;  // row stride of rcl / iul for 8 rows
+
   // ---- foreground: codes, k^T x and q^T x sums
   float cf[FRPT][4];
   float aK[4] = {0.f, 0.f, 0.f, 0.f}, aQ[4] = {0.f, 0.f, 0.f, 0.f};
-  float sKA = 0.f, sQA = 0.f, sQK = 0.f;
   // rows rg + 8r are 8*SEG bytes apart: one base address, immediate offsets
   const int pos0 = C.blk * BLK + C.rg * SEG + C.sub * (W / 2);
   const uint32_t *w32 = (const uint32_t *)(C.code + (pos0 & ~3));
@@ -953,7 +1079,6 @@ __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx
 #pragma unroll
   for (int r = 0; r < FRPT; r++) {
     if ((r % SCHED_ROWS) == SCHED_ROWS - 1) __builtin_amdgcn_sched_barrier(0);
-    const int i = C.rg + 8 * r;
     uint32_t word;
     if (W == 8) word = w32[r * 4 * W];  // 8 rows = 16W bytes = 4W dwords
     else if (W == 4) word = *(const uint16_t *)(C.code + pos0 + r * 8 * SEG);
@@ -961,34 +1086,30 @@ __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx
     else word = __builtin_amdgcn_alignbit(w32[r * 4 * W + 1], w32[r * 4 * W], sh);
 #pragma unroll
     for (int c = 0; c < 4; c++) cf[r][c] = (float)((word >> (c * W)) & MASK);
-    const float a = C.as[i * NG + g], k = C.ks[i];
-    const float ka = k * a;
-#pragma unroll
-    for (int c = 0; c < 4; c++) aK[c] = fmaf(ka, cf[r][c], aK[c]);
-    sKA += ka;
     if (MODE != MODE_WRITE) {
-      const float q = C.qs[i];
-      const float qa = q * a;
+      const float4 rc = rcl[r * RS8];
 #pragma unroll
-      for (int c = 0; c < 4; c++) aQ[c] = fmaf(qa, cf[r][c], aQ[c]);
-      sQA += qa;
-      sQK = fmaf(q, k, sQK);
+      for (int c = 0; c < 4; c++) {
+        aK[c] = fmaf(rc.x, cf[r][c], aK[c]);
+        aQ[c] = fmaf(rc.y, cf[r][c], aQ[c]);
+      }
     }
   }
-  sKA = rg8_sum(sKA);
   float delta[4], o[4];
   if (MODE == MODE_WRITE) {
     const int64_t base = ((int64_t)C.b * P.H + C.h) * FV + C.j0;
 #pragma unroll
     for (int c = 0; c < 4; c++) delta[c] = S.s_delta[base + c];
   } else {
-    sQA = rg8_sum(sQA);
-    sQK = rg8_sum(sQK);
+    const float sKA = C.misc[16 + SUM_KA + g] + C.misc[32 + SUM_KA + g];
+    const float sQA = C.misc[16 + SUM_QA + g] + C.misc[32 + SUM_QA + g];
+    const float sQK = C.misc[16 + SUM_QK] + C.misc[32 + SUM_QK];
+    float vv[4];
+    load4(S.v, S.qkv_dtype, (int64_t)C.b * S.v_stride + (int64_t)C.h * FV + C.j0, vv);
 #pragma unroll
     for (int c = 0; c < 4; c++) {
       const float kS = cj[c] * fmaf(ZS, rg8_sum(aK[c]), -ZO * sKA);
-      const float vv = load_val(S.v, S.qkv_dtype, (int64_t)C.b * S.v_stride + (int64_t)C.h * FV + C.j0 + c);
-      delta[c] = beta * (vv - kS);
+      delta[c] = beta * (vv[c] - kS);
       o[c] = fmaf(delta[c], sQK, cj[c] * fmaf(ZS, rg8_sum(aQ[c]), -ZO * sQA));
     }
     store_out<MODE>(P, S, C, o, delta);
@@ -1003,30 +1124,35 @@ __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx
 #pragma unroll
   for (int r = 0; r < FRPT; r++) {
     if ((r % SCHED_ROWS) == SCHED_ROWS - 1) __builtin_amdgcn_sched_barrier(0);
-    const int i = C.rg + 8 * r;
-    const float a = C.as[i * NG + g], k = C.ks[i];
-    const float A = ZS * a, mL = -ZO * a;
+    const float4 rc = rcl[r * RS8];
+    const float k = ksl[8 * r];
     float acc = 0.f;
 #pragma unroll
     for (int c = 0; c < 4; c++) {
-      const float inner = fmaf(A, cf[r][c], fmaf(k, dj[c], mL));
+      const float inner = fmaf(rc.z, cf[r][c], fmaf(k, dj[c], rc.w));
       cf[r][c] = inner;
       acc = fmaf(cj[c], fabsf(inner), acc);
     }
     rowp[r] = acc;
   }
-  // reduce-scatter over the wave's 8 column groups (lane bits 3,4,5)
+  // reduce-scatter over the wave's 8 column groups (lane bits 3,4,5):
+  // lane halves exchange with v_permlane32_swap (lanes 32-63 of the first
+  // operand trade places with lanes 0-31 of the second), 16-lane rows with
+  // v_permlane16_swap (odd rows of the first with even rows of the second),
+  // so one add leaves row r in the lower and row r + half in the upper lanes
   const int b3 = (C.tid >> 3) & 1, b4 = (C.tid >> 4) & 1, b5 = (C.tid >> 5) & 1;
   float p8[8], p4[4], p2[2];
 #pragma unroll
   for (int r = 0; r < 8; r++) {
-    const float keep = b5 ? rowp[r + 8] : rowp[r], send = b5 ? rowp[r] : rowp[r + 8];
-    p8[r] = keep + __shfl_xor(send, 32);
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(rowp[r]), __float_as_uint(rowp[r + 8]),
+                                                     false, false);
+    p8[r] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
   }
 #pragma unroll
   for (int r = 0; r < 4; r++) {
-    const float keep = b4 ? p8[r + 4] : p8[r], send = b4 ? p8[r] : p8[r + 4];
-    p4[r] = keep + __shfl_xor(send, 16);
+    const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(p8[r]), __float_as_uint(p8[r + 4]),
+                                                     false, false);
+    p4[r] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
   }
 #pragma unroll
   for (int r = 0; r < 2; r++) {
@@ -1051,92 +1177,120 @@ __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx
       uint32_t hb;
       const float wi = C.wv[i];
       const float rn = hw_fp16_scale(__builtin_sqrtf(m / wi), &hb);
-      C.ir[e] = rcp(rn);
-      C.uu[e] = (wi * wi) * (rn * rn);
+      C.iu[e] = make_float2(rcp(rn), (wi * wi) * (rn * rn));
       ((uint16_t *)C.rst)[e] = (uint16_t)hb;
     }
   }
   __syncthreads();
-  // ---- scaled values s = x'/r', column max
+  // ---- t = x'/(r' c) (the scaled value s = x'/r' is t*c), column max of |t|
   float mx[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int r = 0; r < FRPT; r++) {
     if ((r % SCHED_ROWS) == SCHED_ROWS - 1) __builtin_amdgcn_sched_barrier(0);
-    const float ir = C.ir[(C.rg + 8 * r) * NG + g];
+    const float ir = iul[r * RS8].x;
 #pragma unroll
     for (int c = 0; c < 4; c++) {
-      const float sv = cf[r][c] * (cj[c] * ir);
-      cf[r][c] = sv;
-      mx[c] = fmaxf(mx[c], fabsf(sv));
+      const float t = cf[r][c] * ir;
+      cf[r][c] = t;
+      mx[c] = fmaxf(mx[c], fabsf(t));
     }
   }
-  float c0[4], ic0[4], num[4] = {0.f, 0.f, 0.f, 0.f}, den[4] = {0.f, 0.f, 0.f, 0.f};
+  // c0 = fp16(max|s| / L); y = s/c0 = t * (c/c0)
+  float c0[4], f0[4], num[4] = {0.f, 0.f, 0.f, 0.f}, den[4] = {0.f, 0.f, 0.f, 0.f};
+  bool top = false;
 #pragma unroll
   for (int c = 0; c < 4; c++) {
-    c0[c] = hw_fp16_scale(rg8_max_nonneg(mx[c]) * (1.0f / (float)L), nullptr);
-    ic0[c] = rcp(c0[c]);
+    c0[c] = hw_fp16_scale((cj[c] * rg8_max_nonneg(mx[c])) * (1.0f / (float)L), nullptr);
+    f0[c] = cj[c] * rcp(c0[c]);
+    top |= c0[c] >= 65504.0f;
   }
+  // Unless c0 saturated at the fp16 maximum, |y| <= L (1 + 2^-11) and
+  // rint(y) needs no clamp to [-L, L].
 #pragma unroll
   for (int r = 0; r < FRPT; r++) {
     if ((r % SCHED_ROWS) == SCHED_ROWS - 1) __builtin_amdgcn_sched_barrier(0);
-    const float U = C.uu[(C.rg + 8 * r) * NG + g];
+    const float U = iul[r * RS8].y;
 #pragma unroll
     for (int c = 0; c < 4; c++) {
-      const float y = cf[r][c] * ic0[c];
+      const float y = cf[r][c] * f0[c];
       float z;
       if (W == 2) {
         const float mag = fabsf(y) >= 2.0f ? 3.0f : 1.0f;
         z = y >= 0.0f ? mag : -mag;
       } else {
-        z = __builtin_amdgcn_fmed3f(__builtin_rintf(y), -(float)L, (float)L);
+        z = __builtin_rintf(y);
       }
       const float t = U * z;
       num[c] = fmaf(t, cf[r][c], num[c]);
       den[c] = fmaf(t, z, den[c]);
     }
   }
-  float ic[4];
+  if (W != 2 && __any(top)) {
+    // Saturated c0 (states beyond the fp16 range): redo the sums with the
+    // clamp, recomputing t from the staged old codes and the row constants
+    // with the same operations, so the register tile is left untouched.
+#pragma unroll
+    for (int c = 0; c < 4; c++) num[c] = den[c] = 0.f;
+#pragma unroll 1
+    for (int r = 0; r < FRPT; r++) {
+      const int i = C.rg + 8 * r;
+      uint32_t word;
+      if (W == 8) word = w32[r * 4 * W];
+      else if (W == 4) word = *(const uint16_t *)(C.code + pos0 + r * 8 * SEG);
+      else word = __builtin_amdgcn_alignbit(w32[r * 4 * W + 1], w32[r * 4 * W], sh);
+      const float4 rc = C.rc[i * NG + g];
+      const float k = C.ks[i];
+      const float2 iu = C.iu[i * NG + g];
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        const float code = (float)((word >> (c * W)) & MASK);
+        const float t = fmaf(rc.z, code, fmaf(k, dj[c], rc.w)) * iu.x;
+        const float z = __builtin_amdgcn_fmed3f(__builtin_rintf(t * f0[c]), -(float)L, (float)L);
+        const float uz = iu.y * z;
+        num[c] = fmaf(uz, t, num[c]);
+        den[c] = fmaf(uz, z, den[c]);
+      }
+    }
+  }
+  float f[4];
 #pragma unroll
   for (int c = 0; c < 4; c++) {
-    const float n = rg8_sum(num[c]), d = rg8_sum(den[c]);
+    const float n = cj[c] * rg8_sum(num[c]), d = rg8_sum(den[c]);
     const float dc = d < 1e-30f ? 1e-30f : d;
     uint32_t hb;
     const float cc = hw_fp16_scale(d > 0.0f ? n * rcp(dc) : c0[c], &hb);
-    ic[c] = rcp(cc);
+    f[c] = cj[c] * rcp(cc);
     if (C.rg == 0) ((uint16_t *)C.cst)[C.j0 + c] = (uint16_t)hb;
   }
   // ---- final codes, packed back into the staged region
 #pragma unroll
   for (int r = 0; r < FRPT; r++) {
     if ((r % SCHED_ROWS) == SCHED_ROWS - 1) __builtin_amdgcn_sched_barrier(0);
-    const int i = C.rg + 8 * r;
-    uint32_t word = 0;
+    uint32_t word;
+    if (W == 2) {
+      word = 0;
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-      uint32_t code;
-      if (W == 2) {
-        const float y = cf[r][c] * ic[c];
+      for (int c = 0; c < 4; c++) {
+        const float y = cf[r][c] * f[c];
         const bool big = fabsf(y) >= 2.0f;
-        code = y >= 0.0f ? (big ? 3u : 2u) : (big ? 0u : 1u);
-      } else {
-        // floor(y + L + 1/2) saturated to [0, 2L]: the level of rint(y) + L
-        code = (uint32_t)__builtin_amdgcn_fmed3f(fmaf(cf[r][c], ic[c], (float)L + 0.5f), 0.0f,
-                                                 (float)(2 * L) + 0.5f);
+        const uint32_t code = y >= 0.0f ? (big ? 3u : 2u) : (big ? 0u : 1u);
+        word |= code << (c * W);
       }
-      word |= code << (c * W);
+    } else {
+      float v[4];
+#pragma unroll
+      for (int c = 0; c < 4; c++) v[c] = fmaf(cf[r][c], f[c], (float)L);
+      word = pack_codes<W>(v);
     }
     const int pos = pos0 + r * 8 * SEG;
-    (void)i;
     if (W == 8) *(uint32_t *)(C.code + pos) = word;
     else if (W == 4) *(uint16_t *)(C.code + pos) = (uint16_t)word;
     else if (W == 2) C.code[pos] = (uint8_t)word;
     else {
-      // 3 bytes at an odd or even offset: one aligned half-word and one byte
-      const int odd = C.sub & 1;
-      const uint32_t half = odd ? (word >> 8) : (word & 0xffffu);
-      const uint32_t byte = odd ? (word & 0xffu) : (word >> 16);
-      *(uint16_t *)(C.code + pos + odd) = (uint16_t)half;
-      C.code[pos + 2 - 2 * odd] = (uint8_t)byte;
+      // 3 bytes at an odd or even offset, one byte store each
+      C.code[pos] = (uint8_t)word;
+      C.code[pos + 1] = (uint8_t)(word >> 8);
+      C.code[pos + 2] = (uint8_t)(word >> 16);
     }
   }
   __syncthreads();
@@ -1253,14 +1407,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GDN128_WAVE
   C.kraw = C.qraw + FK;
   C.wv = C.kraw + FK;
   C.misc = C.wv + FK;
-  C.red = C.misc + 16;
+  C.red = C.misc + MISC_FLOATS;
   C.ks = C.red + 4 * FK;
   C.qs = C.ks + FK;
   const int ngm = P.G >= 32 ? FV / P.G : 1;
-  C.as = C.qs + FK;
-  C.ir = C.as + FK * ngm;
-  C.uu = C.ir + FK * ngm;
-  C.rnew = C.uu;
+  C.rc = (float4 *)(C.qs + FK);
+  C.iu = (float2 *)(C.rc + FK * ngm);
 
   // inputs: raw q, k rows, norms, beta and the head's retention
   const int64_t bh = (int64_t)C.b * H + C.h;
@@ -1274,12 +1426,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GDN128_WAVE
       const float kv = load_val(S.k, S.qkv_dtype, (int64_t)C.b * S.k_stride + (int64_t)hk * FK + C.tid);
       C.qraw[C.tid] = qv;
       C.kraw[C.tid] = kv;
-      float sq = qv * qv, sk = kv * kv;
-#pragma unroll
-      for (int m = 1; m < 64; m <<= 1) {
-        sq += __shfl_xor(sq, m);
-        sk += __shfl_xor(sk, m);
-      }
+      const float sq = wave_sum(qv * qv), sk = wave_sum(kv * kv);
       if ((C.tid & 63) == 0) {
         C.misc[8 + 2 * (C.tid >> 6)] = sq;
         C.misc[9 + 2 * (C.tid >> 6)] = sk;
@@ -1403,9 +1550,9 @@ int launch_step_mode(const sq_pool *pool, StepDev sd, int64_t batch, hipStream_t
   PoolDev pd = to_dev(pool);
   if (MODE != MODE_DECODE && pd.fast) {
     const int ng_max = pool->group >= 32 ? 128 / pool->group : 1;
-    // staging | rows | columns | q,k raw + w | misc | red | ks, qs | as, ir, uu per (row, group)
-    size_t lds = (size_t)pd.stage + pd.rstage + 2 * 128 + 3 * 128 * 4 + 16 * 4 + 4 * 128 * 4 + 2 * 128 * 4 +
-                 (size_t)3 * 128 * ng_max * 4;
+    // staging | rows | columns | q,k raw + w | misc | red | ks, qs | rc (float4), iu (float2) per (row, group)
+    size_t lds = (size_t)pd.stage + pd.rstage + 2 * 128 + 3 * 128 * 4 + 48 * 4 + 4 * 128 * 4 + 2 * 128 * 4 +
+                 (size_t)6 * 128 * ng_max * 4;
     hipLaunchKernelGGL((gdn128_kernel<MODE>), dim3((unsigned)(batch * pool->heads)), dim3(256), lds, st, pd, sd);
     return check_launch("gdn128_kernel");
   }
