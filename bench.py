@@ -54,13 +54,17 @@ def make_plan(torch, arch, H, K, nominal, seed=0):
     if arch == "gdn":
         if nominal == 6:
             widths = torch.tensor([4] * (H // 4) + [6] * (H // 2) + [8] * (H - H // 4 - H // 2))
-        else:
-            widths = torch.tensor([2] * (H // 4) + [4] * (H // 2) + [6] * (H - H // 4 - H // 2))
+        else:  # {2,4,6,8} averaging 4 (the reference has no 3-bit width)
+            n2 = n4 = 3 * H // 8
+            n6 = (H - n2 - n4) // 2
+            widths = torch.tensor([2] * n2 + [4] * n4 + [6] * n6 + [8] * (H - n2 - n4 - n6))
         widths = widths[torch.randperm(H, generator=g)]
         bits = widths[:, None].expand(H, K).contiguous()
     else:
-        choices = torch.tensor([4, 6, 8] if nominal == 6 else [2, 4, 6])
-        bits = choices[torch.randint(0, 3, (H, K), generator=g)]
+        if nominal == 6:
+            bits = torch.tensor([4, 6, 8])[torch.randint(0, 3, (H, K), generator=g)]
+        else:
+            bits = torch.tensor([2, 2, 2, 4, 4, 4, 6, 8])[torch.randint(0, 8, (H, K), generator=g)]
         bits[torch.rand(H, K, generator=g) < .01] = 16
     impact = torch.rand(H, K, generator=g) + .5
     return bits, impact
@@ -122,10 +126,18 @@ def main():
     pool = PackedStatePool(plan, B + 1, V, writeback_stream=stream)
     g = torch.Generator(device=dev).manual_seed(0)
     slots = torch.arange(1, B + 1, device=dev, dtype=torch.int32)
-    pool.encode(torch.randn(B, H, K, V, device=dev, generator=g) * .05, slots)
+    if a.nominal == 4:
+        # key-row and value-column scales log-normal(0, 0.5)
+        r = torch.exp(torch.randn(B, H, K, 1, device=dev, generator=g) * .5)
+        c = torch.exp(torch.randn(B, H, 1, V, device=dev, generator=g) * .5)
+        pool.encode(r * torch.randn(B, H, K, V, device=dev, generator=g) * c, slots)
+    else:
+        pool.encode(torch.randn(B, H, K, V, device=dev, generator=g) * .05, slots)
     mixed = torch.randn(B, 2 * HK * K + H * V, device=dev, generator=g).to(torch.bfloat16)
     q, k, v = mixed.split([HK * K, HK * K, H * V], -1)
-    gate = torch.randn(B, H, K, device=dev, generator=g) if a.arch == "kda" else torch.randn(B, H, device=dev, generator=g)
+    # raw gates with A_log = 0, dt_bias = 0: g = -softplus(a); KDA a = 0.5 N(0,1) per channel
+    gate = torch.randn(B, H, K, device=dev, generator=g) * .5 if a.arch == "kda" else \
+        torch.randn(B, H, device=dev, generator=g)
     beta = torch.randn(B, H, device=dev, generator=g)
     a_log = torch.zeros(H, device=dev)
     dt_bias = torch.zeros(H * K if a.arch == "kda" else H, device=dev)

@@ -78,8 +78,10 @@ typedef struct sq_pool {
     int32_t reserved;
 } sq_pool;
 
-/* sq_pool.flags: the pool qualifies for the K=V=128 uniform-width GDN kernel */
+/* sq_pool.flags: the pool qualifies for the K=V=128 uniform-width GDN kernel,
+ * or for the K=V=128 KDA kernel */
 #define SQ_POOL_FAST_GDN128 1
+#define SQ_POOL_FAST_KDA128 2
 
 /*
  * Inputs of one decode step (PackedStatePool.step, pool.py:200-282).

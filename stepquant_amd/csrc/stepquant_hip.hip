@@ -284,7 +284,7 @@ struct PoolDev {
   int H, K, V, G, kda;
   int stage;   // bytes of LDS staging per workgroup (largest head window)
   int rstage;  // bytes of LDS for one head's row scales (fast path)
-  int fast;    // pool qualifies for the K=V=128 uniform-width GDN kernel
+  int fast;    // SQ_POOL_FAST_* bits: which K=V=128 kernel the pool qualifies for
 };
 
 __device__ __forceinline__ int tile_of(const PoolDev &P) { return P.kda ? (P.V < 4 ? P.V : 4) : (P.V < 16 ? P.V : 16); }
@@ -888,7 +888,7 @@ struct Ctx {
   uint8_t *cst;    // staged column scales
   float *qraw, *kraw, *wv, *misc, *red;
   float *ks, *qs;  // per-row prepared k, q
-  float4 *rc;      // per (row, group): k*a, q*a, ZS*a, -ZO*a with a = r * retention
+  float4 *rc;      // per (row, group): k*a, q*a, ZS*a, a with a = r * retention
   float2 *iu;      // per (row, group): 1/r', w^2 r'^2
   int b, h, tid, rg, cg, wave, j0, blk, sub;
   int code_start, code_bytes, row_start, row_bytes, colbase;
@@ -897,6 +897,7 @@ struct Ctx {
 // misc[] slots: 0 beta, 1 retention, 8..11 squared norms of q/k halves,
 // 16.. and 32.. per-wave partial sums of k*a (per group), q*a (per group), q*k
 constexpr int MISC_FLOATS = 48;
+constexpr int KDA_COL_STAGE = 288;  // staged column-scale window (2V bytes + alignment)
 constexpr int SUM_KA = 0, SUM_QA = 4, SUM_QK = 8;
 
 // sum over the 64 lanes of a wave, result in every lane: 16-lane rows by
@@ -913,7 +914,7 @@ __device__ __forceinline__ float wave_sum(float x) {
 // Per-row constants of the integer bodies (threads 0..127, row i = tid):
 // rc[i, g] and, for the readout, the sums over rows of k*a, q*a and q*k.
 template <int MODE>
-__device__ __forceinline__ void row_setup_int(const StepDev &S, const Ctx &C, int NG, float ZS, float ZO) {
+__device__ __forceinline__ void row_setup_int(const StepDev &S, const Ctx &C, int NG, float ZS) {
   if (C.tid < FK) {
     const int i = C.tid;
     float nq = 1.0f, nk = 1.0f;
@@ -935,7 +936,7 @@ __device__ __forceinline__ void row_setup_int(const StepDev &S, const Ctx &C, in
         const float a = hw_h2f(r16[i * NG + g]) * retention;
         ska[g] = k * a;
         sqa[g] = q * a;
-        C.rc[i * NG + g] = make_float4(ska[g], sqa[g], ZS * a, -ZO * a);
+        C.rc[i * NG + g] = make_float4(ska[g], sqa[g], ZS * a, a);
       }
     }
     if (MODE != MODE_WRITE) {
@@ -1012,6 +1013,12 @@ __device__ __forceinline__ void stage_back_fast(const Ctx &C, int row_chunks, bo
     ((uint4 *)(C.page + C.colbase))[C.tid - (FNT - 16)] = ((const uint4 *)C.cst)[C.tid - (FNT - 16)];
 }
 
+// signed W-bit field c of a word (sign-extended)
+template <int W>
+__device__ __forceinline__ int sfield(uint32_t word, int c) {
+  return (int)(word << (32 - W * (c + 1))) >> (32 - W);
+}
+
 // Final codes of four values from v = y + L: level(y) = rint(y) + L
 // saturated to [0, 2L].  v_cvt_pk_u8_f32 converts with round-to-nearest-even
 // into one byte lane, so the saturated v converts straight into place; the
@@ -1045,18 +1052,22 @@ template <int W, int MODE>
 __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx &C) {
 #pragma clang fp contract(off)
   constexpr int L = W == 2 ? 3 : (1 << (W - 1)) - 1;
-  constexpr float ZS = W == 2 ? 2.0f : 1.0f;   // z = ZS*code - ZO
-  constexpr float ZO = W == 2 ? 3.0f : (float)L;
+  // Codes are offset binary (code = z + L; 2-bit: code = (z + 3) / 2).  With
+  // the field's top bit flipped they read as a signed W-bit integer
+  // s = code - 2^(W-1), and z = ZS*s + 1.  Sums over s instead of over the
+  // unsigned code keep the cancelled offset at 1 instead of L, so columns
+  // whose codes sit near the middle of the range lose no precision.
+  constexpr float ZS = W == 2 ? 2.0f : 1.0f;
+  constexpr uint32_t XM = W == 8 ? 0x80808080u : W == 6 ? 0x820820u : W == 4 ? 0x8888u : 0xAAu;
   constexpr int SEG = 2 * W;                   // bytes of one row's 16-value segment
   constexpr int BLK = FK * SEG;                // bytes of one 16-column block
-  constexpr uint32_t MASK = (1u << W) - 1u;
   const float beta = C.misc[0];
   const int NG = W == 2 ? FV / P.G : 1;
   const int g = W == 2 ? C.j0 / P.G : 0;
   const uint16_t *c16 = (const uint16_t *)C.cst;
   stage_in_fast<W / 2>(C, 16 * NG, true);
   __syncthreads();
-  row_setup_int<MODE>(S, C, NG, ZS, ZO);
+  row_setup_int<MODE>(S, C, NG, ZS);
   __syncthreads();
 
   float cj[4];
@@ -1084,8 +1095,9 @@ __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx
     else if (W == 4) word = *(const uint16_t *)(C.code + pos0 + r * 8 * SEG);
     else if (W == 2) word = C.code[pos0 + r * 8 * SEG];
     else word = __builtin_amdgcn_alignbit(w32[r * 4 * W + 1], w32[r * 4 * W], sh);
+    word ^= XM;
 #pragma unroll
-    for (int c = 0; c < 4; c++) cf[r][c] = (float)((word >> (c * W)) & MASK);
+    for (int c = 0; c < 4; c++) cf[r][c] = (float)sfield<W>(word, c);
     if (MODE != MODE_WRITE) {
       const float4 rc = rcl[r * RS8];
 #pragma unroll
@@ -1108,9 +1120,9 @@ __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx
     load4(S.v, S.qkv_dtype, (int64_t)C.b * S.v_stride + (int64_t)C.h * FV + C.j0, vv);
 #pragma unroll
     for (int c = 0; c < 4; c++) {
-      const float kS = cj[c] * fmaf(ZS, rg8_sum(aK[c]), -ZO * sKA);
+      const float kS = cj[c] * fmaf(ZS, rg8_sum(aK[c]), sKA);
       delta[c] = beta * (vv[c] - kS);
-      o[c] = fmaf(delta[c], sQK, cj[c] * fmaf(ZS, rg8_sum(aQ[c]), -ZO * sQA));
+      o[c] = fmaf(delta[c], sQK, cj[c] * fmaf(ZS, rg8_sum(aQ[c]), sQA));
     }
     store_out<MODE>(P, S, C, o, delta);
   }
@@ -1129,7 +1141,9 @@ __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx
     float acc = 0.f;
 #pragma unroll
     for (int c = 0; c < 4; c++) {
-      const float inner = fmaf(rc.z, cf[r][c], fmaf(k, dj[c], rc.w));
+      // a*z first (exact zero for z = 0), then the rank-1 term: no offset
+      // is cancelled against k*delta/c
+      const float inner = fmaf(k, dj[c], fmaf(rc.z, cf[r][c], rc.w));
       cf[r][c] = inner;
       acc = fmaf(cj[c], fabsf(inner), acc);
     }
@@ -1241,10 +1255,11 @@ __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx
       const float4 rc = C.rc[i * NG + g];
       const float k = C.ks[i];
       const float2 iu = C.iu[i * NG + g];
+      word ^= XM;
 #pragma unroll
       for (int c = 0; c < 4; c++) {
-        const float code = (float)((word >> (c * W)) & MASK);
-        const float t = fmaf(rc.z, code, fmaf(k, dj[c], rc.w)) * iu.x;
+        const float code = (float)sfield<W>(word, c);
+        const float t = fmaf(k, dj[c], fmaf(rc.z, code, rc.w)) * iu.x;
         const float z = __builtin_amdgcn_fmed3f(__builtin_rintf(t * f0[c]), -(float)L, (float)L);
         const float uz = iu.y * z;
         num[c] = fmaf(uz, t, num[c]);
@@ -1462,6 +1477,472 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GDN128_WAVE
   }
 }
 
+// =====================================================================
+// KDA, K = V = 128: per key-row widths (2/4/6/8-bit codes, FP16 pivot rows),
+// one 4-value tile per row per block, per-channel retention.  One
+// workgroup per (request, head); lane (rg, cg) owns rows rg + 8r (r < 16)
+// and block cg (columns 4cg .. 4cg+3), as the GDN kernel.  Row widths vary
+// per lane, so code fields are extracted and packed with run-time widths.
+// Integer rows use x = a_i c_j z_ij with a_i = r_i * retention_i * norm_i,
+// norm_i = 2^(8 - b_i); pivot rows (x = fp16 * retention, no scales) are
+// handled in a separate pass over the head's pivot rows.
+// =====================================================================
+namespace kfast {
+using namespace fast;
+
+struct KCtx {
+  uint8_t *page, *code, *rst, *cst;
+  int shift_c, shift_r, shift_col;
+  float *qraw, *kraw, *wv, *gv, *misc, *red, *ks, *qs;
+  float4 *rc;   // per row: k*a, q*a, a, a  (zeros for pivot rows)
+  float4 *rl;   // per row: L, 1/L, 1/(r' norm), w^2 r'^2 norm^2 (zeros for pivots)
+  int4 *rm;     // per row: byte position in block 0 (staged), width (0: pivot), top-bit mask, tile bytes
+  uint32_t *pmask;  // 128-bit mask of pivot rows
+  int b, h, tid, rg, cg, wave, j0;
+  int code_start, code_bytes, row_start, row_bytes, colbase, stride;
+};
+
+// sign-extended field of run-time width w at bit offset o
+__device__ __forceinline__ int sbfe(uint32_t word, uint32_t o, uint32_t w) {
+  return __builtin_amdgcn_sbfe((int)word, o, w);
+}
+
+// the 32 bits starting at staged byte p
+__device__ __forceinline__ uint32_t word_at(const uint8_t *lds, int p) {
+  const uint32_t *w = (const uint32_t *)(lds + (p & ~3));
+  return __builtin_amdgcn_alignbit(w[1], w[0], (uint32_t)(p & 3) * 8u);
+}
+
+// Per-row constants (threads 0..127, row i = tid), the pivot-row mask and
+// the readout sums over rows of k*a, q*a (integer rows) and q*k (all rows).
+template <int MODE>
+__device__ __forceinline__ void row_setup(const PoolDev &P, const StepDev &S, const KCtx &C) {
+  if (C.tid < FK) {
+    const int i = C.tid;
+    const int64_t hi = (int64_t)C.h * FK + i;
+    const int bi = P.bits[hi];
+    const bool piv = bi == 16;
+    float nq = 1.0f, nk = 1.0f;
+    if (MODE != MODE_WRITE && S.normalize) {
+      nq = 1.0f / __builtin_sqrtf((C.misc[8] + C.misc[10]) + 1e-6f);
+      nk = 1.0f / __builtin_sqrtf((C.misc[9] + C.misc[11]) + 1e-6f);
+    }
+    const float k = MODE == MODE_WRITE ? C.kraw[i] : C.kraw[i] * nk;
+    const float q = MODE == MODE_WRITE ? 0.0f : (C.qraw[i] * nq) * S.scale;
+    C.ks[i] = k;
+    C.qs[i] = q;
+    const float retention = C.gv[i];
+    const int pos = C.shift_c + (P.offsets[hi] - C.code_start);
+    float ka = 0.f, qa = 0.f;
+    if (piv) {
+      C.rc[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+      C.rl[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+      C.rm[i] = make_int4(pos, 0, 0, 0);  // width 0: no code fields
+    } else {
+      const int L = (1 << (bi - 1)) - 1;
+      const float norm = (float)(1 << (8 - bi));
+      const float r = hw_h2f(*(const uint16_t *)(C.rst + C.shift_r + (P.rows[hi] - C.row_start)));
+      const float a = (r * retention) * norm;
+      ka = k * a;
+      qa = q * a;
+      C.rc[i] = make_float4(ka, qa, a, a);
+      C.rl[i] = make_float4((float)L, 1.0f / (float)L, 0.f, 0.f);
+      uint32_t xm = 0;
+#pragma unroll
+      for (int c = 0; c < 4; c++) xm |= 1u << (c * bi + bi - 1);
+      C.rm[i] = make_int4(pos, bi, (int)xm, bi / 2);
+    }
+    const uint64_t pb = __ballot(piv);
+    if ((i & 63) == 0) {
+      C.pmask[2 * (i >> 6)] = (uint32_t)pb;
+      C.pmask[2 * (i >> 6) + 1] = (uint32_t)(pb >> 32);
+    }
+    if (MODE != MODE_WRITE) {
+      float *part = C.misc + 16 + 16 * (i >> 6);
+      const float s1 = wave_sum(ka), s2 = wave_sum(qa), s3 = wave_sum(q * k);
+      if ((i & 63) == 0) {
+        part[SUM_KA] = s1;
+        part[SUM_QA] = s2;
+        part[SUM_QK] = s3;
+      }
+    }
+  }
+}
+
+// four FP16 values of pivot row p in this lane's block, times `scale`
+__device__ __forceinline__ void pivot_load(const KCtx &C, int p, float scale, float x[4]) {
+  const int pos = C.rm[p].x + C.cg * C.stride;
+  const uint32_t lo = word_at(C.code, pos), hi = word_at(C.code, pos + 4);
+  x[0] = hw_h2f(lo & 0xffffu) * scale;
+  x[1] = hw_h2f(lo >> 16) * scale;
+  x[2] = hw_h2f(hi & 0xffffu) * scale;
+  x[3] = hw_h2f(hi >> 16) * scale;
+}
+
+// Next pivot row of the head after clearing it from the (wave-uniform) mask;
+// -1 when none is left.
+__device__ __forceinline__ int next_pivot(uint32_t m[4]) {
+#pragma unroll
+  for (int d = 0; d < 4; d++) {
+    if (m[d]) {
+      const int bit = __builtin_ctz(m[d]);
+      m[d] &= m[d] - 1u;
+      return 32 * d + bit;
+    }
+  }
+  return -1;
+}
+
+template <int MODE>
+__device__ __forceinline__ void body(const PoolDev &P, const StepDev &S, KCtx &C) {
+#pragma clang fp contract(off)
+  const float beta = C.misc[0];
+  const bool has_cols = C.colbase >= 0;
+  float cj[4];
+#pragma unroll
+  for (int c = 0; c < 4; c++)
+    cj[c] = has_cols ? hw_h2f(*(const uint16_t *)(C.cst + C.shift_col + 2 * (C.j0 + c))) : 1.0f;
+  uint32_t pm0[4];
+#pragma unroll
+  for (int d = 0; d < 4; d++) pm0[d] = __builtin_amdgcn_readfirstlane(C.pmask[d]);
+  const int base = C.cg * C.stride;
+
+  // ---- foreground: signed code fields s = code - 2^(b-1) (z = s + 1)
+  float cf[FRPT][4];
+  float aK[4] = {0.f, 0.f, 0.f, 0.f}, aQ[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int r = 0; r < FRPT; r++) {
+    if ((r % SCHED_ROWS) == SCHED_ROWS - 1) __builtin_amdgcn_sched_barrier(0);
+    const int i = C.rg + 8 * r;
+    const int4 m = C.rm[i];
+    const uint32_t word = word_at(C.code, m.x + base) ^ (uint32_t)m.z;
+    const uint32_t w = (uint32_t)m.y;
+#pragma unroll
+    for (int c = 0; c < 4; c++) cf[r][c] = (float)sbfe(word, c * w, w);
+    if (MODE != MODE_WRITE) {
+      const float4 rc = C.rc[i];
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        aK[c] = fmaf(rc.x, cf[r][c], aK[c]);
+        aQ[c] = fmaf(rc.y, cf[r][c], aQ[c]);
+      }
+    }
+  }
+  float delta[4];
+  if (MODE == MODE_WRITE) {
+    const int64_t bi = ((int64_t)C.b * P.H + C.h) * FV + C.j0;
+#pragma unroll
+    for (int c = 0; c < 4; c++) delta[c] = S.s_delta[bi + c];
+  } else {
+    // pivot rows owned by this lane (row % 8 == rg)
+    float pK[4] = {0.f, 0.f, 0.f, 0.f}, pQ[4] = {0.f, 0.f, 0.f, 0.f};
+    uint32_t pm[4] = {pm0[0], pm0[1], pm0[2], pm0[3]};
+    for (int p = next_pivot(pm); p >= 0; p = next_pivot(pm)) {
+      if ((p & 7) == C.rg) {
+        float x[4];
+        pivot_load(C, p, C.gv[p], x);
+        const float k = C.ks[p], q = C.qs[p];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+          pK[c] = fmaf(k, x[c], pK[c]);
+          pQ[c] = fmaf(q, x[c], pQ[c]);
+        }
+      }
+    }
+    const float sKA = C.misc[16 + SUM_KA] + C.misc[32 + SUM_KA];
+    const float sQA = C.misc[16 + SUM_QA] + C.misc[32 + SUM_QA];
+    const float sQK = C.misc[16 + SUM_QK] + C.misc[32 + SUM_QK];
+    float vv[4], o[4];
+    load4(S.v, S.qkv_dtype, (int64_t)C.b * S.v_stride + (int64_t)C.h * FV + C.j0, vv);
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const float kS = fmaf(cj[c], rg8_sum(aK[c]) + sKA, rg8_sum(pK[c]));
+      delta[c] = beta * (vv[c] - kS);
+      o[c] = fmaf(delta[c], sQK, fmaf(cj[c], rg8_sum(aQ[c]) + sQA, rg8_sum(pQ[c])));
+    }
+    const int64_t base_o = ((int64_t)C.b * P.H + C.h) * FV + C.j0;
+    if (C.rg == 0) {
+      store4(S.out, S.out_dtype, base_o, o);
+      if (MODE == MODE_READ) {
+#pragma unroll
+        for (int c = 0; c < 4; c++) S.s_delta[base_o + c] = delta[c];
+      }
+    }
+  }
+  if (MODE == MODE_READ) return;
+
+  // ---- writer: inner = x'/c = a z + k delta/c; row sums of |x'|
+  float dj[4];
+#pragma unroll
+  for (int c = 0; c < 4; c++) dj[c] = delta[c] * rcp(cj[c]);
+  float rowp[FRPT];
+#pragma unroll
+  for (int r = 0; r < FRPT; r++) {
+    if ((r % SCHED_ROWS) == SCHED_ROWS - 1) __builtin_amdgcn_sched_barrier(0);
+    const int i = C.rg + 8 * r;
+    const float4 rc = C.rc[i];
+    const float k = C.ks[i];
+    float acc = 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const float inner = fmaf(k, dj[c], fmaf(rc.z, cf[r][c], rc.w));
+      cf[r][c] = inner;
+      acc = fmaf(cj[c], fabsf(inner), acc);
+    }
+    rowp[r] = acc;
+  }
+  float p8[8], p4[4], p2[2];
+#pragma unroll
+  for (int r = 0; r < 8; r++) {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(rowp[r]), __float_as_uint(rowp[r + 8]),
+                                                     false, false);
+    p8[r] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+  }
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(p8[r]), __float_as_uint(p8[r + 4]),
+                                                     false, false);
+    p4[r] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+  }
+  const int b3 = (C.tid >> 3) & 1, b4 = (C.tid >> 4) & 1, b5 = (C.tid >> 5) & 1;
+#pragma unroll
+  for (int r = 0; r < 2; r++) {
+    const float keep = b3 ? p4[r + 2] : p4[r], send = b3 ? p4[r] : p4[r + 2];
+    p2[r] = keep + dpp<0x128>(send);
+  }
+#pragma unroll
+  for (int q = 0; q < 2; q++) C.red[C.wave * FK + C.rg + 8 * (8 * b5 + 4 * b4 + 2 * b3 + q)] = p2[q];
+  __syncthreads();
+  if (C.tid < FK) {
+    const int i = C.tid;
+    const int4 m = C.rm[i];
+    if (m.w > 0) {
+      const float sum = ((C.red[i] + C.red[FK + i]) + C.red[2 * FK + i]) + C.red[3 * FK + i];
+      float mean = sum / (float)FV;
+      mean = mean < 1e-20f ? 1e-20f : mean;
+      const float wi = C.wv[i];
+      uint32_t hb;
+      const float rn = hw_fp16_scale(__builtin_sqrtf(mean / wi), &hb);
+      const float norm = (float)(1 << (8 - m.y));
+      const float rnn = rn * norm;
+      C.rl[i].z = rcp(rnn);
+      C.rl[i].w = (wi * wi) * (rnn * rnn);
+      *(uint16_t *)(C.rst + C.shift_r + (P.rows[(int64_t)C.h * FK + i] - C.row_start)) = (uint16_t)hb;
+    }
+  }
+  __syncthreads();
+  // ---- t = x'/(r' norm c); column max of |t| / L (c0 = fp16(c * max))
+  float mx[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int r = 0; r < FRPT; r++) {
+    if ((r % SCHED_ROWS) == SCHED_ROWS - 1) __builtin_amdgcn_sched_barrier(0);
+    const float4 rl = C.rl[C.rg + 8 * r];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const float t = cf[r][c] * rl.z;
+      cf[r][c] = t;
+      mx[c] = fmaxf(mx[c], fabsf(t) * rl.y);
+    }
+  }
+  float c0[4], f0[4], num[4] = {0.f, 0.f, 0.f, 0.f}, den[4] = {0.f, 0.f, 0.f, 0.f};
+  bool top = false;
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    c0[c] = hw_fp16_scale(cj[c] * rg8_max_nonneg(mx[c]), nullptr);
+    f0[c] = cj[c] * rcp(c0[c]);
+    top |= c0[c] >= 65504.0f;
+  }
+  // |y| <= L_i (1 + 2^-11) unless c0 saturated: rint needs no clamp
+#pragma unroll
+  for (int r = 0; r < FRPT; r++) {
+    if ((r % SCHED_ROWS) == SCHED_ROWS - 1) __builtin_amdgcn_sched_barrier(0);
+    const float U = C.rl[C.rg + 8 * r].w;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const float z = __builtin_rintf(cf[r][c] * f0[c]);
+      const float t = U * z;
+      num[c] = fmaf(t, cf[r][c], num[c]);
+      den[c] = fmaf(t, z, den[c]);
+    }
+  }
+  if (__any(top)) {
+    // Saturated c0 (states beyond the fp16 range): redo the sums with the
+    // clamp to [-L, L], recomputing t from the staged old codes and the row
+    // constants with the same operations (the register tile stays as is).
+#pragma unroll
+    for (int c = 0; c < 4; c++) num[c] = den[c] = 0.f;
+#pragma unroll 1
+    for (int r = 0; r < FRPT; r++) {
+      const int i = C.rg + 8 * r;
+      const int4 m = C.rm[i];
+      const float4 rc = C.rc[i];
+      const float4 rl = C.rl[i];
+      const float k = C.ks[i];
+      const uint32_t word = word_at(C.code, m.x + base) ^ (uint32_t)m.z;
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        const float s = (float)sbfe(word, c * (uint32_t)m.y, (uint32_t)m.y);
+        const float t = fmaf(k, dj[c], fmaf(rc.z, s, rc.w)) * rl.z;
+        const float z = __builtin_amdgcn_fmed3f(__builtin_rintf(t * f0[c]), -rl.x, rl.x);
+        const float u = rl.w * z;
+        num[c] = fmaf(u, t, num[c]);
+        den[c] = fmaf(u, z, den[c]);
+      }
+    }
+  }
+  float f[4];
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    const float n = cj[c] * rg8_sum(num[c]), d = rg8_sum(den[c]);
+    const float dc = d < 1e-30f ? 1e-30f : d;
+    uint32_t hb;
+    const float cc = hw_fp16_scale(d > 0.0f ? n * rcp(dc) : c0[c], &hb);
+    f[c] = cj[c] * rcp(cc);
+    if (C.rg == 0 && has_cols) *(uint16_t *)(C.cst + C.shift_col + 2 * (C.j0 + c)) = (uint16_t)hb;
+  }
+  // ---- final codes: level = rint(y) + L saturated to [0, 2L], packed with the row's width
+#pragma unroll
+  for (int r = 0; r < FRPT; r++) {
+    if ((r % SCHED_ROWS) == SCHED_ROWS - 1) __builtin_amdgcn_sched_barrier(0);
+    const int i = C.rg + 8 * r;
+    const float4 rl = C.rl[i];
+    const int4 m = C.rm[i];
+    const uint32_t w = (uint32_t)m.y;
+    uint32_t word = 0;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      // floor(y + L + 1/2) on [0, 2L]: the level of rint(y) + L
+      const float v = __builtin_amdgcn_fmed3f(fmaf(cf[r][c], f[c], rl.x + 0.5f), 0.0f, 2.0f * rl.x + 0.5f);
+      word |= (uint32_t)v << (c * w);
+    }
+    uint8_t *dst = C.code + m.x + base;
+    if (m.w > 0) dst[0] = (uint8_t)word;
+    if (m.w > 1) dst[1] = (uint8_t)(word >> 8);
+    if (m.w > 2) dst[2] = (uint8_t)(word >> 16);
+    if (m.w > 3) dst[3] = (uint8_t)(word >> 24);
+  }
+  // ---- pivot rows: x' = x retention + k delta, stored as FP16
+  {
+    uint32_t pm[4] = {pm0[0], pm0[1], pm0[2], pm0[3]};
+    for (int p = next_pivot(pm); p >= 0; p = next_pivot(pm)) {
+      if ((p & 7) == C.rg) {
+        float x[4];
+        pivot_load(C, p, C.gv[p], x);
+        const float k = C.ks[p];
+        uint16_t *dst = (uint16_t *)(C.code + C.rm[p].x + base);
+#pragma unroll
+        for (int c = 0; c < 4; c++) dst[c] = (uint16_t)f2h(fmaf(k, delta[c], x[c]));
+      }
+    }
+  }
+  __syncthreads();
+  stage_out(C.page + C.code_start, C.code_bytes, C.code, C.tid, FNT);
+  if (C.row_bytes > 0) stage_out(C.page + C.row_start, C.row_bytes, C.rst, C.tid, FNT);
+  if (has_cols) stage_out(C.page + C.colbase, 2 * FV, C.cst, C.tid, FNT);
+}
+
+}  // namespace kfast
+
+template <int MODE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GDN128_WAVES))) void kda128_kernel(PoolDev P,
+                                                                                                      StepDev S) {
+  using namespace kfast;
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int H = P.H;
+  KCtx C;
+  C.b = blockIdx.x / H;
+  C.h = blockIdx.x % H;
+  C.tid = threadIdx.x;
+  C.rg = C.tid & 7;
+  C.cg = C.tid >> 3;
+  C.wave = C.tid >> 6;
+  C.j0 = 4 * C.cg;
+  int64_t slot;
+  if (MODE == MODE_WRITE) {
+    slot = S.s_slots[C.b];
+  } else {
+    slot = load_slot(S.slots, S.slots_dtype, C.b);
+    if (MODE == MODE_READ && C.h == 0 && C.tid == 0) S.s_slots[C.b] = slot;
+  }
+  if (slot <= 0 || slot >= P.num_slots) {
+    if (MODE == MODE_FUSED || MODE == MODE_READ)
+      for (int j = C.tid; j < FV; j += FNT) store_val(S.out, S.out_dtype, ((int64_t)C.b * H + C.h) * FV + j, 0.0f);
+    return;
+  }
+  C.page = P.data + slot * P.page_bytes;
+  const int32_t *hm = P.head_meta + 4 * C.h;
+  C.code_start = hm[0];
+  C.code_bytes = hm[1];
+  C.row_start = hm[2];
+  C.row_bytes = hm[3];
+  C.colbase = P.columns[C.h];
+  C.stride = P.offsets[(int64_t)H * FK + C.h];
+  C.code = smem;
+  C.rst = smem + P.stage;
+  C.cst = C.rst + P.rstage;
+  C.qraw = (float *)(C.cst + KDA_COL_STAGE);
+  C.kraw = C.qraw + FK;
+  C.wv = C.kraw + FK;
+  C.gv = C.wv + FK;
+  C.misc = C.gv + FK;
+  C.red = C.misc + MISC_FLOATS;
+  C.ks = C.red + 4 * FK;
+  C.qs = C.ks + FK;
+  C.rc = (float4 *)(C.qs + FK);
+  C.rl = C.rc + FK;
+  C.rm = (int4 *)(C.rl + FK);
+  C.pmask = (uint32_t *)(C.rm + FK);
+
+  // stage the head's code, row-scale and column-scale regions
+  C.shift_c = stage_in(C.page + C.code_start, C.code_bytes, C.code, C.tid, FNT);
+  C.shift_r = C.row_bytes > 0 ? stage_in(C.page + C.row_start, C.row_bytes, C.rst, C.tid, FNT) : 0;
+  C.shift_col = C.colbase >= 0 ? stage_in(C.page + C.colbase, 2 * FV, C.cst, C.tid, FNT) : 0;
+  // inputs: raw q, k rows and norms; per-row retention; beta
+  const int64_t bh = (int64_t)C.b * H + C.h;
+  if (MODE == MODE_WRITE) {
+    if (C.tid < FK) C.kraw[C.tid] = S.s_key[bh * FK + C.tid];
+    else C.gv[C.tid - FK] = S.s_decay[bh * FK + C.tid - FK];
+  } else {
+    if (C.tid < FK) {
+      const int hk = C.h / (H / S.HK);
+      const float qv = load_val(S.q, S.qkv_dtype, (int64_t)C.b * S.q_stride + (int64_t)hk * FK + C.tid);
+      const float kv = load_val(S.k, S.qkv_dtype, (int64_t)C.b * S.k_stride + (int64_t)hk * FK + C.tid);
+      C.qraw[C.tid] = qv;
+      C.kraw[C.tid] = kv;
+      const float sq = wave_sum(qv * qv), sk = wave_sum(kv * kv);
+      if ((C.tid & 63) == 0) {
+        C.misc[8 + 2 * (C.tid >> 6)] = sq;
+        C.misc[9 + 2 * (C.tid >> 6)] = sk;
+      }
+    } else {
+      const int i = C.tid - FK;
+      float gv = load_val(S.g, S.gate_dtype, bh * FK + i);
+      if (S.a_log) {
+        const float u = gv + load_val(S.dt_bias, S.gate_dtype, (int64_t)C.h * FK + i);
+        const float sp = u > 20.0f ? u : __logf(1.0f + __expf(u < 20.0f ? u : 20.0f));
+        gv = -__expf(load_val(S.a_log, S.gate_dtype, C.h)) * sp;
+      }
+      C.gv[i] = __expf(gv);
+      if (i == 0) {
+        float bt = load_val(S.beta, S.gate_dtype, bh);
+        if (S.a_log) bt = 1.0f / (1.0f + __expf(-bt));
+        C.misc[0] = bt;
+      }
+    }
+  }
+  if (C.tid >= FK) C.wv[C.tid - FK] = P.impact[(int64_t)C.h * FK + C.tid - FK];
+  __syncthreads();
+  if (MODE == MODE_READ && C.tid < FK) {
+    float nk = 1.0f;
+    if (S.normalize) nk = 1.0f / __builtin_sqrtf((C.misc[9] + C.misc[11]) + 1e-6f);
+    S.s_key[bh * FK + C.tid] = C.kraw[C.tid] * nk;
+    S.s_decay[bh * FK + C.tid] = C.gv[C.tid];
+  }
+  row_setup<MODE>(P, S, C);
+  __syncthreads();
+  body<MODE>(P, S, C);
+}
+
 __global__ void clear_kernel(uint8_t *data, int64_t page_bytes, int64_t num_slots, const void *slots,
                              int dtype) {
   int64_t s = load_slot(slots, dtype, blockIdx.y);
@@ -1539,7 +2020,7 @@ PoolDev to_dev(const sq_pool *p) {
   d.kda = p->kda;
   d.stage = (p->max_code_bytes + 47) & ~15;
   d.rstage = (p->max_row_bytes + 15) & ~15;
-  d.fast = p->flags & SQ_POOL_FAST_GDN128;
+  d.fast = p->flags & (SQ_POOL_FAST_GDN128 | SQ_POOL_FAST_KDA128);
   return d;
 }
 
@@ -1548,13 +2029,22 @@ int stage_bytes(const sq_pool *p) { return (p->max_code_bytes + 47) & ~15; }
 template <int MODE>
 int launch_step_mode(const sq_pool *pool, StepDev sd, int64_t batch, hipStream_t st) {
   PoolDev pd = to_dev(pool);
-  if (MODE != MODE_DECODE && pd.fast) {
+  if (MODE != MODE_DECODE && (pd.fast & SQ_POOL_FAST_GDN128)) {
     const int ng_max = pool->group >= 32 ? 128 / pool->group : 1;
     // staging | rows | columns | q,k raw + w | misc | red | ks, qs | rc (float4), iu (float2) per (row, group)
     size_t lds = (size_t)pd.stage + pd.rstage + 2 * 128 + 3 * 128 * 4 + 48 * 4 + 4 * 128 * 4 + 2 * 128 * 4 +
                  (size_t)6 * 128 * ng_max * 4;
     hipLaunchKernelGGL((gdn128_kernel<MODE>), dim3((unsigned)(batch * pool->heads)), dim3(256), lds, st, pd, sd);
     return check_launch("gdn128_kernel");
+  }
+  if (MODE != MODE_DECODE && (pd.fast & SQ_POOL_FAST_KDA128)) {
+    // row-scale regions may start at any even byte: room for the alignment shift
+    pd.rstage = (pool->max_row_bytes + 47) & ~15;
+    // staging | rows | columns | q,k raw, w, retention | misc | red | ks, qs | rc, rl, rm | pivot mask
+    size_t lds = (size_t)pd.stage + pd.rstage + fast::KDA_COL_STAGE + 4 * 128 * 4 + fast::MISC_FLOATS * 4 +
+                 4 * 128 * 4 + 2 * 128 * 4 + 3 * 128 * 16 + 16;
+    hipLaunchKernelGGL((kda128_kernel<MODE>), dim3((unsigned)(batch * pool->heads)), dim3(256), lds, st, pd, sd);
+    return check_launch("kda128_kernel");
   }
   const int K = pool->keys, V = pool->values;
   const int RG = K >= 8 ? 8 : 4;
@@ -1711,6 +2201,7 @@ int sq_pool_flags(const int32_t *bits, const int32_t *head_meta, const int32_t *
     if (w == 2) fast = fast && (group == 32 || group == 64 || group == 128);
   }
   if (fast) flags |= SQ_POOL_FAST_GDN128;
+  if (kda && keys == 128 && values == 128 && storage == 0) flags |= SQ_POOL_FAST_KDA128;
   return flags;
 }
 

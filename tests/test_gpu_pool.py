@@ -163,6 +163,72 @@ def test_decode_step_against_oracle(name, asynchronous):
         _check_requant(got, slots_np, oplan, lay, V, upd)
 
 
+@pytest.mark.parametrize("asynchronous", [False, True])
+def test_decode_step_with_saturated_column_scales(asynchronous):
+    """States beyond the fp16 scale range: c0 clamps at 65504 and the initial
+    codes must be clamped to [-L, L] (the K=V=128 kernel's exact fallback)."""
+    H, K, V, B = 3, 128, 128, 4
+    bits = np.repeat(np.array([6, 4, 8])[:, None], K, 1)
+    impact = np.ones((H, K), np.float32)
+    impact[:, [5, 77]] = 1e6
+    oplan = O.Plan("gdn", bits, impact, 32)
+    stream = torch.cuda.Stream() if asynchronous else None
+    pool = _pool(oplan, B + 1, V, writeback_stream=stream)
+    slots_np = np.array([2, 4, 1, 3])
+    slots = torch.from_numpy(slots_np).to(dev())
+    g = torch.Generator().manual_seed(9)
+    x0 = torch.randn(B, H, K, V, generator=g) * .1
+    x0[:, :, 5, :8] = 1e8
+    x0[:, :, 77, 40:44] = -3e8
+    pool.encode(x0.to(dev()), slots)
+    lay = O.layout(oplan, V)
+    for it in range(2):
+        state = O.decode_page(pool.data.cpu().numpy(), slots_np, oplan, lay, V)
+        q, k, v, ld, beta = _inputs(B, H, K, V, False, 200 + it)
+        out_ref, upd = O.delta_step(state, q.numpy(), k.numpy(), v.numpy(), ld.numpy(), beta.numpy())
+        ref_pages = np.zeros_like(pool.data.cpu().numpy())
+        O.encode_page(upd, slots_np, oplan, lay, ref_pages)
+        cols = np.stack([ref_pages[slots_np, lay.columns[h]:lay.columns[h] + 2 * V].view(np.uint16)
+                         for h in range(H)], 1)
+        assert (cols == 0x7BFF).any(axis=(0, 2)).all(), "every head needs a saturated column scale"
+        out = pool.step(q.to(dev()), k.to(dev()), v.to(dev()), ld.to(dev()), beta.to(dev()), slots)
+        pool.wait()
+        torch.cuda.synchronize()
+        o = out.cpu().numpy()
+        scale = np.abs(out_ref).max(axis=-1, keepdims=True)
+        assert (np.abs(o - out_ref) <= 1e-3 * np.abs(out_ref) + 1e-6 * scale).all()
+        _check_requant(pool.data.cpu().numpy(), slots_np, oplan, lay, V, upd)
+
+
+@pytest.mark.parametrize("arch", ["gdn", "kda"])
+def test_decode_step_lognormal_row_and_column_scales(arch):
+    """States S0 = diag(r) N(0,1) diag(c) with r, c ~ LogNormal(0, 0.5): rows
+    and columns of very different magnitude (the GDN@4 serving config)."""
+    H, K, V, B = 4, 128, 128, 6
+    if arch == "gdn":
+        bits = np.repeat(np.array([2, 4, 6, 8])[:, None], K, 1)
+    else:
+        rng = np.random.default_rng(4)
+        bits = np.where(rng.random((H, K)) < .02, 16, rng.choice([2, 4, 6, 8], (H, K)))
+    oplan = make_plan(arch, bits, seed=5)
+    pool = _pool(oplan, B + 1, V)
+    slots_np = np.arange(1, B + 1)
+    slots = torch.from_numpy(slots_np).to(dev())
+    g = torch.Generator().manual_seed(13)
+    r = torch.exp(torch.randn(B, H, K, 1, generator=g) * .5)
+    c = torch.exp(torch.randn(B, H, 1, V, generator=g) * .5)
+    pool.encode((r * torch.randn(B, H, K, V, generator=g) * c).to(dev()), slots)
+    lay = O.layout(oplan, V)
+    for it in range(3):
+        state = O.decode_page(pool.data.cpu().numpy(), slots_np, oplan, lay, V)
+        q, k, v, ld, beta = _inputs(B, H, K, V, arch == "kda", 300 + it)
+        out_ref, upd = O.delta_step(state, q.numpy(), k.numpy(), v.numpy(), ld.numpy(), beta.numpy())
+        out = pool.step(q.to(dev()), k.to(dev()), v.to(dev()), ld.to(dev()), beta.to(dev()), slots)
+        torch.cuda.synchronize()
+        np.testing.assert_allclose(out.cpu().numpy(), out_ref, rtol=1e-3, atol=1e-4)
+        _check_requant(pool.data.cpu().numpy(), slots_np, oplan, lay, V, upd)
+
+
 def test_async_and_fused_paths_agree_bitwise():
     oplan = make_plan("gdn", np.repeat(np.array([6, 4, 8, 16, 2, 6])[:, None], 128, 1), seed=1)
     B, H, K, V = 8, 6, 128, 128
