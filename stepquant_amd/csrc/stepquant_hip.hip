@@ -150,35 +150,33 @@ __device__ __forceinline__ void put_page_half(uint8_t *page, int64_t byte, uint3
 // byte a.  Returns the offset of gstart inside the staged window.
 __device__ __forceinline__ int stage_in(const uint8_t *gstart, int64_t nbytes, uint8_t *lds, int tid,
                                         int nthreads) {
-  uintptr_t s = (uintptr_t)gstart;
-  uintptr_t w16 = s & ~(uintptr_t)15;
-  uintptr_t e16 = ((uintptr_t)gstart + nbytes + 15) & ~(uintptr_t)15;
-  int n16 = (int)((e16 - w16) >> 4);
-  const uint4 *src = (const uint4 *)w16;
+  // pointer arithmetic (not integer casts) keeps the global address space
+  const int shift = (int)((uintptr_t)gstart & 15);
+  const uint4 *src = (const uint4 *)(gstart - shift);
+  const int n16 = (int)((shift + nbytes + 15) >> 4);
   uint4 *dst = (uint4 *)lds;
   for (int c = tid; c < n16; c += nthreads) dst[c] = src[c];
-  return (int)(s - w16);
+  return shift;
 }
 
-// Write LDS back to [gstart, gend): whole 16-byte chunks inside the region
-// use 16-byte stores, edge chunks store only the region's 2-byte units.
-// `lds` is the staged window as returned by stage_in (global byte a lives at
-// lds + (a - floor16(gstart))).
+// Write LDS back to [gstart, gstart + nbytes): whole 16-byte chunks inside
+// the region use 16-byte stores, edge chunks store only the region's 2-byte
+// units.  `lds` is the staged window as returned by stage_in (global byte a
+// lives at lds + (a - floor16(gstart))).
 __device__ __forceinline__ void stage_out(uint8_t *gstart, int64_t nbytes, const uint8_t *lds, int tid,
                                           int nthreads) {
-  uintptr_t s = (uintptr_t)gstart;
-  uintptr_t e = s + (uintptr_t)nbytes;
-  uintptr_t w16 = s & ~(uintptr_t)15;
-  uintptr_t e16 = (e + 15) & ~(uintptr_t)15;
-  int n16 = (int)((e16 - w16) >> 4);
+  const int shift = (int)((uintptr_t)gstart & 15);
+  uint8_t *w16 = gstart - shift;
+  const int64_t end = shift + nbytes;  // region end relative to w16
+  const int n16 = (int)((end + 15) >> 4);
   for (int c = tid; c < n16; c += nthreads) {
-    uintptr_t a = w16 + ((uintptr_t)c << 4);
-    if (a >= s && a + 16 <= e) {
-      *(uint4 *)a = ((const uint4 *)lds)[c];
+    const int64_t a = 16 * (int64_t)c;
+    if (a >= shift && a + 16 <= end) {
+      *(uint4 *)(w16 + a) = ((const uint4 *)lds)[c];
     } else {
       for (int u = 0; u < 8; u++) {
-        uintptr_t b = a + 2 * u;
-        if (b >= s && b + 2 <= e) *(uint16_t *)b = *(const uint16_t *)(lds + (b - w16));
+        const int64_t b = a + 2 * u;
+        if (b >= shift && b + 2 <= end) *(uint16_t *)(w16 + b) = *(const uint16_t *)(lds + b);
       }
     }
   }
@@ -1492,15 +1490,60 @@ using namespace fast;
 
 struct KCtx {
   uint8_t *page, *code, *rst, *cst;
-  int shift_c, shift_r, shift_col;
+  int lbase, shift_r, shift_col;  // lbase: this lane's block in the staged code
   float *qraw, *kraw, *wv, *gv, *misc, *red, *ks, *qs;
   float4 *rc;   // per row: k*a, q*a, a, a  (zeros for pivot rows)
   float4 *rl;   // per row: L, 1/L, 1/(r' norm), w^2 r'^2 norm^2 (zeros for pivots)
-  int4 *rm;     // per row: byte position in block 0 (staged), width (0: pivot), top-bit mask, tile bytes
+  int4 *rm;     // per row: byte position within a block, width (0: pivot), top-bit mask, tile bytes
   uint32_t *pmask;  // 128-bit mask of pivot rows
+  uint8_t *spare;   // 4 bytes per lane: target of masked-off byte stores
   int b, h, tid, rg, cg, wave, j0;
   int code_start, code_bytes, row_start, row_bytes, colbase, stride;
 };
+
+// The code region is staged block by block (32 blocks of `stride` bytes, one
+// per 4 columns), each block in its own 16-byte aligned LDS window of
+// `pitch` bytes, pitch = 32 (mod 64): the eight blocks a wave reads at once
+// start in different LDS banks.
+__host__ __device__ __forceinline__ int block_chunks(int stride) { return (stride + 15 + 8 + 15) / 16; }
+__host__ __device__ __forceinline__ int block_pitch(int stride) {
+  return 64 * ((16 * block_chunks(stride) - 32 + 63) / 64) + 32;
+}
+
+__device__ __forceinline__ void stage_in_blocks(const uint8_t *g0, int stride, int pitch, uint8_t *lds, int tid) {
+  const int nc = block_chunks(stride);
+  const int gmod = (int)((uintptr_t)g0 & 15);
+  for (int f = tid; f < 32 * nc; f += FNT) {
+    const int blk = f & 31, ch = f >> 5;
+    const int off = blk * stride;
+    const uint4 *src = (const uint4 *)(g0 + (off - ((gmod + off) & 15)));
+    ((uint4 *)(lds + blk * pitch))[ch] = src[ch];
+  }
+}
+
+// Write the staged blocks back: per block, 16-byte chunks inside the block
+// with one store, the chunks at its two edges in 2-byte units (block bounds
+// are even; neighbouring blocks write the other units of shared chunks).
+__device__ __forceinline__ void stage_out_blocks(uint8_t *g0, int stride, int pitch, const uint8_t *lds, int tid) {
+  const int nc = block_chunks(stride);
+  const int gmod = (int)((uintptr_t)g0 & 15);
+  for (int f = tid; f < 32 * nc; f += FNT) {
+    const int blk = f & 31, ch = f >> 5;
+    const int off = blk * stride;
+    const int sb = (gmod + off) & 15;
+    uint8_t *w = g0 + (off - sb);
+    const int a = 16 * ch;
+    const uint8_t *l = lds + blk * pitch + a;
+    if (a >= sb && a + 16 <= sb + stride) {
+      *(uint4 *)(w + a) = *(const uint4 *)l;
+    } else if (a < sb + stride && a + 16 > sb) {
+      for (int u = 0; u < 8; u++) {
+        const int bb = a + 2 * u;
+        if (bb >= sb && bb + 2 <= sb + stride) *(uint16_t *)(w + bb) = *(const uint16_t *)(l + 2 * u);
+      }
+    }
+  }
+}
 
 // sign-extended field of run-time width w at bit offset o
 __device__ __forceinline__ int sbfe(uint32_t word, uint32_t o, uint32_t w) {
@@ -1532,7 +1575,7 @@ __device__ __forceinline__ void row_setup(const PoolDev &P, const StepDev &S, co
     C.ks[i] = k;
     C.qs[i] = q;
     const float retention = C.gv[i];
-    const int pos = C.shift_c + (P.offsets[hi] - C.code_start);
+    const int pos = P.offsets[hi] - C.code_start;  // within a block
     float ka = 0.f, qa = 0.f;
     if (piv) {
       C.rc[i] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -1571,7 +1614,7 @@ __device__ __forceinline__ void row_setup(const PoolDev &P, const StepDev &S, co
 
 // four FP16 values of pivot row p in this lane's block, times `scale`
 __device__ __forceinline__ void pivot_load(const KCtx &C, int p, float scale, float x[4]) {
-  const int pos = C.rm[p].x + C.cg * C.stride;
+  const int pos = C.rm[p].x + C.lbase;
   const uint32_t lo = word_at(C.code, pos), hi = word_at(C.code, pos + 4);
   x[0] = hw_h2f(lo & 0xffffu) * scale;
   x[1] = hw_h2f(lo >> 16) * scale;
@@ -1579,16 +1622,18 @@ __device__ __forceinline__ void pivot_load(const KCtx &C, int p, float scale, fl
   x[3] = hw_h2f(hi >> 16) * scale;
 }
 
-// Next pivot row of the head after clearing it from the (wave-uniform) mask;
-// -1 when none is left.
-__device__ __forceinline__ int next_pivot(uint32_t m[4]) {
-#pragma unroll
-  for (int d = 0; d < 4; d++) {
-    if (m[d]) {
-      const int bit = __builtin_ctz(m[d]);
-      m[d] &= m[d] - 1u;
-      return 32 * d + bit;
-    }
+// Next pivot row of the head from the (wave-uniform) 128-bit mask, cleared
+// from the mask; -1 when none is left.
+__device__ __forceinline__ int next_pivot(uint64_t &lo, uint64_t &hi) {
+  if (lo) {
+    const int p = __builtin_ctzll(lo);
+    lo &= lo - 1u;
+    return p;
+  }
+  if (hi) {
+    const int p = 64 + __builtin_ctzll(hi);
+    hi &= hi - 1u;
+    return p;
   }
   return -1;
 }
@@ -1602,10 +1647,11 @@ __device__ __forceinline__ void body(const PoolDev &P, const StepDev &S, KCtx &C
 #pragma unroll
   for (int c = 0; c < 4; c++)
     cj[c] = has_cols ? hw_h2f(*(const uint16_t *)(C.cst + C.shift_col + 2 * (C.j0 + c))) : 1.0f;
-  uint32_t pm0[4];
-#pragma unroll
-  for (int d = 0; d < 4; d++) pm0[d] = __builtin_amdgcn_readfirstlane(C.pmask[d]);
-  const int base = C.cg * C.stride;
+  const uint64_t pm_lo = ((uint64_t)__builtin_amdgcn_readfirstlane(C.pmask[1]) << 32) |
+                        (uint32_t)__builtin_amdgcn_readfirstlane(C.pmask[0]);
+  const uint64_t pm_hi = ((uint64_t)__builtin_amdgcn_readfirstlane(C.pmask[3]) << 32) |
+                        (uint32_t)__builtin_amdgcn_readfirstlane(C.pmask[2]);
+  const int base = C.lbase;
 
   // ---- foreground: signed code fields s = code - 2^(b-1) (z = s + 1)
   float cf[FRPT][4];
@@ -1636,8 +1682,8 @@ __device__ __forceinline__ void body(const PoolDev &P, const StepDev &S, KCtx &C
   } else {
     // pivot rows owned by this lane (row % 8 == rg)
     float pK[4] = {0.f, 0.f, 0.f, 0.f}, pQ[4] = {0.f, 0.f, 0.f, 0.f};
-    uint32_t pm[4] = {pm0[0], pm0[1], pm0[2], pm0[3]};
-    for (int p = next_pivot(pm); p >= 0; p = next_pivot(pm)) {
+    uint64_t lo = pm_lo, hi = pm_hi;
+    for (int p = next_pivot(lo, hi); p >= 0; p = next_pivot(lo, hi)) {
       if ((p & 7) == C.rg) {
         float x[4];
         pivot_load(C, p, C.gv[p], x);
@@ -1807,24 +1853,26 @@ __device__ __forceinline__ void body(const PoolDev &P, const StepDev &S, KCtx &C
     const int i = C.rg + 8 * r;
     const float4 rl = C.rl[i];
     const int4 m = C.rm[i];
-    const uint32_t w = (uint32_t)m.y;
-    uint32_t word = 0;
+    uint32_t code[4];
 #pragma unroll
     for (int c = 0; c < 4; c++) {
       // floor(y + L + 1/2) on [0, 2L]: the level of rint(y) + L
-      const float v = __builtin_amdgcn_fmed3f(fmaf(cf[r][c], f[c], rl.x + 0.5f), 0.0f, 2.0f * rl.x + 0.5f);
-      word |= (uint32_t)v << (c * w);
+      code[c] = (uint32_t)__builtin_amdgcn_fmed3f(fmaf(cf[r][c], f[c], rl.x + 0.5f), 0.0f, 2.0f * rl.x + 0.5f);
     }
-    uint8_t *dst = C.code + m.x + base;
-    if (m.w > 0) dst[0] = (uint8_t)word;
-    if (m.w > 1) dst[1] = (uint8_t)(word >> 8);
-    if (m.w > 2) dst[2] = (uint8_t)(word >> 16);
-    if (m.w > 3) dst[3] = (uint8_t)(word >> 24);
+    const uint32_t w = (uint32_t)m.y;
+    const uint32_t word = code[0] | (code[1] << w) | (code[2] << (2 * w)) | (code[3] << (3 * w));
+    // the tile's m.w bytes; the other byte stores go to this lane's spare
+    // dword (no branches on the per-lane width)
+    uint8_t *dst = C.code + m.x + base, *spare = C.spare + 4 * C.tid;
+    (m.w > 0 ? dst : spare)[0] = (uint8_t)word;
+    (m.w > 1 ? dst : spare)[1] = (uint8_t)(word >> 8);
+    (m.w > 2 ? dst : spare)[2] = (uint8_t)(word >> 16);
+    (m.w > 3 ? dst : spare)[3] = (uint8_t)(word >> 24);
   }
   // ---- pivot rows: x' = x retention + k delta, stored as FP16
   {
-    uint32_t pm[4] = {pm0[0], pm0[1], pm0[2], pm0[3]};
-    for (int p = next_pivot(pm); p >= 0; p = next_pivot(pm)) {
+    uint64_t lo = pm_lo, hi = pm_hi;
+    for (int p = next_pivot(lo, hi); p >= 0; p = next_pivot(lo, hi)) {
       if ((p & 7) == C.rg) {
         float x[4];
         pivot_load(C, p, C.gv[p], x);
@@ -1836,7 +1884,7 @@ __device__ __forceinline__ void body(const PoolDev &P, const StepDev &S, KCtx &C
     }
   }
   __syncthreads();
-  stage_out(C.page + C.code_start, C.code_bytes, C.code, C.tid, FNT);
+  stage_out_blocks(C.page + C.code_start, C.stride, block_pitch(C.stride), C.code, C.tid);
   if (C.row_bytes > 0) stage_out(C.page + C.row_start, C.row_bytes, C.rst, C.tid, FNT);
   if (has_cols) stage_out(C.page + C.colbase, 2 * FV, C.cst, C.tid, FNT);
 }
@@ -1892,9 +1940,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GDN128_WAVE
   C.rl = C.rc + FK;
   C.rm = (int4 *)(C.rl + FK);
   C.pmask = (uint32_t *)(C.rm + FK);
+  C.spare = (uint8_t *)(C.pmask + 4);
 
   // stage the head's code, row-scale and column-scale regions
-  C.shift_c = stage_in(C.page + C.code_start, C.code_bytes, C.code, C.tid, FNT);
+  const int pitch = block_pitch(C.stride);
+  stage_in_blocks(C.page + C.code_start, C.stride, pitch, C.code, C.tid);
+  C.lbase = C.cg * pitch + (int)((uintptr_t)(C.page + C.code_start + (int64_t)C.cg * C.stride) & 15);
   C.shift_r = C.row_bytes > 0 ? stage_in(C.page + C.row_start, C.row_bytes, C.rst, C.tid, FNT) : 0;
   C.shift_col = C.colbase >= 0 ? stage_in(C.page + C.colbase, 2 * FV, C.cst, C.tid, FNT) : 0;
   // inputs: raw q, k rows and norms; per-row retention; beta
@@ -2040,9 +2091,11 @@ int launch_step_mode(const sq_pool *pool, StepDev sd, int64_t batch, hipStream_t
   if (MODE != MODE_DECODE && (pd.fast & SQ_POOL_FAST_KDA128)) {
     // row-scale regions may start at any even byte: room for the alignment shift
     pd.rstage = (pool->max_row_bytes + 47) & ~15;
-    // staging | rows | columns | q,k raw, w, retention | misc | red | ks, qs | rc, rl, rm | pivot mask
+    // code blocks in padded windows (the largest head's stride)
+    pd.stage = 32 * kfast::block_pitch(pool->max_code_bytes / 32);
+    // staging | rows | columns | q,k raw, w, retention | misc | red | ks, qs | rc, rl, rm | pivot mask | spare
     size_t lds = (size_t)pd.stage + pd.rstage + fast::KDA_COL_STAGE + 4 * 128 * 4 + fast::MISC_FLOATS * 4 +
-                 4 * 128 * 4 + 2 * 128 * 4 + 3 * 128 * 16 + 16;
+                 4 * 128 * 4 + 2 * 128 * 4 + 3 * 128 * 16 + 16 + 4 * 256;
     hipLaunchKernelGGL((kda128_kernel<MODE>), dim3((unsigned)(batch * pool->heads)), dim3(256), lds, st, pd, sd);
     return check_launch("kda128_kernel");
   }
