@@ -175,9 +175,13 @@ def main():
     alg_bytes = 2 * B * page
     achieved = alg_bytes / (ms_step * 1e-3) / 1e9
     updates = B * H / (ms_step * 1e-3)
+    # measured HBM bytes per launch apply only to the workload they were taken on
+    key = f"{a.arch}-{a.nominal}-b{B}-h{H}-hk{HK}-{'async' if stream is not None else 'fused'}"
     traffic = None
     if a.traffic and os.path.exists(a.traffic):
-        traffic = json.load(open(a.traffic)).get("bytes_per_launch")
+        meas = json.load(open(a.traffic))
+        if meas.get("workload_key") == key:
+            traffic = meas.get("bytes_per_launch")
     roof = dict(bound="hbm", achieved=round(achieved, 1), peak=PEAK_GBS, unit="GB/s",
                 frac=round(achieved / PEAK_GBS, 4), traffic=traffic,
                 kernel="step_kernel (fused read+update+readout+requant+store)" if stream is None
