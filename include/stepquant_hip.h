@@ -176,6 +176,56 @@ int sq_writeback(const sq_pool *pool, const sq_writeback_scratch *scratch, int64
                  void *stream);
 
 /*
+ * Chunked prefill of whole sequences (replaces the decode -> upstream chunk
+ * kernel -> encode round trip of kernel_extend, sglang/runtime.py:193-202).
+ *   q, k      [T, HK*K] bf16 rows (row strides in elements, multiples of 8,
+ *             rows 16-byte aligned); v [T, H*V] bf16; T = cu_seqlens[batch].
+ *   g, beta   [T, H] log decay and write strength (raw gate a and logits b
+ *             when a_log/dt_bias are given, as sq_step_args).
+ *   out       [T, H, V], dtype out_dtype.
+ *   cu_seqlens [batch + 1] int32 token offsets of the sequences.
+ *   init_slots [batch] pages holding the initial states (slot <= 0: zero
+ *             state; NULL: all zero).
+ *   checkpoints [batch * n_checkpoints] int32 token counts, ascending per
+ *             sequence, after which the state is requantised into
+ *             slots[b * n_checkpoints + c] (positions <= 0 or beyond the
+ *             sequence are unused and their slots must be <= 0).
+ *   init_state      workspace [batch, H, K, V] f32;
+ *   checkpoint_state workspace [batch * n_checkpoints, H, K, V] f32.
+ * GDN pools with K = V = 128 and packed storage; chunks of 64 tokens.
+ */
+typedef struct sq_prefill_args {
+    const void *q;
+    const void *k;
+    const void *v;
+    const void *g;
+    const void *beta;
+    const void *a_log;
+    const void *dt_bias;
+    void *out;
+    const int32_t *cu_seqlens;
+    const int32_t *checkpoints;
+    const void *init_slots;
+    const void *slots;
+    float *init_state;
+    float *checkpoint_state;
+    int64_t batch;
+    int64_t q_stride;
+    int64_t k_stride;
+    int64_t v_stride;
+    int32_t key_heads;
+    int32_t n_checkpoints;
+    int32_t qkv_dtype;
+    int32_t gate_dtype;
+    int32_t out_dtype;
+    int32_t slots_dtype;
+    int32_t normalize;
+    float scale;
+} sq_prefill_args;
+
+int sq_prefill(const sq_pool *pool, const sq_prefill_args *args, void *stream);
+
+/*
  * Slot operations (pool.py:358-365).  sq_clear_slots zeroes whole pages.
  * sq_copy_slots copies pages src[i] -> dst[i] through `temp`
  * ([n, page_bytes] bytes) so overlapping index sets behave like the

@@ -15,6 +15,11 @@ the reference repository):
 * ``decode_page``     kernels/fused.py:18-59 (``_read``), kernels/byte_codec.py:6-28
 * ``prepare``         kernels/fused.py:155-179 (``prepare_inputs_kernel``)
 * ``delta_step``      stepquant/core.py:5-15
+* ``prefill``         the token recurrence of core.py:5-15 (``delta_step``)
+                      applied to every token of a sequence, in float64, with
+                      the input preparation of kernels/fused.py:155-179; it is
+                      the checker for the chunked prefill that replaces
+                      sglang/runtime.py:193-202 (``kernel_extend``)
 * ``pack``/``unpack`` stepquant/packing.py:6-22
 * ``codec_encode``/``codec_decode``  stepquant/quantization.py:101-152 (``StateCodec``)
 
@@ -22,7 +27,11 @@ Parity status: layout, fit_state, encode_page, decode_page, pack/unpack and
 codec_encode are pinned by golden vectors written from the reference
 (tests/golden) and by the known-answer tests of the reference's own test
 suite.  delta_step and prepare are pinned by closed-form invariants and a
-brute-force sequential check (tests/test_oracle_math.py).
+brute-force sequential check (tests/test_oracle_math.py).  prefill is pinned
+by delta_step on single tokens and by the closed-form chunked (WY) form of
+the same recurrence (tests/test_oracle_prefill.py).  The reference's own
+chunked kernel lives in sglang==0.5.12 (not vendored, not installed here), so
+its exact output is parity unpinned; the sequential recurrence is the oracle.
 """
 from __future__ import annotations
 
@@ -282,3 +291,60 @@ def codec_encode(x, plan: Plan):
     pivots = x.reshape(B, H * K, V)[:, flat_bits == 16].astype(np.float16)
     return dict(codes=streams, rows=r.reshape(B, -1)[:, integer_rows],
                 columns=c[:, integer_heads], pivots=pivots, two_bit_rows=r2, shape=x.shape)
+
+
+def _softplus20(u):
+    return np.where(u > 20.0, u, np.log1p(np.exp(np.minimum(u, 20.0))))
+
+
+def prefill(q, k, v, g, beta, state0, cu_seqlens, checkpoints=None, normalize=False, scale=1.0,
+            a_log=None, dt_bias=None):
+    """Token-sequential GDN prefill in float64.
+
+    q, k: [T, HK, K]; v: [T, H, V]; g: [T, H] log decay (raw gate a when
+    a_log is given: g = -exp(a_log) softplus(a + dt_bias)); beta: [T, H]
+    (logits when a_log is given: beta = sigmoid(b)); state0: [B, H, K, V];
+    cu_seqlens: [B + 1] token offsets; checkpoints: [B, NC] token counts
+    after which the state is recorded (<= 0 or > length: unused).
+    Per token (core.py:5-15): S <- e^g S; delta = beta (v - S^T k);
+    S <- S + k delta^T; o = S^T q, with q, k L2-normalised (eps 1e-6) and q
+    scaled as kernels/fused.py:155-179 prepares them.
+    Returns (out [T, H, V], states [B, NC, H, K, V], final [B, H, K, V]).
+    """
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    g = np.asarray(g, np.float64)
+    beta = np.asarray(beta, np.float64)
+    T, HK, K = q.shape
+    H, V = v.shape[1], v.shape[2]
+    B = len(cu_seqlens) - 1
+    if checkpoints is None:
+        checkpoints = np.zeros((B, 0), np.int64)
+    checkpoints = np.asarray(checkpoints).reshape(B, -1)
+    NC = checkpoints.shape[1]
+    if a_log is not None:
+        g = -np.exp(np.asarray(a_log, np.float64))[None, :] * _softplus20(g + np.asarray(dt_bias, np.float64)[None, :])
+        beta = 1.0 / (1.0 + np.exp(-beta))
+    head_of = np.arange(H) // (H // HK)
+    out = np.zeros((T, H, V))
+    states = np.zeros((B, NC, H, K, V))
+    final = np.zeros((B, H, K, V))
+    for b in range(B):
+        s0, s1 = int(cu_seqlens[b]), int(cu_seqlens[b + 1])
+        S = np.array(state0[b], np.float64)
+        for t in range(s0, s1):
+            qt, kt = q[t][head_of], k[t][head_of]
+            if normalize:
+                qt = qt / np.sqrt((qt * qt).sum(-1, keepdims=True) + 1e-6)
+                kt = kt / np.sqrt((kt * kt).sum(-1, keepdims=True) + 1e-6)
+            qt = qt * scale
+            S = S * np.exp(g[t])[:, None, None]
+            delta = beta[t][:, None] * (v[t] - np.einsum("hk,hkv->hv", kt, S))
+            S = S + kt[:, :, None] * delta[:, None, :]
+            out[t] = np.einsum("hk,hkv->hv", qt, S)
+            for c in range(NC):
+                if checkpoints[b, c] == t - s0 + 1:
+                    states[b, c] = S
+        final[b] = S
+    return out, states, final

@@ -44,9 +44,19 @@ class Scratch(ctypes.Structure):
                 ("capacity", ctypes.c_int64)]
 
 
+class PrefillArgs(ctypes.Structure):
+    _fields_ = [("q", _P), ("k", _P), ("v", _P), ("g", _P), ("beta", _P), ("a_log", _P), ("dt_bias", _P),
+                ("out", _P), ("cu_seqlens", _P), ("checkpoints", _P), ("init_slots", _P), ("slots", _P),
+                ("init_state", _P), ("checkpoint_state", _P), ("batch", ctypes.c_int64),
+                ("q_stride", ctypes.c_int64), ("k_stride", ctypes.c_int64), ("v_stride", ctypes.c_int64),
+                ("key_heads", ctypes.c_int32), ("n_checkpoints", ctypes.c_int32), ("qkv_dtype", ctypes.c_int32),
+                ("gate_dtype", ctypes.c_int32), ("out_dtype", ctypes.c_int32), ("slots_dtype", ctypes.c_int32),
+                ("normalize", ctypes.c_int32), ("scale", ctypes.c_float)]
+
+
 EXPORTS = ("sq_abi_version", "sq_last_error", "sq_encode", "sq_decode_dense", "sq_decode_step",
            "sq_decode_readout", "sq_writeback", "sq_clear_slots", "sq_copy_slots",
-           "sq_stream_capture_id", "sq_create_cu_stream", "sq_pool_flags")
+           "sq_stream_capture_id", "sq_create_cu_stream", "sq_pool_flags", "sq_prefill")
 
 _lib = None
 
@@ -72,6 +82,7 @@ def lib():
     L.sq_decode_step.argtypes = [PP(Pool), PP(StepArgs), _P]
     L.sq_decode_readout.argtypes = [PP(Pool), PP(StepArgs), PP(Scratch), _P]
     L.sq_writeback.argtypes = [PP(Pool), PP(Scratch), ctypes.c_int64, _P]
+    L.sq_prefill.argtypes = [PP(Pool), PP(PrefillArgs), _P]
     L.sq_clear_slots.argtypes = [PP(Pool), _P, ctypes.c_int32, ctypes.c_int64, _P]
     L.sq_copy_slots.argtypes = [PP(Pool), _P, _P, ctypes.c_int32, ctypes.c_int64, _P, _P]
     L.sq_pool_flags.argtypes = [_P, _P, _P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,

@@ -1994,6 +1994,505 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GDN128_WAVE
   body<MODE>(P, S, C);
 }
 
+// =====================================================================
+// Chunked GDN prefill, K = V = 128, chunks of 64 tokens, bf16 MFMA
+// (v_mfma_f32_16x16x32_bf16) with fp32 accumulation.
+//
+// For a chunk with start state S0 [K, V], Gamma_t = prod_{s<=t} g_s:
+//   A_ts  = beta_t (Gamma_t/Gamma_s) k_t.k_s  (s < t),  T = (I + A)^{-1}
+//   W     = T diag(beta Gamma) K,  U = T diag(beta) V,   Delta = U - W S0
+//   O     = diag(Gamma) Q S0 + (M o Q K^T) Delta,        M_ts = Gamma_t/Gamma_s (s <= t)
+//   S_C   = Gamma_C S0 + (diag(Gamma_C/Gamma) K)^T Delta
+// (q, k L2-normalised and q scaled: the norms multiply into the products).
+// One workgroup per (sequence, head, half of V): 4 waves, chunks in order.
+// Operands with a single rounding to bf16 would lose precision (T, W, P,
+// Delta, S); they are split as x = hi + lo (two bf16) and multiplied as
+// hi*hi + hi*lo + lo*hi, leaving ~2^-16 relative error per product; q, k, v
+// are bf16 inputs and enter exactly.
+// MFMA operand layout (checked on gfx950): lane l holds A[l % 16][8(l/16)..+7]
+// and B[8(l/16)..+7][l % 16]; the result lane l holds D[4(l/16)..+3][l % 16].
+// =====================================================================
+namespace pf {
+
+typedef __bf16 bf16x8 __attribute__((__vector_size__(8 * sizeof(__bf16))));
+typedef float f32x4 __attribute__((__vector_size__(4 * sizeof(float))));
+
+constexpr int PC = 64, PKD = 128, PVS = 64;
+constexpr int P136 = 136, P72 = 72, PA = 68;  // row pitches (elements) of the LDS arrays
+constexpr int OFF_KC = 0;                       // bf16 [64 t][136]   k rows (d contiguous)
+constexpr int OFF_KT = OFF_KC + PC * P136 * 2;  // bf16 [128 d][72]   k columns (t contiguous)
+constexpr int OFF_VT = OFF_KT + PKD * P72 * 2;  // bf16 [64 j][72]    v columns of this half
+constexpr int OFF_AT = OFF_VT + PVS * P72 * 2;  // f32  [64][68]      A, then T = (I + A)^{-1}
+constexpr int OFF_P = OFF_AT + PC * PA * 4;     // bf16 2 x [64 t][72] masked, scaled Q K^T (hi, lo)
+constexpr int OFF_WD = OFF_P + 2 * PC * P72 * 2;  // W hi/lo [64 t][136], later Delta, Delta' hi/lo [64 j][72]
+constexpr int WD_BYTES = 4 * PVS * P72 * 2;
+constexpr int OFF_ST = OFF_WD + WD_BYTES;         // bf16 2 x [64 j][136] S transposed (hi, lo)
+constexpr int OFF_SM = OFF_ST + 2 * PVS * P136 * 2;  // f32 [8][64] per-token scalars
+constexpr int OFF_R = OFF_SM + 8 * 64 * 4;        // f32 4 x [16][16] block products
+constexpr int LDS_BYTES = OFF_R + 4 * 256 * 4;
+enum { SM_LC = 0, SM_BETA, SM_NK, SM_NQ, SM_GK, SM_QG, SM_KD, SM_KSQ };
+
+struct PrefillDev {
+  const void *q, *k, *v, *g, *beta, *a_log, *dt_bias;
+  void *out;
+  const int32_t *cu, *ckpt;
+  const float *init;
+  float *ck_state;
+  int64_t q_stride, k_stride, v_stride;
+  int H, HK, NC, gate_dtype, out_dtype, normalize;
+  float scale;
+};
+
+__device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ bf16x8 ld8(const uint8_t *lds, int byte) { return *(const bf16x8 *)(lds + byte); }
+__device__ __forceinline__ float bf2f(__bf16 x) { return (float)x; }
+
+// x = hi + lo with hi = bf16(x), lo = bf16(x - hi)
+__device__ __forceinline__ void split8(const float x[8], bf16x8 &hi, bf16x8 &lo) {
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    const __bf16 h = (__bf16)x[e];
+    hi[e] = h;
+    lo[e] = (__bf16)(x[e] - (float)h);
+  }
+}
+__device__ __forceinline__ uint2 pack4(const float x[4]) {
+  uint2 u;
+  u.x = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x[1]) << 16);
+  u.y = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x[2]) | ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x[3]) << 16);
+  return u;
+}
+// hi/lo halves of four values as two packed bf16 x 4
+__device__ __forceinline__ void split4(const float x[4], uint2 &hi, uint2 &lo) {
+  float h[4], r[4];
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    h[e] = (float)(__bf16)x[e];
+    r[e] = x[e] - h[e];
+  }
+  hi = pack4(h);
+  lo = pack4(r);
+}
+
+// sum over the 16 lanes of a DPP row
+__device__ __forceinline__ float row16_sum(float x) {
+  x = fast::rg8_sum(x);
+  return x + fast::dpp<0x140>(x);  // row_mirror
+}
+
+__global__ __launch_bounds__(256) void prefill_kernel(PrefillDev D) {
+#pragma clang fp contract(off)
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int H = D.H;
+  const int vs = blockIdx.x & 1;
+  const int h = (blockIdx.x >> 1) % H;
+  const int b = (blockIdx.x >> 1) / H;
+  const int hk = h / (H / D.HK);
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, q4 = l >> 4, c16 = l & 15;
+  const int t0 = D.cu[b], len = D.cu[b + 1] - t0;
+  float *sm = (float *)(smem + OFF_SM);
+  uint8_t *Kc = smem + OFF_KC, *Kt = smem + OFF_KT, *Vt = smem + OFF_VT, *WD = smem + OFF_WD, *St = smem + OFF_ST;
+  float *AT = (float *)(smem + OFF_AT);
+  uint8_t *Pl = smem + OFF_P;
+  float *Rs = (float *)(smem + OFF_R) + 256 * w;
+  const __bf16 *qg = (const __bf16 *)D.q, *kg = (const __bf16 *)D.k, *vg = (const __bf16 *)D.v;
+
+  // ---- state S[d][j] of this half in registers: tiles (d-tile 2w + mt, j-tile nj),
+  // lane holds rows d = 16(2w + mt) + 4 q4 + r, column j = 16 nj + c16
+  float S[2][4][4];
+  {
+    const float *src = D.init + ((int64_t)b * H + h) * PKD * 128 + vs * PVS;
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+      for (int nj = 0; nj < 4; nj++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) S[mt][nj][r] = src[(int64_t)(16 * (2 * w + mt) + 4 * q4 + r) * 128 + 16 * nj + c16];
+  }
+  auto store_st = [&]() {
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+      for (int nj = 0; nj < 4; nj++) {
+        uint2 hi, lo;
+        split4(S[mt][nj], hi, lo);
+        const int off = ((16 * nj + c16) * P136 + 16 * (2 * w + mt) + 4 * q4) * 2;
+        *(uint2 *)(St + off) = hi;
+        *(uint2 *)(St + PVS * P136 * 2 + off) = lo;
+      }
+  };
+  store_st();
+
+  int ci = 0;  // next checkpoint index
+  for (int c0 = 0; c0 < len;) {
+    // segment end: the next checkpoint past c0 or the sequence end, at most one chunk
+    int stop = len;
+    for (int c = ci; c < D.NC; c++) {
+      const int p = D.ckpt[(int64_t)b * D.NC + c];
+      if (p > c0 && p <= len) {
+        stop = p < stop ? p : stop;
+        break;
+      }
+    }
+    const int n = stop - c0 < PC ? stop - c0 : PC;
+    const int64_t tb = (int64_t)t0 + c0;
+
+    // ---- loads: k rows (and transposed), q rows of this wave's tile, v columns, gates
+    for (int it = 0; it < 4; it++) {
+      const int idx = tid + 256 * it, t = idx >> 4, d8 = (idx & 15) * 8;
+      uint4 kv = make_uint4(0u, 0u, 0u, 0u);
+      if (t < n) kv = *(const uint4 *)(kg + (tb + t) * D.k_stride + hk * PKD + d8);
+      *(uint4 *)(Kc + (t * P136 + d8) * 2) = kv;
+      const uint16_t *ke = (const uint16_t *)&kv;
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        *(uint16_t *)(Kt + ((d8 + e) * P72 + t) * 2) = ke[e];
+        const float f = __uint_as_float((uint32_t)ke[e] << 16);
+        ss = fmaf(f, f, ss);
+      }
+      ss = row16_sum(ss);
+      if ((tid & 15) == 0) sm[SM_KSQ * 64 + t] = ss;
+    }
+    bf16x8 qa[4];
+    {
+      const int t = 16 * w + c16;
+      float ss = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < 4; ks++) {
+        uint4 u = make_uint4(0u, 0u, 0u, 0u);
+        if (t < n) u = *(const uint4 *)(qg + (tb + t) * D.q_stride + hk * PKD + 8 * q4 + 32 * ks);
+        qa[ks] = __builtin_bit_cast(bf16x8, u);
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const float f = bf2f(qa[ks][e]);
+          ss = fmaf(f, f, ss);
+        }
+      }
+      const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
+      ss = __uint_as_float(s32[0]) + __uint_as_float(s32[1]);
+      const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
+      ss = __uint_as_float(s16[0]) + __uint_as_float(s16[1]);
+      if (q4 == 0) sm[SM_NQ * 64 + t] = (D.normalize ? 1.0f / __builtin_sqrtf(ss + 1e-6f) : 1.0f) * D.scale;
+    }
+    for (int it = 0; it < 2; it++) {
+      const int idx = tid + 256 * it, t = idx >> 3, j8 = (idx & 7) * 8;
+      uint4 vv = make_uint4(0u, 0u, 0u, 0u);
+      if (t < n) vv = *(const uint4 *)(vg + (tb + t) * D.v_stride + h * 128 + vs * PVS + j8);
+      const uint16_t *ve = (const uint16_t *)&vv;
+#pragma unroll
+      for (int e = 0; e < 8; e++) *(uint16_t *)(Vt + ((j8 + e) * P72 + t) * 2) = ve[e];
+    }
+    if (w == 0) {
+      float lg = 0.f, bt = 0.f;
+      if (l < n) {
+        lg = load_val(D.g, D.gate_dtype, (tb + l) * H + h);
+        bt = load_val(D.beta, D.gate_dtype, (tb + l) * H + h);
+        if (D.a_log) {
+          const float u = lg + load_val(D.dt_bias, D.gate_dtype, h);
+          const float sp = u > 20.0f ? u : __logf(1.0f + __expf(u < 20.0f ? u : 20.0f));
+          lg = -__expf(load_val(D.a_log, D.gate_dtype, h)) * sp;
+          bt = 1.0f / (1.0f + __expf(-bt));
+        }
+      }
+      // inclusive prefix sum of the log decays over the 64 tokens
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const float y = __shfl_up(lg, o);
+        if (l >= o) lg += y;
+      }
+      sm[SM_LC * 64 + l] = lg;
+      sm[SM_BETA * 64 + l] = bt;
+    }
+    __syncthreads();
+    if (tid < 64) {
+      const int t = tid;
+      const float nk = D.normalize ? 1.0f / __builtin_sqrtf(sm[SM_KSQ * 64 + t] + 1e-6f) : 1.0f;
+      const float lc = sm[SM_LC * 64 + t], lcC = sm[SM_LC * 64 + 63];
+      const float gam = __expf(lc);
+      sm[SM_NK * 64 + t] = nk;
+      sm[SM_GK * 64 + t] = (sm[SM_BETA * 64 + t] * gam) * nk;
+      sm[SM_QG * 64 + t] = sm[SM_NQ * 64 + t] * gam;
+      sm[SM_KD * 64 + t] = nk * __expf(lcC - lc);
+    }
+    __syncthreads();
+
+    // ---- K K^T and K Q^T tiles: rows s (tile ns), columns t (this wave's tile)
+    {
+      bf16x8 bk[4];
+#pragma unroll
+      for (int ks = 0; ks < 4; ks++) bk[ks] = ld8(Kc, ((16 * w + c16) * P136 + 8 * q4 + 32 * ks) * 2);
+      const int t = 16 * w + c16;
+      const float lct = sm[SM_LC * 64 + t], bnt = sm[SM_BETA * 64 + t] * sm[SM_NK * 64 + t];
+      const float nqt = sm[SM_NQ * 64 + t];
+#pragma unroll
+      for (int ns = 0; ns < 4; ns++) {
+        f32x4 aA = {0.f, 0.f, 0.f, 0.f}, aP = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+          const bf16x8 a = ld8(Kc, ((16 * ns + c16) * P136 + 8 * q4 + 32 * ks) * 2);
+          aA = mfma(a, bk[ks], aA);
+          aP = mfma(a, qa[ks], aP);
+        }
+        const int s0 = 16 * ns + 4 * q4;
+        const float4 lcs = *(const float4 *)(sm + SM_LC * 64 + s0);
+        const float4 nks = *(const float4 *)(sm + SM_NK * 64 + s0);
+        const float lc4[4] = {lcs.x, lcs.y, lcs.z, lcs.w}, nk4[4] = {nks.x, nks.y, nks.z, nks.w};
+        float av[4], pv[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const int s = s0 + r;
+          const float e = s <= t ? __expf(lct - lc4[r]) : 0.0f;
+          av[r] = s < t ? (bnt * nk4[r]) * e * aA[r] : 0.0f;
+          pv[r] = s <= t ? (nqt * nk4[r]) * e * aP[r] : 0.0f;
+        }
+        *(float4 *)(AT + t * PA + s0) = make_float4(av[0], av[1], av[2], av[3]);
+        uint2 hi, lo;
+        split4(pv, hi, lo);
+        *(uint2 *)(Pl + (t * P72 + s0) * 2) = hi;
+        *(uint2 *)(Pl + PC * P72 * 2 + (t * P72 + s0) * 2) = lo;
+      }
+    }
+    __syncthreads();
+
+    // ---- T = (I + A)^{-1}: diagonal 16x16 blocks by forward substitution
+    if (l < 16) {
+      const float *blk = AT + 16 * w * PA + 16 * w;
+      float x[16];
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        float acc = r == l ? 1.0f : 0.0f;
+#pragma unroll
+        for (int s = 0; s < r; s++) acc = fmaf(-blk[r * PA + s], x[s], acc);
+        x[r] = acc;
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int r = 0; r < 16; r++) AT[(16 * w + r) * PA + 16 * w + l] = x[r];
+    }
+    __syncthreads();
+    // off-diagonal blocks, one block row at a time: T_iw = -T_ii sum_{k=w}^{i-1} A_ik T_kw
+    for (int i = 1; i < 4; i++) {
+      const int r = l >> 2, c4 = 4 * (l & 3);
+      if (w < i) {
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int kb = w; kb < i; kb++) {
+#pragma unroll
+          for (int m = 0; m < 16; m++) {
+            const float a = AT[(16 * i + r) * PA + 16 * kb + m];
+            const float4 tv = *(const float4 *)(AT + (16 * kb + m) * PA + 16 * w + c4);
+            acc[0] = fmaf(a, tv.x, acc[0]);
+            acc[1] = fmaf(a, tv.y, acc[1]);
+            acc[2] = fmaf(a, tv.z, acc[2]);
+            acc[3] = fmaf(a, tv.w, acc[3]);
+          }
+        }
+        *(float4 *)(Rs + r * 16 + c4) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+      }
+      __syncthreads();
+      if (w < i) {
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int m = 0; m < 16; m++) {
+          const float a = AT[(16 * i + r) * PA + 16 * i + m];
+          const float4 rv = *(const float4 *)(Rs + m * 16 + c4);
+          acc[0] = fmaf(-a, rv.x, acc[0]);
+          acc[1] = fmaf(-a, rv.y, acc[1]);
+          acc[2] = fmaf(-a, rv.z, acc[2]);
+          acc[3] = fmaf(-a, rv.w, acc[3]);
+        }
+        *(float4 *)(AT + (16 * i + r) * PA + 16 * w + c4) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+      }
+      __syncthreads();
+    }
+
+    // ---- W^T = K^T (T diag(beta Gamma nk))^T and U = T diag(beta) V (rows t of this wave's tile)
+    f32x4 U[4];
+    {
+      const int t = 16 * w + c16;
+      bf16x8 bh[2], bl[2], ah[2], al[2];
+#pragma unroll
+      for (int ks = 0; ks < 2; ks++) {
+        const int s0 = 8 * q4 + 32 * ks;
+        const float4 t0v = *(const float4 *)(AT + t * PA + s0), t1v = *(const float4 *)(AT + t * PA + s0 + 4);
+        const float4 g0 = *(const float4 *)(sm + SM_GK * 64 + s0), g1 = *(const float4 *)(sm + SM_GK * 64 + s0 + 4);
+        const float4 b0 = *(const float4 *)(sm + SM_BETA * 64 + s0), b1 = *(const float4 *)(sm + SM_BETA * 64 + s0 + 4);
+        const float tr[8] = {t0v.x, t0v.y, t0v.z, t0v.w, t1v.x, t1v.y, t1v.z, t1v.w};
+        const float gk[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+        const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+        float xw[8], xu[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          xw[e] = tr[e] * gk[e];
+          xu[e] = tr[e] * bb[e];
+        }
+        split8(xw, bh[ks], bl[ks]);
+        split8(xu, ah[ks], al[ks]);
+      }
+#pragma unroll
+      for (int nd = 0; nd < 8; nd++) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+          const bf16x8 a = ld8(Kt, ((16 * nd + c16) * P72 + 8 * q4 + 32 * ks) * 2);
+          acc = mfma(a, bh[ks], acc);
+          acc = mfma(a, bl[ks], acc);
+        }
+        const float wv[4] = {acc[0], acc[1], acc[2], acc[3]};
+        uint2 hi, lo;
+        split4(wv, hi, lo);
+        const int off = (t * P136 + 16 * nd + 4 * q4) * 2;
+        *(uint2 *)(WD + off) = hi;
+        *(uint2 *)(WD + PC * P136 * 2 + off) = lo;
+      }
+#pragma unroll
+      for (int nj = 0; nj < 4; nj++) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+          const bf16x8 bv = ld8(Vt, ((16 * nj + c16) * P72 + 8 * q4 + 32 * ks) * 2);
+          acc = mfma(ah[ks], bv, acc);
+          acc = mfma(al[ks], bv, acc);
+        }
+        U[nj] = acc;
+      }
+    }
+    __syncthreads();
+    // ---- Delta = U - W S0 (rows t of this wave's tile, columns j)
+    float dl[4][4];
+    {
+      f32x4 acc[4];
+#pragma unroll
+      for (int nj = 0; nj < 4; nj++) acc[nj] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ks++) {
+        const int ao = ((16 * w + c16) * P136 + 8 * q4 + 32 * ks) * 2;
+        const bf16x8 awh = ld8(WD, ao), awl = ld8(WD, PC * P136 * 2 + ao);
+#pragma unroll
+        for (int nj = 0; nj < 4; nj++) {
+          const int bo = ((16 * nj + c16) * P136 + 8 * q4 + 32 * ks) * 2;
+          const bf16x8 bsh = ld8(St, bo), bsl = ld8(St, PVS * P136 * 2 + bo);
+          acc[nj] = mfma(awh, bsh, acc[nj]);
+          acc[nj] = mfma(awh, bsl, acc[nj]);
+          acc[nj] = mfma(awl, bsh, acc[nj]);
+        }
+      }
+#pragma unroll
+      for (int nj = 0; nj < 4; nj++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) dl[nj][r] = U[nj][r] - acc[nj][r];
+    }
+    __syncthreads();  // W is dead: Delta and Delta' take its place
+    {
+      const int tt = 16 * w + 4 * q4;
+      const float4 kd = *(const float4 *)(sm + SM_KD * 64 + tt);
+      const float kd4[4] = {kd.x, kd.y, kd.z, kd.w};
+#pragma unroll
+      for (int nj = 0; nj < 4; nj++) {
+        const int off = ((16 * nj + c16) * P72 + tt) * 2;
+        float d2[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) d2[r] = dl[nj][r] * kd4[r];
+        uint2 hi, lo;
+        split4(dl[nj], hi, lo);
+        *(uint2 *)(WD + off) = hi;
+        *(uint2 *)(WD + PVS * P72 * 2 + off) = lo;
+        split4(d2, hi, lo);
+        *(uint2 *)(WD + 2 * PVS * P72 * 2 + off) = hi;
+        *(uint2 *)(WD + 3 * PVS * P72 * 2 + off) = lo;
+      }
+    }
+    __syncthreads();
+
+    // ---- O^T = diag(nq Gamma) (S0^T Q^T) + Delta^T P^T: rows j, column t of this wave's tile
+    {
+      const int t = 16 * w + c16;
+      bf16x8 bph[2], bpl[2];
+#pragma unroll
+      for (int ks = 0; ks < 2; ks++) {
+        const int o = (t * P72 + 8 * q4 + 32 * ks) * 2;
+        bph[ks] = ld8(Pl, o);
+        bpl[ks] = ld8(Pl, PC * P72 * 2 + o);
+      }
+      const float qgt = sm[SM_QG * 64 + t];
+#pragma unroll
+      for (int nj = 0; nj < 4; nj++) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+          const int ao = ((16 * nj + c16) * P136 + 8 * q4 + 32 * ks) * 2;
+          acc = mfma(ld8(St, ao), qa[ks], acc);
+          acc = mfma(ld8(St, PVS * P136 * 2 + ao), qa[ks], acc);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; r++) acc[r] *= qgt;
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+          const int ao = ((16 * nj + c16) * P72 + 8 * q4 + 32 * ks) * 2;
+          const bf16x8 adh = ld8(WD, ao), adl = ld8(WD, PVS * P72 * 2 + ao);
+          acc = mfma(adh, bph[ks], acc);
+          acc = mfma(adh, bpl[ks], acc);
+          acc = mfma(adl, bph[ks], acc);
+        }
+        if (t < n) {
+          const float o4[4] = {acc[0], acc[1], acc[2], acc[3]};
+          store4(D.out, D.out_dtype, ((tb + t) * H + h) * 128 + vs * PVS + 16 * nj + 4 * q4, o4);
+        }
+      }
+    }
+    // ---- S <- Gamma_C S0 + K^T Delta'
+    {
+      const float gC = __expf(sm[SM_LC * 64 + 63]);
+#pragma unroll
+      for (int mt = 0; mt < 2; mt++) {
+        bf16x8 ak[2];
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) ak[ks] = ld8(Kt, ((16 * (2 * w + mt) + c16) * P72 + 8 * q4 + 32 * ks) * 2);
+#pragma unroll
+        for (int nj = 0; nj < 4; nj++) {
+          f32x4 acc;
+#pragma unroll
+          for (int r = 0; r < 4; r++) acc[r] = S[mt][nj][r] * gC;
+#pragma unroll
+          for (int ks = 0; ks < 2; ks++) {
+            const int bo = ((16 * nj + c16) * P72 + 8 * q4 + 32 * ks) * 2;
+            acc = mfma(ak[ks], ld8(WD, 2 * PVS * P72 * 2 + bo), acc);
+            acc = mfma(ak[ks], ld8(WD, 3 * PVS * P72 * 2 + bo), acc);
+          }
+#pragma unroll
+          for (int r = 0; r < 4; r++) S[mt][nj][r] = acc[r];
+        }
+      }
+    }
+    __syncthreads();
+    store_st();
+    c0 += n;
+    // checkpoints reached at c0
+    for (; ci < D.NC; ci++) {
+      const int p = D.ckpt[(int64_t)b * D.NC + ci];
+      if (p > c0 && p <= len) break;
+      if (p == c0) {
+        float *dst = D.ck_state + (((int64_t)b * D.NC + ci) * H + h) * PKD * 128 + vs * PVS;
+#pragma unroll
+        for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+          for (int nj = 0; nj < 4; nj++)
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+              dst[(int64_t)(16 * (2 * w + mt) + 4 * q4 + r) * 128 + 16 * nj + c16] = S[mt][nj][r];
+      }
+    }
+  }
+}
+
+}  // namespace pf
+
+__global__ void fill_zero_kernel(float *p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) p[i] = 0.0f;
+}
+
 __global__ void clear_kernel(uint8_t *data, int64_t page_bytes, int64_t num_slots, const void *slots,
                              int dtype) {
   int64_t s = load_slot(slots, dtype, blockIdx.y);
@@ -2305,6 +2804,81 @@ int sq_create_cu_stream(int32_t device, int32_t cus, void **stream, int32_t *act
     return (int)e;
   }
   *stream = (void *)s;
+  return 0;
+}
+
+int sq_prefill(const sq_pool *pool, const sq_prefill_args *a, void *stream) {
+  int rc = validate_pool(pool);
+  if (rc) return rc;
+  if (!a) return fail(SQ_EINVAL, "prefill: null arguments");
+  if (pool->kda || pool->keys != 128 || pool->values != 128)
+    return fail(SQ_ESHAPE, "prefill: the chunked kernel handles GDN pools with K = V = 128");
+  if (pool->storage != 0) return fail(SQ_ESTORAGE, "prefill: packed storage only");
+  if (a->batch < 0 || a->n_checkpoints < 0) return fail(SQ_EINVAL, "prefill: negative batch or checkpoint count");
+  if (a->batch == 0) return 0;
+  if (!a->q || !a->k || !a->v || !a->g || !a->beta || !a->out || !a->cu_seqlens || !a->init_state)
+    return fail(SQ_EINVAL, "prefill: null input, output, sequence offsets or initial-state workspace");
+  if (a->n_checkpoints > 0 && (!a->checkpoints || !a->slots || !a->checkpoint_state))
+    return fail(SQ_EINVAL, "prefill: checkpoints need positions, slots and a state workspace");
+  if (a->qkv_dtype != SQ_BF16) return fail(SQ_EINVAL, "prefill: q, k, v must be bf16 (the MFMA operand type)");
+  if (a->gate_dtype != SQ_F32 && a->gate_dtype != SQ_BF16 && a->gate_dtype != SQ_F16)
+    return fail(SQ_EINVAL, "prefill: gate dtype");
+  if (a->out_dtype != SQ_F32 && a->out_dtype != SQ_BF16 && a->out_dtype != SQ_F16)
+    return fail(SQ_EINVAL, "prefill: output dtype");
+  if (a->slots_dtype != SQ_I32 && a->slots_dtype != SQ_I64) return fail(SQ_EINVAL, "prefill: slots dtype");
+  if (a->key_heads < 1 || pool->heads % a->key_heads) return fail(SQ_EINVAL, "prefill: key heads must divide heads");
+  if ((a->a_log == nullptr) != (a->dt_bias == nullptr)) return fail(SQ_EINVAL, "prefill: a_log needs dt_bias");
+  if (a->q_stride % 8 || a->k_stride % 8 || a->v_stride % 8 || ((uintptr_t)a->q & 15) || ((uintptr_t)a->k & 15) ||
+      ((uintptr_t)a->v & 15))
+    return fail(SQ_EINVAL, "prefill: q, k, v rows must start on 16-byte boundaries (strides multiple of 8)");
+  hipStream_t st = (hipStream_t)stream;
+  const int H = pool->heads;
+  const int64_t dense = a->batch * (int64_t)H * 128 * 128;
+  if (a->init_slots) {
+    if (a->slots_dtype != SQ_I32 && a->slots_dtype != SQ_I64) return fail(SQ_EINVAL, "prefill: slots dtype");
+    StepDev sd;
+    memset(&sd, 0, sizeof(sd));
+    sd.slots = a->init_slots;
+    sd.slots_dtype = a->slots_dtype;
+    sd.dense = a->init_state;
+    rc = launch_step_mode<MODE_DECODE>(pool, sd, a->batch, st);
+    if (rc) return rc;
+  } else {
+    hipLaunchKernelGGL(fill_zero_kernel, dim3(1024), dim3(256), 0, st, a->init_state, dense);
+    rc = check_launch("fill_zero_kernel");
+    if (rc) return rc;
+  }
+  pf::PrefillDev D;
+  D.q = a->q;
+  D.k = a->k;
+  D.v = a->v;
+  D.g = a->g;
+  D.beta = a->beta;
+  D.a_log = a->a_log;
+  D.dt_bias = a->dt_bias;
+  D.out = a->out;
+  D.cu = a->cu_seqlens;
+  D.ckpt = a->checkpoints;
+  D.init = a->init_state;
+  D.ck_state = a->checkpoint_state;
+  D.q_stride = a->q_stride;
+  D.k_stride = a->k_stride;
+  D.v_stride = a->v_stride;
+  D.H = H;
+  D.HK = a->key_heads;
+  D.NC = a->n_checkpoints;
+  D.gate_dtype = a->gate_dtype;
+  D.out_dtype = a->out_dtype;
+  D.normalize = a->normalize;
+  D.scale = a->scale;
+  hipError_t e = hipFuncSetAttribute((const void *)pf::prefill_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     pf::LDS_BYTES);
+  if (e != hipSuccess) return fail((int)e, "prefill: cannot raise the kernel's LDS limit");
+  hipLaunchKernelGGL(pf::prefill_kernel, dim3((unsigned)(a->batch * H * 2)), dim3(256), pf::LDS_BYTES, st, D);
+  rc = check_launch("prefill_kernel");
+  if (rc) return rc;
+  if (a->n_checkpoints > 0)
+    return sq_encode(pool, a->checkpoint_state, a->slots, a->slots_dtype, a->batch * a->n_checkpoints, stream);
   return 0;
 }
 

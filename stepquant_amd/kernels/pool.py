@@ -331,6 +331,91 @@ class PackedStatePool:
         self._schedule_writeback(update_key, decay, delta, partial, stable_slots)
         return out
 
+    def extend(self, q, k, v, g, beta, slots, cu_seqlens, *, checkpoints=None, checkpoint_slots=None,
+               init_slots=None, normalize=False, scale=1., a_log=None, dt_bias=None):
+        """Chunked prefill of whole sequences straight from and into the pool.
+
+        The behaviour of the serving adapter's ``kernel_extend``
+        (reference sglang/runtime.py:193-202: decode the slots' states, run
+        the chunked recurrence, encode the final states back) in one call:
+        q, k ``[T, HK*K]`` (or ``[..., T, HK, K]``), v ``[T, H*V]``, g, beta
+        ``[T, H]`` (raw gate and logits with ``a_log``/``dt_bias``),
+        ``cu_seqlens`` ``[B+1]`` token offsets, ``slots`` ``[B]``.  Initial
+        states come from ``init_slots`` (default ``slots``; ``None`` entries
+        or slot <= 0 start from zero).  By default the final state is written
+        to ``slots``; ``checkpoints`` ``[B, NC]`` (token counts, ascending)
+        with ``checkpoint_slots`` ``[B, NC]`` write intermediate prefix states
+        as well.  Returns the outputs ``[T, H, V]`` in q's dtype.
+        """
+        self.wait()
+        if self.plan.architecture != "gdn" or self.keys != 128 or self.values != 128:
+            raise ValueError("chunked prefill handles GDN pools with K = V = 128")
+        dev = self.device
+        cu = torch.as_tensor(cu_seqlens, device=dev).to(torch.int32).reshape(-1).contiguous()
+        batch = cu.numel() - 1
+        if batch < 0:
+            raise ValueError("cu_seqlens needs at least one entry")
+        slots_t = _indices(slots, dev)
+        if slots_t.numel() != batch:
+            raise ValueError("one slot per sequence")
+        total = int(cu[-1].item()) if batch else 0
+        q2 = q.reshape(-1, q.shape[-1] * (q.shape[-2] if q.dim() >= 3 else 1)) if q.dim() >= 3 else q
+        k2 = k.reshape(-1, k.shape[-1] * (k.shape[-2] if k.dim() >= 3 else 1)) if k.dim() >= 3 else k
+        v2 = v.reshape(-1, v.shape[-1] * (v.shape[-2] if v.dim() >= 3 else 1)) if v.dim() >= 3 else v
+        if q2.shape[0] != total or k2.shape[0] != total or v2.shape[0] != total:
+            raise ValueError("q, k, v need cu_seqlens[-1] token rows")
+        if v2.shape[1] != self.heads * self.values or q2.shape[1] % self.keys or q2.shape[1] != k2.shape[1]:
+            raise ValueError("q/k rows must hold HK*K values and v rows H*V")
+        hk = q2.shape[1] // self.keys
+        if self.heads % hk:
+            raise ValueError("value heads must be divisible by key heads")
+        qkv = []
+        for t in (q2, k2, v2):
+            t = t.to(torch.bfloat16)
+            if t.stride(-1) != 1 or t.stride(0) % 8 or t.data_ptr() % 16:
+                t = t.contiguous()
+            qkv.append(t)
+        q2, k2, v2 = qkv
+        gate_dtype = torch.float32 if g.dtype == torch.float64 else g.dtype
+        g2 = g.reshape(total, self.heads).to(gate_dtype).contiguous()
+        b2 = beta.reshape(total, self.heads).to(gate_dtype).contiguous()
+        al = None if a_log is None else a_log.to(gate_dtype).contiguous()
+        db = None if dt_bias is None else dt_bias.to(gate_dtype).contiguous()
+        if (al is None) != (db is None):
+            raise ValueError("a_log and dt_bias go together")
+        lengths = (cu[1:] - cu[:-1]).to(torch.int32)
+        if checkpoints is None:
+            ck = lengths.reshape(batch, 1)
+            ck_slots = slots_t.reshape(batch, 1)
+        else:
+            ck = torch.as_tensor(checkpoints, device=dev).to(torch.int32).reshape(batch, -1)
+            if checkpoint_slots is None:
+                raise ValueError("checkpoints need checkpoint_slots")
+            ck_slots = _indices(checkpoint_slots, dev).reshape(batch, -1)
+            if ck_slots.shape != ck.shape:
+                raise ValueError("one slot per checkpoint")
+        valid = (ck > 0) & (ck <= lengths[:, None])
+        ck_slots = torch.where(valid, ck_slots, torch.zeros_like(ck_slots)).contiguous()
+        ck = ck.contiguous()
+        nc = ck.shape[1]
+        init = slots_t if init_slots is None else _indices(init_slots, dev)
+        out = torch.empty((total, self.heads, self.values), device=dev, dtype=q.dtype)
+        init_state = torch.empty((batch, self.heads, self.keys, self.values), device=dev, dtype=torch.float32)
+        ck_state = torch.empty((batch * nc, self.heads, self.keys, self.values), device=dev, dtype=torch.float32)
+        init = init.to(ck_slots.dtype)
+        args = N.PrefillArgs(
+            q=N.ptr(q2), k=N.ptr(k2), v=N.ptr(v2), g=N.ptr(g2), beta=N.ptr(b2), a_log=N.ptr(al),
+            dt_bias=N.ptr(db), out=N.ptr(out), cu_seqlens=N.ptr(cu), checkpoints=N.ptr(ck),
+            init_slots=N.ptr(init), slots=N.ptr(ck_slots), init_state=N.ptr(init_state),
+            checkpoint_state=N.ptr(ck_state), batch=batch, q_stride=q2.stride(0), k_stride=k2.stride(0),
+            v_stride=v2.stride(0), key_heads=hk, n_checkpoints=nc, qkv_dtype=N.BF16,
+            gate_dtype=N.dtype_code(g2), out_dtype=N.dtype_code(out), slots_dtype=N.dtype_code(ck_slots),
+            normalize=int(bool(normalize)), scale=float(scale))
+        if batch:
+            N.check(N.lib().sq_prefill(self._desc, args, N.stream_handle()), "prefill")
+        self._last_prefill = (q2, k2, v2, g2, b2, al, db, cu, ck, init, ck_slots, init_state, ck_state)
+        return out
+
     @staticmethod
     def _scratch_desc(update_key, decay, delta, stable_slots):
         return N.Scratch(key=update_key.data_ptr(), decay=decay.data_ptr(), delta=delta.data_ptr(),

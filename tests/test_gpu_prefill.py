@@ -1,0 +1,123 @@
+"""Chunked MFMA prefill against the token-sequential oracle (MI355X).
+
+Bars: outputs and checkpoint states within 1e-3 of the float64 recurrence
+(relative to each head's largest magnitude; the chunk products carry ~2^-16
+relative error from hi/lo bf16 operands), and checkpoint pages bit-identical
+to the oracle's fit_state + page layout of the kernel's own fp32 states.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests.helpers import dev, device_plan, make_plan
+
+pytestmark = pytest.mark.gpu
+
+
+def _close(got, ref, tol, what):
+    scale = np.abs(ref).max(axis=-1, keepdims=True) + 1e-30
+    err = np.abs(got - ref) / scale
+    assert err.max() <= tol, f"{what}: max relative error {err.max():.2e}"
+
+
+@pytest.mark.parametrize("raw,normalize", [(False, True), (True, True), (False, False)])
+def test_prefill_against_sequential_oracle(raw, normalize):
+    print(f"case raw={raw} normalize={normalize}", flush=True)
+    from stepquant_amd.kernels.pool import PackedStatePool
+    H, HK, K, V = 4, 2, 128, 128
+    lens = [130, 37, 64]
+    B = len(lens)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    T = int(cu[-1])
+    oplan = make_plan("gdn", np.repeat(np.array([6, 4, 8, 6])[:, None], K, 1), seed=3)
+    pool = PackedStatePool(device_plan(oplan), 12, V)
+    rng = np.random.default_rng(7 + raw + 2 * normalize)
+    g = torch.Generator().manual_seed(11)
+    scale = K ** -.5 if normalize else .05
+    qf = torch.randn(T, HK, K, generator=g)
+    kf = torch.randn(T, HK, K, generator=g)
+    if not normalize:
+        kf = torch.nn.functional.normalize(kf, dim=-1)
+    q = qf.to(torch.bfloat16)
+    k = kf.to(torch.bfloat16)
+    v = torch.randn(T, H, V, generator=g).to(torch.bfloat16)
+    if raw:
+        gate = torch.randn(T, H, generator=g)
+        beta = torch.randn(T, H, generator=g)
+        a_log = torch.randn(H, generator=g) * .3
+        dt_bias = torch.randn(H, generator=g) * .3
+    else:
+        gate = -torch.nn.functional.softplus(torch.randn(T, H, generator=g))
+        beta = torch.sigmoid(torch.randn(T, H, generator=g))
+        a_log = dt_bias = None
+    init = torch.tensor([3, 0, 5])  # the second sequence starts from zero
+    x0 = torch.randn(B, H, K, V, generator=g) * .1
+    pool.encode(x0.to(dev()), init.to(dev()))
+    lay = O.layout(oplan, V)
+    pages0 = pool.data.cpu().numpy()
+    S0 = O.decode_page(pages0, init.numpy(), oplan, lay, V).astype(np.float64)
+    ck = np.array([[50, 130], [37, 0], [10, 64]])
+    ck_slots = torch.tensor([[6, 7], [8, 0], [9, 10]])
+    # q as float32 holding bf16 values: the kernel reads the same bf16 inputs and
+    # the outputs come back in float32, so their error is the kernel's own
+    out = pool.extend(q.float().to(dev()), k.to(dev()), v.to(dev()), gate.to(dev()), beta.to(dev()),
+                      torch.tensor([3, 4, 5]), torch.from_numpy(cu), checkpoints=torch.from_numpy(ck),
+                      checkpoint_slots=ck_slots, init_slots=init, normalize=normalize, scale=scale,
+                      a_log=None if a_log is None else a_log.to(dev()),
+                      dt_bias=None if dt_bias is None else dt_bias.to(dev()))
+    torch.cuda.synchronize()
+    ref_out, ref_states, _ = O.prefill(q.float().numpy(), k.float().numpy(), v.float().numpy(), gate.numpy(),
+                                       beta.numpy(), S0, cu, ck, normalize=normalize, scale=scale,
+                                       a_log=None if a_log is None else a_log.numpy(),
+                                       dt_bias=None if dt_bias is None else dt_bias.numpy())
+    ck_state = pool._last_prefill[-1].cpu().numpy().reshape(B, 2, H, K, V)
+    for b in range(B):
+        for c in range(2):
+            if ck_slots[b, c] > 0:
+                _close(ck_state[b, c], ref_states[b, c], 1e-3, f"state b={b} c={c}")
+    assert out.dtype == torch.float32
+    _close(out.cpu().numpy(), ref_out, 1e-3, "outputs")
+    # checkpoint pages are the oracle encoding of the kernel's fp32 states
+    pages = pool.data.cpu().numpy()
+    live = ck_slots.numpy().reshape(-1)
+    ref_pages = pages0.copy()
+    O.encode_page(ck_state.reshape(B * 2, H, K, V), live, oplan, lay, ref_pages)
+    for s in live[live > 0]:
+        assert np.array_equal(pages[s], ref_pages[s]), f"slot {s} page differs"
+    for s in (1, 2, 11):
+        assert not pages[s].any(), "untouched slots stay empty"
+
+
+def test_extend_defaults_write_final_state_back_to_the_slots():
+    from stepquant_amd.kernels.pool import PackedStatePool
+    H, K, V = 2, 128, 128
+    oplan = make_plan("gdn", np.full((H, K), 6), seed=1)
+    pool = PackedStatePool(device_plan(oplan), 4, V)
+    g = torch.Generator().manual_seed(2)
+    lens = [70, 5]
+    cu = torch.tensor([0, 70, 75])
+    q = torch.randn(75, H * K, generator=g).to(torch.bfloat16)
+    k = torch.randn(75, H * K, generator=g).to(torch.bfloat16)
+    v = torch.randn(75, H * V, generator=g).to(torch.bfloat16)
+    gate = -torch.nn.functional.softplus(torch.randn(75, H, generator=g))
+    beta = torch.sigmoid(torch.randn(75, H, generator=g))
+    slots = torch.tensor([2, 1])
+    pool.encode((torch.randn(2, H, K, V, generator=g) * .1).to(dev()), slots.to(dev()))
+    lay = O.layout(oplan, V)
+    S0 = O.decode_page(pool.data.cpu().numpy(), slots.numpy(), oplan, lay, V).astype(np.float64)
+    out = pool.extend(q.to(dev()), k.to(dev()), v.to(dev()), gate.to(dev()), beta.to(dev()), slots, cu,
+                      normalize=True, scale=K ** -.5)
+    torch.cuda.synchronize()
+    ref_out, _, final = O.prefill(q.float().numpy().reshape(75, H, K), k.float().numpy().reshape(75, H, K),
+                                  v.float().numpy().reshape(75, H, V), gate.numpy(), beta.numpy(), S0,
+                                  cu.numpy(), normalize=True, scale=K ** -.5)
+    dense = pool._last_prefill[-1].cpu().numpy()
+    _close(dense, final, 1e-3, "final states")
+    assert out.dtype == torch.bfloat16
+    _close(out.float().cpu().numpy(), ref_out, 2 ** -8 + 1e-3, "bf16 outputs")
+    ref_pages = np.zeros_like(pool.data.cpu().numpy())
+    O.encode_page(dense, slots.numpy(), oplan, lay, ref_pages)
+    got = pool.data.cpu().numpy()
+    assert np.array_equal(got[slots.numpy()], ref_pages[slots.numpy()])
+    assert len(lens) == 2

@@ -1,0 +1,112 @@
+"""The prefill oracle (token-sequential recurrence, float64) on the CPU.
+
+Pinned by: single tokens against the C delta_step/prepare restatement (itself
+pinned to core.py:5-15 and kernels/fused.py:155-179); the closed-form chunked
+(WY) form of the same recurrence, written here independently; the prefix
+property of checkpoints; sequence boundaries.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+
+def _inputs(rng, T, H, HK, K, V):
+    q = rng.standard_normal((T, HK, K))
+    k = rng.standard_normal((T, HK, K))
+    v = rng.standard_normal((T, H, V))
+    g = -np.log1p(np.exp(rng.standard_normal((T, H))))
+    beta = 1.0 / (1.0 + np.exp(-rng.standard_normal((T, H))))
+    return q, k, v, g, beta
+
+
+@pytest.mark.parametrize("raw", [False, True])
+def test_single_token_equals_delta_step(raw):
+    rng = np.random.default_rng(0)
+    H, HK, K, V, B = 4, 2, 16, 8, 3
+    q, k, v, g, beta = (x.astype(np.float32) for x in _inputs(rng, B, H, HK, K, V))
+    state = (rng.standard_normal((B, H, K, V)) * .3).astype(np.float32)
+    a_log = rng.standard_normal(H).astype(np.float32) if raw else None
+    dt_bias = rng.standard_normal(H).astype(np.float32) if raw else None
+    cu = np.arange(B + 1)
+    out, _, final = O.prefill(q, k, v, g, beta, state, cu, normalize=True, scale=K ** -.5,
+                              a_log=a_log, dt_bias=dt_bias)
+    qp, kp, ld, bo = O.prepare(q.reshape(B, -1), k.reshape(B, -1), g, beta, H, K, False, True, K ** -.5,
+                               a_log, dt_bias)
+    ref_out, ref_state = O.delta_step(state, qp, kp, v, ld, bo)
+    np.testing.assert_allclose(out, ref_out, rtol=2e-5, atol=2e-6)
+    np.testing.assert_allclose(final, ref_state, rtol=2e-5, atol=2e-6)
+
+
+def _chunked(q, k, v, g, beta, S, C):
+    """Closed-form chunk (WY/UT) recurrence for one sequence, heads batched.
+
+    With Gamma_t = prod_{s<=t} g_s inside a chunk and A_ts = beta_t
+    (Gamma_t/Gamma_s) k_t.k_s (s < t): Delta = (I + A)^{-1} beta (V - Gamma K S0),
+    O = Gamma Q S0 + (M o Q K^T) Delta with M_ts = Gamma_t/Gamma_s (s <= t),
+    S_C = Gamma_C S0 + (K Gamma_C / Gamma)^T Delta.
+    """
+    T = q.shape[0]
+    out = np.zeros((T,) + v.shape[1:])
+    for c0 in range(0, T, C):
+        sl = slice(c0, min(c0 + C, T))
+        Q, Kc, Vc = q[sl].transpose(1, 0, 2), k[sl].transpose(1, 0, 2), v[sl].transpose(1, 0, 2)
+        lg = np.cumsum(g[sl].T, axis=1)  # [H, n]
+        n = lg.shape[1]
+        ratio = np.exp(lg[:, :, None] - lg[:, None, :])
+        kk = np.einsum("htd,hsd->hts", Kc, Kc)
+        A = np.tril(beta[sl].T[:, :, None] * ratio * kk, -1)
+        Tm = np.linalg.inv(np.eye(n)[None] + A)
+        R = beta[sl].T[:, :, None] * (Vc - np.exp(lg)[:, :, None] * np.einsum("htd,hdv->htv", Kc, S))
+        D = Tm @ R
+        qk = np.einsum("htd,hsd->hts", Q, Kc)
+        O_ = np.exp(lg)[:, :, None] * np.einsum("htd,hdv->htv", Q, S) + (np.tril(ratio * qk)) @ D
+        out[sl] = O_.transpose(1, 0, 2)
+        S = np.exp(lg[:, -1])[:, None, None] * S + np.einsum(
+            "htd,htv->hdv", Kc * np.exp(lg[:, -1:] - lg)[:, :, None], D)
+    return out, S
+
+
+@pytest.mark.parametrize("C", [1, 4, 8, 16])
+def test_chunked_closed_form_equals_sequential(C):
+    rng = np.random.default_rng(C)
+    H, K, V, T = 3, 8, 6, 29
+    q, k, v, g, beta = _inputs(rng, T, H, H, K, V)
+    S0 = rng.standard_normal((1, H, K, V))
+    out, _, final = O.prefill(q, k, v, g, beta, S0, np.array([0, T]))
+    o2, s2 = _chunked(q, k, v, g, beta, S0[0], C)
+    np.testing.assert_allclose(out, o2, rtol=1e-9, atol=1e-10)
+    np.testing.assert_allclose(final[0], s2, rtol=1e-9, atol=1e-10)
+
+
+def test_checkpoints_are_prefix_states_and_sequences_are_independent():
+    rng = np.random.default_rng(5)
+    H, HK, K, V = 4, 2, 8, 4
+    lens = [13, 0, 7]
+    cu = np.concatenate([[0], np.cumsum(lens)])
+    T = cu[-1]
+    q, k, v, g, beta = _inputs(rng, T, H, HK, K, V)
+    S0 = rng.standard_normal((3, H, K, V))
+    ck = np.array([[5, 13, 0], [1, 0, 0], [7, 3, 9]])
+    out, states, final = O.prefill(q, k, v, g, beta, S0, cu, ck, normalize=True, scale=.5)
+    np.testing.assert_array_equal(final[1], S0[1])          # empty sequence keeps its state
+    assert not states[1].any() and not states[2, 2].any()   # unused / out-of-range checkpoints
+    for b, c in [(0, 0), (0, 1), (2, 0), (2, 1)]:
+        n = ck[b, c]
+        s0 = cu[b]
+        _, _, f = O.prefill(q[s0:s0 + n], k[s0:s0 + n], v[s0:s0 + n], g[s0:s0 + n], beta[s0:s0 + n],
+                            S0[b:b + 1], np.array([0, n]), normalize=True, scale=.5)
+        np.testing.assert_allclose(states[b, c], f[0], rtol=1e-12, atol=1e-12)
+    # sequence 2 alone gives the same outputs as inside the batch
+    o2, _, _ = O.prefill(q[13:], k[13:], v[13:], g[13:], beta[13:], S0[2:], np.array([0, 7]),
+                         normalize=True, scale=.5)
+    np.testing.assert_allclose(out[13:], o2, rtol=1e-12, atol=1e-12)
+
+
+def test_no_write_strength_only_decays():
+    rng = np.random.default_rng(2)
+    H, K, V, T = 2, 4, 3, 6
+    q, k, v, g, beta = _inputs(rng, T, H, H, K, V)
+    S0 = rng.standard_normal((1, H, K, V))
+    _, _, final = O.prefill(q, k, v, g, np.zeros_like(beta), S0, np.array([0, T]))
+    np.testing.assert_allclose(final[0], S0[0] * np.exp(g.sum(0))[:, None, None], rtol=1e-12)
