@@ -46,6 +46,10 @@ def parse():
                    help="launch steps eagerly (for rocprofv3 --pmc runs, which count per dispatch)")
     p.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                    help="only run a device-to-device copy of MIB MiB five times (counter calibration)")
+    p.add_argument("--workload", choices=["decode", "prefill"], default="decode",
+                   help="prefill: configs[4], chunked GDN prefill into 5 prefix slots per request")
+    p.add_argument("--seq-len", type=int, default=2048, help="prefill tokens per sequence")
+    p.add_argument("--checkpoints", type=int, default=5, help="prefill prefix slots per request")
     return p.parse_args()
 
 
@@ -99,6 +103,83 @@ def cpu_baseline(bits, impact, arch, B, H, HK, K, V, sample, group=32):
                        f"(decode page, prepare, delta_step, fit_state + page store), 1 thread, {dt:.1f} s")
 
 
+PEAK_BF16_TFLOPS = 2500.0
+
+
+def prefill_flops(n_chunks, C=64, K=128, V=128):
+    """Algorithmic FLOPs of the chunked recurrence per chunk-head:
+    K K^T and Q K^T (2 x 2C^2K), the triangular inverse (C^3/3 x 2), W and U
+    (2C^2K + 2C^2V), W S and Q S (2 x 2CKV), (M o QK^T) Delta (2C^2V) and
+    K^T Delta (2CKV)."""
+    per = 6 * C * C * K + 4 * C * C * V + 6 * C * K * V + (2 * C ** 3) // 3
+    return n_chunks * per
+
+
+def bench_prefill(a, torch):
+    from stepquant_amd.kernels.pool import PackedStatePool
+    from stepquant_amd.quantization import QuantizationPlan
+    dev = torch.device("cuda:0")
+    B, H, HK, K, V, T = a.batch, a.heads, a.key_heads, 128, 128, a.seq_len
+    NC = a.checkpoints
+    bits, impact = make_plan(torch, "gdn", H, K, 6)
+    plan = QuantizationPlan("gdn", bits.to(dev), impact.to(dev))
+    pool = PackedStatePool(plan, B * (NC + 1) + 1, V)
+    g = torch.Generator(device=dev).manual_seed(0)
+    tot = B * T
+    q = torch.randn(tot, HK * K, device=dev, generator=g).to(torch.bfloat16)
+    k = torch.randn(tot, HK * K, device=dev, generator=g).to(torch.bfloat16)
+    v = torch.randn(tot, H * V, device=dev, generator=g).to(torch.bfloat16)
+    gate = torch.randn(tot, H, device=dev, generator=g)
+    beta = torch.randn(tot, H, device=dev, generator=g)
+    a_log = torch.zeros(H, device=dev)
+    dt_bias = torch.zeros(H, device=dev)
+    cu = torch.arange(0, tot + 1, T, device=dev, dtype=torch.int32)
+    init = torch.arange(1, B + 1, device=dev)
+    pool.encode(torch.randn(B, H, K, V, device=dev, generator=g) * .05, init)
+    # prefix slots at evenly spaced chunk boundaries, the last at the sequence end
+    pos = [((T * (c + 1)) // NC + 63) // 64 * 64 for c in range(NC)]
+    pos[-1] = T
+    ck = torch.tensor(pos, device=dev, dtype=torch.int32).repeat(B, 1)
+    ck_slots = torch.arange(B + 1, B + 1 + B * NC, device=dev).reshape(B, NC)
+
+    def step():
+        return pool.extend(q, k, v, gate, beta, init, cu, checkpoints=ck, checkpoint_slots=ck_slots,
+                           init_slots=init, normalize=True, scale=K ** -.5, a_log=a_log, dt_bias=dt_bias)
+
+    for _ in range(max(a.warmup, 1)):
+        step()
+    torch.cuda.synchronize()
+    cur = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(cur)
+    for _ in range(a.steps):
+        step()
+    end.record(cur)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = start.elapsed_time(end) / a.steps
+    n_chunks = B * H * ((T + 63) // 64)
+    flops = prefill_flops(n_chunks)
+    tflops = flops / (ms_step * 1e-3) / 1e12
+    hbm = (3 * tot * H * K * 2 + tot * H * V * 2 + 2 * tot * H * 4 + B * pool.page_bytes
+           + B * NC * pool.page_bytes)
+    line = dict(metric="prefill tokens/sec (chunked GDN prefill into prefix slots)",
+                value=round(tot / (ms_step * 1e-3), 1), unit="tokens/s", n_gpus=1, steps=a.steps,
+                warmup=a.warmup, ms_per_step=round(ms_step, 6), higher_is_better=True, scaling="weak",
+                vs_baseline=None, dtype="bf16", data="synthetic",
+                config=dict(workload=f"GDN prefill STEPQuant@6, B={B}, T={T}, H={H}, HK={HK}, dk=dv={K}, "
+                                     f"chunk 64, bf16 q/k/v, raw gates, {NC} prefix slots per request",
+                            global_batch=B, seq_len=T, wall_s=round(wall, 3)),
+                roofline=dict(bound="mfma", achieved=round(tflops, 2), peak=PEAK_BF16_TFLOPS, unit="TFLOP/s",
+                              frac=round(tflops / PEAK_BF16_TFLOPS, 4), traffic=None,
+                              algorithmic_flops_per_step=flops,
+                              hbm_fraction=round(hbm / (ms_step * 1e-3) / 1e9 / PEAK_GBS, 4),
+                              algorithmic_bytes_per_step=hbm),
+                cpu_baseline=None)
+    print(json.dumps(line), flush=True)
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -115,6 +196,8 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps(dict(calibrate_copy_bytes=n, launches=5)), flush=True)
         return
+    if a.workload == "prefill":
+        return bench_prefill(a, torch)
     from stepquant_amd.kernels.pool import PackedStatePool
     from stepquant_amd.quantization import QuantizationPlan
 

@@ -2000,7 +2000,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GDN128_WAVE
 //
 // For a chunk with start state S0 [K, V], Gamma_t = prod_{s<=t} g_s:
 //   A_ts  = beta_t (Gamma_t/Gamma_s) k_t.k_s  (s < t),  T = (I + A)^{-1}
-//   W     = T diag(beta Gamma) K,  U = T diag(beta) V,   Delta = U - W S0
+//   Delta = T R,  R = diag(beta) (V - diag(Gamma) K S0)
 //   O     = diag(Gamma) Q S0 + (M o Q K^T) Delta,        M_ts = Gamma_t/Gamma_s (s <= t)
 //   S_C   = Gamma_C S0 + (diag(Gamma_C/Gamma) K)^T Delta
 // (q, k L2-normalised and q scaled: the norms multiply into the products).
@@ -2024,12 +2024,14 @@ constexpr int OFF_KT = OFF_KC + PC * P136 * 2;  // bf16 [128 d][72]   k columns 
 constexpr int OFF_VT = OFF_KT + PKD * P72 * 2;  // bf16 [64 j][72]    v columns of this half
 constexpr int OFF_AT = OFF_VT + PVS * P72 * 2;  // f32  [64][68]      A, then T = (I + A)^{-1}
 constexpr int OFF_P = OFF_AT + PC * PA * 4;     // bf16 2 x [64 t][72] masked, scaled Q K^T (hi, lo)
-constexpr int OFF_WD = OFF_P + 2 * PC * P72 * 2;  // W hi/lo [64 t][136], later Delta, Delta' hi/lo [64 j][72]
+constexpr int OFF_WD = OFF_P + 2 * PC * P72 * 2;  // R^T hi/lo [64 j][72], later Delta^T, Delta'^T hi/lo
 constexpr int WD_BYTES = 4 * PVS * P72 * 2;
 constexpr int OFF_ST = OFF_WD + WD_BYTES;         // bf16 2 x [64 j][136] S transposed (hi, lo)
 constexpr int OFF_SM = OFF_ST + 2 * PVS * P136 * 2;  // f32 [8][64] per-token scalars
 constexpr int OFF_R = OFF_SM + 8 * 64 * 4;        // f32 4 x [16][16] block products
-constexpr int LDS_BYTES = OFF_R + 4 * 256 * 4;
+constexpr int OFF_CK = OFF_R + 4 * 256 * 4;      // int [MAX_CK] this sequence's checkpoints
+constexpr int MAX_CK = 64;
+constexpr int LDS_BYTES = OFF_CK + MAX_CK * 4;
 enum { SM_LC = 0, SM_BETA, SM_NK, SM_NQ, SM_GK, SM_QG, SM_KD, SM_KSQ };
 
 struct PrefillDev {
@@ -2082,6 +2084,28 @@ __device__ __forceinline__ float row16_sum(float x) {
   return x + fast::dpp<0x140>(x);  // row_mirror
 }
 
+__device__ __forceinline__ f32x4 mfma32(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Raw inputs of one chunk, fetched into registers one chunk ahead so the
+// global loads overlap the previous chunk's arithmetic.
+struct Fetch {
+  uint4 k[4], q[4], v[2];
+  float lg, bt;
+  int n;
+  int64_t tb;
+};
+
+// Workgroup barrier ordering LDS accesses only: the prefetched global loads
+// of the next chunk stay in flight across it (a full __syncthreads would
+// wait for them).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __global__ __launch_bounds__(256) void prefill_kernel(PrefillDev D) {
 #pragma clang fp contract(off)
   extern __shared__ __align__(16) uint8_t smem[];
@@ -2123,29 +2147,66 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillDev D) {
         *(uint2 *)(St + PVS * P136 * 2 + off) = lo;
       }
   };
-  store_st();
-
-  int ci = 0;  // next checkpoint index
-  for (int c0 = 0; c0 < len;) {
-    // segment end: the next checkpoint past c0 or the sequence end, at most one chunk
+  // this sequence's checkpoints, once, in LDS
+  int *ck = (int *)(smem + OFF_CK);
+  if (tid < D.NC) ck[tid] = D.ckpt[(int64_t)b * D.NC + tid];
+  lds_barrier();
+  // tokens of the segment starting at c: up to the next checkpoint past c,
+  // the sequence end, or one chunk
+  auto segment = [&](int c) {
     int stop = len;
-    for (int c = ci; c < D.NC; c++) {
-      const int p = D.ckpt[(int64_t)b * D.NC + c];
-      if (p > c0 && p <= len) {
+    for (int i = 0; i < D.NC; i++) {
+      const int p = ck[i];
+      if (p > c && p <= len) {
         stop = p < stop ? p : stop;
         break;
       }
     }
-    const int n = stop - c0 < PC ? stop - c0 : PC;
-    const int64_t tb = (int64_t)t0 + c0;
-
-    // ---- loads: k rows (and transposed), q rows of this wave's tile, v columns, gates
+    return stop - c < PC ? stop - c : PC;
+  };
+  auto fetch = [&](Fetch &F, int c) {
+    F.n = c < len ? segment(c) : 0;
+    F.tb = (int64_t)t0 + c;
+#pragma unroll
     for (int it = 0; it < 4; it++) {
       const int idx = tid + 256 * it, t = idx >> 4, d8 = (idx & 15) * 8;
-      uint4 kv = make_uint4(0u, 0u, 0u, 0u);
-      if (t < n) kv = *(const uint4 *)(kg + (tb + t) * D.k_stride + hk * PKD + d8);
-      *(uint4 *)(Kc + (t * P136 + d8) * 2) = kv;
-      const uint16_t *ke = (const uint16_t *)&kv;
+      F.k[it] = t < F.n ? *(const uint4 *)(kg + (F.tb + t) * D.k_stride + hk * PKD + d8) : make_uint4(0u, 0u, 0u, 0u);
+    }
+    {
+      const int t = 16 * w + c16;
+#pragma unroll
+      for (int ks = 0; ks < 4; ks++)
+        F.q[ks] = t < F.n ? *(const uint4 *)(qg + (F.tb + t) * D.q_stride + hk * PKD + 8 * q4 + 32 * ks)
+                          : make_uint4(0u, 0u, 0u, 0u);
+    }
+#pragma unroll
+    for (int it = 0; it < 2; it++) {
+      const int idx = tid + 256 * it, t = idx >> 3, j8 = (idx & 7) * 8;
+      F.v[it] = t < F.n ? *(const uint4 *)(vg + (F.tb + t) * D.v_stride + h * 128 + vs * PVS + j8)
+                        : make_uint4(0u, 0u, 0u, 0u);
+    }
+    F.lg = 0.f;
+    F.bt = 0.f;
+    if (w == 0 && l < F.n) {
+      F.lg = load_val(D.g, D.gate_dtype, (F.tb + l) * H + h);
+      F.bt = load_val(D.beta, D.gate_dtype, (F.tb + l) * H + h);
+    }
+  };
+
+  store_st();
+  Fetch F;
+  fetch(F, 0);
+  int ci = 0;  // next checkpoint index
+  for (int c0 = 0; c0 < len;) {
+    const int n = F.n;
+    const int64_t tb = F.tb;
+
+    // ---- stage the fetched chunk: k rows and columns, v columns, norms, decays
+#pragma unroll
+    for (int it = 0; it < 4; it++) {
+      const int idx = tid + 256 * it, t = idx >> 4, d8 = (idx & 15) * 8;
+      *(uint4 *)(Kc + (t * P136 + d8) * 2) = F.k[it];
+      const uint16_t *ke = (const uint16_t *)&F.k[it];
       float ss = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; e++) {
@@ -2162,9 +2223,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillDev D) {
       float ss = 0.f;
 #pragma unroll
       for (int ks = 0; ks < 4; ks++) {
-        uint4 u = make_uint4(0u, 0u, 0u, 0u);
-        if (t < n) u = *(const uint4 *)(qg + (tb + t) * D.q_stride + hk * PKD + 8 * q4 + 32 * ks);
-        qa[ks] = __builtin_bit_cast(bf16x8, u);
+        qa[ks] = __builtin_bit_cast(bf16x8, F.q[ks]);
 #pragma unroll
         for (int e = 0; e < 8; e++) {
           const float f = bf2f(qa[ks][e]);
@@ -2177,25 +2236,20 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillDev D) {
       ss = __uint_as_float(s16[0]) + __uint_as_float(s16[1]);
       if (q4 == 0) sm[SM_NQ * 64 + t] = (D.normalize ? 1.0f / __builtin_sqrtf(ss + 1e-6f) : 1.0f) * D.scale;
     }
+#pragma unroll
     for (int it = 0; it < 2; it++) {
       const int idx = tid + 256 * it, t = idx >> 3, j8 = (idx & 7) * 8;
-      uint4 vv = make_uint4(0u, 0u, 0u, 0u);
-      if (t < n) vv = *(const uint4 *)(vg + (tb + t) * D.v_stride + h * 128 + vs * PVS + j8);
-      const uint16_t *ve = (const uint16_t *)&vv;
+      const uint16_t *ve = (const uint16_t *)&F.v[it];
 #pragma unroll
       for (int e = 0; e < 8; e++) *(uint16_t *)(Vt + ((j8 + e) * P72 + t) * 2) = ve[e];
     }
     if (w == 0) {
-      float lg = 0.f, bt = 0.f;
-      if (l < n) {
-        lg = load_val(D.g, D.gate_dtype, (tb + l) * H + h);
-        bt = load_val(D.beta, D.gate_dtype, (tb + l) * H + h);
-        if (D.a_log) {
-          const float u = lg + load_val(D.dt_bias, D.gate_dtype, h);
-          const float sp = u > 20.0f ? u : __logf(1.0f + __expf(u < 20.0f ? u : 20.0f));
-          lg = -__expf(load_val(D.a_log, D.gate_dtype, h)) * sp;
-          bt = 1.0f / (1.0f + __expf(-bt));
-        }
+      float lg = F.lg, bt = F.bt;
+      if (D.a_log && l < n) {
+        const float u = lg + load_val(D.dt_bias, D.gate_dtype, h);
+        const float sp = u > 20.0f ? u : __logf(1.0f + __expf(u < 20.0f ? u : 20.0f));
+        lg = -__expf(load_val(D.a_log, D.gate_dtype, h)) * sp;
+        bt = 1.0f / (1.0f + __expf(-bt));
       }
       // inclusive prefix sum of the log decays over the 64 tokens
 #pragma unroll
@@ -2206,24 +2260,28 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillDev D) {
       sm[SM_LC * 64 + l] = lg;
       sm[SM_BETA * 64 + l] = bt;
     }
-    __syncthreads();
+    // the next segment's inputs are in flight while this one is computed
+    const int c_next = c0 + n;
+    fetch(F, c_next);
+    lds_barrier();
     if (tid < 64) {
       const int t = tid;
       const float nk = D.normalize ? 1.0f / __builtin_sqrtf(sm[SM_KSQ * 64 + t] + 1e-6f) : 1.0f;
       const float lc = sm[SM_LC * 64 + t], lcC = sm[SM_LC * 64 + 63];
       const float gam = __expf(lc);
       sm[SM_NK * 64 + t] = nk;
-      sm[SM_GK * 64 + t] = (sm[SM_BETA * 64 + t] * gam) * nk;
+      sm[SM_GK * 64 + t] = gam * nk;  // Gamma_t nk_t
       sm[SM_QG * 64 + t] = sm[SM_NQ * 64 + t] * gam;
       sm[SM_KD * 64 + t] = nk * __expf(lcC - lc);
     }
-    __syncthreads();
+    lds_barrier();
 
-    // ---- K K^T and K Q^T tiles: rows s (tile ns), columns t (this wave's tile)
-    {
-      bf16x8 bk[4];
+    // ---- K K^T and K Q^T tiles (rows s of tile ns, columns t of this wave's tile);
+    // A_ts = beta_t nk_t nk_s (Gamma_t/Gamma_s) k_t.k_s (s < t), P_ts likewise with q (s <= t)
+    bf16x8 bk[4];
 #pragma unroll
-      for (int ks = 0; ks < 4; ks++) bk[ks] = ld8(Kc, ((16 * w + c16) * P136 + 8 * q4 + 32 * ks) * 2);
+    for (int ks = 0; ks < 4; ks++) bk[ks] = ld8(Kc, ((16 * w + c16) * P136 + 8 * q4 + 32 * ks) * 2);
+    {
       const int t = 16 * w + c16;
       const float lct = sm[SM_LC * 64 + t], bnt = sm[SM_BETA * 64 + t] * sm[SM_NK * 64 + t];
       const float nqt = sm[SM_NQ * 64 + t];
@@ -2255,7 +2313,20 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillDev D) {
         *(uint2 *)(Pl + PC * P72 * 2 + (t * P72 + s0) * 2) = lo;
       }
     }
-    __syncthreads();
+    // ---- K S0 for this wave's rows t (exact k times hi/lo S), overlapping the inverse
+    f32x4 ksv[4];
+#pragma unroll
+    for (int nj = 0; nj < 4; nj++) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ks++) {
+        const int bo = ((16 * nj + c16) * P136 + 8 * q4 + 32 * ks) * 2;
+        acc = mfma(bk[ks], ld8(St, bo), acc);
+        acc = mfma(bk[ks], ld8(St, PVS * P136 * 2 + bo), acc);
+      }
+      ksv[nj] = acc;
+    }
+    lds_barrier();
 
     // ---- T = (I + A)^{-1}: diagonal 16x16 blocks by forward substitution
     if (l < 16) {
@@ -2272,119 +2343,81 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillDev D) {
 #pragma unroll
       for (int r = 0; r < 16; r++) AT[(16 * w + r) * PA + 16 * w + l] = x[r];
     }
-    __syncthreads();
-    // off-diagonal blocks, one block row at a time: T_iw = -T_ii sum_{k=w}^{i-1} A_ik T_kw
+    // ---- R = beta (V - Gamma nk K S0) for rows t of this wave's tile, stored transposed (hi/lo)
+    {
+      const int tt = 16 * w + 4 * q4;
+      const float4 be = *(const float4 *)(sm + SM_BETA * 64 + tt), gk = *(const float4 *)(sm + SM_GK * 64 + tt);
+      const float be4[4] = {be.x, be.y, be.z, be.w}, gk4[4] = {gk.x, gk.y, gk.z, gk.w};
+#pragma unroll
+      for (int nj = 0; nj < 4; nj++) {
+        const int j = 16 * nj + c16;
+        const uint2 vr = *(const uint2 *)(Vt + (j * P72 + tt) * 2);
+        const float v4[4] = {__uint_as_float(vr.x << 16), __uint_as_float(vr.x & 0xffff0000u),
+                             __uint_as_float(vr.y << 16), __uint_as_float(vr.y & 0xffff0000u)};
+        float rv[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) rv[r] = be4[r] * (v4[r] - gk4[r] * ksv[nj][r]);
+        uint2 hi, lo;
+        split4(rv, hi, lo);
+        *(uint2 *)(WD + (j * P72 + tt) * 2) = hi;
+        *(uint2 *)(WD + PVS * P72 * 2 + (j * P72 + tt) * 2) = lo;
+      }
+    }
+    lds_barrier();
+    // off-diagonal blocks, one block row at a time (fp32 MFMA):
+    // T_iw = -T_ii sum_{k=w}^{i-1} A_ik T_kw
     for (int i = 1; i < 4; i++) {
-      const int r = l >> 2, c4 = 4 * (l & 3);
+      f32x4 racc = {0.f, 0.f, 0.f, 0.f};
       if (w < i) {
-        float acc[4] = {0.f, 0.f, 0.f, 0.f};
         for (int kb = w; kb < i; kb++) {
 #pragma unroll
-          for (int m = 0; m < 16; m++) {
-            const float a = AT[(16 * i + r) * PA + 16 * kb + m];
-            const float4 tv = *(const float4 *)(AT + (16 * kb + m) * PA + 16 * w + c4);
-            acc[0] = fmaf(a, tv.x, acc[0]);
-            acc[1] = fmaf(a, tv.y, acc[1]);
-            acc[2] = fmaf(a, tv.z, acc[2]);
-            acc[3] = fmaf(a, tv.w, acc[3]);
-          }
+          for (int kk = 0; kk < 4; kk++)
+            racc = mfma32(AT[(16 * i + c16) * PA + 16 * kb + 4 * kk + q4],
+                          AT[(16 * kb + 4 * kk + q4) * PA + 16 * w + c16], racc);
         }
-        *(float4 *)(Rs + r * 16 + c4) = make_float4(acc[0], acc[1], acc[2], acc[3]);
-      }
-      __syncthreads();
-      if (w < i) {
-        float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int m = 0; m < 16; m++) {
-          const float a = AT[(16 * i + r) * PA + 16 * i + m];
-          const float4 rv = *(const float4 *)(Rs + m * 16 + c4);
-          acc[0] = fmaf(-a, rv.x, acc[0]);
-          acc[1] = fmaf(-a, rv.y, acc[1]);
-          acc[2] = fmaf(-a, rv.z, acc[2]);
-          acc[3] = fmaf(-a, rv.w, acc[3]);
-        }
-        *(float4 *)(AT + (16 * i + r) * PA + 16 * w + c4) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+        for (int r = 0; r < 4; r++) Rs[(4 * q4 + r) * 16 + c16] = racc[r];
       }
-      __syncthreads();
+      lds_barrier();
+      if (w < i) {
+        f32x4 tacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++)
+          tacc = mfma32(-AT[(16 * i + c16) * PA + 16 * i + 4 * kk + q4], Rs[(4 * kk + q4) * 16 + c16], tacc);
+#pragma unroll
+        for (int r = 0; r < 4; r++) AT[(16 * i + 4 * q4 + r) * PA + 16 * w + c16] = tacc[r];
+      }
+      lds_barrier();
     }
 
-    // ---- W^T = K^T (T diag(beta Gamma nk))^T and U = T diag(beta) V (rows t of this wave's tile)
-    f32x4 U[4];
+    // ---- Delta = T R (rows t of this wave's tile, columns j)
+    float dl[4][4];
     {
       const int t = 16 * w + c16;
-      bf16x8 bh[2], bl[2], ah[2], al[2];
+      bf16x8 th[2], tl[2];
 #pragma unroll
       for (int ks = 0; ks < 2; ks++) {
         const int s0 = 8 * q4 + 32 * ks;
-        const float4 t0v = *(const float4 *)(AT + t * PA + s0), t1v = *(const float4 *)(AT + t * PA + s0 + 4);
-        const float4 g0 = *(const float4 *)(sm + SM_GK * 64 + s0), g1 = *(const float4 *)(sm + SM_GK * 64 + s0 + 4);
-        const float4 b0 = *(const float4 *)(sm + SM_BETA * 64 + s0), b1 = *(const float4 *)(sm + SM_BETA * 64 + s0 + 4);
-        const float tr[8] = {t0v.x, t0v.y, t0v.z, t0v.w, t1v.x, t1v.y, t1v.z, t1v.w};
-        const float gk[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
-        const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-        float xw[8], xu[8];
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-          xw[e] = tr[e] * gk[e];
-          xu[e] = tr[e] * bb[e];
-        }
-        split8(xw, bh[ks], bl[ks]);
-        split8(xu, ah[ks], al[ks]);
-      }
-#pragma unroll
-      for (int nd = 0; nd < 8; nd++) {
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < 2; ks++) {
-          const bf16x8 a = ld8(Kt, ((16 * nd + c16) * P72 + 8 * q4 + 32 * ks) * 2);
-          acc = mfma(a, bh[ks], acc);
-          acc = mfma(a, bl[ks], acc);
-        }
-        const float wv[4] = {acc[0], acc[1], acc[2], acc[3]};
-        uint2 hi, lo;
-        split4(wv, hi, lo);
-        const int off = (t * P136 + 16 * nd + 4 * q4) * 2;
-        *(uint2 *)(WD + off) = hi;
-        *(uint2 *)(WD + PC * P136 * 2 + off) = lo;
+        const float4 a0 = *(const float4 *)(AT + t * PA + s0), a1 = *(const float4 *)(AT + t * PA + s0 + 4);
+        const float tr[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+        split8(tr, th[ks], tl[ks]);
       }
 #pragma unroll
       for (int nj = 0; nj < 4; nj++) {
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < 2; ks++) {
-          const bf16x8 bv = ld8(Vt, ((16 * nj + c16) * P72 + 8 * q4 + 32 * ks) * 2);
-          acc = mfma(ah[ks], bv, acc);
-          acc = mfma(al[ks], bv, acc);
+          const int bo = ((16 * nj + c16) * P72 + 8 * q4 + 32 * ks) * 2;
+          const bf16x8 rh = ld8(WD, bo), rl = ld8(WD, PVS * P72 * 2 + bo);
+          acc = mfma(th[ks], rh, acc);
+          acc = mfma(th[ks], rl, acc);
+          acc = mfma(tl[ks], rh, acc);
         }
-        U[nj] = acc;
+#pragma unroll
+        for (int r = 0; r < 4; r++) dl[nj][r] = acc[r];
       }
     }
-    __syncthreads();
-    // ---- Delta = U - W S0 (rows t of this wave's tile, columns j)
-    float dl[4][4];
-    {
-      f32x4 acc[4];
-#pragma unroll
-      for (int nj = 0; nj < 4; nj++) acc[nj] = (f32x4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < 4; ks++) {
-        const int ao = ((16 * w + c16) * P136 + 8 * q4 + 32 * ks) * 2;
-        const bf16x8 awh = ld8(WD, ao), awl = ld8(WD, PC * P136 * 2 + ao);
-#pragma unroll
-        for (int nj = 0; nj < 4; nj++) {
-          const int bo = ((16 * nj + c16) * P136 + 8 * q4 + 32 * ks) * 2;
-          const bf16x8 bsh = ld8(St, bo), bsl = ld8(St, PVS * P136 * 2 + bo);
-          acc[nj] = mfma(awh, bsh, acc[nj]);
-          acc[nj] = mfma(awh, bsl, acc[nj]);
-          acc[nj] = mfma(awl, bsh, acc[nj]);
-        }
-      }
-#pragma unroll
-      for (int nj = 0; nj < 4; nj++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) dl[nj][r] = U[nj][r] - acc[nj][r];
-    }
-    __syncthreads();  // W is dead: Delta and Delta' take its place
+    lds_barrier();  // R is dead: Delta and Delta' take its place
     {
       const int tt = 16 * w + 4 * q4;
       const float4 kd = *(const float4 *)(sm + SM_KD * 64 + tt);
@@ -2404,7 +2437,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillDev D) {
         *(uint2 *)(WD + 3 * PVS * P72 * 2 + off) = lo;
       }
     }
-    __syncthreads();
+    lds_barrier();
 
     // ---- O^T = diag(nq Gamma) (S0^T Q^T) + Delta^T P^T: rows j, column t of this wave's tile
     {
@@ -2466,12 +2499,12 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillDev D) {
         }
       }
     }
-    __syncthreads();
+    lds_barrier();
     store_st();
-    c0 += n;
+    c0 = c_next;
     // checkpoints reached at c0
     for (; ci < D.NC; ci++) {
-      const int p = D.ckpt[(int64_t)b * D.NC + ci];
+      const int p = ck[ci];
       if (p > c0 && p <= len) break;
       if (p == c0) {
         float *dst = D.ck_state + (((int64_t)b * D.NC + ci) * H + h) * PKD * 128 + vs * PVS;
@@ -2488,6 +2521,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillDev D) {
 }
 
 }  // namespace pf
+
 
 __global__ void fill_zero_kernel(float *p, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) p[i] = 0.0f;
@@ -2820,6 +2854,7 @@ int sq_prefill(const sq_pool *pool, const sq_prefill_args *a, void *stream) {
     return fail(SQ_EINVAL, "prefill: null input, output, sequence offsets or initial-state workspace");
   if (a->n_checkpoints > 0 && (!a->checkpoints || !a->slots || !a->checkpoint_state))
     return fail(SQ_EINVAL, "prefill: checkpoints need positions, slots and a state workspace");
+  if (a->n_checkpoints > pf::MAX_CK) return fail(SQ_EINVAL, "prefill: at most 64 checkpoints per sequence");
   if (a->qkv_dtype != SQ_BF16) return fail(SQ_EINVAL, "prefill: q, k, v must be bf16 (the MFMA operand type)");
   if (a->gate_dtype != SQ_F32 && a->gate_dtype != SQ_BF16 && a->gate_dtype != SQ_F16)
     return fail(SQ_EINVAL, "prefill: gate dtype");
