@@ -283,6 +283,7 @@ struct PoolDev {
   int stage;   // bytes of LDS staging per workgroup (largest head window)
   int rstage;  // bytes of LDS for one head's row scales (fast path)
   int fast;    // SQ_POOL_FAST_* bits: which K=V=128 kernel the pool qualifies for
+  int storage; // 0: packed codes; 1: int8 carriers, plane value (i, j) at base + i + j*K
 };
 
 __device__ __forceinline__ int tile_of(const PoolDev &P) { return P.kda ? (P.V < 4 ? P.V : 4) : (P.V < 16 ? P.V : 16); }
@@ -292,6 +293,17 @@ __device__ __forceinline__ int tile_of(const PoolDev &P) { return P.kda ? (P.V <
 __device__ __forceinline__ int group_pos(int off_rel, int stride, int tile, int j0, int width) {
   return off_rel + (j0 / tile) * stride + ((j0 % tile) * width) / 8;
 }
+
+// Byte position of FP16 pivot value j of a row: tiled with the codes in
+// packed pages, a contiguous row of V halves in byte pages (pool.py:33-40).
+__device__ __forceinline__ int pivot_pos(const PoolDev &P, int off_rel, int stride, int tile, int j) {
+  return P.storage ? off_rel + 2 * j : group_pos(off_rel, stride, tile, j, 16);
+}
+
+// int8 carrier of value (i, j) in a byte page: the head's plane starts at
+// offsets[H*K + h] (relative: plane_rel) and holds value (i, j) at i + j*K;
+// the carrier is z (KDA: z * 2^(8 - b), so that x = r c carrier).
+__device__ __forceinline__ int carrier_pos(int plane_rel, int K, int i, int j) { return plane_rel + i + j * K; }
 
 // =====================================================================
 // Encode: dense fp32 -> page, bit-exact fit_state.  Thread j owns column j
@@ -335,7 +347,7 @@ __global__ __launch_bounds__(256) void encode_kernel(PoolDev P, const float *__r
     if (bi == 16) {
       const int off_rel = P.offsets[(int64_t)h * K + i] - code_start;
       for (int j = 0; j < V; j++) {
-        int p = shift + group_pos(off_rel, stride, tile, j, 16);
+        int p = shift + pivot_pos(P, off_rel, stride, tile, j);
         uint32_t hb = f2h(xr[j]);
         stage[p] = (uint8_t)hb;
         stage[p + 1] = (uint8_t)(hb >> 8);
@@ -436,7 +448,17 @@ __global__ __launch_bounds__(256) void encode_kernel(PoolDev P, const float *__r
       if (bi != 16) {
         int bc = bi < 8 ? bi : 8;
         float z = z_of(i, c);
+        if (P.storage) {
+          // int8 carrier at plane value (i, j)
+          if (act) {
+            const int carrier = P.kda ? (int)z * (1 << (8 - bc)) : (int)z;
+            stage[shift + carrier_pos(stride - code_start, K, i, j)] = (uint8_t)(int8_t)carrier;
+          }
+          continue;
+        }
         code = two ? (uint32_t)(((int)z + 3) / 2) : (uint32_t)((int)z + ((1 << (bc - 1)) - 1));
+      } else if (P.storage) {
+        continue;
       }
       const int lane = tid & 3;
       uint32_t c1 = __shfl_xor(code, 1);
@@ -600,7 +622,7 @@ __global__ __launch_bounds__(512) void step_kernel(PoolDev P, StepDev S) {
     const int bi = hbits[i];
     const int off_rel = P.offsets[(int64_t)h * K + i] - code_start;
     if (bi == 16) {
-      const int p = shift + group_pos(off_rel, stride, tile, j0, 16);
+      const int p = shift + pivot_pos(P, off_rel, stride, tile, j0);
       uint32_t w0 = lds_word(stage, p), w1 = lds_word(stage, p + 4);
       float d = (MODE == MODE_DECODE) ? 1.0f : dv[i];
       x[r][0] = h2f(w0 & 0xffffu) * d;
@@ -608,8 +630,8 @@ __global__ __launch_bounds__(512) void step_kernel(PoolDev P, StepDev S) {
       x[r][2] = h2f(w1 & 0xffffu) * d;
       x[r][3] = h2f(w1 >> 16) * d;
     } else {
-      const int p = shift + group_pos(off_rel, stride, tile, j0, bi);
-      const uint32_t word = lds_word(stage, p);
+      const int p = shift + (P.storage ? carrier_pos(stride - code_start, K, i, j0) : group_pos(off_rel, stride, tile, j0, bi));
+      const uint32_t word = P.storage ? 0u : lds_word(stage, p);
       const int bc = bi < 8 ? bi : 8;
       const int L = (1 << (bc - 1)) - 1;
       const float norm = P.kda ? (float)(1 << (8 - bc)) : 1.0f;
@@ -618,7 +640,8 @@ __global__ __launch_bounds__(512) void step_kernel(PoolDev P, StepDev S) {
 #pragma unroll
       for (int c = 0; c < 4; c++) {
         uint32_t code = (word >> (c * bi)) & ((1u << bi) - 1u);
-        float z = two ? 2.0f * (float)code - 3.0f : (float)((int)code - L) * norm;
+        float z = P.storage ? (float)(int8_t)stage[p + c * K]
+                            : (two ? 2.0f * (float)code - 3.0f : (float)((int)code - L) * norm);
         if (MODE == MODE_DECODE) x[r][c] = (rr * cj[c]) * z;
         else x[r][c] = ((rr * dv[i]) * cj[c]) * z;
       }
@@ -689,7 +712,7 @@ __global__ __launch_bounds__(512) void step_kernel(PoolDev P, StepDev S) {
     const int i = rg + RG * r;
     if (hbits[i] == 16 && act) {
       const int off_rel = P.offsets[(int64_t)h * K + i] - code_start;
-      const int p = shift + group_pos(off_rel, stride, tile, j0, 16);
+      const int p = shift + pivot_pos(P, off_rel, stride, tile, j0);
       uint16_t *d16 = (uint16_t *)(stage + p);
 #pragma unroll
       for (int c = 0; c < 4; c++) d16[c] = (uint16_t)f2h(x[r][c]);
@@ -796,16 +819,22 @@ __global__ __launch_bounds__(512) void step_kernel(PoolDev P, StepDev S) {
       for (int c = 0; c < 4; c++) {
         float y = x[r][c] * icn[c];
         uint32_t code;
+        int carrier;
         if (two) {
           code = y >= 0.0f ? (fabsf(y) >= 2.0f ? 3u : 2u) : (fabsf(y) >= 2.0f ? 0u : 1u);
+          carrier = 2 * (int)code - 3;
         } else {
           float z = fminf(fmaxf(__builtin_rintf(y), -(float)L), (float)L);
           code = (uint32_t)((int)z + L);
+          carrier = P.kda ? (int)z * (1 << (8 - bc)) : (int)z;
         }
+        if (P.storage) stage[shift + carrier_pos(stride - code_start, K, i, j0 + c)] = (uint8_t)(int8_t)carrier;
         word |= code << (c * bi);
       }
-      const int off_rel = P.offsets[(int64_t)h * K + i] - code_start;
-      lds_put_bytes(stage, shift + group_pos(off_rel, stride, tile, j0, bi), word, bi / 2);
+      if (!P.storage) {
+        const int off_rel = P.offsets[(int64_t)h * K + i] - code_start;
+        lds_put_bytes(stage, shift + group_pos(off_rel, stride, tile, j0, bi), word, bi / 2);
+      }
     }
   }
   __syncthreads();
@@ -2582,7 +2611,7 @@ int validate_pool(const sq_pool *p) {
     return fail(SQ_ESHAPE, "pool: K*V above 16384 (K, V <= 256) is not supported");
   if (!p->kda && (p->group < 4 || p->values % p->group))
     return fail(SQ_ESHAPE, "pool: GDN value_group_size must divide V and be >= 4");
-  if (p->storage != 0) return fail(SQ_ESTORAGE, "pool: only packed storage is implemented");
+  if (p->storage != 0 && p->storage != 1) return fail(SQ_ESTORAGE, "pool: storage must be packed (0) or byte (1)");
   return 0;
 }
 
@@ -2605,6 +2634,7 @@ PoolDev to_dev(const sq_pool *p) {
   d.stage = (p->max_code_bytes + 47) & ~15;
   d.rstage = (p->max_row_bytes + 15) & ~15;
   d.fast = p->flags & (SQ_POOL_FAST_GDN128 | SQ_POOL_FAST_KDA128);
+  d.storage = p->storage;
   return d;
 }
 

@@ -86,15 +86,25 @@ def packed_layout(plan, value_dim, storage="packed"):
     return offsets, rows, columns, cursor
 
 
-def _head_meta(plan, value_dim, offsets, rows):
-    """Per head: code-region start/bytes and row-scale region start/bytes."""
+def _head_meta(plan, value_dim, offsets, rows, storage="packed"):
+    """Per head: code-region start/bytes and row-scale region start/bytes.
+
+    Packed pages: the head's tile blocks.  Byte pages: the head's int8 plane
+    (when it has integer rows) followed by its FP16 pivot rows.
+    """
     H, K = plan.bits.shape
     kda = plan.architecture == "kda"
     tile = min(4 if kda else 16, value_dim)
     meta = []
     for h in range(H):
-        start = offsets[h * K]
-        nbytes = offsets[H * K + h] * (value_dim // tile)
+        if storage == "byte":
+            widths = plan.bits[h].tolist()
+            n_pivot = sum(1 for w in widths if w == 16)
+            start = offsets[H * K + h]
+            nbytes = (K * value_dim if n_pivot < K else 0) + 2 * n_pivot * value_dim
+        else:
+            start = offsets[h * K]
+            nbytes = offsets[H * K + h] * (value_dim // tile)
         row_offs = [rows[h * K + i] for i in range(K) if rows[h * K + i] >= 0]
         if row_offs:
             rstart = min(row_offs)
@@ -125,8 +135,6 @@ class PackedStatePool:
             raise ValueError("state storage must be packed or byte")
         if storage == "byte" and writeback_stream is None:
             raise ValueError("byte storage requires a writeback stream")
-        if storage == "byte":
-            raise NotImplementedError("byte-carrier pages are not implemented by the MI355X kernels yet")
         self.storage = storage
         self.early_writeback = True
         self.plan = plan
@@ -143,7 +151,7 @@ class PackedStatePool:
         self.offsets = torch.tensor(offsets, device=dev, dtype=torch.int32)
         self.rows = torch.tensor(rows, device=dev, dtype=torch.int32)
         self.columns = torch.tensor(columns, device=dev, dtype=torch.int32)
-        meta = _head_meta(plan, value_dim, offsets, rows)
+        meta = _head_meta(plan, value_dim, offsets, rows, storage)
         self.head_meta = torch.tensor(meta, device=dev, dtype=torch.int32)
         # Kernels over-read up to 15 bytes past a head region with 16-byte loads.
         self._pages = torch.zeros(slots * cursor + 64, device=dev, dtype=torch.uint8)
@@ -171,10 +179,11 @@ class PackedStatePool:
             offsets=self.offsets.data_ptr(), rows=self.rows.data_ptr(), columns=self.columns.data_ptr(),
             impact=self.impact.data_ptr(), head_meta=self.head_meta.data_ptr(), heads=self.heads,
             keys=self.keys, values=value_dim, group=plan.value_group_size,
-            kda=int(plan.architecture == "kda"), storage=0,
+            kda=int(plan.architecture == "kda"), storage=int(storage == "byte"),
             max_code_bytes=max(meta[1::4]) if meta else 0, max_row_bytes=max(meta[3::4]) if meta else 0,
             flags=N.pool_flags(self.bits.cpu().reshape(-1).tolist(), meta, columns, self.heads, self.keys,
-                               value_dim, plan.value_group_size, int(plan.architecture == "kda"), 0, cursor),
+                               value_dim, plan.value_group_size, int(plan.architecture == "kda"),
+                               int(storage == "byte"), cursor),
             reserved=0)
         self._init_writeback(writeback_stream, writeback_chunk)
         self._init_workspace(slots, writeback_workspace)
