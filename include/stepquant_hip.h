@@ -230,12 +230,63 @@ int sq_prefill(const sq_pool *pool, const sq_prefill_args *args, void *stream);
  * sq_copy_slots copies pages src[i] -> dst[i] through `temp`
  * ([n, page_bytes] bytes) so overlapping index sets behave like the
  * reference's gather-then-scatter.  Negative indices wrap like Python;
- * indices outside the pool are skipped.
+ * indices outside the pool are skipped.  Only data, page_bytes and num_slots
+ * of `pool` are read, so format pools pass an sq_pool holding just those.
  */
 int sq_clear_slots(const sq_pool *pool, const void *slots, int32_t slots_dtype, int64_t n,
                    void *stream);
 int sq_copy_slots(const sq_pool *pool, const void *src, const void *dst, int32_t slots_dtype,
                   int64_t n, uint8_t *temp, void *stream);
+
+/*
+ * Baseline state formats: one layer's pool of FormatStatePool pages
+ * (reference kernels/format_pool.py:29-128; layout format_layout,
+ * format_pool.py:9-25).  Every row of the pool has the same code width.
+ *   kind      SQ_FMT_FP32 (fp32 state, bits = 32), SQ_FMT_SYMMETRIC (per row
+ *             and 128-value group: fp16 scale and zero point, bits 4/6/8) or
+ *             SQ_FMT_DSQ (fp16 row and column scales, bits 4/6/8)
+ *   offsets   [H*K] byte offset of each row's codes (fp32 values)
+ *   rows      [H*K] byte offset of each row's fp16 metadata (unused for FP32)
+ *   columns   [H]   byte offset of each head's column metadata (DSQ)
+ * K is a power of two <= 128; V a power of two >= 4 (SYMMETRIC: a multiple
+ * of 128; DSQ: <= 128).
+ */
+enum {
+    SQ_FMT_FP32 = 0,
+    SQ_FMT_SYMMETRIC = 1,
+    SQ_FMT_DSQ = 2
+};
+
+typedef struct sq_format_pool {
+    uint8_t *data;
+    int64_t page_bytes;
+    int64_t num_slots;
+    const int32_t *offsets;
+    const int32_t *rows;
+    const int32_t *columns;
+    int32_t heads;
+    int32_t keys;
+    int32_t values;
+    int32_t kind;       /* SQ_FMT_* */
+    int32_t bits;       /* code width (32 for SQ_FMT_FP32) */
+    int32_t group;      /* value group of SQ_FMT_SYMMETRIC (128) */
+    int32_t kda;        /* 1: per-key-row retention g [B, H*K] */
+    int32_t reserved;
+} sq_format_pool;
+
+/*
+ * Dense fp32 [B,H,K,V] -> pages (FormatStatePool.encode, format_pool.py:68-80);
+ * bit-identical to the CPU group_fit / dual_fit (formats.py:53-86) of the
+ * same input.  Pages -> dense fp32 (FormatStatePool.decode,
+ * format_pool.py:82-90).  One fused decode step: read, gated delta update,
+ * readout, re-encode (FormatStatePool.step, format_pool.py:92-113).  The
+ * step's arguments are those of sq_decode_step.
+ */
+int sq_format_encode(const sq_format_pool *pool, const float *state, const void *slots,
+                     int32_t slots_dtype, int64_t batch, void *stream);
+int sq_format_decode(const sq_format_pool *pool, const void *slots, int32_t slots_dtype,
+                     int64_t batch, float *state, void *stream);
+int sq_format_step(const sq_format_pool *pool, const sq_step_args *args, void *stream);
 
 /*
  * Flags for sq_pool.flags, computed from host copies of bits [H*K],

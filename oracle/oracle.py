@@ -22,6 +22,10 @@ the reference repository):
                       sglang/runtime.py:193-202 (``kernel_extend``)
 * ``pack``/``unpack`` stepquant/packing.py:6-22
 * ``codec_encode``/``codec_decode``  stepquant/quantization.py:101-152 (``StateCodec``)
+* ``format_layout``   stepquant/kernels/format_pool.py:9-25
+* ``group_fit``/``dual_fit``  stepquant/formats.py:53-86 (baseline formats)
+* ``format_encode_page``/``format_decode_page``  kernels/format_pool.py:68-90
+                      with the page stores and reads of kernels/formats.py
 
 Parity status: layout, fit_state, encode_page, decode_page, pack/unpack and
 codec_encode are pinned by golden vectors written from the reference
@@ -32,6 +36,11 @@ by delta_step on single tokens and by the closed-form chunked (WY) form of
 the same recurrence (tests/test_oracle_prefill.py).  The reference's own
 chunked kernel lives in sglang==0.5.12 (not vendored, not installed here), so
 its exact output is parity unpinned; the sequential recurrence is the oracle.
+The baseline formats are pinned without the reference's code: group_fit by
+brute force (every code is the nearest level of its group's grid, ties to
+even) and closed forms; dual_fit through the same PyTorch-order row mean
+that the fit_state golden vectors pin, plus brute force on its column step;
+format_layout by closed-form region sizes (tests/test_oracle_formats.py).
 """
 from __future__ import annotations
 
@@ -291,6 +300,152 @@ def codec_encode(x, plan: Plan):
     pivots = x.reshape(B, H * K, V)[:, flat_bits == 16].astype(np.float16)
     return dict(codes=streams, rows=r.reshape(B, -1)[:, integer_rows],
                 columns=c[:, integer_heads], pivots=pivots, two_bit_rows=r2, shape=x.shape)
+
+
+# ------------------------------------------------------ baseline formats
+
+def format_spec(name):
+    """formats.py:30-44 (get_format) for the baseline names: (kind, bits, group)."""
+    import re
+    if name == "fp32":
+        return "fp32", 32, 32
+    m = re.fullmatch(r"sym_int([468])_g128", name)
+    if m:
+        return "symmetric", int(m[1]), 128
+    m = re.fullmatch(r"dsq_int([46])", name)
+    if m:
+        return "dsq", int(m[1]), 128
+    raise ValueError(f"unknown state format: {name}")
+
+
+def format_layout(bits, value_dim, kind, group=128) -> Layout:
+    """kernels/format_pool.py:9-25: row code offsets (FP16 rows at even
+    bytes), then per-row metadata (symmetric: fp16 scale + fp16 zero point per
+    value group; dsq: one fp16 row scale), then per-head dsq column metadata
+    (fp16 scale + fp16 zero per column), each region 4-byte aligned."""
+    flat = [int(b) for b in np.asarray(bits).reshape(-1)]
+    H = np.asarray(bits).shape[0]
+    offsets, rows, columns = [], [], []
+    cursor = 0
+    for b in flat:
+        if b == 16:
+            cursor += cursor & 1
+        offsets.append(cursor)
+        cursor += value_dim * b // 8
+    cursor = -(-cursor // 4) * 4
+    for b in flat:
+        meta = b != 16 and kind != "fp32"
+        rows.append(cursor if meta else -1)
+        if meta:
+            cursor += 2 if kind == "dsq" else value_dim // group * 4
+    cursor = -(-cursor // 4) * 4
+    for _ in range(H):
+        columns.append(cursor)
+        cursor += value_dim * 4 if kind == "dsq" else 0
+    return Layout(np.array(offsets, np.int32), np.array(rows, np.int32), np.array(columns, np.int32), cursor)
+
+
+def _half_scale(x):
+    """formats.py:47-48: clamp(2^-24, 65504) -> fp16 (round to nearest even) -> fp32."""
+    return np.clip(np.asarray(x, np.float32), np.float32(2.0 ** -24), np.float32(65504)).astype(
+        np.float16).astype(np.float32)
+
+
+def group_fit(x, bits, group=128):
+    """formats.py:53-70 (symmetric kind): codes, scale s, zero point z, reconstruction."""
+    x = _c(x, np.float32)
+    y = x.reshape(x.shape[:-1] + (x.shape[-1] // group, group))
+    limit = np.float32(2 ** (bits - 1) - 1)
+    s = _half_scale(np.abs(y).max(-1, keepdims=True) / limit)
+    z = np.full_like(s, limit)
+    q = np.clip(np.round(y / s), -limit, limit) + z
+    return q.reshape(x.shape), s[..., 0], z[..., 0], ((q - z) * s).reshape(x.shape)
+
+
+def dual_fit(x, bits):
+    """formats.py:73-86 (dsq kind, uniform widths): codes, r, c, reconstruction.
+
+    r = fp16(sqrt(max(mean_j |x|, 1e-20))) with the mean in PyTorch's CPU
+    order (sum / V), y = x / r, c = fp16(max_i |y| / L), q = clamp(rint(y / c)),
+    reconstruction (r c) q."""
+    x = _c(x, np.float32)
+    B, H, K, V = x.shape
+    levels = np.float32(2 ** (min(bits, 8) - 1) - 1)
+    ax = np.abs(x)
+    mean = np.array([inner_sum(row) for row in ax.reshape(-1, V)], np.float32).reshape(B, H, K, 1) / np.float32(V)
+    r = _half_scale(np.sqrt(np.maximum(mean, np.float32(1e-20))))
+    y = x / r
+    c = _half_scale((np.abs(y) / levels).max(-2, keepdims=True))
+    q = np.minimum(np.maximum(np.round(y / c), -levels), levels)
+    return q + levels, r[..., 0], c[..., 0, :], (r * c) * q
+
+
+def _put_half(data, slot, pos, values):
+    v = np.asarray(values, np.float32).astype(np.float16).view(np.uint8).reshape(-1)
+    data[slot, pos:pos + v.size] = v
+
+
+def format_encode_page(x, slots, name, lay: Layout, data):
+    """FormatStatePool.encode (format_pool.py:68-80 with kernels/formats.py
+    store and kernels/bitpack.py store_words): x [B,H,K,V] into data[slots]."""
+    kind, bits, group = format_spec(name)
+    x = _c(x, np.float32)
+    B, H, K, V = x.shape
+    if kind == "symmetric":
+        codes, s, z, _ = group_fit(x, bits, group)
+    elif kind == "dsq":
+        codes, r, c, _ = dual_fit(x, bits)
+    for b, slot in enumerate(np.asarray(slots).reshape(-1)):
+        if slot <= 0:
+            continue
+        for h in range(H):
+            if kind == "dsq":
+                for j in range(V):
+                    _put_half(data, slot, lay.columns[h] + 4 * j, [c[b, h, j], 0.0])
+            for i in range(K):
+                off = lay.offsets[h * K + i]
+                if kind == "fp32":
+                    data[slot, off:off + 4 * V] = x[b, h, i].view(np.uint8)
+                    continue
+                row = pack(codes[b, h, i].astype(np.int64), bits)
+                data[slot, off:off + row.size] = row
+                if kind == "dsq":
+                    _put_half(data, slot, lay.rows[h * K + i], [r[b, h, i]])
+                else:
+                    for g in range(V // group):
+                        _put_half(data, slot, lay.rows[h * K + i] + 4 * g, [s[b, h, i, g], z[b, h, i, g]])
+    return data
+
+
+def format_decode_page(data, slots, name, lay: Layout, H, K, V):
+    """FormatStatePool.decode (kernels/formats.py read): (code - z) s for
+    symmetric pages, (r c)(code - L) for dsq pages; zeros for slot <= 0."""
+    kind, bits, group = format_spec(name)
+    slots = np.asarray(slots).reshape(-1)
+    out = np.zeros((slots.size, H, K, V), np.float32)
+    L = np.float32(2 ** (min(bits, 8) - 1) - 1)
+    half = lambda slot, pos: np.float32(data[slot, pos:pos + 2].view(np.float16)[0])
+    for b, slot in enumerate(slots):
+        if slot <= 0:
+            continue
+        for h in range(H):
+            cj = None
+            if kind == "dsq":
+                cj = np.array([half(slot, lay.columns[h] + 4 * j) for j in range(V)], np.float32)
+            for i in range(K):
+                off = lay.offsets[h * K + i]
+                if kind == "fp32":
+                    out[b, h, i] = data[slot, off:off + 4 * V].view(np.float32)
+                    continue
+                code = unpack(data[slot, off:off + V * bits // 8], bits, V).astype(np.float32)
+                if kind == "dsq":
+                    out[b, h, i] = (half(slot, lay.rows[h * K + i]) * cj) * (code - L)
+                else:
+                    for g in range(V // group):
+                        m = lay.rows[h * K + i] + 4 * g
+                        sl = slice(g * group, (g + 1) * group)
+                        out[b, h, i, sl] = (code[sl] - half(slot, m + 2)) * half(slot, m)
+    return out
 
 
 def _softplus20(u):

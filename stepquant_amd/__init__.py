@@ -13,7 +13,7 @@ from .quantization import QuantizationPlan
 __all__ = ["QuantizationPlan", "install_alias"]
 
 _ALIASED = ("quantization", "formats", "packing", "kernels", "kernels.pool", "kernels.writeback",
-            "kernels.resources", "kernels.profiles", "kernels.priority_graph")
+            "kernels.resources", "kernels.profiles", "kernels.priority_graph", "kernels.format_pool")
 
 
 def install_alias(name="stepquant"):

@@ -54,9 +54,20 @@ class PrefillArgs(ctypes.Structure):
                 ("normalize", ctypes.c_int32), ("scale", ctypes.c_float)]
 
 
+class FormatPool(ctypes.Structure):
+    _fields_ = [("data", _P), ("page_bytes", ctypes.c_int64), ("num_slots", ctypes.c_int64),
+                ("offsets", _P), ("rows", _P), ("columns", _P), ("heads", ctypes.c_int32),
+                ("keys", ctypes.c_int32), ("values", ctypes.c_int32), ("kind", ctypes.c_int32),
+                ("bits", ctypes.c_int32), ("group", ctypes.c_int32), ("kda", ctypes.c_int32),
+                ("reserved", ctypes.c_int32)]
+
+
+FMT_FP32, FMT_SYMMETRIC, FMT_DSQ = 0, 1, 2
+
 EXPORTS = ("sq_abi_version", "sq_last_error", "sq_encode", "sq_decode_dense", "sq_decode_step",
            "sq_decode_readout", "sq_writeback", "sq_clear_slots", "sq_copy_slots",
-           "sq_stream_capture_id", "sq_create_cu_stream", "sq_pool_flags", "sq_prefill")
+           "sq_stream_capture_id", "sq_create_cu_stream", "sq_pool_flags", "sq_prefill",
+           "sq_format_encode", "sq_format_decode", "sq_format_step")
 
 _lib = None
 
@@ -83,6 +94,9 @@ def lib():
     L.sq_decode_readout.argtypes = [PP(Pool), PP(StepArgs), PP(Scratch), _P]
     L.sq_writeback.argtypes = [PP(Pool), PP(Scratch), ctypes.c_int64, _P]
     L.sq_prefill.argtypes = [PP(Pool), PP(PrefillArgs), _P]
+    L.sq_format_encode.argtypes = [PP(FormatPool), _P, _P, ctypes.c_int32, ctypes.c_int64, _P]
+    L.sq_format_decode.argtypes = [PP(FormatPool), _P, ctypes.c_int32, ctypes.c_int64, _P, _P]
+    L.sq_format_step.argtypes = [PP(FormatPool), PP(StepArgs), _P]
     L.sq_clear_slots.argtypes = [PP(Pool), _P, ctypes.c_int32, ctypes.c_int64, _P]
     L.sq_copy_slots.argtypes = [PP(Pool), _P, _P, ctypes.c_int32, ctypes.c_int64, _P, _P]
     L.sq_pool_flags.argtypes = [_P, _P, _P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,

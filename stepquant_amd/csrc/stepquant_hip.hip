@@ -2581,6 +2581,312 @@ __global__ void gather_kernel(const uint8_t *data, int64_t page_bytes, int64_t n
   }
 }
 
+// =====================================================================
+// Baseline state formats (reference kernels/format_pool.py:29-128 with the
+// programs of kernels/formats.py and kernels/floating.py; CPU definitions
+// formats.py:53-86 group_fit / dual_fit):
+//   FP32       the page is the fp32 state: value (i, j) at offsets[hK+i] + 4j.
+//   SYMMETRIC  per (row, 128-value group g): fp16 s = fp16(max|x| / L) at
+//              rows[hK+i] + 4g and an fp16 zero point z = L two bytes after
+//              it; codes rint(x / s) clamped to [-L, L], plus L.
+//   DSQ        fp16 r_i = fp16(sqrt(max(mean_j |x_ij|, 1e-20))) at rows[hK+i];
+//              fp16 c_j = fp16(max_i |x_ij / r_i| / L) and a zero half at
+//              columns[h] + 4j; codes rint((x / r) / c) clamped, plus L.
+// L = 2^(b-1) - 1.  Codes of a row are a little-endian bit stream at
+// offsets[hK+i] (value j at bit j*b).  Decoding: (code - z) * s and
+// (r * c) * (code - L).  Every product, quotient and sum rounds separately
+// (IEEE division and square root), as in PyTorch's CPU ops; row means use
+// PyTorch's CPU summation order, so encoding is bit-identical to the CPU
+// definitions for the same fp32 input.
+// One workgroup per (request, head, tile of up to 128 value columns); lane
+// (rg, cg) owns rows rg + 8r and columns 4cg .. 4cg+3 of the tile.
+// =====================================================================
+enum { FMT_ENCODE = 0, FMT_DECODE = 1, FMT_STEP = 2 };
+constexpr int FMT_TV = 128, FMT_RPT = 16, FMT_SMALL_LDS = (3 * 128 + 16 + 128) * 4;
+
+struct FmtDev {
+  uint8_t *data;
+  int64_t page_bytes, num_slots;
+  const int32_t *offsets, *rows, *columns;
+  int H, K, V, kind, bits, kda;
+  const float *in;  // FMT_ENCODE: dense [B, H, K, V]
+  float *dense;     // FMT_DECODE: dense [B, H, K, V]
+  const void *slots;
+  int slots_dtype;
+};
+
+// the 4 codes of columns j0..j0+3 (j0 % 4 == 0) of a row: W/2 bytes
+__device__ __forceinline__ uint32_t fmt_read_codes(const uint8_t *row, int j0, int W) {
+  const uint8_t *p = row + (j0 * W) / 8;
+  uint32_t w = 0;
+  for (int t = 0; t < W / 2; t++) w |= (uint32_t)p[t] << (8 * t);
+  return w;
+}
+
+__device__ __forceinline__ void fmt_write_codes(uint8_t *row, int j0, int W, uint32_t w) {
+  uint8_t *p = row + (j0 * W) / 8;
+  for (int t = 0; t < W / 2; t++) p[t] = (uint8_t)(w >> (8 * t));
+}
+
+template <int MODE>
+__global__ __launch_bounds__(256) void format_kernel(FmtDev F, StepDev S) {
+#pragma clang fp contract(off)
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int H = F.H, K = F.K, V = F.V;
+  const int TV = V < FMT_TV ? V : FMT_TV;
+  const int b = blockIdx.x / H, h = blockIdx.x % H, tile = blockIdx.y;
+  const int tid = threadIdx.x, rg = tid & 7, cg = tid >> 3;
+  const bool act = 4 * cg < TV;
+  const int j0 = tile * TV + (act ? 4 * cg : 0);
+  const int64_t bh = (int64_t)b * H + h;
+  const int64_t slot = load_slot(F.slots, F.slots_dtype, b);
+  if (slot <= 0 || slot >= F.num_slots) {  // masked: zero readout / zero state, no page access
+    if (MODE == FMT_STEP)
+      for (int j = tid; j < TV; j += 256) store_val(S.out, S.out_dtype, bh * V + tile * TV + j, 0.0f);
+    if (MODE == FMT_DECODE)
+      for (int e = tid; e < K * TV; e += 256) F.dense[(bh * K + e / TV) * V + tile * TV + e % TV] = 0.0f;
+    return;
+  }
+  uint8_t *page = F.data + slot * F.page_bytes;
+  const int W = F.bits;
+  const int L = (1 << ((W < 8 ? W : 8) - 1)) - 1;
+  // LDS: q, k, retention per row | misc | per-row scale | reduction space
+  float *qs = (float *)smem;
+  float *ks = qs + 128;
+  float *ds = ks + 128;
+  float *misc = ds + 128;
+  float *rowv = misc + 16;
+  float *big = rowv + 128;
+
+  float beta = 0.0f;
+  if (MODE == FMT_STEP) {
+    // input preparation as kernels/formats.py:120-146
+    const int hk = h / (H / S.HK);
+    const int64_t qb = (int64_t)b * S.q_stride + (int64_t)hk * K;
+    const int64_t kb = (int64_t)b * S.k_stride + (int64_t)hk * K;
+    if (tid < 64) {
+      float sq = 0.0f, sk = 0.0f;
+      for (int i = tid; i < K; i += 64) {
+        const float a = load_val(S.q, S.qkv_dtype, qb + i), c = load_val(S.k, S.qkv_dtype, kb + i);
+        sq += a * a;
+        sk += c * c;
+      }
+#pragma unroll
+      for (int m = 1; m < 64; m <<= 1) {
+        sq += __shfl_xor(sq, m);
+        sk += __shfl_xor(sk, m);
+      }
+      if (tid == 0) {
+        misc[0] = S.normalize ? 1.0f / __builtin_sqrtf(sq + 1e-6f) : 1.0f;
+        misc[1] = S.normalize ? 1.0f / __builtin_sqrtf(sk + 1e-6f) : 1.0f;
+        float bt = load_val(S.beta, S.gate_dtype, bh);
+        if (S.a_log) bt = 1.0f / (1.0f + __expf(-bt));
+        misc[2] = bt;
+      }
+    }
+    __syncthreads();
+    const float nq = misc[0], nk = misc[1];
+    beta = misc[2];
+    const float alog = S.a_log ? __expf(load_val(S.a_log, S.gate_dtype, h)) : 0.0f;
+    for (int i = tid; i < K; i += 256) {
+      qs[i] = (load_val(S.q, S.qkv_dtype, qb + i) * nq) * S.scale;
+      ks[i] = load_val(S.k, S.qkv_dtype, kb + i) * nk;
+      const int64_t gi = F.kda ? bh * K + i : bh;
+      float gv = load_val(S.g, S.gate_dtype, gi);
+      if (S.a_log) {
+        const float u = gv + load_val(S.dt_bias, S.gate_dtype, F.kda ? (int64_t)h * K + i : (int64_t)h);
+        const float sp = u > 20.0f ? u : __logf(1.0f + __expf(u < 20.0f ? u : 20.0f));
+        gv = -alog * sp;
+      }
+      ds[i] = __expf(gv);
+    }
+    __syncthreads();
+  }
+
+  // ---- this lane's values
+  float x[FMT_RPT][4];
+  if (MODE == FMT_ENCODE) {
+#pragma unroll
+    for (int r = 0; r < FMT_RPT; r++) {
+      const int i = rg + 8 * r;
+#pragma unroll
+      for (int c = 0; c < 4; c++) x[r][c] = (act && i < K) ? F.in[(bh * K + i) * V + j0 + c] : 0.0f;
+    }
+  } else {
+    float cj[4] = {0.f, 0.f, 0.f, 0.f};
+    if (F.kind == SQ_FMT_DSQ && act) {
+#pragma unroll
+      for (int c = 0; c < 4; c++) cj[c] = h2f(page_half(page, F.columns[h] + 4 * (j0 + c)));
+    }
+#pragma unroll
+    for (int r = 0; r < FMT_RPT; r++) {
+      const int i = rg + 8 * r;
+#pragma unroll
+      for (int c = 0; c < 4; c++) x[r][c] = 0.0f;
+      if (!act || i >= K) continue;
+      const uint8_t *row = page + F.offsets[(int64_t)h * K + i];
+      if (F.kind == SQ_FMT_FP32) {
+        const float *fr = (const float *)row + j0;
+#pragma unroll
+        for (int c = 0; c < 4; c++) x[r][c] = fr[c];
+        continue;
+      }
+      const uint32_t word = fmt_read_codes(row, j0, W);
+      const int64_t ro = F.rows[(int64_t)h * K + i];
+      if (F.kind == SQ_FMT_SYMMETRIC) {
+        const int64_t meta = ro + 4 * (j0 / FMT_TV);
+        const float s = h2f(page_half(page, meta)), z = h2f(page_half(page, meta + 2));
+#pragma unroll
+        for (int c = 0; c < 4; c++) x[r][c] = ((float)((word >> (c * W)) & ((1u << W) - 1u)) - z) * s;
+      } else {
+        const float rr = h2f(page_half(page, ro));
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+          x[r][c] = (rr * cj[c]) * (float)((int)((word >> (c * W)) & ((1u << W) - 1u)) - L);
+      }
+    }
+  }
+  if (MODE == FMT_DECODE) {
+#pragma unroll
+    for (int r = 0; r < FMT_RPT; r++) {
+      const int i = rg + 8 * r;
+      if (act && i < K)
+#pragma unroll
+        for (int c = 0; c < 4; c++) F.dense[(bh * K + i) * V + j0 + c] = x[r][c];
+    }
+    return;
+  }
+
+  if (MODE == FMT_STEP) {
+    // retained = S e^g; residual = v - k^T retained; x = retained + k (beta residual); o = q^T x
+    float kr[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int r = 0; r < FMT_RPT; r++) {
+      const int i = rg + 8 * r;
+      if (i >= K) continue;
+      const float d = ds[i], k = ks[i];
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        x[r][c] = x[r][c] * d;
+        kr[c] += k * x[r][c];
+      }
+    }
+    float vv[4] = {0.f, 0.f, 0.f, 0.f}, o[4] = {0.f, 0.f, 0.f, 0.f};
+    if (act) load4(S.v, S.qkv_dtype, (int64_t)b * S.v_stride + (int64_t)h * V + j0, vv);
+    float br[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) br[c] = beta * (vv[c] - fast::rg8_sum(kr[c]));
+#pragma unroll
+    for (int r = 0; r < FMT_RPT; r++) {
+      const int i = rg + 8 * r;
+      if (i >= K) continue;
+      const float k = ks[i], q = qs[i];
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        x[r][c] = x[r][c] + k * br[c];
+        o[c] += q * x[r][c];
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; c++) o[c] = fast::rg8_sum(o[c]);
+    if (act && rg == 0) store4(S.out, S.out_dtype, bh * V + j0, o);
+  }
+
+  // ---- encode x into the page
+  if (F.kind == SQ_FMT_FP32) {
+#pragma unroll
+    for (int r = 0; r < FMT_RPT; r++) {
+      const int i = rg + 8 * r;
+      if (!act || i >= K) continue;
+      float *fr = (float *)(page + F.offsets[(int64_t)h * K + i]) + j0;
+#pragma unroll
+      for (int c = 0; c < 4; c++) fr[c] = x[r][c];
+    }
+    return;
+  }
+  const float Lf = (float)L;
+  float div[4];  // per column (DSQ) divisor; SYMMETRIC uses the per-row s
+  if (F.kind == SQ_FMT_SYMMETRIC) {
+    // s_i = fp16(max_j |x_ij| / L) over the tile's 128 columns (one group)
+    float *red = big;  // [TV/4][K]
+#pragma unroll
+    for (int r = 0; r < FMT_RPT; r++) {
+      const int i = rg + 8 * r;
+      if (!act || i >= K) continue;
+      red[cg * K + i] = fmaxf(fmaxf(fabsf(x[r][0]), fabsf(x[r][1])), fmaxf(fabsf(x[r][2]), fabsf(x[r][3])));
+    }
+    __syncthreads();
+    for (int i = tid; i < K; i += 256) {
+      float m = 0.0f;
+      for (int t = 0; t < TV / 4; t++) m = fmaxf(m, red[t * K + i]);
+      uint32_t hb;
+      rowv[i] = fp16_scale(m / Lf, &hb);
+      const int64_t meta = F.rows[(int64_t)h * K + i] + 4 * (tile * TV / FMT_TV);
+      put_page_half(page, meta, hb);
+      put_page_half(page, meta + 2, f2h(Lf));
+    }
+    __syncthreads();
+  } else {
+    // r_i = fp16(sqrt(max(mean_j |x_ij|, 1e-20))), mean in PyTorch's order
+    const int XS = TV + 1;  // row pitch of the staged |x| (odd: no bank conflicts)
+    float *xs = big;
+#pragma unroll
+    for (int r = 0; r < FMT_RPT; r++) {
+      const int i = rg + 8 * r;
+      if (!act || i >= K) continue;
+#pragma unroll
+      for (int c = 0; c < 4; c++) xs[i * XS + 4 * cg + c] = fabsf(x[r][c]);
+    }
+    __syncthreads();
+    for (int i = tid; i < K; i += 256) {
+      const float s = torch_inner_sum(V, [&](int64_t t) { return xs[i * XS + t]; });
+      float m = s / (float)V;
+      m = m < 1e-20f ? 1e-20f : m;
+      uint32_t hb;
+      rowv[i] = fp16_scale(__builtin_sqrtf(m), &hb);
+      put_page_half(page, F.rows[(int64_t)h * K + i], hb);
+    }
+    __syncthreads();
+    // y = x / r; c_j = fp16(max_i |y_ij| / L)
+    float mx[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int r = 0; r < FMT_RPT; r++) {
+      const int i = rg + 8 * r;
+      if (i >= K) continue;
+      const float rr = rowv[i];
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        x[r][c] = x[r][c] / rr;
+        mx[c] = fmaxf(mx[c], fabsf(x[r][c]));
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      uint32_t hb;
+      div[c] = fp16_scale(fast::rg8_max_nonneg(mx[c]) / Lf, &hb);
+      if (act && rg == 0) {
+        put_page_half(page, F.columns[h] + 4 * (int64_t)(j0 + c), hb);
+        put_page_half(page, F.columns[h] + 4 * (int64_t)(j0 + c) + 2, 0u);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < FMT_RPT; r++) {
+    const int i = rg + 8 * r;
+    if (!act || i >= K) continue;
+    uint32_t word = 0;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const float d = F.kind == SQ_FMT_SYMMETRIC ? rowv[i] : div[c];
+      float q = __builtin_rintf(x[r][c] / d);
+      q = q > -Lf ? q : -Lf;
+      q = q < Lf ? q : Lf;
+      word |= (uint32_t)(int)(q + Lf) << (c * W);
+    }
+    fmt_write_codes(page + F.offsets[(int64_t)h * K + i], j0, W, word);
+  }
+}
+
 // ------------------------------------------------------------ host side
 
 thread_local char g_err[512] = "";
@@ -2688,11 +2994,11 @@ int launch_step_mode(const sq_pool *pool, StepDev sd, int64_t batch, hipStream_t
   return check_launch("step_kernel");
 }
 
-int fill_step(const sq_pool *pool, const sq_step_args *a, StepDev &sd) {
+int fill_step(int heads, const sq_step_args *a, StepDev &sd) {
   if (!a || !a->q || !a->k || !a->v || !a->g || !a->beta || !a->out || !a->slots)
     return fail(SQ_EINVAL, "step: null input pointer");
   if (a->batch < 0) return fail(SQ_EINVAL, "step: negative batch");
-  if (a->key_heads < 1 || pool->heads % a->key_heads) return fail(SQ_EINVAL, "step: heads not divisible by key heads");
+  if (a->key_heads < 1 || heads % a->key_heads) return fail(SQ_EINVAL, "step: heads not divisible by key heads");
   if ((a->a_log == nullptr) != (a->dt_bias == nullptr)) return fail(SQ_EINVAL, "step: a_log and dt_bias go together");
   if (a->qkv_dtype < 0 || a->qkv_dtype > 2 || a->gate_dtype < 0 || a->gate_dtype > 2 || a->out_dtype < 0 ||
       a->out_dtype > 2 || (a->slots_dtype != SQ_I32 && a->slots_dtype != SQ_I64))
@@ -2718,6 +3024,68 @@ int fill_step(const sq_pool *pool, const sq_step_args *a, StepDev &sd) {
   sd.normalize = a->normalize;
   sd.scale = a->scale;
   return 0;
+}
+
+int validate_format(const sq_format_pool *f) {
+  if (!f || !f->data || !f->offsets || !f->rows || !f->columns) return fail(SQ_EINVAL, "format pool: null pointer");
+  if (f->heads < 1 || f->page_bytes <= 0 || f->num_slots < 1) return fail(SQ_EINVAL, "format pool: bad sizes");
+  if (!pow2(f->keys) || f->keys > 128 || !pow2(f->values) || f->values < 4)
+    return fail(SQ_ESHAPE, "format pool: K must be a power of two <= 128, V a power of two >= 4");
+  if (f->page_bytes % 4) return fail(SQ_EINVAL, "format pool: page_bytes must be a multiple of 4");
+  switch (f->kind) {
+    case SQ_FMT_FP32:
+      if (f->bits != 32) return fail(SQ_ESHAPE, "format pool: fp32 pages hold 32-bit values");
+      break;
+    case SQ_FMT_SYMMETRIC:
+      if (f->bits != 4 && f->bits != 6 && f->bits != 8) return fail(SQ_ESHAPE, "format pool: code width 4, 6 or 8");
+      if (f->group != 128 || f->values % 128) return fail(SQ_ESHAPE, "format pool: symmetric groups are 128 values");
+      break;
+    case SQ_FMT_DSQ:
+      if (f->bits != 4 && f->bits != 6 && f->bits != 8) return fail(SQ_ESHAPE, "format pool: code width 4, 6 or 8");
+      if (f->values > 128) return fail(SQ_ESHAPE, "format pool: dual-axis pages need V <= 128");
+      break;
+    default:
+      return fail(SQ_EINVAL, "format pool: unknown kind");
+  }
+  return 0;
+}
+
+FmtDev to_fmt(const sq_format_pool *f) {
+  FmtDev d;
+  memset(&d, 0, sizeof(d));
+  d.data = f->data;
+  d.page_bytes = f->page_bytes;
+  d.num_slots = f->num_slots;
+  d.offsets = f->offsets;
+  d.rows = f->rows;
+  d.columns = f->columns;
+  d.H = f->heads;
+  d.K = f->keys;
+  d.V = f->values;
+  d.kind = f->kind;
+  d.bits = f->bits;
+  d.kda = f->kda;
+  return d;
+}
+
+template <int MODE>
+int launch_format(const sq_format_pool *f, const FmtDev &fd, const StepDev &sd, int64_t batch, hipStream_t st) {
+  if (batch == 0) return 0;
+  if (batch * f->heads > 0x7fffffffLL) return fail(SQ_EINVAL, "format: batch * heads too large");
+  const int TV = f->values < FMT_TV ? f->values : FMT_TV;
+  size_t lds = FMT_SMALL_LDS;
+  if (MODE != FMT_DECODE) {
+    if (f->kind == SQ_FMT_SYMMETRIC) lds += (size_t)(TV / 4) * f->keys * 4;
+    if (f->kind == SQ_FMT_DSQ) lds += (size_t)f->keys * (TV + 1) * 4;
+  }
+  if (lds > 65536) {
+    hipError_t e = hipFuncSetAttribute((const void *)format_kernel<MODE>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return fail((int)e, "format: LDS attribute");
+  }
+  hipLaunchKernelGGL((format_kernel<MODE>), dim3((unsigned)(batch * f->heads), (unsigned)(f->values / TV)),
+                     dim3(256), lds, st, fd, sd);
+  return check_launch("format_kernel");
 }
 
 }  // namespace
@@ -2763,7 +3131,7 @@ int sq_decode_step(const sq_pool *pool, const sq_step_args *args, void *stream) 
   int rc = validate_pool(pool);
   if (rc) return rc;
   StepDev sd;
-  rc = fill_step(pool, args, sd);
+  rc = fill_step(pool->heads, args, sd);
   if (rc) return rc;
   if (args->batch == 0) return 0;
   return launch_step_mode<MODE_FUSED>(pool, sd, args->batch, (hipStream_t)stream);
@@ -2774,7 +3142,7 @@ int sq_decode_readout(const sq_pool *pool, const sq_step_args *args, const sq_wr
   int rc = validate_pool(pool);
   if (rc) return rc;
   StepDev sd;
-  rc = fill_step(pool, args, sd);
+  rc = fill_step(pool->heads, args, sd);
   if (rc) return rc;
   if (!scratch || !scratch->key || !scratch->decay || !scratch->delta || !scratch->stable_slots)
     return fail(SQ_EINVAL, "readout: null scratch");
@@ -2974,6 +3342,48 @@ int sq_copy_slots(const sq_pool *pool, const void *src, const void *dst, int32_t
   hipLaunchKernelGGL(gather_kernel, dim3(gx, (unsigned)n), dim3(256), 0, (hipStream_t)stream, pool->data,
                      pool->page_bytes, pool->num_slots, dst, slots_dtype, temp, 1);
   return check_launch("scatter_kernel");
+}
+
+int sq_format_encode(const sq_format_pool *pool, const float *state, const void *slots, int32_t slots_dtype,
+                     int64_t batch, void *stream) {
+  int rc = validate_format(pool);
+  if (rc) return rc;
+  if (batch < 0 || (batch && (!state || !slots))) return fail(SQ_EINVAL, "format encode: bad arguments");
+  if (slots_dtype != SQ_I32 && slots_dtype != SQ_I64) return fail(SQ_EINVAL, "format encode: slots dtype");
+  FmtDev fd = to_fmt(pool);
+  fd.in = state;
+  fd.slots = slots;
+  fd.slots_dtype = slots_dtype;
+  StepDev sd;
+  memset(&sd, 0, sizeof(sd));
+  return launch_format<FMT_ENCODE>(pool, fd, sd, batch, (hipStream_t)stream);
+}
+
+int sq_format_decode(const sq_format_pool *pool, const void *slots, int32_t slots_dtype, int64_t batch,
+                     float *state, void *stream) {
+  int rc = validate_format(pool);
+  if (rc) return rc;
+  if (batch < 0 || (batch && (!state || !slots))) return fail(SQ_EINVAL, "format decode: bad arguments");
+  if (slots_dtype != SQ_I32 && slots_dtype != SQ_I64) return fail(SQ_EINVAL, "format decode: slots dtype");
+  FmtDev fd = to_fmt(pool);
+  fd.dense = state;
+  fd.slots = slots;
+  fd.slots_dtype = slots_dtype;
+  StepDev sd;
+  memset(&sd, 0, sizeof(sd));
+  return launch_format<FMT_DECODE>(pool, fd, sd, batch, (hipStream_t)stream);
+}
+
+int sq_format_step(const sq_format_pool *pool, const sq_step_args *args, void *stream) {
+  int rc = validate_format(pool);
+  if (rc) return rc;
+  StepDev sd;
+  rc = fill_step(pool->heads, args, sd);
+  if (rc) return rc;
+  FmtDev fd = to_fmt(pool);
+  fd.slots = args->slots;
+  fd.slots_dtype = args->slots_dtype;
+  return launch_format<FMT_STEP>(pool, fd, sd, args->batch, (hipStream_t)stream);
 }
 
 }  // extern "C"
