@@ -135,6 +135,18 @@ __device__ __forceinline__ int64_t load_slot(const void *p, int dtype, int64_t i
   return dtype == SQ_I64 ? ((const int64_t *)p)[idx] : (int64_t)((const int32_t *)p)[idx];
 }
 
+// A workgroup-uniform read of memory that no kernel writes while it runs
+// (tables, slot lists, inputs), through the constant address space so that
+// it becomes a scalar load: its wait does not wait for the vector loads.
+template <typename T>
+__device__ __forceinline__ T ld_uniform(const T *p) {
+  return *(const __attribute__((address_space(4))) T *)p;
+}
+
+__device__ __forceinline__ int64_t load_slot_uniform(const void *p, int dtype, int64_t idx) {
+  return dtype == SQ_I64 ? ld_uniform((const int64_t *)p + idx) : (int64_t)ld_uniform((const int32_t *)p + idx);
+}
+
 __device__ __forceinline__ uint32_t page_half(const uint8_t *page, int64_t byte) {
   return (uint32_t)page[byte] | ((uint32_t)page[byte + 1] << 8);
 }
@@ -856,8 +868,11 @@ __global__ __launch_bounds__(512) void step_kernel(PoolDev P, StepDev S) {
 // so the foreground needs two FMAs per value and no dequantised tile.
 // The writer works on inner_ij = x'_ij / c_j = a_i z_ij + k_i delta_j / c_j.
 // =====================================================================
+// Four waves per SIMD (128 VGPRs): four workgroups per CU hide the page and
+// input latency of each tile behind the others' arithmetic (a 64-bit address
+// is kept in scratch across the tile, its only spill).
 #ifndef GDN128_WAVES
-#define GDN128_WAVES 3
+#define GDN128_WAVES 4
 #endif
 #ifndef SCHED_ROWS
 #define SCHED_ROWS 4  // rows between scheduling fences (bounds hoisted LDS loads)
@@ -1014,19 +1029,127 @@ __device__ __forceinline__ void store_out(const PoolDev &P, const StepDev &S, co
   }
 }
 
-// Stage the head's regions into LDS with a compile-time number of 16-byte
-// chunks per lane (the code region of a W-bit head is 128*W chunks, W/2 per
-// lane; FP16 pivot heads: 2048 chunks, 8 per lane).  Row scales use lanes
-// 0..16*NG-1, column scales lanes 240..255.
-template <int CODE_CHUNKS_PER_LANE>
-__device__ __forceinline__ void stage_in_fast(const Ctx &C, int row_chunks, bool cols) {
-  const uint4 *src = (const uint4 *)(C.page + C.code_start);
-  uint4 *dst = (uint4 *)C.code;
+// The head's regions are staged into LDS with direct global-to-LDS loads
+// (no registers, no waits until the barrier that follows): CH 16-byte chunks
+// per lane of the code region (a W-bit head has 128*W chunks, W/2 per lane;
+// FP16 pivot heads: 2048 chunks, 8 per lane), row scales on lanes
+// 0..row_chunks-1, column scales on lanes 240..255.  Each wave's chunks are
+// 64 consecutive 16-byte units, so one LDS base per wave addresses them.
+typedef const __attribute__((address_space(1))) void *gptr_t;
+typedef __attribute__((address_space(3))) void *lptr_t;
+
+template <int CH>
+__device__ __forceinline__ void stage_async(const Ctx &C, int row_chunks, bool cols) {
+  const int wv = C.tid >> 6;
+  const uint4 *src = (const uint4 *)(C.page + C.code_start) + C.tid;
 #pragma unroll
-  for (int k = 0; k < CODE_CHUNKS_PER_LANE; k++) dst[C.tid + FNT * k] = src[C.tid + FNT * k];
-  if (C.tid < row_chunks) ((uint4 *)C.rst)[C.tid] = ((const uint4 *)(C.page + C.row_start))[C.tid];
+  for (int k = 0; k < CH; k++)
+    __builtin_amdgcn_global_load_lds((gptr_t)(src + FNT * k), (lptr_t)(C.code + 16 * (FNT * k + 64 * wv)), 16, 0, 0);
+  if (C.tid < row_chunks)
+    __builtin_amdgcn_global_load_lds((gptr_t)((const uint4 *)(C.page + C.row_start) + C.tid),
+                                     (lptr_t)(C.rst + 16 * 64 * wv), 16, 0, 0);
   if (cols && C.tid >= FNT - 16)
-    ((uint4 *)C.cst)[C.tid - (FNT - 16)] = ((const uint4 *)(C.page + C.colbase))[C.tid - (FNT - 16)];
+    __builtin_amdgcn_global_load_lds((gptr_t)((const uint4 *)(C.page + C.colbase) + (C.tid - (FNT - 16))),
+                                     (lptr_t)(C.cst + 16 * (64 * wv - (FNT - 16))), 16, 0, 0);
+}
+
+// Per-head inputs into LDS (raw q, k rows, their squared norms per wave,
+// beta and the head's retention, the fit weights), and this lane's 4 values
+// of v (the writer: delta) as raw bits in registers.  Issued after the
+// page's global-to-LDS loads; every vector load is issued before any value
+// is used (the q/k/v element width QW is a compile-time choice), so all
+// their latencies overlap in one round trip.  F32 gate scalars are scalar
+// loads.
+template <int MODE, bool QW4>
+__device__ __forceinline__ void prologue(const PoolDev &P, const StepDev &S, const Ctx &C, uint32_t vraw[4]) {
+  const int64_t bh = (int64_t)C.b * P.H + C.h;
+  const float w = P.impact[(int64_t)C.h * FK + (C.tid & (FK - 1))];
+  if (MODE == MODE_WRITE) {
+    __builtin_memcpy(vraw, S.s_delta + bh * FV + C.j0, 16);
+    const float k = S.s_key[bh * FK + (C.tid & (FK - 1))];
+    const float d = ld_uniform(S.s_decay + bh * FK);
+    if (C.tid < FK) C.kraw[C.tid] = k;
+    if (C.tid == FK) C.misc[1] = d;
+  } else {
+    const int hk = C.h / (P.H / S.HK);
+    const int i = C.tid & (FK - 1);  // waves 2, 3 read rows too (no divergence); threads < 128 use them
+    const int64_t qi = (int64_t)C.b * S.q_stride + (int64_t)hk * FK + i;
+    const int64_t ki = (int64_t)C.b * S.k_stride + (int64_t)hk * FK + i;
+    const int64_t vi = (int64_t)C.b * S.v_stride + (int64_t)C.h * FV + C.j0;
+    uint32_t qr, kr;
+    if (QW4) {
+      __builtin_memcpy(vraw, (const float *)S.v + vi, 16);
+      qr = ((const uint32_t *)S.q)[qi];
+      kr = ((const uint32_t *)S.k)[ki];
+    } else {
+      __builtin_memcpy(vraw, (const uint16_t *)S.v + vi, 8);
+      qr = ((const uint16_t *)S.q)[qi];
+      kr = ((const uint16_t *)S.k)[ki];
+    }
+    float bt, gv, dtb = 0.0f, al = 0.0f;
+    if (S.gate_dtype == SQ_F32) {
+      bt = __uint_as_float(ld_uniform((const uint32_t *)S.beta + bh));
+      gv = __uint_as_float(ld_uniform((const uint32_t *)S.g + bh));
+      if (S.a_log) {
+        dtb = __uint_as_float(ld_uniform((const uint32_t *)S.dt_bias + C.h));
+        al = __uint_as_float(ld_uniform((const uint32_t *)S.a_log + C.h));
+      }
+    } else {
+      bt = load_val(S.beta, S.gate_dtype, bh);
+      gv = load_val(S.g, S.gate_dtype, bh);
+      if (S.a_log) {
+        dtb = load_val(S.dt_bias, S.gate_dtype, C.h);
+        al = load_val(S.a_log, S.gate_dtype, C.h);
+      }
+    }
+    const float qv = QW4 ? __uint_as_float(qr) : S.qkv_dtype == SQ_BF16 ? __uint_as_float(qr << 16) : hw_h2f(qr);
+    const float kv = QW4 ? __uint_as_float(kr) : S.qkv_dtype == SQ_BF16 ? __uint_as_float(kr << 16) : hw_h2f(kr);
+    if (C.tid < FK) {
+      C.qraw[C.tid] = qv;
+      C.kraw[C.tid] = kv;
+      const float sq = wave_sum(qv * qv), sk = wave_sum(kv * kv);
+      if ((C.tid & 63) == 0) {
+        C.misc[8 + 2 * (C.tid >> 6)] = sq;
+        C.misc[9 + 2 * (C.tid >> 6)] = sk;
+      }
+    } else if (C.tid == FK) {
+      if (S.a_log) {
+        bt = 1.0f / (1.0f + __expf(-bt));
+        const float u = gv + dtb;
+        const float sp = u > 20.0f ? u : __logf(1.0f + __expf(u < 20.0f ? u : 20.0f));
+        gv = -__expf(al) * sp;
+      }
+      C.misc[0] = bt;
+      C.misc[1] = __expf(gv);
+    }
+  }
+  if (C.tid >= FK) C.wv[C.tid - FK] = w;
+}
+
+// this lane's v (the writer: delta) from its raw bits
+template <int MODE, bool QW4>
+__device__ __forceinline__ void raw_v(const StepDev &S, const uint32_t vraw[4], float v[4]) {
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    if (MODE == MODE_WRITE || QW4) {
+      v[c] = __uint_as_float(vraw[c]);
+    } else {
+      const uint32_t h = (vraw[c >> 1] >> (16 * (c & 1))) & 0xffffu;
+      v[c] = S.qkv_dtype == SQ_BF16 ? __uint_as_float(h << 16) : hw_h2f(h);
+    }
+  }
+}
+
+// Writer hand-off of the readout pass: prepared key rows and per-row retention.
+template <int MODE>
+__device__ __forceinline__ void handoff(const PoolDev &P, const StepDev &S, const Ctx &C) {
+  if (MODE == MODE_READ && C.tid < FK) {
+    const int64_t bh = (int64_t)C.b * P.H + C.h;
+    float nk = 1.0f;
+    if (S.normalize) nk = 1.0f / __builtin_sqrtf((C.misc[9] + C.misc[11]) + 1e-6f);
+    S.s_key[bh * FK + C.tid] = C.kraw[C.tid] * nk;
+    S.s_decay[bh * FK + C.tid] = C.misc[1];
+  }
 }
 
 template <int CODE_CHUNKS_PER_LANE>
@@ -1075,7 +1198,7 @@ __device__ __forceinline__ uint32_t pack_codes(const float v[4]) {
   return w;
 }
 
-template <int W, int MODE>
+template <int W, int MODE, bool QW4>
 __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx &C) {
 #pragma clang fp contract(off)
   constexpr int L = W == 2 ? 3 : (1 << (W - 1)) - 1;
@@ -1088,12 +1211,15 @@ __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx
   constexpr uint32_t XM = W == 8 ? 0x80808080u : W == 6 ? 0x820820u : W == 4 ? 0x8888u : 0xAAu;
   constexpr int SEG = 2 * W;                   // bytes of one row's 16-value segment
   constexpr int BLK = FK * SEG;                // bytes of one 16-column block
-  const float beta = C.misc[0];
   const int NG = W == 2 ? FV / P.G : 1;
   const int g = W == 2 ? C.j0 / P.G : 0;
   const uint16_t *c16 = (const uint16_t *)C.cst;
-  stage_in_fast<W / 2>(C, 16 * NG, true);
+  stage_async<W / 2>(C, 16 * NG, true);
+  uint32_t vraw[4];
+  prologue<MODE, QW4>(P, S, C, vraw);
   __syncthreads();
+  const float beta = C.misc[0];
+  handoff<MODE>(P, S, C);
   row_setup_int<MODE>(S, C, NG, ZS);
   __syncthreads();
 
@@ -1134,17 +1260,15 @@ __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx
       }
     }
   }
-  float delta[4], o[4];
+  float delta[4], o[4], vv[4];
+  raw_v<MODE, QW4>(S, vraw, vv);
   if (MODE == MODE_WRITE) {
-    const int64_t base = ((int64_t)C.b * P.H + C.h) * FV + C.j0;
 #pragma unroll
-    for (int c = 0; c < 4; c++) delta[c] = S.s_delta[base + c];
+    for (int c = 0; c < 4; c++) delta[c] = vv[c];
   } else {
     const float sKA = C.misc[16 + SUM_KA + g] + C.misc[32 + SUM_KA + g];
     const float sQA = C.misc[16 + SUM_QA + g] + C.misc[32 + SUM_QA + g];
     const float sQK = C.misc[16 + SUM_QK] + C.misc[32 + SUM_QK];
-    float vv[4];
-    load4(S.v, S.qkv_dtype, (int64_t)C.b * S.v_stride + (int64_t)C.h * FV + C.j0, vv);
 #pragma unroll
     for (int c = 0; c < 4; c++) {
       const float kS = cj[c] * fmaf(ZS, rg8_sum(aK[c]), sKA);
@@ -1339,13 +1463,16 @@ __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx
   stage_back_fast<W / 2>(C, 16 * NG, true);
 }
 
-template <int MODE>
+template <int MODE, bool QW4>
 __device__ __forceinline__ void pivot_body(const PoolDev &P, const StepDev &S, Ctx &C) {
 #pragma clang fp contract(off)
   constexpr int SEG = 32, BLK = FK * SEG;
-  const float beta = C.misc[0], decay = C.misc[1];
-  stage_in_fast<8>(C, 0, false);
+  stage_async<8>(C, 0, false);
+  uint32_t vraw[4];
+  prologue<MODE, QW4>(P, S, C, vraw);
   __syncthreads();
+  const float beta = C.misc[0], decay = C.misc[1];
+  handoff<MODE>(P, S, C);
   row_setup<MODE>(S, C, 0);
   __syncthreads();
   float qi[FRPT], ki[FRPT];
@@ -1367,16 +1494,12 @@ __device__ __forceinline__ void pivot_body(const PoolDev &P, const StepDev &S, C
 #pragma unroll
     for (int c = 0; c < 4; c++) sk[c] = fmaf(ki[r], x[r][c], sk[c]);
   }
-  float delta[4], o[4];
-  const int64_t base = ((int64_t)C.b * P.H + C.h) * FV + C.j0;
+  float delta[4], o[4], vv[4];
+  raw_v<MODE, QW4>(S, vraw, vv);
 #pragma unroll
   for (int c = 0; c < 4; c++) {
-    if (MODE == MODE_WRITE) {
-      delta[c] = S.s_delta[base + c];
-    } else {
-      const float vv = load_val(S.v, S.qkv_dtype, (int64_t)C.b * S.v_stride + (int64_t)C.h * FV + C.j0 + c);
-      delta[c] = beta * (vv - rg8_sum(sk[c]));
-    }
+    if (MODE == MODE_WRITE) delta[c] = vv[c];
+    else delta[c] = beta * (vv[c] - rg8_sum(sk[c]));
   }
   float oq[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -1406,7 +1529,7 @@ __device__ __forceinline__ void pivot_body(const PoolDev &P, const StepDev &S, C
 
 }  // namespace fast
 
-template <int MODE>
+template <int MODE, bool QW4>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GDN128_WAVES))) void gdn128_kernel(PoolDev P,
                                                                                                        StepDev S) {
   using namespace fast;
@@ -1422,26 +1545,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GDN128_WAVE
   C.j0 = 4 * C.cg;
   C.blk = C.cg >> 2;
   C.sub = C.cg & 3;
+  // The slot and the head's metadata are scalar loads; the page's
+  // global-to-LDS loads are issued as soon as they arrive, the per-head
+  // inputs after them (int_body), so all those latencies overlap.
   int64_t slot;
-  if (MODE == MODE_WRITE) {
-    slot = S.s_slots[C.b];
-  } else {
-    slot = load_slot(S.slots, S.slots_dtype, C.b);
-    if (MODE == MODE_READ && C.h == 0 && C.tid == 0) S.s_slots[C.b] = slot;
-  }
+  if (MODE == MODE_WRITE) slot = ld_uniform(S.s_slots + C.b);
+  else slot = load_slot_uniform(S.slots, S.slots_dtype, C.b);
+  const int32_t *hm = P.head_meta + 4 * C.h;
+  const int W = ld_uniform(P.bits + (int64_t)C.h * FK);
+  const int code_start = ld_uniform(hm), code_bytes = ld_uniform(hm + 1);
+  const int row_start = ld_uniform(hm + 2), row_bytes = ld_uniform(hm + 3);
+  const int colbase = ld_uniform(P.columns + C.h);
+  if (MODE == MODE_READ && C.h == 0 && C.tid == 0) S.s_slots[C.b] = slot;
   if (slot <= 0 || slot >= P.num_slots) {
     if (MODE == MODE_FUSED || MODE == MODE_READ)
       for (int j = C.tid; j < FV; j += FNT) store_val(S.out, S.out_dtype, ((int64_t)C.b * H + C.h) * FV + j, 0.0f);
     return;
   }
   C.page = P.data + slot * P.page_bytes;
-  const int32_t *hm = P.head_meta + 4 * C.h;
-  C.code_start = hm[0];
-  C.code_bytes = hm[1];
-  C.row_start = hm[2];
-  C.row_bytes = hm[3];
-  C.colbase = P.columns[C.h];
-  const int W = P.bits[(int64_t)C.h * FK];
+  C.code_start = code_start;
+  C.code_bytes = code_bytes;
+  C.row_start = row_start;
+  C.row_bytes = row_bytes;
+  C.colbase = colbase;
   C.code = smem;
   C.rst = smem + P.stage;
   C.cst = C.rst + P.rstage;
@@ -1455,52 +1581,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GDN128_WAVE
   const int ngm = P.G >= 32 ? FV / P.G : 1;
   C.rc = (float4 *)(C.qs + FK);
   C.iu = (float2 *)(C.rc + FK * ngm);
-
-  // inputs: raw q, k rows, norms, beta and the head's retention
-  const int64_t bh = (int64_t)C.b * H + C.h;
-  if (MODE == MODE_WRITE) {
-    if (C.tid < FK) C.kraw[C.tid] = S.s_key[bh * FK + C.tid];
-    if (C.tid == FK) C.misc[1] = S.s_decay[bh * FK];
-  } else {
-    if (C.tid < FK) {
-      const int hk = C.h / (H / S.HK);
-      const float qv = load_val(S.q, S.qkv_dtype, (int64_t)C.b * S.q_stride + (int64_t)hk * FK + C.tid);
-      const float kv = load_val(S.k, S.qkv_dtype, (int64_t)C.b * S.k_stride + (int64_t)hk * FK + C.tid);
-      C.qraw[C.tid] = qv;
-      C.kraw[C.tid] = kv;
-      const float sq = wave_sum(qv * qv), sk = wave_sum(kv * kv);
-      if ((C.tid & 63) == 0) {
-        C.misc[8 + 2 * (C.tid >> 6)] = sq;
-        C.misc[9 + 2 * (C.tid >> 6)] = sk;
-      }
-    } else if (C.tid == FK) {
-      float bt = load_val(S.beta, S.gate_dtype, bh);
-      float gv = load_val(S.g, S.gate_dtype, bh);
-      if (S.a_log) {
-        bt = 1.0f / (1.0f + __expf(-bt));
-        const float u = gv + load_val(S.dt_bias, S.gate_dtype, C.h);
-        const float sp = u > 20.0f ? u : __logf(1.0f + __expf(u < 20.0f ? u : 20.0f));
-        gv = -__expf(load_val(S.a_log, S.gate_dtype, C.h)) * sp;
-      }
-      C.misc[0] = bt;
-      C.misc[1] = __expf(gv);
-    }
-  }
-  if (C.tid >= FK && C.tid < 2 * FK) C.wv[C.tid - FK] = P.impact[(int64_t)C.h * FK + C.tid - FK];
-  __syncthreads();
-  if (MODE == MODE_READ && C.tid < FK) {
-    // writer hand-off: prepared key rows and per-row retention
-    float nk = 1.0f;
-    if (S.normalize) nk = 1.0f / __builtin_sqrtf((C.misc[9] + C.misc[11]) + 1e-6f);
-    S.s_key[bh * FK + C.tid] = C.kraw[C.tid] * nk;
-    S.s_decay[bh * FK + C.tid] = C.misc[1];
-  }
   switch (W) {
-    case 2: int_body<2, MODE>(P, S, C); break;
-    case 4: int_body<4, MODE>(P, S, C); break;
-    case 6: int_body<6, MODE>(P, S, C); break;
-    case 8: int_body<8, MODE>(P, S, C); break;
-    default: pivot_body<MODE>(P, S, C); break;
+    case 2: int_body<2, MODE, QW4>(P, S, C); break;
+    case 4: int_body<4, MODE, QW4>(P, S, C); break;
+    case 6: int_body<6, MODE, QW4>(P, S, C); break;
+    case 8: int_body<8, MODE, QW4>(P, S, C); break;
+    default: pivot_body<MODE, QW4>(P, S, C); break;
   }
 }
 
@@ -2954,7 +3040,13 @@ int launch_step_mode(const sq_pool *pool, StepDev sd, int64_t batch, hipStream_t
     // staging | rows | columns | q,k raw + w | misc | red | ks, qs | rc (float4), iu (float2) per (row, group)
     size_t lds = (size_t)pd.stage + pd.rstage + 2 * 128 + 3 * 128 * 4 + 48 * 4 + 4 * 128 * 4 + 2 * 128 * 4 +
                  (size_t)6 * 128 * ng_max * 4;
-    hipLaunchKernelGGL((gdn128_kernel<MODE>), dim3((unsigned)(batch * pool->heads)), dim3(256), lds, st, pd, sd);
+    // q, k, v element width as a compile-time choice (the writer reads fp32 only)
+    if (MODE == MODE_WRITE || sd.qkv_dtype == SQ_F32)
+      hipLaunchKernelGGL((gdn128_kernel<MODE, true>), dim3((unsigned)(batch * pool->heads)), dim3(256), lds, st, pd,
+                         sd);
+    else
+      hipLaunchKernelGGL((gdn128_kernel<MODE, MODE == MODE_WRITE>), dim3((unsigned)(batch * pool->heads)), dim3(256),
+                         lds, st, pd, sd);
     return check_launch("gdn128_kernel");
   }
   if (MODE != MODE_DECODE && (pd.fast & SQ_POOL_FAST_KDA128)) {
