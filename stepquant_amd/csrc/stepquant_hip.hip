@@ -961,8 +961,8 @@ __device__ __forceinline__ void row_setup_int(const StepDev &S, const Ctx &C, in
     const int i = C.tid;
     float nq = 1.0f, nk = 1.0f;
     if (MODE != MODE_WRITE && S.normalize) {
-      nq = 1.0f / __builtin_sqrtf((C.misc[8] + C.misc[10]) + 1e-6f);
-      nk = 1.0f / __builtin_sqrtf((C.misc[9] + C.misc[11]) + 1e-6f);
+      nq = __builtin_amdgcn_rsqf((C.misc[8] + C.misc[10]) + 1e-6f);
+      nk = __builtin_amdgcn_rsqf((C.misc[9] + C.misc[11]) + 1e-6f);
     }
     const float k = MODE == MODE_WRITE ? C.kraw[i] : C.kraw[i] * nk;
     const float q = MODE == MODE_WRITE ? 0.0f : (C.qraw[i] * nq) * S.scale;
@@ -1007,8 +1007,8 @@ __device__ __forceinline__ void row_setup(const StepDev &S, const Ctx &C, int NG
     const int i = C.tid;
     float nq = 1.0f, nk = 1.0f;
     if (MODE != MODE_WRITE && S.normalize) {
-      nq = 1.0f / __builtin_sqrtf((C.misc[8] + C.misc[10]) + 1e-6f);
-      nk = 1.0f / __builtin_sqrtf((C.misc[9] + C.misc[11]) + 1e-6f);
+      nq = __builtin_amdgcn_rsqf((C.misc[8] + C.misc[10]) + 1e-6f);
+      nk = __builtin_amdgcn_rsqf((C.misc[9] + C.misc[11]) + 1e-6f);
     }
     const float k = MODE == MODE_WRITE ? C.kraw[i] : C.kraw[i] * nk;
     C.ks[i] = k;
@@ -1146,7 +1146,7 @@ __device__ __forceinline__ void handoff(const PoolDev &P, const StepDev &S, cons
   if (MODE == MODE_READ && C.tid < FK) {
     const int64_t bh = (int64_t)C.b * P.H + C.h;
     float nk = 1.0f;
-    if (S.normalize) nk = 1.0f / __builtin_sqrtf((C.misc[9] + C.misc[11]) + 1e-6f);
+    if (S.normalize) nk = __builtin_amdgcn_rsqf((C.misc[9] + C.misc[11]) + 1e-6f);
     S.s_key[bh * FK + C.tid] = C.kraw[C.tid] * nk;
     S.s_decay[bh * FK + C.tid] = C.misc[1];
   }
@@ -1184,11 +1184,17 @@ __device__ __forceinline__ uint32_t pack_codes(const float v[4]) {
     w = __builtin_amdgcn_cvt_pk_u8_f32(lvl(v[2]), 2, w);
     return __builtin_amdgcn_cvt_pk_u8_f32(lvl(v[3]), 3, w);
   }
-  // even columns in bytes 0 and 2, odd columns in bytes 0 and 2 of a second word
-  uint32_t e = __builtin_amdgcn_cvt_pk_u8_f32(lvl(v[0]), 0, 0u);
-  e = __builtin_amdgcn_cvt_pk_u8_f32(lvl(v[2]), 2, e);
-  uint32_t o = __builtin_amdgcn_cvt_pk_u8_f32(lvl(v[1]), 0, 0u);
-  o = __builtin_amdgcn_cvt_pk_u8_f32(lvl(v[3]), 2, o);
+  // even columns in bytes 0 and 2, odd columns in bytes 0 and 2 of a second
+  // word; the conversion saturates at 0 and the upper clamp to 2L is one
+  // packed 16-bit minimum per word (each byte sits alone in its 16-bit half)
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+  const u16x2 top2 = {(unsigned short)TOP, (unsigned short)TOP};
+  uint32_t e = __builtin_amdgcn_cvt_pk_u8_f32(v[0], 0, 0u);
+  e = __builtin_amdgcn_cvt_pk_u8_f32(v[2], 2, e);
+  uint32_t o = __builtin_amdgcn_cvt_pk_u8_f32(v[1], 0, 0u);
+  o = __builtin_amdgcn_cvt_pk_u8_f32(v[3], 2, o);
+  e = __builtin_bit_cast(uint32_t, __builtin_elementwise_min(__builtin_bit_cast(u16x2, e), top2));
+  o = __builtin_bit_cast(uint32_t, __builtin_elementwise_min(__builtin_bit_cast(u16x2, o), top2));
   const uint32_t x = e | (o << W);  // columns 0,1 at bit 0; columns 2,3 at bit 16
   if (W == 4) return __builtin_amdgcn_perm(0u, x, 0x0c0c0200u);  // bytes 0 and 2
   // W == 6: bits [0,12) from x, bits [12,24) from x >> 4, as one bitfield
@@ -1682,8 +1688,8 @@ __device__ __forceinline__ void row_setup(const PoolDev &P, const StepDev &S, co
     const bool piv = bi == 16;
     float nq = 1.0f, nk = 1.0f;
     if (MODE != MODE_WRITE && S.normalize) {
-      nq = 1.0f / __builtin_sqrtf((C.misc[8] + C.misc[10]) + 1e-6f);
-      nk = 1.0f / __builtin_sqrtf((C.misc[9] + C.misc[11]) + 1e-6f);
+      nq = __builtin_amdgcn_rsqf((C.misc[8] + C.misc[10]) + 1e-6f);
+      nk = __builtin_amdgcn_rsqf((C.misc[9] + C.misc[11]) + 1e-6f);
     }
     const float k = MODE == MODE_WRITE ? C.kraw[i] : C.kraw[i] * nk;
     const float q = MODE == MODE_WRITE ? 0.0f : (C.qraw[i] * nq) * S.scale;
@@ -2100,7 +2106,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GDN128_WAVE
   __syncthreads();
   if (MODE == MODE_READ && C.tid < FK) {
     float nk = 1.0f;
-    if (S.normalize) nk = 1.0f / __builtin_sqrtf((C.misc[9] + C.misc[11]) + 1e-6f);
+    if (S.normalize) nk = __builtin_amdgcn_rsqf((C.misc[9] + C.misc[11]) + 1e-6f);
     S.s_key[bh * FK + C.tid] = C.kraw[C.tid] * nk;
     S.s_decay[bh * FK + C.tid] = C.gv[C.tid];
   }
