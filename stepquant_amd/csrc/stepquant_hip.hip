@@ -1642,6 +1642,38 @@ __device__ __forceinline__ void stage_in_blocks(const uint8_t *g0, int stride, i
   }
 }
 
+// The same staging with direct global-to-LDS loads (no registers, no waits
+// until the next barrier): wave w copies blocks 8w..8w+7, one instruction
+// per block and 64 chunks (a block's window is contiguous in LDS).
+__device__ __forceinline__ void stage_blocks_async(const uint8_t *g0, int stride, int pitch, uint8_t *lds, int tid) {
+  const int nc = block_chunks(stride);
+  const int gmod = (int)((uintptr_t)g0 & 15);
+  const int lane = tid & 63, w = tid >> 6;
+  for (int c0 = 0; c0 < nc; c0 += 64) {
+#pragma unroll
+    for (int bb = 0; bb < 8; bb++) {
+      const int blk = 8 * w + bb;
+      const int off = blk * stride;
+      const uint4 *src = (const uint4 *)(g0 + (off - ((gmod + off) & 15))) + c0 + lane;
+      if (c0 + lane < nc)
+        __builtin_amdgcn_global_load_lds((gptr_t)src, (lptr_t)(lds + blk * pitch + 16 * c0), 16, 0, 0);
+    }
+  }
+}
+
+// stage_in with direct global-to-LDS loads; returns the offset of gstart in
+// the staged window (chunk c of the aligned window lands at lds + 16c)
+__device__ __forceinline__ int stage_region_async(const uint8_t *gstart, int64_t nbytes, uint8_t *lds, int tid) {
+  const int shift = (int)((uintptr_t)gstart & 15);
+  const uint4 *src = (const uint4 *)(gstart - shift);
+  const int n16 = (int)((shift + nbytes + 15) >> 4);
+  const int wbase = tid & ~63;
+  for (int c0 = 0; c0 < n16; c0 += FNT)
+    if (c0 + tid < n16)
+      __builtin_amdgcn_global_load_lds((gptr_t)(src + c0 + tid), (lptr_t)(lds + 16 * (c0 + wbase)), 16, 0, 0);
+  return shift;
+}
+
 // Write the staged blocks back: per block, 16-byte chunks inside the block
 // with one store, the chunks at its two edges in 2-byte units (block bounds
 // are even; neighbouring blocks write the other units of shared chunks).
@@ -2012,8 +2044,78 @@ __device__ __forceinline__ void body(const PoolDev &P, const StepDev &S, KCtx &C
 
 }  // namespace kfast
 
-template <int MODE>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GDN128_WAVES))) void kda128_kernel(PoolDev P,
+// Per-head inputs of the KDA kernel into LDS: raw q, k rows and their squared
+// norms, per-row retention, beta, the fit weights (the writer: prepared k and
+// retention).  Every vector load is issued before any value is used (q/k
+// width QW4 and gate width are branch-free runs), after the page's
+// global-to-LDS loads, so all latencies overlap.
+template <int MODE, bool QW4>
+__device__ __forceinline__ void kda_prologue(const PoolDev &P, const StepDev &S, const kfast::KCtx &C) {
+  using namespace kfast;
+  const int64_t bh = (int64_t)C.b * P.H + C.h;
+  const int i = C.tid & (FK - 1);
+  const float w = P.impact[(int64_t)C.h * FK + i];
+  if (MODE == MODE_WRITE) {
+    const float k = S.s_key[bh * FK + i], d = S.s_decay[bh * FK + i];
+    if (C.tid < FK) C.kraw[C.tid] = k;
+    else C.gv[i] = d;
+  } else {
+    const int hk = C.h / (P.H / S.HK);
+    const int64_t qi = (int64_t)C.b * S.q_stride + (int64_t)hk * FK + i;
+    const int64_t ki = (int64_t)C.b * S.k_stride + (int64_t)hk * FK + i;
+    uint32_t qr, kr, gr, dr = 0u;
+    if (QW4) {
+      qr = ((const uint32_t *)S.q)[qi];
+      kr = ((const uint32_t *)S.k)[ki];
+    } else {
+      qr = ((const uint16_t *)S.q)[qi];
+      kr = ((const uint16_t *)S.k)[ki];
+    }
+    float bt, al = 0.0f;
+    const bool g4 = S.gate_dtype == SQ_F32;
+    if (g4) {
+      gr = ((const uint32_t *)S.g)[bh * FK + i];
+      if (S.a_log) dr = ((const uint32_t *)S.dt_bias)[(int64_t)C.h * FK + i];
+      bt = __uint_as_float(ld_uniform((const uint32_t *)S.beta + bh));
+      if (S.a_log) al = __uint_as_float(ld_uniform((const uint32_t *)S.a_log + C.h));
+    } else {
+      gr = ((const uint16_t *)S.g)[bh * FK + i];
+      if (S.a_log) dr = ((const uint16_t *)S.dt_bias)[(int64_t)C.h * FK + i];
+      bt = load_val(S.beta, S.gate_dtype, bh);
+      if (S.a_log) al = load_val(S.a_log, S.gate_dtype, C.h);
+    }
+    const float qv = QW4 ? __uint_as_float(qr) : S.qkv_dtype == SQ_BF16 ? __uint_as_float(qr << 16) : hw_h2f(qr);
+    const float kv = QW4 ? __uint_as_float(kr) : S.qkv_dtype == SQ_BF16 ? __uint_as_float(kr << 16) : hw_h2f(kr);
+    if (C.tid < FK) {
+      C.qraw[C.tid] = qv;
+      C.kraw[C.tid] = kv;
+      const float sq = wave_sum(qv * qv), sk = wave_sum(kv * kv);
+      if ((C.tid & 63) == 0) {
+        C.misc[8 + 2 * (C.tid >> 6)] = sq;
+        C.misc[9 + 2 * (C.tid >> 6)] = sk;
+      }
+    } else {
+      auto gate_val = [&](uint32_t u) {
+        return g4 ? __uint_as_float(u) : S.gate_dtype == SQ_BF16 ? __uint_as_float(u << 16) : hw_h2f(u);
+      };
+      float gv = gate_val(gr);
+      if (S.a_log) {
+        const float u = gv + gate_val(dr);
+        const float sp = u > 20.0f ? u : __logf(1.0f + __expf(u < 20.0f ? u : 20.0f));
+        gv = -__expf(al) * sp;
+      }
+      C.gv[i] = __expf(gv);
+      if (i == 0) C.misc[0] = S.a_log ? 1.0f / (1.0f + __expf(-bt)) : bt;
+    }
+  }
+  if (C.tid >= FK) C.wv[i] = w;
+}
+
+#ifndef KDA128_WAVES
+#define KDA128_WAVES 3
+#endif
+template <int MODE, bool QW4>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KDA128_WAVES))) void kda128_kernel(PoolDev P,
                                                                                                       StepDev S) {
   using namespace kfast;
   extern __shared__ __align__(16) uint8_t smem[];
@@ -2026,26 +2128,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GDN128_WAVE
   C.cg = C.tid >> 3;
   C.wave = C.tid >> 6;
   C.j0 = 4 * C.cg;
+  // slot and head metadata as scalar loads; the page's global-to-LDS loads
+  // go out as soon as they arrive, the per-head inputs after them
   int64_t slot;
-  if (MODE == MODE_WRITE) {
-    slot = S.s_slots[C.b];
-  } else {
-    slot = load_slot(S.slots, S.slots_dtype, C.b);
-    if (MODE == MODE_READ && C.h == 0 && C.tid == 0) S.s_slots[C.b] = slot;
-  }
+  if (MODE == MODE_WRITE) slot = ld_uniform(S.s_slots + C.b);
+  else slot = load_slot_uniform(S.slots, S.slots_dtype, C.b);
+  const int32_t *hm = P.head_meta + 4 * C.h;
+  const int code_start = ld_uniform(hm), code_bytes = ld_uniform(hm + 1);
+  const int row_start = ld_uniform(hm + 2), row_bytes = ld_uniform(hm + 3);
+  const int colbase = ld_uniform(P.columns + C.h);
+  const int stride = ld_uniform(P.offsets + (int64_t)H * FK + C.h);
+  if (MODE == MODE_READ && C.h == 0 && C.tid == 0) S.s_slots[C.b] = slot;
   if (slot <= 0 || slot >= P.num_slots) {
     if (MODE == MODE_FUSED || MODE == MODE_READ)
       for (int j = C.tid; j < FV; j += FNT) store_val(S.out, S.out_dtype, ((int64_t)C.b * H + C.h) * FV + j, 0.0f);
     return;
   }
   C.page = P.data + slot * P.page_bytes;
-  const int32_t *hm = P.head_meta + 4 * C.h;
-  C.code_start = hm[0];
-  C.code_bytes = hm[1];
-  C.row_start = hm[2];
-  C.row_bytes = hm[3];
-  C.colbase = P.columns[C.h];
-  C.stride = P.offsets[(int64_t)H * FK + C.h];
+  C.code_start = code_start;
+  C.code_bytes = code_bytes;
+  C.row_start = row_start;
+  C.row_bytes = row_bytes;
+  C.colbase = colbase;
+  C.stride = stride;
   C.code = smem;
   C.rst = smem + P.stage;
   C.cst = C.rst + P.rstage;
@@ -2065,46 +2170,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GDN128_WAVE
 
   // stage the head's code, row-scale and column-scale regions
   const int pitch = block_pitch(C.stride);
-  stage_in_blocks(C.page + C.code_start, C.stride, pitch, C.code, C.tid);
+  stage_blocks_async(C.page + C.code_start, C.stride, pitch, C.code, C.tid);
   C.lbase = C.cg * pitch + (int)((uintptr_t)(C.page + C.code_start + (int64_t)C.cg * C.stride) & 15);
-  C.shift_r = C.row_bytes > 0 ? stage_in(C.page + C.row_start, C.row_bytes, C.rst, C.tid, FNT) : 0;
-  C.shift_col = C.colbase >= 0 ? stage_in(C.page + C.colbase, 2 * FV, C.cst, C.tid, FNT) : 0;
-  // inputs: raw q, k rows and norms; per-row retention; beta
-  const int64_t bh = (int64_t)C.b * H + C.h;
-  if (MODE == MODE_WRITE) {
-    if (C.tid < FK) C.kraw[C.tid] = S.s_key[bh * FK + C.tid];
-    else C.gv[C.tid - FK] = S.s_decay[bh * FK + C.tid - FK];
-  } else {
-    if (C.tid < FK) {
-      const int hk = C.h / (H / S.HK);
-      const float qv = load_val(S.q, S.qkv_dtype, (int64_t)C.b * S.q_stride + (int64_t)hk * FK + C.tid);
-      const float kv = load_val(S.k, S.qkv_dtype, (int64_t)C.b * S.k_stride + (int64_t)hk * FK + C.tid);
-      C.qraw[C.tid] = qv;
-      C.kraw[C.tid] = kv;
-      const float sq = wave_sum(qv * qv), sk = wave_sum(kv * kv);
-      if ((C.tid & 63) == 0) {
-        C.misc[8 + 2 * (C.tid >> 6)] = sq;
-        C.misc[9 + 2 * (C.tid >> 6)] = sk;
-      }
-    } else {
-      const int i = C.tid - FK;
-      float gv = load_val(S.g, S.gate_dtype, bh * FK + i);
-      if (S.a_log) {
-        const float u = gv + load_val(S.dt_bias, S.gate_dtype, (int64_t)C.h * FK + i);
-        const float sp = u > 20.0f ? u : __logf(1.0f + __expf(u < 20.0f ? u : 20.0f));
-        gv = -__expf(load_val(S.a_log, S.gate_dtype, C.h)) * sp;
-      }
-      C.gv[i] = __expf(gv);
-      if (i == 0) {
-        float bt = load_val(S.beta, S.gate_dtype, bh);
-        if (S.a_log) bt = 1.0f / (1.0f + __expf(-bt));
-        C.misc[0] = bt;
-      }
-    }
-  }
-  if (C.tid >= FK) C.wv[C.tid - FK] = P.impact[(int64_t)C.h * FK + C.tid - FK];
+  C.shift_r = C.row_bytes > 0 ? stage_region_async(C.page + C.row_start, C.row_bytes, C.rst, C.tid) : 0;
+  C.shift_col = C.colbase >= 0 ? stage_region_async(C.page + C.colbase, 2 * FV, C.cst, C.tid) : 0;
+  kda_prologue<MODE, QW4>(P, S, C);
   __syncthreads();
   if (MODE == MODE_READ && C.tid < FK) {
+    const int64_t bh = (int64_t)C.b * H + C.h;
     float nk = 1.0f;
     if (S.normalize) nk = __builtin_amdgcn_rsqf((C.misc[9] + C.misc[11]) + 1e-6f);
     S.s_key[bh * FK + C.tid] = C.kraw[C.tid] * nk;
@@ -3063,7 +3136,12 @@ int launch_step_mode(const sq_pool *pool, StepDev sd, int64_t batch, hipStream_t
     // staging | rows | columns | q,k raw, w, retention | misc | red | ks, qs | rc, rl, rm | pivot mask | spare
     size_t lds = (size_t)pd.stage + pd.rstage + fast::KDA_COL_STAGE + 4 * 128 * 4 + fast::MISC_FLOATS * 4 +
                  4 * 128 * 4 + 2 * 128 * 4 + 3 * 128 * 16 + 16 + 4 * 256;
-    hipLaunchKernelGGL((kda128_kernel<MODE>), dim3((unsigned)(batch * pool->heads)), dim3(256), lds, st, pd, sd);
+    if (MODE == MODE_WRITE || sd.qkv_dtype == SQ_F32)
+      hipLaunchKernelGGL((kda128_kernel<MODE, true>), dim3((unsigned)(batch * pool->heads)), dim3(256), lds, st, pd,
+                         sd);
+    else
+      hipLaunchKernelGGL((kda128_kernel<MODE, MODE == MODE_WRITE>), dim3((unsigned)(batch * pool->heads)), dim3(256),
+                         lds, st, pd, sd);
     return check_launch("kda128_kernel");
   }
   const int K = pool->keys, V = pool->values;
