@@ -869,8 +869,7 @@ __global__ __launch_bounds__(512) void step_kernel(PoolDev P, StepDev S) {
 // The writer works on inner_ij = x'_ij / c_j = a_i z_ij + k_i delta_j / c_j.
 // =====================================================================
 // Four waves per SIMD (128 VGPRs): four workgroups per CU hide the page and
-// input latency of each tile behind the others' arithmetic (a 64-bit address
-// is kept in scratch across the tile, its only spill).
+// input latency of each tile behind the others' arithmetic.
 #ifndef GDN128_WAVES
 #define GDN128_WAVES 4
 #endif
@@ -1154,7 +1153,11 @@ __device__ __forceinline__ void handoff(const PoolDev &P, const StepDev &S, cons
 
 template <int CODE_CHUNKS_PER_LANE>
 __device__ __forceinline__ void stage_back_fast(const Ctx &C, int row_chunks, bool cols) {
-  uint4 *dst = (uint4 *)(C.page + C.code_start);
+  // the offset re-read as a wave-uniform value: the store address is then
+  // formed here from the scalar page base instead of being kept in vector
+  // registers since the loads at the start of the tile
+  const int cs = __builtin_amdgcn_readfirstlane(C.code_start);
+  uint4 *dst = (uint4 *)(C.page + cs);
   const uint4 *src = (const uint4 *)C.code;
 #pragma unroll
   for (int k = 0; k < CODE_CHUNKS_PER_LANE; k++) dst[C.tid + FNT * k] = src[C.tid + FNT * k];
