@@ -31,7 +31,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=1024)
     p.add_argument("--warmup", type=int, default=32)
-    p.add_argument("--batch", type=int, default=256)
+    p.add_argument("--batch", type=int, default=None, help="requests (default 256; prefill: 8)")
     p.add_argument("--heads", type=int, default=32)
     p.add_argument("--key-heads", type=int, default=16)
     p.add_argument("--arch", choices=["gdn", "kda"], default="gdn")
@@ -50,7 +50,10 @@ def parse():
                    help="prefill: configs[4], chunked GDN prefill into 5 prefix slots per request")
     p.add_argument("--seq-len", type=int, default=2048, help="prefill tokens per sequence")
     p.add_argument("--checkpoints", type=int, default=5, help="prefill prefix slots per request")
-    return p.parse_args()
+    a = p.parse_args()
+    if a.batch is None:
+        a.batch = 8 if a.workload == "prefill" else 256
+    return a
 
 
 def make_plan(torch, arch, H, K, nominal, seed=0):
