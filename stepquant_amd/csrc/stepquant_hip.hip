@@ -317,12 +317,14 @@ __device__ __forceinline__ int pivot_pos(const PoolDev &P, int off_rel, int stri
 // the carrier is z (KDA: z * 2^(8 - b), so that x = r c carrier).
 __device__ __forceinline__ int carrier_pos(int plane_rel, int K, int i, int j) { return plane_rel + i + j * K; }
 
+__device__ __forceinline__ int colbase_of(const PoolDev &P, int h) { return P.columns[h]; }
+
 // =====================================================================
 // Encode: dense fp32 -> page, bit-exact fit_state.  Thread j owns column j
 // (NT >= V); rows are processed by thread i in the row phase.
 // =====================================================================
-__global__ __launch_bounds__(256) void encode_kernel(PoolDev P, const float *__restrict__ state,
-                                                     const void *slots, int slots_dtype) {
+__global__ __launch_bounds__(512) void encode_kernel(PoolDev P, const float *__restrict__ state,
+                                                     const void *slots, int slots_dtype, int split) {
   // Every product and sum rounds separately, as PyTorch's CPU ops do.
 #pragma clang fp contract(off)
   extern __shared__ __align__(16) uint8_t smem[];
@@ -343,15 +345,70 @@ __global__ __launch_bounds__(256) void encode_kernel(PoolDev P, const float *__r
   const int stride = P.offsets[(int64_t)H * K + h];
   const float *X = state + ((int64_t)b * H + h) * K * V;
 
-  // LDS: staging window | row scale per (row, group) f32 [K * NG]
+  // LDS: staging window | row scale per (row, group) f32 [K * NG] | with a
+  // row split: per-part column maxima [split][4][V] and 16-row block sums [K/16][2][V]
   uint8_t *stage = smem;
   float *rsc = (float *)(smem + P.stage);
+  float *cmax = rsc + ((K * NG + 3) & ~3);
+  float *bsum = cmax + split * 4 * V;
 
   int shift = 0;
   if (code_bytes > 0) shift = stage_in(page + code_start, code_bytes, stage, tid, NT);
   __syncthreads();
 
-  // ---- row phase: r (and GDN 2-bit group r), pivots
+  // ---- row phase: r (and GDN 2-bit group r), pivots.
+  // Fast form for rows summed in groups of n = 32..256 values (n a multiple
+  // of 32): 32 lanes per row, lane (l, k) = (lane / 4, lane % 4) adds
+  // |x[8(4 ii + k) + l]| for ii ascending, exactly PyTorch's vectorised
+  // inner sum (8 vector lanes, 4 accumulators each, no cascade level below
+  // 512 values); the partial sums are then combined in PyTorch's order:
+  // s_l = ((a_l0 + a_l1) + a_l2) + a_l3, total = (...(s_0 + s_1) + ...) + s_7.
+  // Loads of a row are coalesced.
+  const int ngrp = two ? Geff : V;
+  if (ngrp >= 32 && ngrp <= 256 && (ngrp & 31) == 0 && (NT & 31) == 0) {
+    const int lane = tid & 31, l = lane >> 2, k = lane & 3;
+    const int per_pass = NT >> 5;
+    for (int i = tid >> 5; i < K; i += per_pass) {
+      const float *xr = X + (int64_t)i * V;
+      const int bi = hbits[i];
+      if (bi == 16) {
+        const int off_rel = P.offsets[(int64_t)h * K + i] - code_start;
+        for (int j = lane; j < V; j += 32) {
+          int p = shift + pivot_pos(P, off_rel, stride, tile, j);
+          uint32_t hb = f2h(xr[j]);
+          stage[p] = (uint8_t)hb;
+          stage[p + 1] = (uint8_t)(hb >> 8);
+        }
+        if (lane == 0) rsc[i * NG] = 1.0f;
+        continue;
+      }
+      const float wi = hw[i];
+      const int64_t ro = P.rows[(int64_t)h * K + i];
+      const int ng = two ? NG : 1;
+      for (int g = 0; g < ng; g++) {
+        const float *xg = xr + g * ngrp;
+        float acc = 0.0f;
+        for (int ii = 0; ii < ngrp / 32; ii++) acc += fabsf(xg[8 * (4 * ii + k) + l]);
+        // combine within the quad (k = 0..3) and then over l, in order
+        const float a1 = __shfl_down(acc, 1, 32), a2 = __shfl_down(acc, 2, 32), a3 = __shfl_down(acc, 3, 32);
+        float sl = acc;
+        sl += a1;
+        sl += a2;
+        sl += a3;
+        float total = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 8; q++) total += __shfl(sl, 4 * q, 32);
+        if (lane == 0) {
+          float m = total / (float)ngrp;
+          m = m < 1e-20f ? 1e-20f : m;
+          uint32_t hb;
+          float r = fp16_scale(__builtin_sqrtf(m / wi), &hb);
+          rsc[i * NG + g] = r;
+          put_page_half(page, ro + 2 * g, hb);
+        }
+      }
+    }
+  } else
   for (int i = tid; i < K; i += NT) {
     const float *xr = X + (int64_t)i * V;
     const int bi = hbits[i];
@@ -390,6 +447,111 @@ __global__ __launch_bounds__(256) void encode_kernel(PoolDev P, const float *__r
   }
   __syncthreads();
 
+  // ---- column phase with the rows of every column split over `split`
+  // threads (thread j + V*hf owns rows [hf*K/split, (hf+1)*K/split) of column
+  // j; K is a multiple of 16*split).  PyTorch's key-axis sum of the refit
+  // (V >= 32) adds rows in 16-row blocks, each block from zero, and the block
+  // sums in order; below 512 rows no other level changes the value, so the
+  // blocks are summed in parallel and combined in order.
+  if (split > 1) {
+    const int j = tid % V, hf = tid / V;
+    const int rows = K / split, i0 = hf * rows;
+    const int g = two ? j / P.G : 0;
+    float amax[4] = {0.f, 0.f, 0.f, 0.f};  // widths 2, 4, 6, 8
+    for (int i = i0; i < i0 + rows; i++) {
+      const int bi = hbits[i];
+      if (bi == 16) continue;
+      const float a = fabsf(X[(int64_t)i * V + j] / rsc[i * NG + g]);
+      const int wsel = (bi < 8 ? bi : 8) / 2 - 1;
+#pragma unroll
+      for (int q = 0; q < 4; q++)
+        if (q == wsel) amax[q] = a > amax[q] ? a : amax[q];
+    }
+#pragma unroll
+    for (int q = 0; q < 4; q++) cmax[(hf * 4 + q) * V + j] = amax[q];
+    __syncthreads();
+    float mx = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      float am = 0.0f;
+      for (int u = 0; u < split; u++) {
+        const float a = cmax[(u * 4 + q) * V + j];
+        am = a > am ? a : am;
+      }
+      const int bc = 2 * q + 2;
+      const float qmax = two ? 3.0f : (float)((1 << (bc - 1)) - 1);
+      const float norm = P.kda ? (float)(1 << (8 - bc)) : 1.0f;
+      const float t = am / (qmax * norm);
+      mx = t > mx ? t : mx;
+    }
+    const float c0 = fp16_scale(mx, nullptr);
+    auto z_at = [&](int i, float cdiv) -> float {
+      const int bi = hbits[i];
+      const int bc = bi < 8 ? bi : 8;
+      const float qmax = (float)((1 << (bc - 1)) - 1);
+      const float norm = P.kda ? (float)(1 << (8 - bc)) : 1.0f;
+      const float sc = X[(int64_t)i * V + j] / rsc[i * NG + (bi == 16 ? 0 : g)];
+      float y = sc / cdiv;
+      if (P.kda) y = y * (1.0f / norm);  // exact: norm is a power of two
+      if (two) return (y >= 0.0f ? 1.0f : -1.0f) * (fabsf(y) >= 2.0f ? 3.0f : 1.0f);
+      float z = __builtin_rintf(y);
+      z = z > -qmax ? z : -qmax;
+      z = z < qmax ? z : qmax;
+      return z;
+    };
+    for (int m = i0 / 16; m < (i0 + rows) / 16; m++) {
+      float bn = 0.0f, bd = 0.0f;
+      for (int i = 16 * m; i < 16 * m + 16; i++) {
+        const int bi = hbits[i];
+        const int bc = bi < 8 ? bi : 8;
+        const float norm = P.kda ? (float)(1 << (8 - bc)) : 1.0f;
+        const float wsq = (hw[i] * hw[i]) * (bi != 16 ? 1.0f : 0.0f);
+        const float z = z_at(i, c0);
+        const float v = (rsc[i * NG + (bi == 16 ? 0 : g)] * norm) * z;
+        bn += (wsq * v) * X[(int64_t)i * V + j];
+        bd += wsq * (v * v);
+      }
+      bsum[(2 * m) * V + j] = bn;
+      bsum[(2 * m + 1) * V + j] = bd;
+    }
+    __syncthreads();
+    float num = 0.0f, den = 0.0f;
+    for (int m = 0; m < K / 16; m++) {
+      num += bsum[(2 * m) * V + j];
+      den += bsum[(2 * m + 1) * V + j];
+    }
+    const float denc = den < 1e-30f ? 1e-30f : den;
+    uint32_t chb;
+    const float c = fp16_scale(den > 0.0f ? num / denc : c0, &chb);
+    if (hf == 0 && colbase_of(P, h) >= 0) put_page_half(page, colbase_of(P, h) + 2 * (int64_t)j, chb);
+    // final codes of this thread's rows; quads of lanes assemble 4-value groups
+    for (int i = i0; i < i0 + rows; i++) {
+      const int bi = hbits[i];
+      uint32_t code = 0;
+      if (bi != 16) {
+        const int bc = bi < 8 ? bi : 8;
+        const float z = z_at(i, c);
+        if (P.storage) {
+          const int carrier = P.kda ? (int)z * (1 << (8 - bc)) : (int)z;
+          stage[shift + carrier_pos(stride - code_start, K, i, j)] = (uint8_t)(int8_t)carrier;
+          continue;
+        }
+        code = two ? (uint32_t)(((int)z + 3) / 2) : (uint32_t)((int)z + ((1 << (bc - 1)) - 1));
+      } else if (P.storage) {
+        continue;
+      }
+      const uint32_t c1 = __shfl_xor(code, 1), c2 = __shfl_xor(code, 2), c3 = __shfl_xor(code, 3);
+      if (bi != 16 && (tid & 3) == 0) {
+        const uint32_t word = code | (c1 << bi) | (c2 << (2 * bi)) | (c3 << (3 * bi));
+        const int off_rel = P.offsets[(int64_t)h * K + i] - code_start;
+        lds_put_bytes(stage, shift + group_pos(off_rel, stride, tile, j, bi), word, bi / 2);
+      }
+    }
+    __syncthreads();
+    if (code_bytes > 0) stage_out(page + code_start, code_bytes, stage, tid, NT);
+    return;
+  }
+
   // ---- column phase (thread j <-> column j; lanes of a quad are adjacent columns)
   const int colbase = P.columns[h];
   for (int jb = 0; jb < V; jb += NT) {
@@ -397,16 +559,26 @@ __global__ __launch_bounds__(256) void encode_kernel(PoolDev P, const float *__r
     const bool act = j < V;
     const int jj = act ? j : V - 1;
     const int g = two ? jj / P.G : 0;
-    // pass 1: c0 = fp16(max_i where(int, |x/r|/(qmax*norm), 0))
-    float mx = 0.0f;
+    // pass 1: c0 = fp16(max_i where(int, |x/r|/(qmax*norm), 0)).  Division
+    // by a positive constant is monotone, so the maximum of the quotients is
+    // the quotient of the largest |x/r| among the rows of each width.
+    float amax[4] = {0.f, 0.f, 0.f, 0.f};  // widths 2, 4, 6, 8
     for (int i = 0; i < K; i++) {
-      int bi = hbits[i];
+      const int bi = hbits[i];
       if (bi == 16) continue;
-      int bc = bi < 8 ? bi : 8;
-      float qmax = two ? 3.0f : (float)((1 << (bc - 1)) - 1);
-      float norm = P.kda ? (float)(1 << (8 - bc)) : 1.0f;
-      float sc = X[(int64_t)i * V + jj] / rsc[i * NG + g];
-      float t = fabsf(sc) / (qmax * norm);
+      const float a = fabsf(X[(int64_t)i * V + jj] / rsc[i * NG + g]);
+      const int wsel = (bi < 8 ? bi : 8) / 2 - 1;
+#pragma unroll
+      for (int q = 0; q < 4; q++)
+        if (q == wsel) amax[q] = a > amax[q] ? a : amax[q];
+    }
+    float mx = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const int bc = 2 * q + 2;
+      const float qmax = two ? 3.0f : (float)((1 << (bc - 1)) - 1);
+      const float norm = P.kda ? (float)(1 << (8 - bc)) : 1.0f;
+      const float t = amax[q] / (qmax * norm);
       mx = t > mx ? t : mx;
     }
     const float c0 = fp16_scale(mx, nullptr);
@@ -418,7 +590,7 @@ __global__ __launch_bounds__(256) void encode_kernel(PoolDev P, const float *__r
       float norm = P.kda ? (float)(1 << (8 - bc)) : 1.0f;
       float sc = X[(int64_t)i * V + jj] / rsc[i * NG + (bi == 16 ? 0 : g)];
       float y = sc / cdiv;
-      if (P.kda) y = y / norm;
+      if (P.kda) y = y * (1.0f / norm);  // exact: norm is a power of two
       if (two) return (y >= 0.0f ? 1.0f : -1.0f) * (fabsf(y) >= 2.0f ? 3.0f : 1.0f);
       float z = __builtin_rintf(y);
       z = z > -qmax ? z : -qmax;
@@ -440,8 +612,15 @@ __global__ __launch_bounds__(256) void encode_kernel(PoolDev P, const float *__r
       cn.init(K);
       cd.init(K);
       for (int i = 0; i < K; i++) {
-        cn.push(term(i, true));
-        cd.push(term(i, false));
+        // term(i, true) and term(i, false) with one z
+        const int bi = hbits[i];
+        const int bc = bi < 8 ? bi : 8;
+        const float norm = P.kda ? (float)(1 << (8 - bc)) : 1.0f;
+        const float wsq = (hw[i] * hw[i]) * (bi != 16 ? 1.0f : 0.0f);
+        const float z = z_of(i, c0);
+        const float v = (rsc[i * NG + (bi == 16 ? 0 : g)] * norm) * z;
+        cn.push((wsq * v) * X[(int64_t)i * V + jj]);
+        cd.push(wsq * (v * v));
       }
       cn.finish(&num);
       cd.finish(&den);
@@ -3284,10 +3463,16 @@ int sq_encode(const sq_pool *pool, const float *state, const void *slots, int32_
   if (slots_dtype != SQ_I32 && slots_dtype != SQ_I64) return fail(SQ_EINVAL, "encode: slots dtype");
   PoolDev pd = to_dev(pool);
   const int NG = (!pool->kda) ? pool->values / pd.G : 1;
-  size_t lds = (size_t)stage_bytes(pool) + (size_t)pool->keys * NG * 4 + 16;
-  const int NT = pool->values < 64 ? 64 : pool->values;  // one lane per value column
+  const int K = pool->keys, V = pool->values;
+  // rows of a column split over up to 4 threads (whole 16-row blocks each)
+  int split = V >= 32 ? 512 / V : 1;
+  split = split > 4 ? 4 : split;
+  while (split > 1 && K % (16 * split)) split >>= 1;
+  const int NT = split > 1 ? split * V : (V < 64 ? 64 : V);  // lanes per value column
+  size_t lds = (size_t)stage_bytes(pool) + (size_t)((K * NG + 3) & ~3) * 4 + 16;
+  if (split > 1) lds += (size_t)split * 4 * V * 4 + (size_t)(K / 16) * 2 * V * 4;
   hipLaunchKernelGGL(encode_kernel, dim3((unsigned)(batch * pool->heads)), dim3(NT), lds, (hipStream_t)stream, pd,
-                     state, slots, slots_dtype);
+                     state, slots, slots_dtype, split);
   return check_launch("encode_kernel");
 }
 
