@@ -49,6 +49,8 @@ def parse():
     p.add_argument("--workload", choices=["decode", "prefill"], default="decode",
                    help="prefill: configs[4], chunked GDN prefill into 5 prefix slots per request")
     p.add_argument("--seq-len", type=int, default=2048, help="prefill tokens per sequence")
+    p.add_argument("--state-format", default="stepquant",
+                   help="decode on a baseline-format pool (fp32, sym_int{4,6,8}_g128, dsq_int{4,6}) instead")
     p.add_argument("--checkpoints", type=int, default=5, help="prefill prefix slots per request")
     a = p.parse_args()
     if a.batch is None:
@@ -207,9 +209,19 @@ def main():
     dev = torch.device("cuda:0")
     B, H, HK, K, V = a.batch, a.heads, a.key_heads, 128, 128
     bits, impact = make_plan(torch, a.arch, H, K, a.nominal)
-    plan = QuantizationPlan(a.arch, bits.to(dev), impact.to(dev))
     stream = torch.cuda.Stream() if a.async_writeback else None
-    pool = PackedStatePool(plan, B + 1, V, writeback_stream=stream)
+    if a.state_format != "stepquant":
+        from stepquant_amd.formats import FormatPlan, get_format
+        from stepquant_amd.kernels.format_pool import FormatStatePool
+        spec = get_format(a.state_format)
+        bits = torch.full((H, K), spec.bits, dtype=torch.long)
+        impact = torch.ones(H, K)
+        pool = FormatStatePool(FormatPlan(a.arch, bits.to(dev), impact.to(dev)), B + 1, V, spec)
+        stream = None
+        a.cpu_sample = 0  # the CPU port restates the STEPQuant path only
+    else:
+        plan = QuantizationPlan(a.arch, bits.to(dev), impact.to(dev))
+        pool = PackedStatePool(plan, B + 1, V, writeback_stream=stream)
     g = torch.Generator(device=dev).manual_seed(0)
     slots = torch.arange(1, B + 1, device=dev, dtype=torch.int32)
     if a.nominal == 4:
@@ -263,6 +275,8 @@ def main():
     updates = B * H / (ms_step * 1e-3)
     # measured HBM bytes per launch apply only to the workload they were taken on
     key = f"{a.arch}-{a.nominal}-b{B}-h{H}-hk{HK}-{'async' if stream is not None else 'fused'}"
+    if a.state_format != "stepquant":
+        key = f"{a.state_format}-{a.arch}-b{B}-h{H}-hk{HK}"
     traffic = None
     if a.traffic and os.path.exists(a.traffic):
         meas = json.load(open(a.traffic))
@@ -279,7 +293,9 @@ def main():
     line = dict(metric=METRIC, value=round(updates, 1), unit="state-head updates/s", n_gpus=1, steps=a.steps,
                 warmup=a.warmup, ms_per_step=round(ms_step, 6), higher_is_better=True, scaling="weak",
                 vs_baseline=None, dtype="f32", data="synthetic",
-                config=dict(workload=f"{a.arch.upper()} decode STEPQuant@{a.nominal}, one layer, B={B}, H={H}, "
+                config=dict(workload=(f"{a.arch.upper()} decode STEPQuant@{a.nominal}" if a.state_format == "stepquant"
+                                      else f"{a.arch.upper()} decode {a.state_format} pages")
+                                     + f", one layer, B={B}, H={H}, "
                                      f"HK={HK}, dk=dv={K}, bf16 q/k/v, raw gates, graph-replayed steps"
                                      + (", async writeback" if stream is not None else ", fused writeback"),
                             page_bytes=page, global_batch=B, wall_s=round(wall, 3)),

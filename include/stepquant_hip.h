@@ -271,8 +271,10 @@ typedef struct sq_format_pool {
     int32_t bits;       /* code width (32 for SQ_FMT_FP32) */
     int32_t group;      /* value group of SQ_FMT_SYMMETRIC (128) */
     int32_t kda;        /* 1: per-key-row retention g [B, H*K] */
-    int32_t reserved;
+    int32_t flags;      /* SQ_FMT_ROWS_CONTIGUOUS: offsets[h*K + i] = offsets[0] + (h*K + i) * V * bits / 8 */
 } sq_format_pool;
+
+#define SQ_FMT_ROWS_CONTIGUOUS 1
 
 /*
  * Dense fp32 [B,H,K,V] -> pages (FormatStatePool.encode, format_pool.py:68-80);

@@ -59,10 +59,11 @@ class FormatPool(ctypes.Structure):
                 ("offsets", _P), ("rows", _P), ("columns", _P), ("heads", ctypes.c_int32),
                 ("keys", ctypes.c_int32), ("values", ctypes.c_int32), ("kind", ctypes.c_int32),
                 ("bits", ctypes.c_int32), ("group", ctypes.c_int32), ("kda", ctypes.c_int32),
-                ("reserved", ctypes.c_int32)]
+                ("flags", ctypes.c_int32)]
 
 
 FMT_FP32, FMT_SYMMETRIC, FMT_DSQ = 0, 1, 2
+FMT_ROWS_CONTIGUOUS = 1
 
 EXPORTS = ("sq_abi_version", "sq_last_error", "sq_encode", "sq_decode_dense", "sq_decode_step",
            "sq_decode_readout", "sq_writeback", "sq_clear_slots", "sq_copy_slots",

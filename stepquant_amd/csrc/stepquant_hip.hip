@@ -1108,8 +1108,8 @@ struct Ctx {
   uint8_t *cst;    // staged column scales
   float *qraw, *kraw, *wv, *misc, *red;
   float *ks, *qs;  // per-row prepared k, q
-  float4 *rc;      // per (row, group): k*a, q*a, ZS*a, a with a = r * retention
-  float2 *iu;      // per (row, group): 1/r', w^2 r'^2
+  float4 *rc;      // per (group, row), at [g*128 + i]: k*a, q*a, ZS*a, a with a = r * retention
+  float2 *iu;      // per (group, row), at [g*128 + i]: 1/r', w^2 r'^2
   int b, h, tid, rg, cg, wave, j0, blk, sub;
   int code_start, code_bytes, row_start, row_bytes, colbase;
 };
@@ -1156,7 +1156,7 @@ __device__ __forceinline__ void row_setup_int(const StepDev &S, const Ctx &C, in
         const float a = hw_h2f(r16[i * NG + g]) * retention;
         ska[g] = k * a;
         sqa[g] = q * a;
-        C.rc[i * NG + g] = make_float4(ska[g], sqa[g], ZS * a, a);
+        C.rc[g * FK + i] = make_float4(ska[g], sqa[g], ZS * a, a);
       }
     }
     if (MODE != MODE_WRITE) {
@@ -1416,10 +1416,10 @@ __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx
   for (int c = 0; c < 4; c++) cj[c] = hw_h2f(c16[C.j0 + c]);
 
   // per-lane row pointers: row rg + 8r of this lane's value group
-  const float4 *rcl = C.rc + C.rg * NG + g;
-  const float2 *iul = C.iu + C.rg * NG + g;
+  const float4 *rcl = C.rc + g * FK + C.rg;
+  const float2 *iul = C.iu + g * FK + C.rg;
   const float *ksl = C.ks + C.rg;
-  const int RS8 = 8 * NG;  // row stride of rcl / iul for 8 rows
+  const int RS8 = 8;  // row stride of rcl / iul for 8 rows (group-major [g][i]: no bank conflicts)
 
   // ---- foreground: codes, k^T x and q^T x sums
   float cf[FRPT][4];
@@ -1530,7 +1530,7 @@ __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx
       uint32_t hb;
       const float wi = C.wv[i];
       const float rn = hw_fp16_scale(__builtin_sqrtf(m / wi), &hb);
-      C.iu[e] = make_float2(rcp(rn), (wi * wi) * (rn * rn));
+      C.iu[gq * FK + i] = make_float2(rcp(rn), (wi * wi) * (rn * rn));
       ((uint16_t *)C.rst)[e] = (uint16_t)hb;
     }
   }
@@ -1591,9 +1591,9 @@ __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx
       if (W == 8) word = w32[r * 4 * W];
       else if (W == 4) word = *(const uint16_t *)(C.code + pos0 + r * 8 * SEG);
       else word = __builtin_amdgcn_alignbit(w32[r * 4 * W + 1], w32[r * 4 * W], sh);
-      const float4 rc = C.rc[i * NG + g];
+      const float4 rc = C.rc[g * FK + i];
       const float k = C.ks[i];
-      const float2 iu = C.iu[i * NG + g];
+      const float2 iu = C.iu[g * FK + i];
       word ^= XM;
 #pragma unroll
       for (int c = 0; c < 4; c++) {
@@ -2956,6 +2956,7 @@ struct FmtDev {
   int64_t page_bytes, num_slots;
   const int32_t *offsets, *rows, *columns;
   int H, K, V, kind, bits, kda;
+  int stage;        // bytes of LDS staging for the head's code rows (0: rows read from the page)
   const float *in;  // FMT_ENCODE: dense [B, H, K, V]
   float *dense;     // FMT_DECODE: dense [B, H, K, V]
   const void *slots;
@@ -2997,13 +2998,24 @@ __global__ __launch_bounds__(256) void format_kernel(FmtDev F, StepDev S) {
   uint8_t *page = F.data + slot * F.page_bytes;
   const int W = F.bits;
   const int L = (1 << ((W < 8 ? W : 8) - 1)) - 1;
-  // LDS: q, k, retention per row | misc | per-row scale | reduction space
-  float *qs = (float *)smem;
+  // LDS: staged code rows | q, k, retention per row | misc | per-row scale | reduction space
+  uint8_t *stg = smem;
+  float *qs = (float *)(smem + F.stage);
   float *ks = qs + 128;
   float *ds = ks + 128;
   float *misc = ds + 128;
   float *rowv = misc + 16;
   float *big = rowv + 128;
+
+  // Code rows of the head are one contiguous region (every row has the same
+  // width): staged through LDS with 16-byte loads and stores instead of
+  // per-lane byte accesses.
+  const bool staged = F.stage > 0;
+  const int64_t code_start = staged ? F.offsets[(int64_t)h * K] : 0;
+  const int64_t code_bytes = (int64_t)K * V * W / 8;
+  int shift = staged ? (int)((uintptr_t)(page + code_start) & 15) : 0;
+  if (staged && MODE != FMT_ENCODE) shift = stage_in(page + code_start, code_bytes, stg, tid, 256);
+  if (staged) __syncthreads();
 
   float beta = 0.0f;
   if (MODE == FMT_STEP) {
@@ -3078,7 +3090,8 @@ __global__ __launch_bounds__(256) void format_kernel(FmtDev F, StepDev S) {
         for (int c = 0; c < 4; c++) x[r][c] = fr[c];
         continue;
       }
-      const uint32_t word = fmt_read_codes(row, j0, W);
+      const uint32_t word = staged ? lds_word(stg, shift + (int)(((int64_t)i * V + j0) * W / 8))
+                                   : fmt_read_codes(row, j0, W);
       const int64_t ro = F.rows[(int64_t)h * K + i];
       if (F.kind == SQ_FMT_SYMMETRIC) {
         const int64_t meta = ro + 4 * (j0 / FMT_TV);
@@ -3230,7 +3243,12 @@ __global__ __launch_bounds__(256) void format_kernel(FmtDev F, StepDev S) {
       q = q < Lf ? q : Lf;
       word |= (uint32_t)(int)(q + Lf) << (c * W);
     }
-    fmt_write_codes(page + F.offsets[(int64_t)h * K + i], j0, W, word);
+    if (staged) lds_put_bytes(stg, shift + (int)(((int64_t)i * V + j0) * W / 8), word, W / 2);
+    else fmt_write_codes(page + F.offsets[(int64_t)h * K + i], j0, W, word);
+  }
+  if (staged) {
+    __syncthreads();
+    stage_out(page + code_start, code_bytes, stg, tid, 256);
   }
 }
 
@@ -3411,6 +3429,8 @@ int validate_format(const sq_format_pool *f) {
 FmtDev to_fmt(const sq_format_pool *f) {
   FmtDev d;
   memset(&d, 0, sizeof(d));
+  if ((f->flags & SQ_FMT_ROWS_CONTIGUOUS) && f->kind != SQ_FMT_FP32 && f->values <= 128)
+    d.stage = (int)(((int64_t)f->keys * f->values * f->bits / 8 + 47) & ~15);
   d.data = f->data;
   d.page_bytes = f->page_bytes;
   d.num_slots = f->num_slots;
@@ -3431,7 +3451,7 @@ int launch_format(const sq_format_pool *f, const FmtDev &fd, const StepDev &sd, 
   if (batch == 0) return 0;
   if (batch * f->heads > 0x7fffffffLL) return fail(SQ_EINVAL, "format: batch * heads too large");
   const int TV = f->values < FMT_TV ? f->values : FMT_TV;
-  size_t lds = FMT_SMALL_LDS;
+  size_t lds = FMT_SMALL_LDS + (size_t)fd.stage;
   if (MODE != FMT_DECODE) {
     if (f->kind == SQ_FMT_SYMMETRIC) lds += (size_t)(TV / 4) * f->keys * 4;
     if (f->kind == SQ_FMT_DSQ) lds += (size_t)f->keys * (TV + 1) * 4;

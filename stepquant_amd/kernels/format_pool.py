@@ -103,7 +103,9 @@ class FormatStatePool(PackedStatePool):
             data=self._pages.data_ptr(), page_bytes=self.page_bytes, num_slots=slots,
             offsets=self.offsets.data_ptr(), rows=self.rows.data_ptr(), columns=self.columns.data_ptr(),
             heads=self.heads, keys=self.keys, values=value_dim, kind=_KINDS[spec.kind], bits=spec.bits,
-            group=spec.group_size, kda=int(plan.architecture == "kda"), reserved=0)
+            group=spec.group_size, kda=int(plan.architecture == "kda"),
+            flags=N.FMT_ROWS_CONTIGUOUS if all(o == offsets[0] + r * (value_dim * spec.bits // 8)
+                                               for r, o in enumerate(offsets)) else 0)
         # page operations (clear, copy) read only data, page_bytes and num_slots
         self._desc = N.Pool(data=self._pages.data_ptr(), page_bytes=self.page_bytes, num_slots=slots)
 

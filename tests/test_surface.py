@@ -49,7 +49,7 @@ def test_invalid_arguments_are_reported_without_a_device():
     assert rc == -22 and b"format pool" in lib.sq_last_error()
     # a DSQ pool wider than 128 values is rejected before any device access
     fmt = N.FormatPool(data=1, page_bytes=1024, num_slots=2, offsets=1, rows=1, columns=1, heads=1, keys=32,
-                       values=256, kind=N.FMT_DSQ, bits=4, group=128, kda=0, reserved=0)
+                       values=256, kind=N.FMT_DSQ, bits=4, group=128, kda=0, flags=0)
     assert lib.sq_format_encode(fmt, None, None, 4, 0, None) == -23
 
 
