@@ -31,44 +31,17 @@ namespace {
 
 __device__ __forceinline__ float bits_to_f32(uint32_t u) { return __uint_as_float(u); }
 
-// IEEE half -> float, exact for every input (subnormals included).
-__device__ __forceinline__ float h2f(uint32_t h) {
-  uint32_t sign = (h & 0x8000u) << 16;
-  uint32_t e = (h >> 10) & 0x1fu;
-  uint32_t m = h & 0x3ffu;
-  if (e == 0) {
-    // subnormal or zero: m * 2^-24, exact in float
-    float v = (float)m * 5.9604644775390625e-08f;
-    return __uint_as_float(__float_as_uint(v) | sign);
-  }
-  if (e == 31) return __uint_as_float(sign | 0x7f800000u | (m << 13));
-  return __uint_as_float(sign | ((e + 112u) << 23) | (m << 13));
-}
-
-// float -> IEEE half bits, round to nearest even (torch .half()).
+// IEEE half <-> float by the hardware conversions (v_cvt_f32_f16,
+// v_cvt_f16_f32): exact one way, round to nearest even the other, subnormal
+// halves kept (f16 denormals are on in these kernels), overflow to infinity:
+// torch's .half() for every non-NaN input.
+__device__ __forceinline__ float h2f(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
+// The empty asm keeps the conversion apart from the operation that produced
+// f: merged into one v_fma_mixlo_f16 the pair would round once instead of to
+// fp32 first and then to half, as the fp32 reference does.
 __device__ __forceinline__ uint32_t f2h(float f) {
-  uint32_t x = __float_as_uint(f);
-  uint32_t sign = (x >> 16) & 0x8000u;
-  uint32_t ax = x & 0x7fffffffu;
-  if (ax >= 0x7f800000u) return sign | 0x7c00u | (ax > 0x7f800000u ? 0x200u : 0u);
-  if (ax >= 0x477ff000u) return sign | 0x7c00u;
-  if (ax < 0x38800000u) {
-    if (ax < 0x33000000u) return sign;
-    uint32_t e = ax >> 23;
-    uint32_t m = (ax & 0x7fffffu) | 0x800000u;
-    uint32_t shift = 126u - e;
-    uint32_t q = m >> shift;
-    uint32_t rem = m & ((1u << shift) - 1u);
-    uint32_t half = 1u << (shift - 1u);
-    if (rem > half || (rem == half && (q & 1u))) q++;
-    return sign | q;
-  }
-  uint32_t e = (ax >> 23) - 112u;
-  uint32_t m = ax & 0x7fffffu;
-  uint32_t q = (e << 10) | (m >> 13);
-  uint32_t rem = m & 0x1fffu;
-  if (rem > 0x1000u || (rem == 0x1000u && (q & 1u))) q++;
-  return sign | q;
+  asm("" : "+v"(f));
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
 
 // quantization.py:49-51: clamp(2^-24, 65504).half().float()
@@ -80,10 +53,11 @@ __device__ __forceinline__ float fp16_scale(float x, uint32_t *hbits) {
   return h2f(h);
 }
 
+// float -> bfloat16 bits by v_cvt_pk_bf16_f32 (round to nearest even, as
+// torch's .bfloat16() for every non-NaN input)
 __device__ __forceinline__ uint32_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
-  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  asm("" : "+v"(f));  // a separate rounding step, as for f2h
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
 }
 
 __device__ __forceinline__ float load_val(const void *p, int dtype, int64_t idx) {
@@ -1084,6 +1058,36 @@ __device__ __forceinline__ float rg8_max_nonneg(float x) {
   return __uint_as_float(u);
 }
 
+// Reduce-scatter of four per-column values over the 8 row-group lanes: every
+// lane ends with the full reduction of column (rg >> 1) of its four.  Lane
+// partners rg ^ 7 (row_half_mirror, other bit 2), rg ^ 2 and rg ^ 1: after
+// each exchange a lane keeps the half of its columns that matches its bit.
+template <class OP>
+__device__ __forceinline__ uint32_t rs4(const uint32_t v[4], int rg, OP op) {
+  const bool b2 = rg & 4, b1 = rg & 2;
+  const uint32_t m0 = op(b2 ? v[2] : v[0], dpp_u<0x141>(b2 ? v[0] : v[2]));
+  const uint32_t m1 = op(b2 ? v[3] : v[1], dpp_u<0x141>(b2 ? v[1] : v[3]));
+  const uint32_t m = op(b1 ? m1 : m0, dpp_u<0x4E>(b1 ? m0 : m1));
+  return op(m, dpp_u<0xB1>(m));
+}
+__device__ __forceinline__ float rs4_sum(const float v[4], int rg) {
+  const uint32_t u[4] = {__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])};
+  return __uint_as_float(
+      rs4(u, rg, [](uint32_t a, uint32_t b) { return __float_as_uint(__uint_as_float(a) + __uint_as_float(b)); }));
+}
+// maximum of non-negative floats, compared as integers
+__device__ __forceinline__ float rs4_max_nonneg(const float v[4], int rg) {
+  const uint32_t u[4] = {__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])};
+  return __uint_as_float(rs4(u, rg, [](uint32_t a, uint32_t b) { return a > b ? a : b; }));
+}
+// the value of column c (held by row-group lanes 2c, 2c + 1) in every lane
+// of the group: ds_swizzle in bit mode reads lane (lane & 0x18) | 2c of each
+// 32-lane half, on the LDS crossbar (no VALU work)
+template <int c>
+__device__ __forceinline__ float from_col(float x) {
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x18 | ((2 * c) << 5)));
+}
+
 __device__ __forceinline__ float hw_h2f(uint32_t h) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
@@ -1238,7 +1242,7 @@ __device__ __forceinline__ void stage_async(const Ctx &C, int row_chunks, bool c
 // is used (the q/k/v element width QW is a compile-time choice), so all
 // their latencies overlap in one round trip.  F32 gate scalars are scalar
 // loads.
-template <int MODE, bool QW4>
+template <int MODE, bool QW4, bool COLV = false>
 __device__ __forceinline__ void prologue(const PoolDev &P, const StepDev &S, const Ctx &C, uint32_t vraw[4]) {
   const int64_t bh = (int64_t)C.b * P.H + C.h;
   const float w = P.impact[(int64_t)C.h * FK + (C.tid & (FK - 1))];
@@ -1250,17 +1254,20 @@ __device__ __forceinline__ void prologue(const PoolDev &P, const StepDev &S, con
     if (C.tid == FK) C.misc[1] = d;
   } else {
     const int hk = C.h / (P.H / S.HK);
-    const int i = C.tid & (FK - 1);  // waves 2, 3 read rows too (no divergence); threads < 128 use them
+    const int i = C.tid & (FK - 1);  // every wave reads rows (no divergence); threads >= 128 keep them
     const int64_t qi = (int64_t)C.b * S.q_stride + (int64_t)hk * FK + i;
     const int64_t ki = (int64_t)C.b * S.k_stride + (int64_t)hk * FK + i;
-    const int64_t vi = (int64_t)C.b * S.v_stride + (int64_t)C.h * FV + C.j0;
+    // COLV: only this lane's readout column j0 + (rg >> 1), in vraw[0]
+    const int64_t vi = (int64_t)C.b * S.v_stride + (int64_t)C.h * FV + C.j0 + (COLV ? C.rg >> 1 : 0);
     uint32_t qr, kr;
     if (QW4) {
-      __builtin_memcpy(vraw, (const float *)S.v + vi, 16);
+      if (COLV) vraw[0] = ((const uint32_t *)S.v)[vi];
+      else __builtin_memcpy(vraw, (const float *)S.v + vi, 16);
       qr = ((const uint32_t *)S.q)[qi];
       kr = ((const uint32_t *)S.k)[ki];
     } else {
-      __builtin_memcpy(vraw, (const uint16_t *)S.v + vi, 8);
+      if (COLV) vraw[0] = ((const uint16_t *)S.v)[vi];
+      else __builtin_memcpy(vraw, (const uint16_t *)S.v + vi, 8);
       qr = ((const uint16_t *)S.q)[qi];
       kr = ((const uint16_t *)S.k)[ki];
     }
@@ -1282,17 +1289,19 @@ __device__ __forceinline__ void prologue(const PoolDev &P, const StepDev &S, con
     }
     const float qv = QW4 ? __uint_as_float(qr) : S.qkv_dtype == SQ_BF16 ? __uint_as_float(qr << 16) : hw_h2f(qr);
     const float kv = QW4 ? __uint_as_float(kr) : S.qkv_dtype == SQ_BF16 ? __uint_as_float(kr << 16) : hw_h2f(kr);
-    if (C.tid < FK) {
-      C.qraw[C.tid] = qv;
-      C.kraw[C.tid] = kv;
+    // waves 2 and 3 store the rows and their norms, wave 0 the gates: waves
+    // 0 and 1 set up the rows after the barrier, waves 2 and 3 fit r'
+    if (C.tid >= FK) {
+      C.qraw[i] = qv;
+      C.kraw[i] = kv;
       const float sq = wave_sum(qv * qv), sk = wave_sum(kv * kv);
       if ((C.tid & 63) == 0) {
-        C.misc[8 + 2 * (C.tid >> 6)] = sq;
-        C.misc[9 + 2 * (C.tid >> 6)] = sk;
+        C.misc[8 + 2 * ((C.tid - FK) >> 6)] = sq;
+        C.misc[9 + 2 * ((C.tid - FK) >> 6)] = sk;
       }
-    } else if (C.tid == FK) {
+    } else if (C.tid == 0) {
       if (S.a_log) {
-        bt = 1.0f / (1.0f + __expf(-bt));
+        bt = __builtin_amdgcn_rcpf(1.0f + __expf(-bt));
         const float u = gv + dtb;
         const float sp = u > 20.0f ? u : __logf(1.0f + __expf(u < 20.0f ? u : 20.0f));
         gv = -__expf(al) * sp;
@@ -1301,7 +1310,7 @@ __device__ __forceinline__ void prologue(const PoolDev &P, const StepDev &S, con
       C.misc[1] = __expf(gv);
     }
   }
-  if (C.tid >= FK) C.wv[C.tid - FK] = w;
+  if (C.tid < FK) C.wv[C.tid] = w;
 }
 
 // this lane's v (the writer: delta) from its raw bits
@@ -1316,6 +1325,13 @@ __device__ __forceinline__ void raw_v(const StepDev &S, const uint32_t vraw[4], 
       v[c] = S.qkv_dtype == SQ_BF16 ? __uint_as_float(h << 16) : hw_h2f(h);
     }
   }
+}
+
+// one value of v from its raw bits (the prologue's COLV load)
+template <bool QW4>
+__device__ __forceinline__ float raw_v1(const StepDev &S, uint32_t bits) {
+  if (QW4) return __uint_as_float(bits);
+  return S.qkv_dtype == SQ_BF16 ? __uint_as_float(bits << 16) : hw_h2f(bits);
 }
 
 // Writer hand-off of the readout pass: prepared key rows and per-row retention.
@@ -1343,6 +1359,22 @@ __device__ __forceinline__ void stage_back_fast(const Ctx &C, int row_chunks, bo
   if (C.tid < row_chunks) ((uint4 *)(C.page + C.row_start))[C.tid] = ((const uint4 *)C.rst)[C.tid];
   if (cols && C.tid >= FNT - 16)
     ((uint4 *)(C.page + C.colbase))[C.tid - (FNT - 16)] = ((const uint4 *)C.cst)[C.tid - (FNT - 16)];
+}
+
+// x through an empty asm: the compiler cannot reuse an earlier value derived
+// from it, so addresses formed from it late are not kept in registers (or
+// spilled) across the whole tile
+__device__ __forceinline__ int opaque(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+// byte offset of this lane's first code row segment in the staged region:
+// rows rg + 8r follow 8 * 2W bytes apart
+template <int W>
+__device__ __forceinline__ int code_pos0(int tid) {
+  const int cg = tid >> 3;
+  return (cg >> 2) * (FK * 2 * W) + (tid & 7) * (2 * W) + (cg & 3) * (W / 2);
 }
 
 // signed W-bit field c of a word (sign-extended)
@@ -1404,7 +1436,7 @@ __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx
   const uint16_t *c16 = (const uint16_t *)C.cst;
   stage_async<W / 2>(C, 16 * NG, true);
   uint32_t vraw[4];
-  prologue<MODE, QW4>(P, S, C, vraw);
+  prologue<MODE, QW4, MODE != MODE_WRITE>(P, S, C, vraw);
   __syncthreads();
   const float beta = C.misc[0];
   handoff<MODE>(P, S, C);
@@ -1425,7 +1457,7 @@ __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx
   float cf[FRPT][4];
   float aK[4] = {0.f, 0.f, 0.f, 0.f}, aQ[4] = {0.f, 0.f, 0.f, 0.f};
   // rows rg + 8r are 8*SEG bytes apart: one base address, immediate offsets
-  const int pos0 = C.blk * BLK + C.rg * SEG + C.sub * (W / 2);
+  const int pos0 = code_pos0<W>(C.tid);
   const uint32_t *w32 = (const uint32_t *)(C.code + (pos0 & ~3));
   const uint32_t sh = (uint32_t)(pos0 & 3) * 8u;
 #pragma unroll
@@ -1448,29 +1480,38 @@ __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx
       }
     }
   }
-  float delta[4], o[4], vv[4];
-  raw_v<MODE, QW4>(S, vraw, vv);
+  // Per-column work runs once per column: the row-group lanes 2c, 2c + 1
+  // finish column c of their four (reduce-scatter), and results every lane
+  // needs come back by swizzle.
+  const int cl = C.rg >> 1;
+  const float cjc = hw_h2f(c16[C.j0 + cl]);
+  float dj[4];  // delta / c
   if (MODE == MODE_WRITE) {
+    float vv[4];
+    raw_v<MODE, QW4>(S, vraw, vv);
 #pragma unroll
-    for (int c = 0; c < 4; c++) delta[c] = vv[c];
+    for (int c = 0; c < 4; c++) dj[c] = vv[c] * rcp(cj[c]);
   } else {
     const float sKA = C.misc[16 + SUM_KA + g] + C.misc[32 + SUM_KA + g];
     const float sQA = C.misc[16 + SUM_QA + g] + C.misc[32 + SUM_QA + g];
     const float sQK = C.misc[16 + SUM_QK] + C.misc[32 + SUM_QK];
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-      const float kS = cj[c] * fmaf(ZS, rg8_sum(aK[c]), sKA);
-      delta[c] = beta * (vv[c] - kS);
-      o[c] = fmaf(delta[c], sQK, cj[c] * fmaf(ZS, rg8_sum(aQ[c]), sQA));
+    const float kS = cjc * fmaf(ZS, rs4_sum(aK, C.rg), sKA);
+    const float delta = beta * (raw_v1<QW4>(S, vraw[0]) - kS);
+    const float o = fmaf(delta, sQK, cjc * fmaf(ZS, rs4_sum(aQ, C.rg), sQA));
+    if ((C.rg & 1) == 0) {
+      const int64_t at = ((int64_t)C.b * P.H + C.h) * FV + C.j0 + cl;
+      store_val(S.out, S.out_dtype, at, o);
+      if (MODE == MODE_READ) S.s_delta[at] = delta;
     }
-    store_out<MODE>(P, S, C, o, delta);
+    if (MODE == MODE_READ) return;
+    const float djc = delta * rcp(cjc);
+    dj[0] = from_col<0>(djc);
+    dj[1] = from_col<1>(djc);
+    dj[2] = from_col<2>(djc);
+    dj[3] = from_col<3>(djc);
   }
-  if (MODE == MODE_READ) return;
 
   // ---- writer: inner = x'/c = a z + k delta/c, row sums of |x'|
-  float dj[4];
-#pragma unroll
-  for (int c = 0; c < 4; c++) dj[c] = delta[c] * rcp(cj[c]);
   float rowp[FRPT];
 #pragma unroll
   for (int r = 0; r < FRPT; r++) {
@@ -1521,7 +1562,7 @@ __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx
   {
     const int Geff = W == 2 ? P.G : FV;
     const int wpg = Geff / 32;  // waves per value group
-    for (int e = C.tid; e < FK * NG; e += FNT) {
+    for (int e = C.tid ^ FK; e < FK * NG; e += FNT) {  // rows on waves 2, 3 first
       const int i = e / NG, gq = e % NG;
       float sum = C.red[(gq * wpg) * FK + i];
       for (int w = 1; w < wpg; w++) sum += C.red[(gq * wpg + w) * FK + i];
@@ -1549,13 +1590,15 @@ __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx
     }
   }
   // c0 = fp16(max|s| / L); y = s/c0 = t * (c/c0)
-  float c0[4], f0[4], num[4] = {0.f, 0.f, 0.f, 0.f}, den[4] = {0.f, 0.f, 0.f, 0.f};
-  bool top = false;
-#pragma unroll
-  for (int c = 0; c < 4; c++) {
-    c0[c] = hw_fp16_scale((cj[c] * rg8_max_nonneg(mx[c])) * (1.0f / (float)L), nullptr);
-    f0[c] = cj[c] * rcp(c0[c]);
-    top |= c0[c] >= 65504.0f;
+  float f0[4], num[4] = {0.f, 0.f, 0.f, 0.f}, den[4] = {0.f, 0.f, 0.f, 0.f};
+  const float c0 = hw_fp16_scale((cjc * rs4_max_nonneg(mx, C.rg)) * (1.0f / (float)L), nullptr);
+  const bool top = c0 >= 65504.0f;
+  {
+    const float f0c = cjc * rcp(c0);
+    f0[0] = from_col<0>(f0c);
+    f0[1] = from_col<1>(f0c);
+    f0[2] = from_col<2>(f0c);
+    f0[3] = from_col<3>(f0c);
   }
   // Unless c0 saturated at the fp16 maximum, |y| <= L (1 + 2^-11) and
   // rint(y) needs no clamp to [-L, L].
@@ -1584,13 +1627,15 @@ __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx
     // with the same operations, so the register tile is left untouched.
 #pragma unroll
     for (int c = 0; c < 4; c++) num[c] = den[c] = 0.f;
+    const int p0 = code_pos0<W>(opaque(C.tid));
+    const uint32_t *w32s = (const uint32_t *)(C.code + (p0 & ~3));
 #pragma unroll 1
     for (int r = 0; r < FRPT; r++) {
       const int i = C.rg + 8 * r;
       uint32_t word;
-      if (W == 8) word = w32[r * 4 * W];
-      else if (W == 4) word = *(const uint16_t *)(C.code + pos0 + r * 8 * SEG);
-      else word = __builtin_amdgcn_alignbit(w32[r * 4 * W + 1], w32[r * 4 * W], sh);
+      if (W == 8) word = w32s[r * 4 * W];
+      else if (W == 4) word = *(const uint16_t *)(C.code + p0 + r * 8 * SEG);
+      else word = __builtin_amdgcn_alignbit(w32s[r * 4 * W + 1], w32s[r * 4 * W], (uint32_t)(p0 & 3) * 8u);
       const float4 rc = C.rc[g * FK + i];
       const float k = C.ks[i];
       const float2 iu = C.iu[g * FK + i];
@@ -1607,16 +1652,21 @@ __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx
     }
   }
   float f[4];
-#pragma unroll
-  for (int c = 0; c < 4; c++) {
-    const float n = cj[c] * rg8_sum(num[c]), d = rg8_sum(den[c]);
+  {
+    const float n = cjc * rs4_sum(num, C.rg), d = rs4_sum(den, C.rg);
     const float dc = d < 1e-30f ? 1e-30f : d;
     uint32_t hb;
-    const float cc = hw_fp16_scale(d > 0.0f ? n * rcp(dc) : c0[c], &hb);
-    f[c] = cj[c] * rcp(cc);
-    if (C.rg == 0) ((uint16_t *)C.cst)[C.j0 + c] = (uint16_t)hb;
+    const float cc = hw_fp16_scale(d > 0.0f ? n * rcp(dc) : c0, &hb);
+    const float fc = cjc * rcp(cc);
+    const int tl = opaque(C.tid);  // column 4 (tid >> 3) + (rg >> 1), address formed here
+    if ((tl & 1) == 0) ((uint16_t *)C.cst)[4 * (tl >> 3) + ((tl & 7) >> 1)] = (uint16_t)hb;
+    f[0] = from_col<0>(fc);
+    f[1] = from_col<1>(fc);
+    f[2] = from_col<2>(fc);
+    f[3] = from_col<3>(fc);
   }
   // ---- final codes, packed back into the staged region
+  const int pend = code_pos0<W>(opaque(C.tid));
 #pragma unroll
   for (int r = 0; r < FRPT; r++) {
     if ((r % SCHED_ROWS) == SCHED_ROWS - 1) __builtin_amdgcn_sched_barrier(0);
@@ -1636,7 +1686,7 @@ __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx
       for (int c = 0; c < 4; c++) v[c] = fmaf(cf[r][c], f[c], (float)L);
       word = pack_codes<W>(v);
     }
-    const int pos = pos0 + r * 8 * SEG;
+    const int pos = pend + r * 8 * SEG;
     if (W == 8) *(uint32_t *)(C.code + pos) = word;
     else if (W == 4) *(uint16_t *)(C.code + pos) = (uint16_t)word;
     else if (W == 2) C.code[pos] = (uint8_t)word;
@@ -2094,8 +2144,8 @@ __device__ __forceinline__ void body(const PoolDev &P, const StepDev &S, KCtx &C
 #pragma unroll
   for (int q = 0; q < 2; q++) C.red[C.wave * FK + C.rg + 8 * (8 * b5 + 4 * b4 + 2 * b3 + q)] = p2[q];
   __syncthreads();
-  if (C.tid < FK) {
-    const int i = C.tid;
+  if (C.tid >= FK) {  // waves 2, 3 (0 and 1 did the row set-up)
+    const int i = C.tid - FK;
     const int4 m = C.rm[i];
     if (m.w > 0) {
       const float sum = ((C.red[i] + C.red[FK + i]) + C.red[2 * FK + i]) + C.red[3 * FK + i];
@@ -3314,35 +3364,37 @@ int stage_bytes(const sq_pool *p) { return (p->max_code_bytes + 47) & ~15; }
 template <int MODE>
 int launch_step_mode(const sq_pool *pool, StepDev sd, int64_t batch, hipStream_t st) {
   PoolDev pd = to_dev(pool);
-  if (MODE != MODE_DECODE && (pd.fast & SQ_POOL_FAST_GDN128)) {
-    const int ng_max = pool->group >= 32 ? 128 / pool->group : 1;
-    // staging | rows | columns | q,k raw + w | misc | red | ks, qs | rc (float4), iu (float2) per (row, group)
-    size_t lds = (size_t)pd.stage + pd.rstage + 2 * 128 + 3 * 128 * 4 + 48 * 4 + 4 * 128 * 4 + 2 * 128 * 4 +
-                 (size_t)6 * 128 * ng_max * 4;
-    // q, k, v element width as a compile-time choice (the writer reads fp32 only)
-    if (MODE == MODE_WRITE || sd.qkv_dtype == SQ_F32)
-      hipLaunchKernelGGL((gdn128_kernel<MODE, true>), dim3((unsigned)(batch * pool->heads)), dim3(256), lds, st, pd,
-                         sd);
-    else
-      hipLaunchKernelGGL((gdn128_kernel<MODE, MODE == MODE_WRITE>), dim3((unsigned)(batch * pool->heads)), dim3(256),
-                         lds, st, pd, sd);
-    return check_launch("gdn128_kernel");
-  }
-  if (MODE != MODE_DECODE && (pd.fast & SQ_POOL_FAST_KDA128)) {
-    // row-scale regions may start at any even byte: room for the alignment shift
-    pd.rstage = (pool->max_row_bytes + 47) & ~15;
-    // code blocks in padded windows (the largest head's stride)
-    pd.stage = 32 * kfast::block_pitch(pool->max_code_bytes / 32);
-    // staging | rows | columns | q,k raw, w, retention | misc | red | ks, qs | rc, rl, rm | pivot mask | spare
-    size_t lds = (size_t)pd.stage + pd.rstage + fast::KDA_COL_STAGE + 4 * 128 * 4 + fast::MISC_FLOATS * 4 +
-                 4 * 128 * 4 + 2 * 128 * 4 + 3 * 128 * 16 + 16 + 4 * 256;
-    if (MODE == MODE_WRITE || sd.qkv_dtype == SQ_F32)
-      hipLaunchKernelGGL((kda128_kernel<MODE, true>), dim3((unsigned)(batch * pool->heads)), dim3(256), lds, st, pd,
-                         sd);
-    else
-      hipLaunchKernelGGL((kda128_kernel<MODE, MODE == MODE_WRITE>), dim3((unsigned)(batch * pool->heads)), dim3(256),
-                         lds, st, pd, sd);
-    return check_launch("kda128_kernel");
+  if constexpr (MODE != MODE_DECODE) {  // the K=V=128 kernels read and step pages only
+    if (pd.fast & SQ_POOL_FAST_GDN128) {
+      const int ng_max = pool->group >= 32 ? 128 / pool->group : 1;
+      // staging | rows | columns | q,k raw + w | misc | red | ks, qs | rc (float4), iu (float2) per (row, group)
+      size_t lds = (size_t)pd.stage + pd.rstage + 2 * 128 + 3 * 128 * 4 + 48 * 4 + 4 * 128 * 4 + 2 * 128 * 4 +
+                   (size_t)6 * 128 * ng_max * 4;
+      // q, k, v element width as a compile-time choice (the writer reads fp32 only)
+      if (MODE == MODE_WRITE || sd.qkv_dtype == SQ_F32)
+        hipLaunchKernelGGL((gdn128_kernel<MODE, true>), dim3((unsigned)(batch * pool->heads)), dim3(256), lds, st, pd,
+                           sd);
+      else
+        hipLaunchKernelGGL((gdn128_kernel<MODE, MODE == MODE_WRITE>), dim3((unsigned)(batch * pool->heads)), dim3(256),
+                           lds, st, pd, sd);
+      return check_launch("gdn128_kernel");
+    }
+    if (pd.fast & SQ_POOL_FAST_KDA128) {
+      // row-scale regions may start at any even byte: room for the alignment shift
+      pd.rstage = (pool->max_row_bytes + 47) & ~15;
+      // code blocks in padded windows (the largest head's stride)
+      pd.stage = 32 * kfast::block_pitch(pool->max_code_bytes / 32);
+      // staging | rows | columns | q,k raw, w, retention | misc | red | ks, qs | rc, rl, rm | pivot mask | spare
+      size_t lds = (size_t)pd.stage + pd.rstage + fast::KDA_COL_STAGE + 4 * 128 * 4 + fast::MISC_FLOATS * 4 +
+                   4 * 128 * 4 + 2 * 128 * 4 + 3 * 128 * 16 + 16 + 4 * 256;
+      if (MODE == MODE_WRITE || sd.qkv_dtype == SQ_F32)
+        hipLaunchKernelGGL((kda128_kernel<MODE, true>), dim3((unsigned)(batch * pool->heads)), dim3(256), lds, st, pd,
+                           sd);
+      else
+        hipLaunchKernelGGL((kda128_kernel<MODE, MODE == MODE_WRITE>), dim3((unsigned)(batch * pool->heads)), dim3(256),
+                           lds, st, pd, sd);
+      return check_launch("kda128_kernel");
+    }
   }
   const int K = pool->keys, V = pool->values;
   const int RG = K >= 8 ? 8 : 4;
