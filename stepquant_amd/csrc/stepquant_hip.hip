@@ -2023,8 +2023,8 @@ __device__ __forceinline__ int next_pivot(uint64_t &lo, uint64_t &hi) {
   return -1;
 }
 
-template <int MODE>
-__device__ __forceinline__ void body(const PoolDev &P, const StepDev &S, KCtx &C) {
+template <int MODE, bool QW4>
+__device__ __forceinline__ void body(const PoolDev &P, const StepDev &S, KCtx &C, uint32_t vraw) {
 #pragma clang fp contract(off)
   const float beta = C.misc[0];
   const bool has_cols = C.colbase >= 0;
@@ -2059,11 +2059,19 @@ __device__ __forceinline__ void body(const PoolDev &P, const StepDev &S, KCtx &C
       }
     }
   }
-  float delta[4];
+  // Per-column work runs once per column: row-group lanes 2c, 2c + 1 finish
+  // column c of their four (reduce-scatter), results come back by swizzle.
+  const int cl = C.rg >> 1;
+  const float cjc = has_cols ? hw_h2f(*(const uint16_t *)(C.cst + C.shift_col + 2 * (C.j0 + cl))) : 1.0f;
+  const bool pivots = (pm_lo | pm_hi) != 0;  // wave-uniform
+  float delta[4], dj[4];  // delta (for pivot rows) and delta / c
   if (MODE == MODE_WRITE) {
     const int64_t bi = ((int64_t)C.b * P.H + C.h) * FV + C.j0;
 #pragma unroll
-    for (int c = 0; c < 4; c++) delta[c] = S.s_delta[bi + c];
+    for (int c = 0; c < 4; c++) {
+      delta[c] = S.s_delta[bi + c];
+      dj[c] = delta[c] * rcp(cj[c]);
+    }
   } else {
     // pivot rows owned by this lane (row % 8 == rg)
     float pK[4] = {0.f, 0.f, 0.f, 0.f}, pQ[4] = {0.f, 0.f, 0.f, 0.f};
@@ -2083,29 +2091,32 @@ __device__ __forceinline__ void body(const PoolDev &P, const StepDev &S, KCtx &C
     const float sKA = C.misc[16 + SUM_KA] + C.misc[32 + SUM_KA];
     const float sQA = C.misc[16 + SUM_QA] + C.misc[32 + SUM_QA];
     const float sQK = C.misc[16 + SUM_QK] + C.misc[32 + SUM_QK];
-    float vv[4], o[4];
-    load4(S.v, S.qkv_dtype, (int64_t)C.b * S.v_stride + (int64_t)C.h * FV + C.j0, vv);
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-      const float kS = fmaf(cj[c], rg8_sum(aK[c]) + sKA, rg8_sum(pK[c]));
-      delta[c] = beta * (vv[c] - kS);
-      o[c] = fmaf(delta[c], sQK, fmaf(cj[c], rg8_sum(aQ[c]) + sQA, rg8_sum(pQ[c])));
+    const float vc = QW4 ? __uint_as_float(vraw)
+                         : S.qkv_dtype == SQ_BF16 ? __uint_as_float(vraw << 16) : hw_h2f(vraw);
+    const float pKc = pivots ? rs4_sum(pK, C.rg) : 0.0f, pQc = pivots ? rs4_sum(pQ, C.rg) : 0.0f;
+    const float kS = fmaf(cjc, rs4_sum(aK, C.rg) + sKA, pKc);
+    const float dl = beta * (vc - kS);
+    const float o = fmaf(dl, sQK, fmaf(cjc, rs4_sum(aQ, C.rg) + sQA, pQc));
+    if ((C.rg & 1) == 0) {
+      const int64_t at = ((int64_t)C.b * P.H + C.h) * FV + C.j0 + cl;
+      store_val(S.out, S.out_dtype, at, o);
+      if (MODE == MODE_READ) S.s_delta[at] = dl;
     }
-    const int64_t base_o = ((int64_t)C.b * P.H + C.h) * FV + C.j0;
-    if (C.rg == 0) {
-      store4(S.out, S.out_dtype, base_o, o);
-      if (MODE == MODE_READ) {
-#pragma unroll
-        for (int c = 0; c < 4; c++) S.s_delta[base_o + c] = delta[c];
-      }
+    if (MODE == MODE_READ) return;
+    const float djc = dl * rcp(cjc);
+    dj[0] = from_col<0>(djc);
+    dj[1] = from_col<1>(djc);
+    dj[2] = from_col<2>(djc);
+    dj[3] = from_col<3>(djc);
+    if (pivots) {
+      delta[0] = from_col<0>(dl);
+      delta[1] = from_col<1>(dl);
+      delta[2] = from_col<2>(dl);
+      delta[3] = from_col<3>(dl);
     }
   }
-  if (MODE == MODE_READ) return;
 
   // ---- writer: inner = x'/c = a z + k delta/c; row sums of |x'|
-  float dj[4];
-#pragma unroll
-  for (int c = 0; c < 4; c++) dj[c] = delta[c] * rcp(cj[c]);
   float rowp[FRPT];
 #pragma unroll
   for (int r = 0; r < FRPT; r++) {
@@ -2175,13 +2186,15 @@ __device__ __forceinline__ void body(const PoolDev &P, const StepDev &S, KCtx &C
       mx[c] = fmaxf(mx[c], fabsf(t) * rl.y);
     }
   }
-  float c0[4], f0[4], num[4] = {0.f, 0.f, 0.f, 0.f}, den[4] = {0.f, 0.f, 0.f, 0.f};
-  bool top = false;
-#pragma unroll
-  for (int c = 0; c < 4; c++) {
-    c0[c] = hw_fp16_scale(cj[c] * rg8_max_nonneg(mx[c]), nullptr);
-    f0[c] = cj[c] * rcp(c0[c]);
-    top |= c0[c] >= 65504.0f;
+  float f0[4], num[4] = {0.f, 0.f, 0.f, 0.f}, den[4] = {0.f, 0.f, 0.f, 0.f};
+  const float c0 = hw_fp16_scale(cjc * rs4_max_nonneg(mx, C.rg), nullptr);
+  const bool top = c0 >= 65504.0f;
+  {
+    const float f0c = cjc * rcp(c0);
+    f0[0] = from_col<0>(f0c);
+    f0[1] = from_col<1>(f0c);
+    f0[2] = from_col<2>(f0c);
+    f0[3] = from_col<3>(f0c);
   }
   // |y| <= L_i (1 + 2^-11) unless c0 saturated: rint needs no clamp
 #pragma unroll
@@ -2222,14 +2235,19 @@ __device__ __forceinline__ void body(const PoolDev &P, const StepDev &S, KCtx &C
     }
   }
   float f[4];
-#pragma unroll
-  for (int c = 0; c < 4; c++) {
-    const float n = cj[c] * rg8_sum(num[c]), d = rg8_sum(den[c]);
+  {
+    const float n = cjc * rs4_sum(num, C.rg), d = rs4_sum(den, C.rg);
     const float dc = d < 1e-30f ? 1e-30f : d;
     uint32_t hb;
-    const float cc = hw_fp16_scale(d > 0.0f ? n * rcp(dc) : c0[c], &hb);
-    f[c] = cj[c] * rcp(cc);
-    if (C.rg == 0 && has_cols) *(uint16_t *)(C.cst + C.shift_col + 2 * (C.j0 + c)) = (uint16_t)hb;
+    const float cc = hw_fp16_scale(d > 0.0f ? n * rcp(dc) : c0, &hb);
+    const float fc = cjc * rcp(cc);
+    const int tl = opaque(C.tid);  // column 4 (tid >> 3) + (rg >> 1), address formed here
+    if ((tl & 1) == 0 && has_cols)
+      *(uint16_t *)(C.cst + C.shift_col + 2 * (4 * (tl >> 3) + ((tl & 7) >> 1))) = (uint16_t)hb;
+    f[0] = from_col<0>(fc);
+    f[1] = from_col<1>(fc);
+    f[2] = from_col<2>(fc);
+    f[3] = from_col<3>(fc);
   }
   // ---- final codes: level = rint(y) + L saturated to [0, 2L], packed with the row's width
 #pragma unroll
@@ -2282,7 +2300,8 @@ __device__ __forceinline__ void body(const PoolDev &P, const StepDev &S, KCtx &C
 // width QW4 and gate width are branch-free runs), after the page's
 // global-to-LDS loads, so all latencies overlap.
 template <int MODE, bool QW4>
-__device__ __forceinline__ void kda_prologue(const PoolDev &P, const StepDev &S, const kfast::KCtx &C) {
+__device__ __forceinline__ void kda_prologue(const PoolDev &P, const StepDev &S, const kfast::KCtx &C,
+                                             uint32_t &vraw) {
   using namespace kfast;
   const int64_t bh = (int64_t)C.b * P.H + C.h;
   const int i = C.tid & (FK - 1);
@@ -2295,13 +2314,17 @@ __device__ __forceinline__ void kda_prologue(const PoolDev &P, const StepDev &S,
     const int hk = C.h / (P.H / S.HK);
     const int64_t qi = (int64_t)C.b * S.q_stride + (int64_t)hk * FK + i;
     const int64_t ki = (int64_t)C.b * S.k_stride + (int64_t)hk * FK + i;
+    // this lane's readout column j0 + (rg >> 1) of v, raw
+    const int64_t vi = (int64_t)C.b * S.v_stride + (int64_t)C.h * FV + C.j0 + (C.rg >> 1);
     uint32_t qr, kr, gr, dr = 0u;
     if (QW4) {
       qr = ((const uint32_t *)S.q)[qi];
       kr = ((const uint32_t *)S.k)[ki];
+      vraw = ((const uint32_t *)S.v)[vi];
     } else {
       qr = ((const uint16_t *)S.q)[qi];
       kr = ((const uint16_t *)S.k)[ki];
+      vraw = ((const uint16_t *)S.v)[vi];
     }
     float bt, al = 0.0f;
     const bool g4 = S.gate_dtype == SQ_F32;
@@ -2406,7 +2429,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KDA128_WAVE
   C.lbase = C.cg * pitch + (int)((uintptr_t)(C.page + C.code_start + (int64_t)C.cg * C.stride) & 15);
   C.shift_r = C.row_bytes > 0 ? stage_region_async(C.page + C.row_start, C.row_bytes, C.rst, C.tid) : 0;
   C.shift_col = C.colbase >= 0 ? stage_region_async(C.page + C.colbase, 2 * FV, C.cst, C.tid) : 0;
-  kda_prologue<MODE, QW4>(P, S, C);
+  uint32_t vraw = 0u;
+  kda_prologue<MODE, QW4>(P, S, C, vraw);
   __syncthreads();
   if (MODE == MODE_READ && C.tid < FK) {
     const int64_t bh = (int64_t)C.b * H + C.h;
@@ -2417,7 +2441,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KDA128_WAVE
   }
   row_setup<MODE>(P, S, C);
   __syncthreads();
-  body<MODE>(P, S, C);
+  body<MODE, QW4>(P, S, C, vraw);
 }
 
 // =====================================================================
