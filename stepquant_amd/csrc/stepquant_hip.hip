@@ -2470,8 +2470,8 @@ typedef float f32x4 __attribute__((__vector_size__(4 * sizeof(float))));
 constexpr int PC = 64, PKD = 128, PVS = 64;
 constexpr int P136 = 136, P72 = 72, PA = 68;  // row pitches (elements) of the LDS arrays
 constexpr int OFF_KC = 0;                       // bf16 [64 t][136]   k rows (d contiguous)
-constexpr int OFF_KT = OFF_KC + PC * P136 * 2;  // bf16 [128 d][72]   k columns (t contiguous)
-constexpr int OFF_VT = OFF_KT + PKD * P72 * 2;  // bf16 [64 j][72]    v columns of this half
+constexpr int OFF_KT = OFF_KC + PC * P136 * 2;  // bf16 [128 d][72]   k columns (t contiguous, swizzled)
+constexpr int OFF_VT = OFF_KT + PKD * P72 * 2;  // bf16 [64 j][72]    v columns of this half (swizzled)
 constexpr int OFF_AT = OFF_VT + PVS * P72 * 2;  // f32  [64][68]      A, then T = (I + A)^{-1}
 constexpr int OFF_P = OFF_AT + PC * PA * 4;     // bf16 2 x [64 t][72] masked, scaled Q K^T (hi, lo)
 constexpr int OFF_WD = OFF_P + 2 * PC * P72 * 2;  // R^T hi/lo [64 j][72], later Delta^T, Delta'^T hi/lo
@@ -2494,6 +2494,29 @@ struct PrefillDev {
   int H, HK, NC, gate_dtype, out_dtype, normalize;
   float scale;
 };
+
+// Element (r, t) of the transposed k and v tiles sits in row r at column
+// tcol(r, t): the 8-token block index is XORed with bits 3-5 of r, so the
+// staging stores (8 consecutive rows r per lane group, one token) spread
+// over the banks instead of landing 72 elements apart in one bank; reads of
+// 8 (or 4 aligned) consecutive tokens stay contiguous.
+__device__ __forceinline__ int tcol(int r, int t) { return (((t >> 3) ^ (r >> 3)) & 7) * 8 + (t & 7); }
+
+// inclusive prefix sum over the 64 lanes: 16-lane rows by DPP shifts with
+// zero fill, then rows 1, 3 add lane 15 of the row before, rows 2, 3 lane 31
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp0(float v) {  // DPP move, 0 where the source lane is outside the row
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWS, 0xF, false));
+}
+__device__ __forceinline__ float wave_scan(float x) {
+  x += dpp0<0x111, 0xF>(x);  // row_shr:1
+  x += dpp0<0x112, 0xF>(x);  // row_shr:2
+  x += dpp0<0x114, 0xF>(x);  // row_shr:4
+  x += dpp0<0x118, 0xF>(x);  // row_shr:8
+  x += dpp0<0x142, 0xA>(x);  // row_bcast:15 into rows 1, 3
+  x += dpp0<0x143, 0xC>(x);  // row_bcast:31 into rows 2, 3
+  return x;
+}
 
 __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -2644,6 +2667,9 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillDev D) {
   };
 
   store_st();
+  // the head's gate constants, once: dt_bias and e^{A_log}
+  const float dt_h = D.a_log ? load_val(D.dt_bias, D.gate_dtype, h) : 0.0f;
+  const float ea_h = D.a_log ? __expf(load_val(D.a_log, D.gate_dtype, h)) : 0.0f;
   Fetch F;
   fetch(F, 0);
   int ci = 0;  // next checkpoint index
@@ -2660,7 +2686,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillDev D) {
       float ss = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; e++) {
-        *(uint16_t *)(Kt + ((d8 + e) * P72 + t) * 2) = ke[e];
+        *(uint16_t *)(Kt + ((d8 + e) * P72 + tcol(d8 + e, t)) * 2) = ke[e];
         const float f = __uint_as_float((uint32_t)ke[e] << 16);
         ss = fmaf(f, f, ss);
       }
@@ -2691,22 +2717,17 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillDev D) {
       const int idx = tid + 256 * it, t = idx >> 3, j8 = (idx & 7) * 8;
       const uint16_t *ve = (const uint16_t *)&F.v[it];
 #pragma unroll
-      for (int e = 0; e < 8; e++) *(uint16_t *)(Vt + ((j8 + e) * P72 + t) * 2) = ve[e];
+      for (int e = 0; e < 8; e++) *(uint16_t *)(Vt + ((j8 + e) * P72 + tcol(j8 + e, t)) * 2) = ve[e];
     }
     if (w == 0) {
       float lg = F.lg, bt = F.bt;
       if (D.a_log && l < n) {
-        const float u = lg + load_val(D.dt_bias, D.gate_dtype, h);
+        const float u = lg + dt_h;
         const float sp = u > 20.0f ? u : __logf(1.0f + __expf(u < 20.0f ? u : 20.0f));
-        lg = -__expf(load_val(D.a_log, D.gate_dtype, h)) * sp;
+        lg = -ea_h * sp;
         bt = 1.0f / (1.0f + __expf(-bt));
       }
-      // inclusive prefix sum of the log decays over the 64 tokens
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const float y = __shfl_up(lg, o);
-        if (l >= o) lg += y;
-      }
+      lg = wave_scan(lg);  // inclusive prefix sum of the log decays over the 64 tokens
       sm[SM_LC * 64 + l] = lg;
       sm[SM_BETA * 64 + l] = bt;
     }
@@ -2801,7 +2822,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillDev D) {
 #pragma unroll
       for (int nj = 0; nj < 4; nj++) {
         const int j = 16 * nj + c16;
-        const uint2 vr = *(const uint2 *)(Vt + (j * P72 + tt) * 2);
+        const uint2 vr = *(const uint2 *)(Vt + (j * P72 + tcol(j, tt)) * 2);
         const float v4[4] = {__uint_as_float(vr.x << 16), __uint_as_float(vr.x & 0xffff0000u),
                              __uint_as_float(vr.y << 16), __uint_as_float(vr.y & 0xffff0000u)};
         float rv[4];
@@ -2932,7 +2953,10 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillDev D) {
       for (int mt = 0; mt < 2; mt++) {
         bf16x8 ak[2];
 #pragma unroll
-        for (int ks = 0; ks < 2; ks++) ak[ks] = ld8(Kt, ((16 * (2 * w + mt) + c16) * P72 + 8 * q4 + 32 * ks) * 2);
+        for (int ks = 0; ks < 2; ks++) {
+          const int d = 16 * (2 * w + mt) + c16;
+          ak[ks] = ld8(Kt, (d * P72 + tcol(d, 8 * q4 + 32 * ks)) * 2);
+        }
 #pragma unroll
         for (int nj = 0; nj < 4; nj++) {
           f32x4 acc;
