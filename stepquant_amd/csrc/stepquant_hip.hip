@@ -2454,7 +2454,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KDA128_WAVE
 //   O     = diag(Gamma) Q S0 + (M o Q K^T) Delta,        M_ts = Gamma_t/Gamma_s (s <= t)
 //   S_C   = Gamma_C S0 + (diag(Gamma_C/Gamma) K)^T Delta
 // (q, k L2-normalised and q scaled: the norms multiply into the products).
-// One workgroup per (sequence, head, half of V): 4 waves, chunks in order.
+// One workgroup per (sequence, head): 8 waves, chunks in order.
 // Operands with a single rounding to bf16 would lose precision (T, W, P,
 // Delta, S); they are split as x = hi + lo (two bf16) and multiplied as
 // hi*hi + hi*lo + lo*hi, leaving ~2^-16 relative error per product; q, k, v
@@ -2467,22 +2467,21 @@ namespace pf {
 typedef __bf16 bf16x8 __attribute__((__vector_size__(8 * sizeof(__bf16))));
 typedef float f32x4 __attribute__((__vector_size__(4 * sizeof(float))));
 
-constexpr int PC = 64, PKD = 128, PVS = 64;
+constexpr int PC = 64, PKD = 128, PV = 128;
+constexpr int NW = 8, NT = 64 * NW;            // waves and threads of a workgroup
 constexpr int P136 = 136, P72 = 72, PA = 68;  // row pitches (elements) of the LDS arrays
-constexpr int OFF_KC = 0;                       // bf16 [64 t][136]   k rows (d contiguous)
-constexpr int OFF_KT = OFF_KC + PC * P136 * 2;  // bf16 [128 d][72]   k columns (t contiguous, swizzled)
-constexpr int OFF_VT = OFF_KT + PKD * P72 * 2;  // bf16 [64 j][72]    v columns of this half (swizzled)
-constexpr int OFF_AT = OFF_VT + PVS * P72 * 2;  // f32  [64][68]      A, then T = (I + A)^{-1}
-constexpr int OFF_P = OFF_AT + PC * PA * 4;     // bf16 2 x [64 t][72] masked, scaled Q K^T (hi, lo)
-constexpr int OFF_WD = OFF_P + 2 * PC * P72 * 2;  // R^T hi/lo [64 j][72], later Delta^T, Delta'^T hi/lo
-constexpr int WD_BYTES = 4 * PVS * P72 * 2;
-constexpr int OFF_ST = OFF_WD + WD_BYTES;         // bf16 2 x [64 j][136] S transposed (hi, lo)
-constexpr int OFF_SM = OFF_ST + 2 * PVS * P136 * 2;  // f32 [8][64] per-token scalars
-constexpr int OFF_R = OFF_SM + 8 * 64 * 4;        // f32 4 x [16][16] block products
-constexpr int OFF_CK = OFF_R + 4 * 256 * 4;      // int [MAX_CK] this sequence's checkpoints
+constexpr int OFF_KC = 0;                          // bf16 [64 t][136]   k rows (d contiguous)
+constexpr int OFF_QC = OFF_KC + PC * P136 * 2;     // bf16 [64 t][136]   q rows
+constexpr int OFF_KT = OFF_QC + PC * P136 * 2;     // bf16 [128 d][72]   k columns (t contiguous, swizzled)
+constexpr int OFF_VT = OFF_KT + PKD * P72 * 2;     // bf16 [128 j][72]   v columns (swizzled)
+constexpr int OFF_AT = OFF_VT + PV * P72 * 2;      // f32  [64 t][68]    A, then T = (I + A)^{-1}
+constexpr int OFF_P = OFF_AT + PC * PA * 4;        // bf16 2 x [64 t][72] masked, scaled Q K^T (hi, lo)
+constexpr int OFF_SM = OFF_P + 2 * PC * P72 * 2;   // f32 [10][64] per-token scalars
+constexpr int OFF_R = OFF_SM + 10 * 64 * 4;        // f32 4 x [16][16] block products
+constexpr int OFF_CK = OFF_R + 4 * 256 * 4;        // int [MAX_CK] this sequence's checkpoints
 constexpr int MAX_CK = 64;
 constexpr int LDS_BYTES = OFF_CK + MAX_CK * 4;
-enum { SM_LC = 0, SM_BETA, SM_NK, SM_NQ, SM_GK, SM_QG, SM_KD, SM_KSQ };
+enum { SM_LC = 0, SM_BETA, SM_NK, SM_NQ, SM_GK, SM_QG, SM_KD, SM_KSQ, SM_QSQ };
 
 struct PrefillDev {
   const void *q, *k, *v, *g, *beta, *a_log, *dt_bias;
@@ -2502,12 +2501,12 @@ struct PrefillDev {
 // 8 (or 4 aligned) consecutive tokens stay contiguous.
 __device__ __forceinline__ int tcol(int r, int t) { return (((t >> 3) ^ (r >> 3)) & 7) * 8 + (t & 7); }
 
-// inclusive prefix sum over the 64 lanes: 16-lane rows by DPP shifts with
-// zero fill, then rows 1, 3 add lane 15 of the row before, rows 2, 3 lane 31
 template <int CTRL, int ROWS>
 __device__ __forceinline__ float dpp0(float v) {  // DPP move, 0 where the source lane is outside the row
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWS, 0xF, false));
 }
+// inclusive prefix sum over the 64 lanes: 16-lane rows by DPP shifts with
+// zero fill, then rows 1, 3 add lane 15 of the row before, rows 2, 3 lane 31
 __device__ __forceinline__ float wave_scan(float x) {
   x += dpp0<0x111, 0xF>(x);  // row_shr:1
   x += dpp0<0x112, 0xF>(x);  // row_shr:2
@@ -2522,7 +2521,7 @@ __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 __device__ __forceinline__ bf16x8 ld8(const uint8_t *lds, int byte) { return *(const bf16x8 *)(lds + byte); }
-__device__ __forceinline__ float bf2f(__bf16 x) { return (float)x; }
+__device__ __forceinline__ float bf2f(uint16_t x) { return __uint_as_float((uint32_t)x << 16); }
 
 // x = hi + lo with hi = bf16(x), lo = bf16(x - hi)
 __device__ __forceinline__ void split8(const float x[8], bf16x8 &hi, bf16x8 &lo) {
@@ -2533,11 +2532,8 @@ __device__ __forceinline__ void split8(const float x[8], bf16x8 &hi, bf16x8 &lo)
     lo[e] = (__bf16)(x[e] - (float)h);
   }
 }
-__device__ __forceinline__ uint2 pack4(const float x[4]) {
-  uint2 u;
-  u.x = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x[1]) << 16);
-  u.y = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x[2]) | ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x[3]) << 16);
-  return u;
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)a) | ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)b) << 16);
 }
 // hi/lo halves of four values as two packed bf16 x 4
 __device__ __forceinline__ void split4(const float x[4], uint2 &hi, uint2 &lo) {
@@ -2547,8 +2543,44 @@ __device__ __forceinline__ void split4(const float x[4], uint2 &hi, uint2 &lo) {
     h[e] = (float)(__bf16)x[e];
     r[e] = x[e] - h[e];
   }
-  hi = pack4(h);
-  lo = pack4(r);
+  hi = make_uint2(pack2(h[0], h[1]), pack2(h[2], h[3]));
+  lo = make_uint2(pack2(r[0], r[1]), pack2(r[2], r[3]));
+}
+
+// MFMA operand (hi and lo bf16 halves) of a 32-row chunk held as two
+// accumulator tiles: x0 = rows 0-15, x1 = rows 16-31, this lane's values at
+// rows 4 q4 + r, column c16.  The operand lane (c16, q4) needs rows
+// 8 q4 .. 8 q4 + 7 of column c16: as B that is B[k][c16], as A the row c16
+// of the transpose.  Packed pairs move between the 16-lane rows with
+// v_permlane32_swap (upper half of the first operand <-> lower half of the
+// second) and v_permlane16_swap (odd rows of the first <-> even rows of the
+// second); no LDS round trip.
+__device__ __forceinline__ void to_operand(const f32x4 &x0, const f32x4 &x1, bf16x8 &hi, bf16x8 &lo) {
+  uint32_t h[2][2], l[2][2];  // [tile][pair]
+#pragma unroll
+  for (int p = 0; p < 2; p++) {
+    const float a0 = x0[2 * p], a1 = x0[2 * p + 1], b0 = x1[2 * p], b1 = x1[2 * p + 1];
+    const float ha0 = (float)(__bf16)a0, ha1 = (float)(__bf16)a1, hb0 = (float)(__bf16)b0, hb1 = (float)(__bf16)b1;
+    h[0][p] = pack2(ha0, ha1);
+    h[1][p] = pack2(hb0, hb1);
+    l[0][p] = pack2(a0 - ha0, a1 - ha1);
+    l[1][p] = pack2(b0 - hb0, b1 - hb1);
+  }
+  auto conv = [](const uint32_t (&t)[2][2]) {
+    uint32_t o[4];
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+      // [t0 rows 0,1 | t1 rows 0,1] and [t0 rows 2,3 | t1 rows 2,3]
+      const auto s = __builtin_amdgcn_permlane32_swap(t[0][p], t[1][p], false, false);
+      // [t0 r0, t0 r2, t1 r0, t1 r2] and [t0 r1, t0 r3, t1 r1, t1 r3]
+      const auto u = __builtin_amdgcn_permlane16_swap(s[0], s[1], false, false);
+      o[p] = u[0];      // elements 2p, 2p + 1: rows 8 q4 + 2p, + 1
+      o[2 + p] = u[1];  // elements 4 + 2p, 5 + 2p
+    }
+    return __builtin_bit_cast(bf16x8, make_uint4(o[0], o[1], o[2], o[3]));
+  };
+  hi = conv(h);
+  lo = conv(l);
 }
 
 // sum over the 16 lanes of a DPP row
@@ -2564,7 +2596,7 @@ __device__ __forceinline__ f32x4 mfma32(float a, float b, f32x4 c) {
 // Raw inputs of one chunk, fetched into registers one chunk ahead so the
 // global loads overlap the previous chunk's arithmetic.
 struct Fetch {
-  uint4 k[4], q[4], v[2];
+  uint4 k[2], q[2], v[2];
   float lg, bt;
   int n;
   int64_t tb;
@@ -2579,47 +2611,38 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-__global__ __launch_bounds__(256) void prefill_kernel(PrefillDev D) {
+// One workgroup of 8 waves per (sequence, head), chunks in order.  Wave w
+// owns the 16 state columns j = 16 w .. 16 w + 15 for all 128 rows d (in
+// registers, accumulator layout); R, Delta and Delta' of its columns stay in
+// registers too and reach the next product through to_operand.  The chunk's
+// k, q, v, A, T and P are shared through LDS.  Transposed products keep every
+// operand in a layout it already has: O^T = S0^T Q^T + Delta^T P^T gives
+// each lane 4 consecutive output columns for one token.
+__global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
 #pragma clang fp contract(off)
   extern __shared__ __align__(16) uint8_t smem[];
   const int H = D.H;
-  const int vs = blockIdx.x & 1;
-  const int h = (blockIdx.x >> 1) % H;
-  const int b = (blockIdx.x >> 1) / H;
+  const int h = blockIdx.x % H;
+  const int b = blockIdx.x / H;
   const int hk = h / (H / D.HK);
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, q4 = l >> 4, c16 = l & 15;
   const int t0 = D.cu[b], len = D.cu[b + 1] - t0;
   float *sm = (float *)(smem + OFF_SM);
-  uint8_t *Kc = smem + OFF_KC, *Kt = smem + OFF_KT, *Vt = smem + OFF_VT, *WD = smem + OFF_WD, *St = smem + OFF_ST;
+  uint8_t *Kc = smem + OFF_KC, *Qc = smem + OFF_QC, *Kt = smem + OFF_KT, *Vt = smem + OFF_VT;
   float *AT = (float *)(smem + OFF_AT);
   uint8_t *Pl = smem + OFF_P;
-  float *Rs = (float *)(smem + OFF_R) + 256 * w;
   const __bf16 *qg = (const __bf16 *)D.q, *kg = (const __bf16 *)D.k, *vg = (const __bf16 *)D.v;
+  const int jw = 16 * w;  // this wave's first state column
 
-  // ---- state S[d][j] of this half in registers: tiles (d-tile 2w + mt, j-tile nj),
-  // lane holds rows d = 16(2w + mt) + 4 q4 + r, column j = 16 nj + c16
-  float S[2][4][4];
+  // ---- state S[d][j] of this wave's columns: tile dt holds rows d = 16 dt + 4 q4 + r, column jw + c16
+  f32x4 S[8];
   {
-    const float *src = D.init + ((int64_t)b * H + h) * PKD * 128 + vs * PVS;
+    const float *src = D.init + ((int64_t)b * H + h) * PKD * PV + jw + c16;
 #pragma unroll
-    for (int mt = 0; mt < 2; mt++)
+    for (int dt = 0; dt < 8; dt++)
 #pragma unroll
-      for (int nj = 0; nj < 4; nj++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) S[mt][nj][r] = src[(int64_t)(16 * (2 * w + mt) + 4 * q4 + r) * 128 + 16 * nj + c16];
+      for (int r = 0; r < 4; r++) S[dt][r] = src[(int64_t)(16 * dt + 4 * q4 + r) * PV];
   }
-  auto store_st = [&]() {
-#pragma unroll
-    for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-      for (int nj = 0; nj < 4; nj++) {
-        uint2 hi, lo;
-        split4(S[mt][nj], hi, lo);
-        const int off = ((16 * nj + c16) * P136 + 16 * (2 * w + mt) + 4 * q4) * 2;
-        *(uint2 *)(St + off) = hi;
-        *(uint2 *)(St + PVS * P136 * 2 + off) = lo;
-      }
-  };
   // this sequence's checkpoints, once, in LDS
   int *ck = (int *)(smem + OFF_CK);
   if (tid < D.NC) ck[tid] = D.ckpt[(int64_t)b * D.NC + tid];
@@ -2641,22 +2664,13 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillDev D) {
     F.n = c < len ? segment(c) : 0;
     F.tb = (int64_t)t0 + c;
 #pragma unroll
-    for (int it = 0; it < 4; it++) {
-      const int idx = tid + 256 * it, t = idx >> 4, d8 = (idx & 15) * 8;
-      F.k[it] = t < F.n ? *(const uint4 *)(kg + (F.tb + t) * D.k_stride + hk * PKD + d8) : make_uint4(0u, 0u, 0u, 0u);
-    }
-    {
-      const int t = 16 * w + c16;
-#pragma unroll
-      for (int ks = 0; ks < 4; ks++)
-        F.q[ks] = t < F.n ? *(const uint4 *)(qg + (F.tb + t) * D.q_stride + hk * PKD + 8 * q4 + 32 * ks)
-                          : make_uint4(0u, 0u, 0u, 0u);
-    }
-#pragma unroll
     for (int it = 0; it < 2; it++) {
-      const int idx = tid + 256 * it, t = idx >> 3, j8 = (idx & 7) * 8;
-      F.v[it] = t < F.n ? *(const uint4 *)(vg + (F.tb + t) * D.v_stride + h * 128 + vs * PVS + j8)
-                        : make_uint4(0u, 0u, 0u, 0u);
+      const int idx = tid + NT * it, t = idx >> 4, d8 = (idx & 15) * 8;
+      const bool in = t < F.n;
+      const int64_t row = F.tb + t;
+      F.k[it] = in ? *(const uint4 *)(kg + row * D.k_stride + hk * PKD + d8) : make_uint4(0u, 0u, 0u, 0u);
+      F.q[it] = in ? *(const uint4 *)(qg + row * D.q_stride + hk * PKD + d8) : make_uint4(0u, 0u, 0u, 0u);
+      F.v[it] = in ? *(const uint4 *)(vg + row * D.v_stride + h * PV + d8) : make_uint4(0u, 0u, 0u, 0u);
     }
     F.lg = 0.f;
     F.bt = 0.f;
@@ -2666,7 +2680,6 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillDev D) {
     }
   };
 
-  store_st();
   // the head's gate constants, once: dt_bias and e^{A_log}
   const float dt_h = D.a_log ? load_val(D.dt_bias, D.gate_dtype, h) : 0.0f;
   const float ea_h = D.a_log ? __expf(load_val(D.a_log, D.gate_dtype, h)) : 0.0f;
@@ -2676,48 +2689,37 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillDev D) {
   for (int c0 = 0; c0 < len;) {
     const int n = F.n;
     const int64_t tb = F.tb;
+    // lane indices re-derived each chunk through an empty asm: the LDS
+    // addresses formed from them (swizzled, not base + offset) are then
+    // computed where used instead of being held across the loop
+    const int tid = fast::opaque(threadIdx.x), l = tid & 63, q4 = l >> 4, c16 = l & 15;
 
-    // ---- stage the fetched chunk: k rows and columns, v columns, norms, decays
-#pragma unroll
-    for (int it = 0; it < 4; it++) {
-      const int idx = tid + 256 * it, t = idx >> 4, d8 = (idx & 15) * 8;
-      *(uint4 *)(Kc + (t * P136 + d8) * 2) = F.k[it];
-      const uint16_t *ke = (const uint16_t *)&F.k[it];
-      float ss = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; e++) {
-        *(uint16_t *)(Kt + ((d8 + e) * P72 + tcol(d8 + e, t)) * 2) = ke[e];
-        const float f = __uint_as_float((uint32_t)ke[e] << 16);
-        ss = fmaf(f, f, ss);
-      }
-      ss = row16_sum(ss);
-      if ((tid & 15) == 0) sm[SM_KSQ * 64 + t] = ss;
-    }
-    bf16x8 qa[4];
-    {
-      const int t = 16 * w + c16;
-      float ss = 0.f;
-#pragma unroll
-      for (int ks = 0; ks < 4; ks++) {
-        qa[ks] = __builtin_bit_cast(bf16x8, F.q[ks]);
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-          const float f = bf2f(qa[ks][e]);
-          ss = fmaf(f, f, ss);
-        }
-      }
-      const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
-      ss = __uint_as_float(s32[0]) + __uint_as_float(s32[1]);
-      const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
-      ss = __uint_as_float(s16[0]) + __uint_as_float(s16[1]);
-      if (q4 == 0) sm[SM_NQ * 64 + t] = (D.normalize ? 1.0f / __builtin_sqrtf(ss + 1e-6f) : 1.0f) * D.scale;
-    }
+    // ---- stage the fetched chunk: k and q rows, k and v columns, squared norms, decays
 #pragma unroll
     for (int it = 0; it < 2; it++) {
-      const int idx = tid + 256 * it, t = idx >> 3, j8 = (idx & 7) * 8;
+      const int idx = tid + NT * it, t = idx >> 4, d8 = (idx & 15) * 8;
+      *(uint4 *)(Kc + (t * P136 + d8) * 2) = F.k[it];
+      *(uint4 *)(Qc + (t * P136 + d8) * 2) = F.q[it];
+      const uint16_t *ke = (const uint16_t *)&F.k[it], *qe = (const uint16_t *)&F.q[it];
       const uint16_t *ve = (const uint16_t *)&F.v[it];
+      float sk = 0.f, sq = 0.f;
+      // rows d8 .. d8 + 7 share their swizzle (bits 3-5 of the row): one
+      // base address, the rows at immediate offsets
+      const int cb = (d8 * P72 + tcol(d8, t)) * 2;
 #pragma unroll
-      for (int e = 0; e < 8; e++) *(uint16_t *)(Vt + ((j8 + e) * P72 + tcol(j8 + e, t)) * 2) = ve[e];
+      for (int e = 0; e < 8; e++) {
+        *(uint16_t *)(Kt + cb + e * P72 * 2) = ke[e];
+        *(uint16_t *)(Vt + cb + e * P72 * 2) = ve[e];
+        const float fk = bf2f(ke[e]), fq = bf2f(qe[e]);
+        sk = fmaf(fk, fk, sk);
+        sq = fmaf(fq, fq, sq);
+      }
+      sk = row16_sum(sk);
+      sq = row16_sum(sq);
+      if ((idx & 15) == 0) {
+        sm[SM_KSQ * 64 + t] = sk;
+        sm[SM_QSQ * 64 + t] = sq;
+      }
     }
     if (w == 0) {
       float lg = F.lg, bt = F.bt;
@@ -2738,32 +2740,40 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillDev D) {
     if (tid < 64) {
       const int t = tid;
       const float nk = D.normalize ? 1.0f / __builtin_sqrtf(sm[SM_KSQ * 64 + t] + 1e-6f) : 1.0f;
+      const float nq = (D.normalize ? 1.0f / __builtin_sqrtf(sm[SM_QSQ * 64 + t] + 1e-6f) : 1.0f) * D.scale;
       const float lc = sm[SM_LC * 64 + t], lcC = sm[SM_LC * 64 + 63];
       const float gam = __expf(lc);
       sm[SM_NK * 64 + t] = nk;
+      sm[SM_NQ * 64 + t] = nq;
       sm[SM_GK * 64 + t] = gam * nk;  // Gamma_t nk_t
-      sm[SM_QG * 64 + t] = sm[SM_NQ * 64 + t] * gam;
+      sm[SM_QG * 64 + t] = nq * gam;
       sm[SM_KD * 64 + t] = nk * __expf(lcC - lc);
     }
     lds_barrier();
 
-    // ---- K K^T and K Q^T tiles (rows s of tile ns, columns t of this wave's tile);
-    // A_ts = beta_t nk_t nk_s (Gamma_t/Gamma_s) k_t.k_s (s < t), P_ts likewise with q (s <= t)
-    bf16x8 bk[4];
-#pragma unroll
-    for (int ks = 0; ks < 4; ks++) bk[ks] = ld8(Kc, ((16 * w + c16) * P136 + 8 * q4 + 32 * ks) * 2);
+    // ---- A and P tiles (t-tile w % 4, s-tiles 2 (w / 4) and 2 (w / 4) + 1):
+    // A_ts = beta_t nk_t nk_s (Gamma_t/Gamma_s) k_t.k_s (s < t), P_ts likewise with q_t (s <= t)
     {
-      const int t = 16 * w + c16;
+      const int tw = w & 3, t = 16 * tw + c16;
+      bf16x8 bk[4], bq[4];
+#pragma unroll
+      for (int ks = 0; ks < 4; ks++) {
+        bk[ks] = ld8(Kc, (t * P136 + 8 * q4 + 32 * ks) * 2);
+        bq[ks] = ld8(Qc, (t * P136 + 8 * q4 + 32 * ks) * 2);
+      }
       const float lct = sm[SM_LC * 64 + t], bnt = sm[SM_BETA * 64 + t] * sm[SM_NK * 64 + t];
       const float nqt = sm[SM_NQ * 64 + t];
 #pragma unroll
-      for (int ns = 0; ns < 4; ns++) {
+      for (int u = 0; u < 2; u++) {
+        const int ns = 2 * (w >> 2) + u;
         f32x4 aA = {0.f, 0.f, 0.f, 0.f}, aP = {0.f, 0.f, 0.f, 0.f};
+        if (ns <= tw) {  // wave-uniform: tiles above the diagonal are zero
 #pragma unroll
-        for (int ks = 0; ks < 4; ks++) {
-          const bf16x8 a = ld8(Kc, ((16 * ns + c16) * P136 + 8 * q4 + 32 * ks) * 2);
-          aA = mfma(a, bk[ks], aA);
-          aP = mfma(a, qa[ks], aP);
+          for (int ks = 0; ks < 4; ks++) {
+            const bf16x8 a = ld8(Kc, ((16 * ns + c16) * P136 + 8 * q4 + 32 * ks) * 2);
+            aA = mfma(a, bk[ks], aA);
+            aP = mfma(a, bq[ks], aP);
+          }
         }
         const int s0 = 16 * ns + 4 * q4;
         const float4 lcs = *(const float4 *)(sm + SM_LC * 64 + s0);
@@ -2784,23 +2794,52 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillDev D) {
         *(uint2 *)(Pl + PC * P72 * 2 + (t * P72 + s0) * 2) = lo;
       }
     }
-    // ---- K S0 for this wave's rows t (exact k times hi/lo S), overlapping the inverse
-    f32x4 ksv[4];
+    // ---- K S0 (rows t, this wave's columns), consumed at once by
+    // R = beta (V - Gamma nk K S0), and diag(nq Gamma) (S0^T Q^T), the first
+    // term of O^T; S0 (hi/lo) is the shared operand, k and q enter exactly
+    f32x4 R[4], oq[4];
+    {
+      bf16x8 sh[4], sl[4];
 #pragma unroll
-    for (int nj = 0; nj < 4; nj++) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      for (int kc = 0; kc < 4; kc++) to_operand(S[2 * kc], S[2 * kc + 1], sh[kc], sl[kc]);
 #pragma unroll
-      for (int ks = 0; ks < 4; ks++) {
-        const int bo = ((16 * nj + c16) * P136 + 8 * q4 + 32 * ks) * 2;
-        acc = mfma(bk[ks], ld8(St, bo), acc);
-        acc = mfma(bk[ks], ld8(St, PVS * P136 * 2 + bo), acc);
+      for (int tt = 0; tt < 4; tt++) {
+        f32x4 ak = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kc = 0; kc < 4; kc++) {
+          const bf16x8 kr = ld8(Kc, ((16 * tt + c16) * P136 + 32 * kc + 8 * q4) * 2);
+          ak = mfma(kr, sh[kc], ak);
+          ak = mfma(kr, sl[kc], ak);
+        }
+        const int ta = 16 * tt + 4 * q4, j = jw + c16;
+        const float4 be = *(const float4 *)(sm + SM_BETA * 64 + ta), gk = *(const float4 *)(sm + SM_GK * 64 + ta);
+        const float be4[4] = {be.x, be.y, be.z, be.w}, gk4[4] = {gk.x, gk.y, gk.z, gk.w};
+        const uint2 vr = *(const uint2 *)(Vt + (j * P72 + tcol(j, ta)) * 2);
+        const float v4[4] = {__uint_as_float(vr.x << 16), __uint_as_float(vr.x & 0xffff0000u),
+                             __uint_as_float(vr.y << 16), __uint_as_float(vr.y & 0xffff0000u)};
+#pragma unroll
+        for (int r = 0; r < 4; r++) R[tt][r] = be4[r] * (v4[r] - gk4[r] * ak[r]);
+        __builtin_amdgcn_sched_barrier(0);  // one tile's operand loads in flight at a time
       }
-      ksv[nj] = acc;
+#pragma unroll
+      for (int tt = 0; tt < 4; tt++) {
+        f32x4 aq = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kc = 0; kc < 4; kc++) {
+          const bf16x8 qr = ld8(Qc, ((16 * tt + c16) * P136 + 32 * kc + 8 * q4) * 2);
+          aq = mfma(sh[kc], qr, aq);
+          aq = mfma(sl[kc], qr, aq);
+        }
+        const float qgt = sm[SM_QG * 64 + 16 * tt + c16];
+#pragma unroll
+        for (int r = 0; r < 4; r++) oq[tt][r] = aq[r] * qgt;
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
     lds_barrier();
 
-    // ---- T = (I + A)^{-1}: diagonal 16x16 blocks by forward substitution
-    if (l < 16) {
+    // ---- T = (I + A)^{-1}: diagonal 16x16 blocks by forward substitution (waves 0-3)
+    if (w < 4 && l < 16) {
       const float *blk = AT + 16 * w * PA + 16 * w;
       float x[16];
 #pragma unroll
@@ -2814,181 +2853,124 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillDev D) {
 #pragma unroll
       for (int r = 0; r < 16; r++) AT[(16 * w + r) * PA + 16 * w + l] = x[r];
     }
-    // ---- R = beta (V - Gamma nk K S0) for rows t of this wave's tile, stored transposed (hi/lo)
-    {
-      const int tt = 16 * w + 4 * q4;
-      const float4 be = *(const float4 *)(sm + SM_BETA * 64 + tt), gk = *(const float4 *)(sm + SM_GK * 64 + tt);
-      const float be4[4] = {be.x, be.y, be.z, be.w}, gk4[4] = {gk.x, gk.y, gk.z, gk.w};
-#pragma unroll
-      for (int nj = 0; nj < 4; nj++) {
-        const int j = 16 * nj + c16;
-        const uint2 vr = *(const uint2 *)(Vt + (j * P72 + tcol(j, tt)) * 2);
-        const float v4[4] = {__uint_as_float(vr.x << 16), __uint_as_float(vr.x & 0xffff0000u),
-                             __uint_as_float(vr.y << 16), __uint_as_float(vr.y & 0xffff0000u)};
-        float rv[4];
-#pragma unroll
-        for (int r = 0; r < 4; r++) rv[r] = be4[r] * (v4[r] - gk4[r] * ksv[nj][r]);
-        uint2 hi, lo;
-        split4(rv, hi, lo);
-        *(uint2 *)(WD + (j * P72 + tt) * 2) = hi;
-        *(uint2 *)(WD + PVS * P72 * 2 + (j * P72 + tt) * 2) = lo;
-      }
-    }
     lds_barrier();
-    // off-diagonal blocks, one block row at a time (fp32 MFMA):
+    // off-diagonal blocks, one block row at a time (fp32 MFMA, waves 0-2):
     // T_iw = -T_ii sum_{k=w}^{i-1} A_ik T_kw
-    for (int i = 1; i < 4; i++) {
-      f32x4 racc = {0.f, 0.f, 0.f, 0.f};
-      if (w < i) {
-        for (int kb = w; kb < i; kb++) {
+    {
+      float *Rs = (float *)(smem + OFF_R) + 256 * (w & 3);
+      for (int i = 1; i < 4; i++) {
+        f32x4 racc = {0.f, 0.f, 0.f, 0.f};
+        if (w < i) {
+          for (int kb = w; kb < i; kb++) {
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++)
+              racc = mfma32(AT[(16 * i + c16) * PA + 16 * kb + 4 * kk + q4],
+                            AT[(16 * kb + 4 * kk + q4) * PA + 16 * w + c16], racc);
+          }
+#pragma unroll
+          for (int r = 0; r < 4; r++) Rs[(4 * q4 + r) * 16 + c16] = racc[r];
+        }
+        lds_barrier();
+        if (w < i) {
+          f32x4 tacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int kk = 0; kk < 4; kk++)
-            racc = mfma32(AT[(16 * i + c16) * PA + 16 * kb + 4 * kk + q4],
-                          AT[(16 * kb + 4 * kk + q4) * PA + 16 * w + c16], racc);
+            tacc = mfma32(-AT[(16 * i + c16) * PA + 16 * i + 4 * kk + q4], Rs[(4 * kk + q4) * 16 + c16], tacc);
+#pragma unroll
+          for (int r = 0; r < 4; r++) AT[(16 * i + 4 * q4 + r) * PA + 16 * w + c16] = tacc[r];
         }
-#pragma unroll
-        for (int r = 0; r < 4; r++) Rs[(4 * q4 + r) * 16 + c16] = racc[r];
+        lds_barrier();
       }
-      lds_barrier();
-      if (w < i) {
-        f32x4 tacc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kk = 0; kk < 4; kk++)
-          tacc = mfma32(-AT[(16 * i + c16) * PA + 16 * i + 4 * kk + q4], Rs[(4 * kk + q4) * 16 + c16], tacc);
-#pragma unroll
-        for (int r = 0; r < 4; r++) AT[(16 * i + 4 * q4 + r) * PA + 16 * w + c16] = tacc[r];
-      }
-      lds_barrier();
     }
 
-    // ---- Delta = T R (rows t of this wave's tile, columns j)
-    float dl[4][4];
+    // ---- Delta = T R and Delta' = diag(nk Gamma_C / Gamma) Delta (rows t, this wave's columns)
+    f32x4 dl[4], dp[4];
     {
-      const int t = 16 * w + c16;
-      bf16x8 th[2], tl[2];
+      bf16x8 rh[2], rl[2];
+      to_operand(R[0], R[1], rh[0], rl[0]);
+      to_operand(R[2], R[3], rh[1], rl[1]);
 #pragma unroll
-      for (int ks = 0; ks < 2; ks++) {
-        const int s0 = 8 * q4 + 32 * ks;
-        const float4 a0 = *(const float4 *)(AT + t * PA + s0), a1 = *(const float4 *)(AT + t * PA + s0 + 4);
-        const float tr[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-        split8(tr, th[ks], tl[ks]);
-      }
-#pragma unroll
-      for (int nj = 0; nj < 4; nj++) {
+      for (int tt = 0; tt < 4; tt++) {
+        const int t = 16 * tt + c16;
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int ks = 0; ks < 2; ks++) {
-          const int bo = ((16 * nj + c16) * P72 + 8 * q4 + 32 * ks) * 2;
-          const bf16x8 rh = ld8(WD, bo), rl = ld8(WD, PVS * P72 * 2 + bo);
-          acc = mfma(th[ks], rh, acc);
-          acc = mfma(th[ks], rl, acc);
-          acc = mfma(tl[ks], rh, acc);
+        for (int kc = 0; kc < 2; kc++) {
+          const int s0 = 32 * kc + 8 * q4;
+          const float4 a0 = *(const float4 *)(AT + t * PA + s0), a1 = *(const float4 *)(AT + t * PA + s0 + 4);
+          const float tr[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+          bf16x8 th, tl;
+          split8(tr, th, tl);
+          acc = mfma(th, rh[kc], acc);
+          acc = mfma(th, rl[kc], acc);
+          acc = mfma(tl, rh[kc], acc);
         }
-#pragma unroll
-        for (int r = 0; r < 4; r++) dl[nj][r] = acc[r];
+        dl[tt] = acc;
+        const float4 kd = *(const float4 *)(sm + SM_KD * 64 + 16 * tt + 4 * q4);
+        dp[tt][0] = acc[0] * kd.x;
+        dp[tt][1] = acc[1] * kd.y;
+        dp[tt][2] = acc[2] * kd.z;
+        dp[tt][3] = acc[3] * kd.w;
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
-    lds_barrier();  // R is dead: Delta and Delta' take its place
+    // ---- O^T = diag(nq Gamma) (S0^T Q^T) + Delta^T P^T: rows j of this wave, column t
     {
-      const int tt = 16 * w + 4 * q4;
-      const float4 kd = *(const float4 *)(sm + SM_KD * 64 + tt);
-      const float kd4[4] = {kd.x, kd.y, kd.z, kd.w};
+      bf16x8 dh[2], dlo[2];
+      to_operand(dl[0], dl[1], dh[0], dlo[0]);
+      to_operand(dl[2], dl[3], dh[1], dlo[1]);
 #pragma unroll
-      for (int nj = 0; nj < 4; nj++) {
-        const int off = ((16 * nj + c16) * P72 + tt) * 2;
-        float d2[4];
+      for (int tt = 0; tt < 4; tt++) {
+        const int t = 16 * tt + c16;
+        f32x4 acc = oq[tt];
 #pragma unroll
-        for (int r = 0; r < 4; r++) d2[r] = dl[nj][r] * kd4[r];
-        uint2 hi, lo;
-        split4(dl[nj], hi, lo);
-        *(uint2 *)(WD + off) = hi;
-        *(uint2 *)(WD + PVS * P72 * 2 + off) = lo;
-        split4(d2, hi, lo);
-        *(uint2 *)(WD + 2 * PVS * P72 * 2 + off) = hi;
-        *(uint2 *)(WD + 3 * PVS * P72 * 2 + off) = lo;
-      }
-    }
-    lds_barrier();
-
-    // ---- O^T = diag(nq Gamma) (S0^T Q^T) + Delta^T P^T: rows j, column t of this wave's tile
-    {
-      const int t = 16 * w + c16;
-      bf16x8 bph[2], bpl[2];
-#pragma unroll
-      for (int ks = 0; ks < 2; ks++) {
-        const int o = (t * P72 + 8 * q4 + 32 * ks) * 2;
-        bph[ks] = ld8(Pl, o);
-        bpl[ks] = ld8(Pl, PC * P72 * 2 + o);
-      }
-      const float qgt = sm[SM_QG * 64 + t];
-#pragma unroll
-      for (int nj = 0; nj < 4; nj++) {
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < 4; ks++) {
-          const int ao = ((16 * nj + c16) * P136 + 8 * q4 + 32 * ks) * 2;
-          acc = mfma(ld8(St, ao), qa[ks], acc);
-          acc = mfma(ld8(St, PVS * P136 * 2 + ao), qa[ks], acc);
-        }
-#pragma unroll
-        for (int r = 0; r < 4; r++) acc[r] *= qgt;
-#pragma unroll
-        for (int ks = 0; ks < 2; ks++) {
-          const int ao = ((16 * nj + c16) * P72 + 8 * q4 + 32 * ks) * 2;
-          const bf16x8 adh = ld8(WD, ao), adl = ld8(WD, PVS * P72 * 2 + ao);
-          acc = mfma(adh, bph[ks], acc);
-          acc = mfma(adh, bpl[ks], acc);
-          acc = mfma(adl, bph[ks], acc);
+        for (int kc = 0; kc < 2; kc++) {
+          const int o = (t * P72 + 32 * kc + 8 * q4) * 2;
+          const bf16x8 ph = ld8(Pl, o), pl = ld8(Pl, PC * P72 * 2 + o);
+          acc = mfma(dh[kc], ph, acc);
+          acc = mfma(dh[kc], pl, acc);
+          acc = mfma(dlo[kc], ph, acc);
         }
         if (t < n) {
           const float o4[4] = {acc[0], acc[1], acc[2], acc[3]};
-          store4(D.out, D.out_dtype, ((tb + t) * H + h) * 128 + vs * PVS + 16 * nj + 4 * q4, o4);
+          store4(D.out, D.out_dtype, ((tb + t) * H + h) * PV + jw + 4 * q4, o4);
         }
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
-    // ---- S <- Gamma_C S0 + K^T Delta'
+    // ---- S <- Gamma_C S0 + K^T Delta' (rows d, this wave's columns)
     {
+      bf16x8 eh[2], el[2];
+      to_operand(dp[0], dp[1], eh[0], el[0]);
+      to_operand(dp[2], dp[3], eh[1], el[1]);
       const float gC = __expf(sm[SM_LC * 64 + 63]);
 #pragma unroll
-      for (int mt = 0; mt < 2; mt++) {
-        bf16x8 ak[2];
+      for (int dt = 0; dt < 8; dt++) {
+        const int d = 16 * dt + c16;
+        f32x4 acc;
 #pragma unroll
-        for (int ks = 0; ks < 2; ks++) {
-          const int d = 16 * (2 * w + mt) + c16;
-          ak[ks] = ld8(Kt, (d * P72 + tcol(d, 8 * q4 + 32 * ks)) * 2);
+        for (int r = 0; r < 4; r++) acc[r] = S[dt][r] * gC;
+#pragma unroll
+        for (int kc = 0; kc < 2; kc++) {
+          const bf16x8 a = ld8(Kt, (d * P72 + tcol(d, 32 * kc + 8 * q4)) * 2);
+          acc = mfma(a, eh[kc], acc);
+          acc = mfma(a, el[kc], acc);
         }
-#pragma unroll
-        for (int nj = 0; nj < 4; nj++) {
-          f32x4 acc;
-#pragma unroll
-          for (int r = 0; r < 4; r++) acc[r] = S[mt][nj][r] * gC;
-#pragma unroll
-          for (int ks = 0; ks < 2; ks++) {
-            const int bo = ((16 * nj + c16) * P72 + 8 * q4 + 32 * ks) * 2;
-            acc = mfma(ak[ks], ld8(WD, 2 * PVS * P72 * 2 + bo), acc);
-            acc = mfma(ak[ks], ld8(WD, 3 * PVS * P72 * 2 + bo), acc);
-          }
-#pragma unroll
-          for (int r = 0; r < 4; r++) S[mt][nj][r] = acc[r];
-        }
+        S[dt] = acc;
+        if (dt & 1) __builtin_amdgcn_sched_barrier(0);
       }
     }
-    lds_barrier();
-    store_st();
+    lds_barrier();  // the next chunk's staging overwrites the shared tiles
     c0 = c_next;
     // checkpoints reached at c0
     for (; ci < D.NC; ci++) {
       const int p = ck[ci];
       if (p > c0 && p <= len) break;
       if (p == c0) {
-        float *dst = D.ck_state + (((int64_t)b * D.NC + ci) * H + h) * PKD * 128 + vs * PVS;
+        float *dst = D.ck_state + (((int64_t)b * D.NC + ci) * H + h) * PKD * PV + jw + c16;
 #pragma unroll
-        for (int mt = 0; mt < 2; mt++)
+        for (int dt = 0; dt < 8; dt++)
 #pragma unroll
-          for (int nj = 0; nj < 4; nj++)
-#pragma unroll
-            for (int r = 0; r < 4; r++)
-              dst[(int64_t)(16 * (2 * w + mt) + 4 * q4 + r) * 128 + 16 * nj + c16] = S[mt][nj][r];
+          for (int r = 0; r < 4; r++) dst[(int64_t)(16 * dt + 4 * q4 + r) * PV] = S[dt][r];
       }
     }
   }
@@ -3791,7 +3773,7 @@ int sq_prefill(const sq_pool *pool, const sq_prefill_args *a, void *stream) {
   hipError_t e = hipFuncSetAttribute((const void *)pf::prefill_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                                      pf::LDS_BYTES);
   if (e != hipSuccess) return fail((int)e, "prefill: cannot raise the kernel's LDS limit");
-  hipLaunchKernelGGL(pf::prefill_kernel, dim3((unsigned)(a->batch * H * 2)), dim3(256), pf::LDS_BYTES, st, D);
+  hipLaunchKernelGGL(pf::prefill_kernel, dim3((unsigned)(a->batch * H)), dim3(pf::NT), pf::LDS_BYTES, st, D);
   rc = check_launch("prefill_kernel");
   if (rc) return rc;
   if (a->n_checkpoints > 0)
