@@ -294,6 +294,191 @@ __device__ __forceinline__ int carrier_pos(int plane_rel, int K, int i, int j) {
 __device__ __forceinline__ int colbase_of(const PoolDev &P, int h) { return P.columns[h]; }
 
 // =====================================================================
+// Encode, GDN heads of one width (no FP16 pivots), K = V = 128, packed,
+// 512 threads.  Every value of the tile is loaded once per layout, in one
+// batch of independent loads: row layout for the row scales (row group
+// tid / 32 takes rows rw + 16p, lane (l, k) = (lane / 4, lane % 4) the values
+// 32u + 8k + l), column layout (thread j + 128 hf: rows 32 hf .. 32 hf + 31 of
+// column j) for the column scales and codes.  A tile then waits for memory
+// twice rather than once per row and pass.  The operations and their order
+// are those of the general path below (the sums in PyTorch's order).
+// =====================================================================
+__device__ __forceinline__ void encode_fast128(const PoolDev &P, const float *__restrict__ X, uint8_t *page,
+                                               uint8_t *smem, int h, int W) {
+#pragma clang fp contract(off)
+  constexpr int K = 128, V = 128;
+  const int tid = threadIdx.x;
+  const bool two = W == 2;
+  const int NG = two ? V / 32 : 1;
+  const int ngrp = two ? 32 : V;
+  const int32_t *hm = P.head_meta + 4 * h;
+  const int code_start = hm[0], code_bytes = hm[1];
+  const int stride = P.offsets[(int64_t)P.H * K + h];
+  const int shift = (int)((uintptr_t)(page + code_start) & 15);
+  uint8_t *stage = smem;
+  float *rsc = (float *)(smem + P.stage);  // [K][NG]
+  float *wl = rsc + K * 4;                 // [K] fit weights
+  int *orel = (int *)(wl + K);             // [K] row offsets within the code region
+  float *cmax = (float *)(orel + K);       // [4][V]
+  float *bsum = cmax + 4 * V;              // [K/16][2][V]
+
+  // ---- row phase
+  {
+    const int lane = tid & 31, l = lane >> 2, k = lane & 3, rw = tid >> 5;
+    float v[8][4], wi[8];
+    int ro[8], of[8];
+#pragma unroll
+    for (int p = 0; p < 8; p++) {
+      const int i = rw + 16 * p;
+#pragma unroll
+      for (int u = 0; u < 4; u++) v[p][u] = X[i * V + 32 * u + 8 * k + l];
+      wi[p] = P.impact[(int64_t)h * K + i];
+      ro[p] = P.rows[(int64_t)h * K + i];
+      of[p] = P.offsets[(int64_t)h * K + i];
+    }
+#pragma unroll
+    for (int p = 0; p < 8; p++) {
+      const int i = rw + 16 * p;
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        if (g >= NG) break;
+        // 2-bit: one term per lane and group; otherwise four (ii ascending)
+        float acc = 0.0f;
+        if (two) {
+          acc += fabsf(v[p][g]);
+        } else {
+#pragma unroll
+          for (int u = 0; u < 4; u++) acc += fabsf(v[p][u]);
+        }
+        const float a1 = __shfl_down(acc, 1, 32), a2 = __shfl_down(acc, 2, 32), a3 = __shfl_down(acc, 3, 32);
+        float sl = acc;
+        sl += a1;
+        sl += a2;
+        sl += a3;
+        float total = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 8; q++) total += __shfl(sl, 4 * q, 32);
+        if (lane == 0) {
+          float m = total / (float)ngrp;
+          m = m < 1e-20f ? 1e-20f : m;
+          uint32_t hb;
+          const float r = fp16_scale(__builtin_sqrtf(m / wi[p]), &hb);
+          rsc[i * NG + g] = r;
+          put_page_half(page, ro[p] + 2 * g, hb);
+        }
+      }
+      if (lane == 0) {
+        wl[i] = wi[p];
+        orel[i] = of[p] - code_start;
+      }
+    }
+  }
+  // ---- column phase: this thread's 32 values of column j, raw and scaled
+  const int j = tid & (V - 1), hf = tid >> 7, i0 = 32 * hf;
+  const int g = two ? j / 32 : 0;
+  float xs[32], sc[32];
+#pragma unroll
+  for (int r = 0; r < 32; r++) xs[r] = X[(i0 + r) * V + j];
+  __syncthreads();
+  float amax = 0.0f;
+#pragma unroll
+  for (int r = 0; r < 32; r++) {
+    sc[r] = xs[r] / rsc[(i0 + r) * NG + g];
+    const float a = fabsf(sc[r]);
+    amax = a > amax ? a : amax;
+  }
+  cmax[hf * V + j] = amax;
+  __syncthreads();
+  float am = 0.0f;
+#pragma unroll
+  for (int u = 0; u < 4; u++) {
+    const float a = cmax[u * V + j];
+    am = a > am ? a : am;
+  }
+  const float qmax = two ? 3.0f : (float)((1 << (W - 1)) - 1);
+  const float t0 = am / (qmax * 1.0f);
+  const float c0 = fp16_scale(t0 > 0.0f ? t0 : 0.0f, nullptr);
+  auto zq = [&](float s, float cdiv) -> float {
+    const float y = s / cdiv;
+    if (two) return (y >= 0.0f ? 1.0f : -1.0f) * (fabsf(y) >= 2.0f ? 3.0f : 1.0f);
+    float z = __builtin_rintf(y);
+    z = z > -qmax ? z : -qmax;
+    z = z < qmax ? z : qmax;
+    return z;
+  };
+  // refit sums: two 16-row blocks per thread, each from zero
+#pragma unroll
+  for (int mb = 0; mb < 2; mb++) {
+    float bn = 0.0f, bd = 0.0f;
+#pragma unroll
+    for (int rr = 0; rr < 16; rr++) {
+      const int r = 16 * mb + rr, i = i0 + r;
+      const float wsq = (wl[i] * wl[i]) * 1.0f;
+      const float z = zq(sc[r], c0);
+      const float v = (rsc[i * NG + g] * 1.0f) * z;
+      bn += (wsq * v) * xs[r];
+      bd += wsq * (v * v);
+    }
+    const int m = 2 * hf + mb;
+    bsum[(2 * m) * V + j] = bn;
+    bsum[(2 * m + 1) * V + j] = bd;
+  }
+  __syncthreads();
+  float num = 0.0f, den = 0.0f;
+#pragma unroll
+  for (int m = 0; m < K / 16; m++) {
+    num += bsum[(2 * m) * V + j];
+    den += bsum[(2 * m + 1) * V + j];
+  }
+  const float denc = den < 1e-30f ? 1e-30f : den;
+  uint32_t chb;
+  const float c = fp16_scale(den > 0.0f ? num / denc : c0, &chb);
+  const int colbase = P.columns[h];
+  if (hf == 0 && colbase >= 0) put_page_half(page, colbase + 2 * (int64_t)j, chb);
+  // final codes; quads of lanes assemble each 4-value group
+  const int L = two ? 3 : (1 << (W - 1)) - 1;
+#pragma unroll
+  for (int r = 0; r < 32; r++) {
+    const int i = i0 + r;
+    const float z = zq(sc[r], c);
+    const uint32_t code = two ? (uint32_t)(((int)z + 3) / 2) : (uint32_t)((int)z + L);
+    const uint32_t c1 = __shfl_xor(code, 1), c2 = __shfl_xor(code, 2), c3 = __shfl_xor(code, 3);
+    if ((tid & 3) == 0) {
+      const uint32_t word = code | (c1 << W) | (c2 << (2 * W)) | (c3 << (3 * W));
+      lds_put_bytes(stage, shift + group_pos(orel[i], stride, 16, j, W), word, W / 2);
+    }
+  }
+  __syncthreads();
+  stage_out(page + code_start, code_bytes, stage, tid, 512);
+}
+
+// GDN pools with K = V = 128 (packed, 2-bit groups of 32): the fast form
+// above, FP16 pivot heads as halves of every value.
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void encode128_kernel(
+    PoolDev P, const float *__restrict__ state, const void *slots, int slots_dtype) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int H = P.H;
+  const int b = blockIdx.x / H, h = blockIdx.x % H;
+  const int64_t slot = load_slot(slots, slots_dtype, b);
+  if (slot <= 0 || slot >= P.num_slots) return;  // masked (or outside the pool)
+  uint8_t *page = P.data + slot * P.page_bytes;
+  const float *X = state + ((int64_t)b * H + h) * 128 * 128;
+  const int W = P.bits[(int64_t)h * 128];
+  if (W != 16) {
+    encode_fast128(P, X, page, smem, h, W);
+    return;
+  }
+  // pivot head: value (i, j) as a half at its tiled position
+  const int code_start = P.head_meta[4 * h];
+  const int stride = P.offsets[(int64_t)H * 128 + h];
+  for (int e = threadIdx.x; e < 128 * 128; e += 512) {
+    const int i = e >> 7, j = e & 127;
+    const int off = P.offsets[(int64_t)h * 128 + i];
+    put_page_half(page, (int64_t)code_start + (off - code_start) + (j / 16) * stride + (j % 16) * 2, f2h(X[e]));
+  }
+}
+
+// =====================================================================
 // Encode: dense fp32 -> page, bit-exact fit_state.  Thread j owns column j
 // (NT >= V); rows are processed by thread i in the row phase.
 // =====================================================================
@@ -318,7 +503,6 @@ __global__ __launch_bounds__(512) void encode_kernel(PoolDev P, const float *__r
   const int tile = tile_of(P);
   const int stride = P.offsets[(int64_t)H * K + h];
   const float *X = state + ((int64_t)b * H + h) * K * V;
-
   // LDS: staging window | row scale per (row, group) f32 [K * NG] | with a
   // row split: per-part column maxima [split][4][V] and 16-row block sums [K/16][2][V]
   uint8_t *stage = smem;
@@ -2476,11 +2660,11 @@ constexpr int OFF_KT = OFF_QC + PC * P136 * 2;     // bf16 [128 d][72]   k colum
 constexpr int OFF_VT = OFF_KT + PKD * P72 * 2;     // bf16 [128 j][72]   v columns (swizzled)
 constexpr int OFF_AT = OFF_VT + PV * P72 * 2;      // f32  [64 t][68]    A, then T = (I + A)^{-1}
 constexpr int OFF_P = OFF_AT + PC * PA * 4;        // bf16 2 x [64 t][72] masked, scaled Q K^T (hi, lo)
-constexpr int OFF_SM = OFF_P + 2 * PC * P72 * 2;   // f32 [10][64] per-token scalars
+constexpr int OFF_T = OFF_P + 2 * PC * P72 * 2;    // bf16 2 x [64 t][72] T (hi, lo)
+constexpr int OFF_SM = OFF_T + 2 * PC * P72 * 2;   // f32 [10][64] per-token scalars
 constexpr int OFF_R = OFF_SM + 10 * 64 * 4;        // f32 4 x [16][16] block products
-constexpr int OFF_CK = OFF_R + 4 * 256 * 4;        // int [MAX_CK] this sequence's checkpoints
-constexpr int MAX_CK = 64;
-constexpr int LDS_BYTES = OFF_CK + MAX_CK * 4;
+constexpr int LDS_BYTES = OFF_R + 4 * 256 * 4;
+constexpr int MAX_CK = 64;                          // checkpoints per sequence (one per lane)
 enum { SM_LC = 0, SM_BETA, SM_NK, SM_NQ, SM_GK, SM_QG, SM_KD, SM_KSQ, SM_QSQ };
 
 struct PrefillDev {
@@ -2523,15 +2707,6 @@ __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
 __device__ __forceinline__ bf16x8 ld8(const uint8_t *lds, int byte) { return *(const bf16x8 *)(lds + byte); }
 __device__ __forceinline__ float bf2f(uint16_t x) { return __uint_as_float((uint32_t)x << 16); }
 
-// x = hi + lo with hi = bf16(x), lo = bf16(x - hi)
-__device__ __forceinline__ void split8(const float x[8], bf16x8 &hi, bf16x8 &lo) {
-#pragma unroll
-  for (int e = 0; e < 8; e++) {
-    const __bf16 h = (__bf16)x[e];
-    hi[e] = h;
-    lo[e] = (__bf16)(x[e] - (float)h);
-  }
-}
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
   return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)a) | ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)b) << 16);
 }
@@ -2630,9 +2805,18 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
   float *sm = (float *)(smem + OFF_SM);
   uint8_t *Kc = smem + OFF_KC, *Qc = smem + OFF_QC, *Kt = smem + OFF_KT, *Vt = smem + OFF_VT;
   float *AT = (float *)(smem + OFF_AT);
-  uint8_t *Pl = smem + OFF_P;
+  uint8_t *Pl = smem + OFF_P, *Tb = smem + OFF_T;
   const __bf16 *qg = (const __bf16 *)D.q, *kg = (const __bf16 *)D.k, *vg = (const __bf16 *)D.v;
   const int jw = 16 * w;  // this wave's first state column
+  // T in bf16 hi/lo: blocks above the diagonal stay zero, the others are
+  // rewritten every chunk
+  for (int e = tid; e < 2 * PC * P72 / 2; e += NT) ((uint32_t *)Tb)[e] = 0u;
+  // T entry (t, s) as hi/lo bf16 next to its fp32 value
+  auto put_t = [&](int t, int s, float x) {
+    const __bf16 hi = (__bf16)x;
+    ((__bf16 *)Tb)[t * P72 + s] = hi;
+    ((__bf16 *)Tb)[PC * P72 + t * P72 + s] = (__bf16)(x - (float)hi);
+  };
 
   // ---- state S[d][j] of this wave's columns: tile dt holds rows d = 16 dt + 4 q4 + r, column jw + c16
   f32x4 S[8];
@@ -2643,23 +2827,16 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
 #pragma unroll
       for (int r = 0; r < 4; r++) S[dt][r] = src[(int64_t)(16 * dt + 4 * q4 + r) * PV];
   }
-  // this sequence's checkpoints, once, in LDS
-  int *ck = (int *)(smem + OFF_CK);
-  if (tid < D.NC) ck[tid] = D.ckpt[(int64_t)b * D.NC + tid];
-  lds_barrier();
-  // tokens of the segment starting at c: up to the next checkpoint past c,
-  // the sequence end, or one chunk
+  // this sequence's checkpoints (ascending), one per lane
+  const int ckv = l < D.NC ? D.ckpt[(int64_t)b * D.NC + l] : 0x7fffffff;
+  // tokens of the segment starting at c: up to the first listed checkpoint
+  // past c (within the sequence), the sequence end, or one chunk
   auto segment = [&](int c) {
-    int stop = len;
-    for (int i = 0; i < D.NC; i++) {
-      const int p = ck[i];
-      if (p > c && p <= len) {
-        stop = p < stop ? p : stop;
-        break;
-      }
-    }
+    const uint64_t m = __ballot(ckv > c && ckv <= len);
+    const int stop = m ? __builtin_amdgcn_readlane(ckv, __builtin_ctzll(m)) : len;
     return stop - c < PC ? stop - c : PC;
   };
+  lds_barrier();
   auto fetch = [&](Fetch &F, int c) {
     F.n = c < len ? segment(c) : 0;
     F.tb = (int64_t)t0 + c;
@@ -2851,7 +3028,10 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
       }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int r = 0; r < 16; r++) AT[(16 * w + r) * PA + 16 * w + l] = x[r];
+      for (int r = 0; r < 16; r++) {
+        AT[(16 * w + r) * PA + 16 * w + l] = x[r];
+        put_t(16 * w + r, 16 * w + l, x[r]);
+      }
     }
     lds_barrier();
     // off-diagonal blocks, one block row at a time (fp32 MFMA, waves 0-2):
@@ -2869,15 +3049,16 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
           }
 #pragma unroll
           for (int r = 0; r < 4; r++) Rs[(4 * q4 + r) * 16 + c16] = racc[r];
-        }
-        lds_barrier();
-        if (w < i) {
+          // Rs is this wave's own: its LDS accesses complete in order, no barrier
           f32x4 tacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int kk = 0; kk < 4; kk++)
             tacc = mfma32(-AT[(16 * i + c16) * PA + 16 * i + 4 * kk + q4], Rs[(4 * kk + q4) * 16 + c16], tacc);
 #pragma unroll
-          for (int r = 0; r < 4; r++) AT[(16 * i + 4 * q4 + r) * PA + 16 * w + c16] = tacc[r];
+          for (int r = 0; r < 4; r++) {
+            AT[(16 * i + 4 * q4 + r) * PA + 16 * w + c16] = tacc[r];
+            put_t(16 * i + 4 * q4 + r, 16 * w + c16, tacc[r]);
+          }
         }
         lds_barrier();
       }
@@ -2895,11 +3076,8 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kc = 0; kc < 2; kc++) {
-          const int s0 = 32 * kc + 8 * q4;
-          const float4 a0 = *(const float4 *)(AT + t * PA + s0), a1 = *(const float4 *)(AT + t * PA + s0 + 4);
-          const float tr[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-          bf16x8 th, tl;
-          split8(tr, th, tl);
+          const int o = (t * P72 + 32 * kc + 8 * q4) * 2;
+          const bf16x8 th = ld8(Tb, o), tl = ld8(Tb, PC * P72 * 2 + o);
           acc = mfma(th, rh[kc], acc);
           acc = mfma(th, rl[kc], acc);
           acc = mfma(tl, rh[kc], acc);
@@ -2963,7 +3141,7 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
     c0 = c_next;
     // checkpoints reached at c0
     for (; ci < D.NC; ci++) {
-      const int p = ck[ci];
+      const int p = __builtin_amdgcn_readlane(ckv, ci);
       if (p > c0 && p <= len) break;
       if (p == c0) {
         float *dst = D.ck_state + (((int64_t)b * D.NC + ci) * H + h) * PKD * PV + jw + c16;
@@ -3573,6 +3751,13 @@ int sq_encode(const sq_pool *pool, const float *state, const void *slots, int32_
   const int NT = split > 1 ? split * V : (V < 64 ? 64 : V);  // lanes per value column
   size_t lds = (size_t)stage_bytes(pool) + (size_t)((K * NG + 3) & ~3) * 4 + 16;
   if (split > 1) lds += (size_t)split * 4 * V * 4 + (size_t)(K / 16) * 2 * V * 4;
+  if (!pool->kda && pool->storage == 0 && K == 128 && V == 128 && pd.G == 32) {
+    // rows [K][4] | w [K] | row offsets [K] | column maxima [4][V] | block sums [K/16][2][V]
+    const size_t fl = (size_t)stage_bytes(pool) + (size_t)(K * 4 + 2 * K + 4 * V + (K / 16) * 2 * V) * 4;
+    hipLaunchKernelGGL(encode128_kernel, dim3((unsigned)(batch * pool->heads)), dim3(512), fl, (hipStream_t)stream,
+                       pd, state, slots, slots_dtype);
+    return check_launch("encode128_kernel");
+  }
   hipLaunchKernelGGL(encode_kernel, dim3((unsigned)(batch * pool->heads)), dim3(NT), lds, (hipStream_t)stream, pd,
                      state, slots, slots_dtype, split);
   return check_launch("encode_kernel");
