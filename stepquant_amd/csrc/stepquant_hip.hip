@@ -257,6 +257,19 @@ __device__ float torch_inner_sum(int64_t n, F f) {
   return total;
 }
 
+// torch_inner_sum of row[0..n-1], one vector lane at a time: the same
+// operations in the same order, with the lanes' loads not all in flight at
+// once (fully unrolled, they would hold n registers)
+__device__ float inner_sum_lanewise(const float *row, int n) {
+  if (n < 8) return torch_row_sum_ilp4(n, [&](int64_t t) { return row[t]; });
+  const int nvec = n / 8;
+  float total = 0.0f;
+  for (int t = nvec * 8; t < n; t++) total += row[t];
+#pragma unroll 1
+  for (int l = 0; l < 8; l++) total += torch_row_sum_ilp4(nvec, [&](int64_t m) { return row[8 * m + l]; });
+  return total;
+}
+
 // -------------------------------------------------------- pool metadata
 
 struct PoolDev {
@@ -3234,7 +3247,7 @@ __device__ __forceinline__ void fmt_write_codes(uint8_t *row, int j0, int W, uin
   for (int t = 0; t < W / 2; t++) p[t] = (uint8_t)(w >> (8 * t));
 }
 
-template <int MODE>
+template <int MODE, int KIND>  // KIND: the format (F.kind), fixed per instantiation
 __global__ __launch_bounds__(256) void format_kernel(FmtDev F, StepDev S) {
 #pragma clang fp contract(off)
   extern __shared__ __align__(16) uint8_t smem[];
@@ -3331,7 +3344,7 @@ __global__ __launch_bounds__(256) void format_kernel(FmtDev F, StepDev S) {
     }
   } else {
     float cj[4] = {0.f, 0.f, 0.f, 0.f};
-    if (F.kind == SQ_FMT_DSQ && act) {
+    if (KIND == SQ_FMT_DSQ && act) {
 #pragma unroll
       for (int c = 0; c < 4; c++) cj[c] = h2f(page_half(page, F.columns[h] + 4 * (j0 + c)));
     }
@@ -3342,7 +3355,7 @@ __global__ __launch_bounds__(256) void format_kernel(FmtDev F, StepDev S) {
       for (int c = 0; c < 4; c++) x[r][c] = 0.0f;
       if (!act || i >= K) continue;
       const uint8_t *row = page + F.offsets[(int64_t)h * K + i];
-      if (F.kind == SQ_FMT_FP32) {
+      if (KIND == SQ_FMT_FP32) {
         const float *fr = (const float *)row + j0;
 #pragma unroll
         for (int c = 0; c < 4; c++) x[r][c] = fr[c];
@@ -3351,7 +3364,7 @@ __global__ __launch_bounds__(256) void format_kernel(FmtDev F, StepDev S) {
       const uint32_t word = staged ? lds_word(stg, shift + (int)(((int64_t)i * V + j0) * W / 8))
                                    : fmt_read_codes(row, j0, W);
       const int64_t ro = F.rows[(int64_t)h * K + i];
-      if (F.kind == SQ_FMT_SYMMETRIC) {
+      if (KIND == SQ_FMT_SYMMETRIC) {
         const int64_t meta = ro + 4 * (j0 / FMT_TV);
         const float s = h2f(page_half(page, meta)), z = h2f(page_half(page, meta + 2));
 #pragma unroll
@@ -3411,7 +3424,7 @@ __global__ __launch_bounds__(256) void format_kernel(FmtDev F, StepDev S) {
   }
 
   // ---- encode x into the page
-  if (F.kind == SQ_FMT_FP32) {
+  if (KIND == SQ_FMT_FP32) {
 #pragma unroll
     for (int r = 0; r < FMT_RPT; r++) {
       const int i = rg + 8 * r;
@@ -3424,7 +3437,7 @@ __global__ __launch_bounds__(256) void format_kernel(FmtDev F, StepDev S) {
   }
   const float Lf = (float)L;
   float div[4];  // per column (DSQ) divisor; SYMMETRIC uses the per-row s
-  if (F.kind == SQ_FMT_SYMMETRIC) {
+  if (KIND == SQ_FMT_SYMMETRIC) {
     // s_i = fp16(max_j |x_ij| / L) over the tile's 128 columns (one group)
     float *red = big;  // [TV/4][K]
 #pragma unroll
@@ -3456,13 +3469,35 @@ __global__ __launch_bounds__(256) void format_kernel(FmtDev F, StepDev S) {
       for (int c = 0; c < 4; c++) xs[i * XS + 4 * cg + c] = fabsf(x[r][c]);
     }
     __syncthreads();
-    for (int i = tid; i < K; i += 256) {
-      const float s = torch_inner_sum(V, [&](int64_t t) { return xs[i * XS + t]; });
+    auto put_r = [&](int i, float s) {
       float m = s / (float)V;
       m = m < 1e-20f ? 1e-20f : m;
       uint32_t hb;
       rowv[i] = fp16_scale(__builtin_sqrtf(m), &hb);
       put_page_half(page, F.rows[(int64_t)h * K + i], hb);
+    };
+    if (V == 128) {
+      // 32 lanes per row: lane (l, k) = (lane / 4, lane % 4) adds columns
+      // 8(4ii + k) + l for ii ascending (PyTorch's 8 vector lanes with 4
+      // accumulators each), then the partial sums combine in PyTorch's order
+      const int lane = tid & 31, l = lane >> 2, kq = lane & 3;
+      for (int i = tid >> 5; i < K; i += 8) {
+        const float *row = xs + i * XS;
+        float acc = 0.0f;
+#pragma unroll
+        for (int ii = 0; ii < 4; ii++) acc += row[8 * (4 * ii + kq) + l];
+        const float a1 = __shfl_down(acc, 1, 32), a2 = __shfl_down(acc, 2, 32), a3 = __shfl_down(acc, 3, 32);
+        float sl = acc;
+        sl += a1;
+        sl += a2;
+        sl += a3;
+        float total = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 8; q++) total += __shfl(sl, 4 * q, 32);
+        if (lane == 0) put_r(i, total);
+      }
+    } else {
+      for (int i = tid; i < K; i += 256) put_r(i, inner_sum_lanewise(xs + i * XS, V));
     }
     __syncthreads();
     // y = x / r; c_j = fp16(max_i |y_ij| / L)
@@ -3495,7 +3530,7 @@ __global__ __launch_bounds__(256) void format_kernel(FmtDev F, StepDev S) {
     uint32_t word = 0;
 #pragma unroll
     for (int c = 0; c < 4; c++) {
-      const float d = F.kind == SQ_FMT_SYMMETRIC ? rowv[i] : div[c];
+      const float d = KIND == SQ_FMT_SYMMETRIC ? rowv[i] : div[c];
       float q = __builtin_rintf(x[r][c] / d);
       q = q > -Lf ? q : -Lf;
       q = q < Lf ? q : Lf;
@@ -3716,14 +3751,18 @@ int launch_format(const sq_format_pool *f, const FmtDev &fd, const StepDev &sd, 
     if (f->kind == SQ_FMT_SYMMETRIC) lds += (size_t)(TV / 4) * f->keys * 4;
     if (f->kind == SQ_FMT_DSQ) lds += (size_t)f->keys * (TV + 1) * 4;
   }
-  if (lds > 65536) {
-    hipError_t e = hipFuncSetAttribute((const void *)format_kernel<MODE>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return fail((int)e, "format: LDS attribute");
-  }
-  hipLaunchKernelGGL((format_kernel<MODE>), dim3((unsigned)(batch * f->heads), (unsigned)(f->values / TV)),
-                     dim3(256), lds, st, fd, sd);
-  return check_launch("format_kernel");
+  const dim3 grid((unsigned)(batch * f->heads), (unsigned)(f->values / TV));
+  auto go = [&](auto kernel) {
+    if (lds > 65536) {
+      hipError_t e = hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      if (e != hipSuccess) return fail((int)e, "format: LDS attribute");
+    }
+    hipLaunchKernelGGL(kernel, grid, dim3(256), lds, st, fd, sd);
+    return check_launch("format_kernel");
+  };
+  if (f->kind == SQ_FMT_FP32) return go(format_kernel<MODE, SQ_FMT_FP32>);
+  if (f->kind == SQ_FMT_SYMMETRIC) return go(format_kernel<MODE, SQ_FMT_SYMMETRIC>);
+  return go(format_kernel<MODE, SQ_FMT_DSQ>);
 }
 
 }  // namespace
