@@ -1,0 +1,127 @@
+"""The benchmark shapes themselves (MI355X): G6 and K6 decode steps over
+B=256 requests x 32 heads, and a P6-sized prefill (2048-token sequences,
+32 value heads over 16 key heads).  The whole problem runs on the GPU; the
+float oracle checks a sample of requests or heads (tiles are independent),
+and the properties that need no oracle are checked everywhere: the fused
+step equals the split readout + writer bit for bit, every output and page
+byte is finite/written, masked slots stay untouched.
+"""
+import numpy as np
+import pytest
+import torch
+
+import bench
+from oracle import oracle as O
+from tests.helpers import dev, make_plan
+from tests.test_gpu_pool import _check_requant
+
+pytestmark = pytest.mark.gpu
+
+
+def _oracle_plan(arch, bits, impact):
+    return make_plan(arch, bits.numpy(), impact=impact.numpy())
+
+
+@pytest.mark.parametrize("arch", ["gdn", "kda"])
+def test_decode_step_at_bench_shape(arch):
+    print(f"case {arch} B=256 H=32", flush=True)
+    from stepquant_amd.kernels.pool import PackedStatePool
+    from stepquant_amd.quantization import QuantizationPlan
+    B, H, K, V = 256, 32, 128, 128
+    HK = 16 if arch == "gdn" else 32
+    bits, impact = bench.make_plan(torch, arch, H, K, 6)
+    plan = QuantizationPlan(arch, bits.to(dev()), impact.to(dev()))
+    oplan = _oracle_plan(arch, bits, impact)
+    fused = PackedStatePool(plan, B + 1, V)
+    split = PackedStatePool(plan, B + 1, V, writeback_stream=torch.cuda.Stream())
+    g = torch.Generator(device=dev()).manual_seed(5)
+    slots = torch.arange(1, B + 1, device=dev())
+    x0 = torch.randn(B, H, K, V, device=dev(), generator=g) * .05
+    fused.encode(x0, slots)
+    split.encode(x0, slots)
+    pages0 = fused.data.cpu().numpy()
+    mixed = torch.randn(B, 2 * HK * K + H * V, device=dev(), generator=g).to(torch.bfloat16)
+    q, k, v = mixed.split([HK * K, HK * K, H * V], -1)  # column views with the row stride of mixed
+    gate = torch.randn(B, H * K if arch == "kda" else H, device=dev(), generator=g)
+    beta = torch.randn(B, H, device=dev(), generator=g)
+    a_log = torch.randn(H, device=dev(), generator=g) * .3  # per head; dt_bias per channel for KDA
+    dt_bias = torch.randn(H * K if arch == "kda" else H, device=dev(), generator=g) * .3
+    kw = dict(normalize=True, scale=K ** -.5, a_log=a_log, dt_bias=dt_bias)
+    out = fused.step(q, k, v, gate, beta, slots, **kw)
+    out_split = split.step(q, k, v, gate, beta, slots, **kw)
+    split.wait()
+    torch.cuda.synchronize()
+    assert torch.equal(out, out_split), "fused and split readouts differ"
+    assert torch.equal(fused.data, split.data), "fused and split pages differ"
+    assert torch.isfinite(out.float()).all()
+    assert not fused.data[0].any(), "slot 0 (sentinel) stays zero"
+    # oracle on a sample of requests: first and last
+    pick = np.array([0, B - 1])
+    lay = O.layout(oplan, V)
+    state = O.decode_page(pages0, pick + 1, oplan, lay, V)
+    qp, kp, ld, bo = O.prepare(q.float().cpu().numpy()[pick], k.float().cpu().numpy()[pick],
+                               gate.cpu().numpy()[pick], beta.cpu().numpy()[pick], H, K, arch == "kda",
+                               normalize=True, scale=K ** -.5, a_log=a_log.cpu().numpy(),
+                               dt_bias=dt_bias.cpu().numpy())
+    ref_out, upd = O.delta_step(state, qp, kp, v.float().cpu().numpy()[pick].reshape(len(pick), H, V), ld, bo)
+    np.testing.assert_allclose(out.float().cpu().numpy()[pick], ref_out, rtol=2 ** -8, atol=1e-4)
+    _check_requant(fused.data.cpu().numpy(), pick + 1, oplan, lay, V, upd)
+
+
+def test_prefill_at_bench_heads():
+    """Two 2048-token sequences over all 32 heads, checkpoints inside and at
+    the end; value heads 0, 1 (key head 0) and 30, 31 (key head 15) against
+    the float64 recurrence."""
+    print("case prefill B=2 T=2048 H=32 HK=16", flush=True)
+    from stepquant_amd.kernels.pool import PackedStatePool
+    from stepquant_amd.quantization import QuantizationPlan
+    H, HK, K, V, T = 32, 16, 128, 128, 2048
+    bits, impact = bench.make_plan(torch, "gdn", H, K, 6)
+    oplan = _oracle_plan("gdn", bits, impact)
+    pool = PackedStatePool(QuantizationPlan("gdn", bits.to(dev()), impact.to(dev())), 8, V)
+    g = torch.Generator().manual_seed(9)
+    init = torch.tensor([1, 2])
+    pool.encode((torch.randn(2, H, K, V, generator=g) * .05).to(dev()), init.to(dev()))
+    lay = O.layout(oplan, V)
+    pages0 = pool.data.cpu().numpy()
+    S0 = O.decode_page(pages0, init.numpy(), oplan, lay, V).astype(np.float64)
+    q = torch.randn(2 * T, HK, K, generator=g).to(torch.bfloat16)
+    k = torch.randn(2 * T, HK, K, generator=g).to(torch.bfloat16)
+    v = torch.randn(2 * T, H, V, generator=g).to(torch.bfloat16)
+    gate = torch.randn(2 * T, H, generator=g)
+    beta = torch.randn(2 * T, H, generator=g)
+    a_log = torch.zeros(H)
+    dt_bias = torch.zeros(H)
+    cu = np.array([0, T, 2 * T])
+    ck = np.array([[1000, T], [640, T]])
+    ck_slots = torch.tensor([[3, 4], [5, 6]])
+    out = pool.extend(q.to(dev()), k.to(dev()), v.to(dev()), gate.to(dev()), beta.to(dev()), init,
+                      torch.from_numpy(cu), checkpoints=torch.from_numpy(ck), checkpoint_slots=ck_slots,
+                      init_slots=init, normalize=True, scale=K ** -.5, a_log=a_log.to(dev()),
+                      dt_bias=dt_bias.to(dev()))
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    states = pool._last_prefill[-1].cpu().numpy().reshape(2, 2, H, K, V)
+    assert np.isfinite(got).all()
+    for heads in ([0, 1], [30, 31]):
+        hk = heads[0] // 2
+        ref_out, ref_states, _ = O.prefill(q.float().numpy()[:, [hk]], k.float().numpy()[:, [hk]],
+                                           v.float().numpy()[:, heads], gate.numpy()[:, heads],
+                                           beta.numpy()[:, heads], S0[:, heads], cu, ck, normalize=True,
+                                           scale=K ** -.5, a_log=a_log.numpy()[heads],
+                                           dt_bias=dt_bias.numpy()[heads])
+        scale = np.abs(ref_out).max(-1, keepdims=True) + 1e-30
+        err = np.abs(got[:, heads] - ref_out) / scale
+        assert err.max() <= 2 ** -8 + 1e-3, f"heads {heads}: output error {err.max():.2e}"
+        for b in range(2):
+            for c in range(2):
+                ref = ref_states[b, c]
+                e = np.abs(states[b, c][heads] - ref) / (np.abs(ref).max(-1, keepdims=True) + 1e-30)
+                assert e.max() <= 1e-3, f"heads {heads} b={b} c={c}: state error {e.max():.2e}"
+    # the prefix pages are the oracle encoding of the kernel's states
+    ref_pages = pages0.copy()
+    O.encode_page(states.reshape(4, H, K, V), ck_slots.numpy().reshape(-1), oplan, lay, ref_pages)
+    pages = pool.data.cpu().numpy()
+    for s in ck_slots.numpy().reshape(-1):
+        assert np.array_equal(pages[s], ref_pages[s]), f"slot {s} page differs"
+    assert not pages[7].any(), "unused slot stays empty"
