@@ -29,8 +29,6 @@ namespace {
 
 // ------------------------------------------------------------------ fp16
 
-__device__ __forceinline__ float bits_to_f32(uint32_t u) { return __uint_as_float(u); }
-
 // IEEE half <-> float by the hardware conversions (v_cvt_f32_f16,
 // v_cvt_f16_f32): exact one way, round to nearest even the other, subnormal
 // halves kept (f16 denormals are on in these kernels), overflow to infinity:
@@ -1378,10 +1376,10 @@ __device__ __forceinline__ void row_setup_int(const StepDev &S, const Ctx &C, in
   }
 }
 
-// Per-row inputs, once per workgroup into LDS (threads 0..127, row i = tid):
-// prepared q (scaled), prepared k, and a_i = r_i * retention per value group.
+// Per-row inputs of FP16 pivot heads, once per workgroup into LDS (threads
+// 0..127, row i = tid): prepared q (scaled) and prepared k.
 template <int MODE>
-__device__ __forceinline__ void row_setup(const StepDev &S, const Ctx &C, int NG) {
+__device__ __forceinline__ void row_setup(const StepDev &S, const Ctx &C) {
   if (C.tid < FK) {
     const int i = C.tid;
     float nq = 1.0f, nk = 1.0f;
@@ -1627,7 +1625,6 @@ __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx
   constexpr float ZS = W == 2 ? 2.0f : 1.0f;
   constexpr uint32_t XM = W == 8 ? 0x80808080u : W == 6 ? 0x820820u : W == 4 ? 0x8888u : 0xAAu;
   constexpr int SEG = 2 * W;                   // bytes of one row's 16-value segment
-  constexpr int BLK = FK * SEG;                // bytes of one 16-column block
   const int NG = W == 2 ? FV / P.G : 1;
   const int g = W == 2 ? C.j0 / P.G : 0;
   const uint16_t *c16 = (const uint16_t *)C.cst;
@@ -1908,7 +1905,7 @@ __device__ __forceinline__ void pivot_body(const PoolDev &P, const StepDev &S, C
   __syncthreads();
   const float beta = C.misc[0], decay = C.misc[1];
   handoff<MODE>(P, S, C);
-  row_setup<MODE>(S, C, 0);
+  row_setup<MODE>(S, C);
   __syncthreads();
   float qi[FRPT], ki[FRPT];
 #pragma unroll
@@ -2060,19 +2057,8 @@ __host__ __device__ __forceinline__ int block_pitch(int stride) {
   return 64 * ((16 * block_chunks(stride) - 32 + 63) / 64) + 32;
 }
 
-__device__ __forceinline__ void stage_in_blocks(const uint8_t *g0, int stride, int pitch, uint8_t *lds, int tid) {
-  const int nc = block_chunks(stride);
-  const int gmod = (int)((uintptr_t)g0 & 15);
-  for (int f = tid; f < 32 * nc; f += FNT) {
-    const int blk = f & 31, ch = f >> 5;
-    const int off = blk * stride;
-    const uint4 *src = (const uint4 *)(g0 + (off - ((gmod + off) & 15)));
-    ((uint4 *)(lds + blk * pitch))[ch] = src[ch];
-  }
-}
-
-// The same staging with direct global-to-LDS loads (no registers, no waits
-// until the next barrier): wave w copies blocks 8w..8w+7, one instruction
+// Staging with direct global-to-LDS loads (no registers, no waits until the
+// next barrier): wave w copies blocks 8w..8w+7, one instruction
 // per block and 64 chunks (a block's window is contiguous in LDS).
 __device__ __forceinline__ void stage_blocks_async(const uint8_t *g0, int stride, int pitch, uint8_t *lds, int tid) {
   const int nc = block_chunks(stride);
