@@ -1224,6 +1224,9 @@ __global__ __launch_bounds__(512) void step_kernel(PoolDev P, StepDev S) {
 #ifndef SCHED_ROWS
 #define SCHED_ROWS 4  // rows between scheduling fences (bounds hoisted LDS loads)
 #endif
+#ifndef KDA_SCHED_ROWS
+#define KDA_SCHED_ROWS 2  // the KDA tile's per-row metadata loads need the tighter bound
+#endif
 
 namespace fast {
 
@@ -2226,7 +2229,7 @@ __device__ __forceinline__ void body(const PoolDev &P, const StepDev &S, KCtx &C
   float aK[4] = {0.f, 0.f, 0.f, 0.f}, aQ[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int r = 0; r < FRPT; r++) {
-    if ((r % SCHED_ROWS) == SCHED_ROWS - 1) __builtin_amdgcn_sched_barrier(0);
+    if ((r % KDA_SCHED_ROWS) == KDA_SCHED_ROWS - 1) __builtin_amdgcn_sched_barrier(0);
     const int i = C.rg + 8 * r;
     const int4 m = C.rm[i];
     const uint32_t word = word_at(C.code, m.x + base) ^ (uint32_t)m.z;
@@ -2303,7 +2306,7 @@ __device__ __forceinline__ void body(const PoolDev &P, const StepDev &S, KCtx &C
   float rowp[FRPT];
 #pragma unroll
   for (int r = 0; r < FRPT; r++) {
-    if ((r % SCHED_ROWS) == SCHED_ROWS - 1) __builtin_amdgcn_sched_barrier(0);
+    if ((r % KDA_SCHED_ROWS) == KDA_SCHED_ROWS - 1) __builtin_amdgcn_sched_barrier(0);
     const int i = C.rg + 8 * r;
     const float4 rc = C.rc[i];
     const float k = C.ks[i];
@@ -2360,7 +2363,7 @@ __device__ __forceinline__ void body(const PoolDev &P, const StepDev &S, KCtx &C
   float mx[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int r = 0; r < FRPT; r++) {
-    if ((r % SCHED_ROWS) == SCHED_ROWS - 1) __builtin_amdgcn_sched_barrier(0);
+    if ((r % KDA_SCHED_ROWS) == KDA_SCHED_ROWS - 1) __builtin_amdgcn_sched_barrier(0);
     const float4 rl = C.rl[C.rg + 8 * r];
 #pragma unroll
     for (int c = 0; c < 4; c++) {
@@ -2382,7 +2385,7 @@ __device__ __forceinline__ void body(const PoolDev &P, const StepDev &S, KCtx &C
   // |y| <= L_i (1 + 2^-11) unless c0 saturated: rint needs no clamp
 #pragma unroll
   for (int r = 0; r < FRPT; r++) {
-    if ((r % SCHED_ROWS) == SCHED_ROWS - 1) __builtin_amdgcn_sched_barrier(0);
+    if ((r % KDA_SCHED_ROWS) == KDA_SCHED_ROWS - 1) __builtin_amdgcn_sched_barrier(0);
     const float U = C.rl[C.rg + 8 * r].w;
 #pragma unroll
     for (int c = 0; c < 4; c++) {
@@ -2435,7 +2438,7 @@ __device__ __forceinline__ void body(const PoolDev &P, const StepDev &S, KCtx &C
   // ---- final codes: level = rint(y) + L saturated to [0, 2L], packed with the row's width
 #pragma unroll
   for (int r = 0; r < FRPT; r++) {
-    if ((r % SCHED_ROWS) == SCHED_ROWS - 1) __builtin_amdgcn_sched_barrier(0);
+    if ((r % KDA_SCHED_ROWS) == KDA_SCHED_ROWS - 1) __builtin_amdgcn_sched_barrier(0);
     const int i = C.rg + 8 * r;
     const float4 rl = C.rl[i];
     const int4 m = C.rm[i];
@@ -2549,8 +2552,12 @@ __device__ __forceinline__ void kda_prologue(const PoolDev &P, const StepDev &S,
   if (C.tid >= FK) C.wv[i] = w;
 }
 
+// Four waves per SIMD (128 VGPRs) leave 14 values spilled to scratch, stored
+// once before the pivot rows and reloaded once: still faster on the K6 step
+// than three waves without spills (155 us against 164 us), because the extra
+// wave hides the tile's LDS and input latency.
 #ifndef KDA128_WAVES
-#define KDA128_WAVES 3
+#define KDA128_WAVES 4
 #endif
 template <int MODE, bool QW4>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KDA128_WAVES))) void kda128_kernel(PoolDev P,
