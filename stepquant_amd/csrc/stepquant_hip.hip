@@ -1567,6 +1567,15 @@ __device__ __forceinline__ int opaque(int x) {
   return x;
 }
 
+// w + w + [bit set for this lane] in one add with carry-in: the lane mask
+// (a compare's ballot) is the carry, so a bit is shifted in without a select
+__device__ __forceinline__ uint32_t shift_in(uint32_t w, uint64_t mask) {
+  uint32_t r;
+  uint64_t carry;
+  asm("v_addc_co_u32_e64 %0, %1, %2, %2, %3" : "=v"(r), "=s"(carry) : "v"(w), "s"(mask));
+  return r;
+}
+
 // byte offset of this lane's first code row segment in the staged region:
 // rows rg + 8r follow 8 * 2W bytes apart
 template <int W>
@@ -1806,16 +1815,20 @@ __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx
 #pragma unroll
     for (int c = 0; c < 4; c++) {
       const float y = cf[r][c] * f0[c];
-      float z;
       if (W == 2) {
+        // z = +-mag carries the sign of t (f0 > 0, and y = -0 gives +mag for
+        // t = -0, whose term is zero either way), so U z t = (U mag) |t| and
+        // U z z = (U mag) mag with the same roundings: no sign select needed
         const float mag = fabsf(y) >= 2.0f ? 3.0f : 1.0f;
-        z = y >= 0.0f ? mag : -mag;
+        const float t = U * mag;
+        num[c] = fmaf(t, fabsf(cf[r][c]), num[c]);
+        den[c] = fmaf(t, mag, den[c]);
       } else {
-        z = __builtin_rintf(y);
+        const float z = __builtin_rintf(y);
+        const float t = U * z;
+        num[c] = fmaf(t, cf[r][c], num[c]);
+        den[c] = fmaf(t, z, den[c]);
       }
-      const float t = U * z;
-      num[c] = fmaf(t, cf[r][c], num[c]);
-      den[c] = fmaf(t, z, den[c]);
     }
   }
   if (W != 2 && __any(top)) {
@@ -1869,13 +1882,16 @@ __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx
     if ((r % SCHED_ROWS) == SCHED_ROWS - 1) __builtin_amdgcn_sched_barrier(0);
     uint32_t word;
     if (W == 2) {
+      // code = 2 [y >= 0] + [(y >= 0) == (|y| >= 2)] ({0,1,2,3} for levels
+      // -3, -1, 1, 3), shifted in from the last column: one add with carry-in
+      // per bit
       word = 0;
 #pragma unroll
-      for (int c = 0; c < 4; c++) {
+      for (int c = 3; c >= 0; c--) {
         const float y = cf[r][c] * f[c];
-        const bool big = fabsf(y) >= 2.0f;
-        const uint32_t code = y >= 0.0f ? (big ? 3u : 2u) : (big ? 0u : 1u);
-        word |= code << (c * W);
+        const uint64_t pos = __builtin_amdgcn_ballot_w64(y >= 0.0f);
+        const uint64_t big = __builtin_amdgcn_ballot_w64(fabsf(y) >= 2.0f);
+        word = shift_in(shift_in(word, pos), ~(pos ^ big));
       }
     } else {
       float v[4];
