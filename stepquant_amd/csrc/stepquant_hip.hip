@@ -103,6 +103,19 @@ __device__ __forceinline__ void store4(void *p, int dtype, int64_t idx, const fl
   }
 }
 
+// four consecutive elements starting at a multiple of 4 of an 8-byte aligned
+// array: 16-bit values go out as one 8-byte store instead of four 2-byte ones
+__device__ __forceinline__ void store4_aligned(void *p, int dtype, int64_t idx, const float v[4]) {
+  if (dtype == SQ_F32) {
+    *(float4 *)((float *)p + idx) = make_float4(v[0], v[1], v[2], v[3]);
+    return;
+  }
+  uint32_t e[4];
+#pragma unroll
+  for (int c = 0; c < 4; c++) e[c] = dtype == SQ_BF16 ? f2bf(v[c]) : f2h(v[c]);
+  *(uint2 *)((uint16_t *)p + idx) = make_uint2(e[0] | (e[1] << 16), e[2] | (e[3] << 16));
+}
+
 __device__ __forceinline__ int64_t load_slot(const void *p, int dtype, int64_t idx) {
   return dtype == SQ_I64 ? ((const int64_t *)p)[idx] : (int64_t)((const int32_t *)p)[idx];
 }
@@ -2794,7 +2807,7 @@ __device__ __forceinline__ f32x4 mfma32(float a, float b, f32x4 c) {
 // global loads overlap the previous chunk's arithmetic.
 struct Fetch {
   uint4 k[2], q[2], v[2];
-  float lg, bt;
+  uint32_t lg, bt;  // raw gate and beta bits (an f32 word or a 16-bit value)
   int n;
   int64_t tb;
 };
@@ -2824,12 +2837,16 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
   const int hk = h / (H / D.HK);
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, q4 = l >> 4, c16 = l & 15;
   const int t0 = D.cu[b], len = D.cu[b + 1] - t0;
+  if (len <= 0) return;  // whole workgroup: an empty sequence has no chunk and no checkpoint
   float *sm = (float *)(smem + OFF_SM);
   uint8_t *Kc = smem + OFF_KC, *Qc = smem + OFF_QC, *Kt = smem + OFF_KT, *Vt = smem + OFF_VT;
   float *AT = (float *)(smem + OFF_AT);
   uint8_t *Pl = smem + OFF_P, *Tb = smem + OFF_T;
   const __bf16 *qg = (const __bf16 *)D.q, *kg = (const __bf16 *)D.k, *vg = (const __bf16 *)D.v;
   const int jw = 16 * w;  // this wave's first state column
+  // one store per 4 output values when the output array's alignment allows
+  // it (16 bytes for fp32, 8 for 16-bit values)
+  const bool out_aligned = ((uintptr_t)D.out & (D.out_dtype == SQ_F32 ? 15 : 7)) == 0;
   // T in bf16 hi/lo: blocks above the diagonal stay zero, the others are
   // rewritten every chunk
   for (int e = tid; e < 2 * PC * P72 / 2; e += NT) ((uint32_t *)Tb)[e] = 0u;
@@ -2859,23 +2876,32 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
     return stop - c < PC ? stop - c : PC;
   };
   lds_barrier();
+  // The loads are unconditional, from rows clamped into the sequence (tokens
+  // past the segment are zeroed when staged): nothing computed from a loaded
+  // value may sit here, or the wait for the load would too.
   auto fetch = [&](Fetch &F, int c) {
     F.n = c < len ? segment(c) : 0;
     F.tb = (int64_t)t0 + c;
 #pragma unroll
     for (int it = 0; it < 2; it++) {
       const int idx = tid + NT * it, t = idx >> 4, d8 = (idx & 15) * 8;
-      const bool in = t < F.n;
-      const int64_t row = F.tb + t;
-      F.k[it] = in ? *(const uint4 *)(kg + row * D.k_stride + hk * PKD + d8) : make_uint4(0u, 0u, 0u, 0u);
-      F.q[it] = in ? *(const uint4 *)(qg + row * D.q_stride + hk * PKD + d8) : make_uint4(0u, 0u, 0u, 0u);
-      F.v[it] = in ? *(const uint4 *)(vg + row * D.v_stride + h * PV + d8) : make_uint4(0u, 0u, 0u, 0u);
+      const int tc = c + t < len ? c + t : len - 1;
+      const int64_t row = (int64_t)t0 + tc;
+      F.k[it] = *(const uint4 *)(kg + row * D.k_stride + hk * PKD + d8);
+      F.q[it] = *(const uint4 *)(qg + row * D.q_stride + hk * PKD + d8);
+      F.v[it] = *(const uint4 *)(vg + row * D.v_stride + h * PV + d8);
     }
-    F.lg = 0.f;
-    F.bt = 0.f;
-    if (w == 0 && l < F.n) {
-      F.lg = load_val(D.g, D.gate_dtype, (F.tb + l) * H + h);
-      F.bt = load_val(D.beta, D.gate_dtype, (F.tb + l) * H + h);
+    if (w == 0) {
+      const int64_t at = ((int64_t)t0 + (c + l < len ? c + l : len - 1)) * H + h;
+      if (D.gate_dtype == SQ_F32) {
+        F.lg = ((const uint32_t *)D.g)[at];
+        F.bt = ((const uint32_t *)D.beta)[at];
+      } else {
+        F.lg = ((const uint16_t *)D.g)[at];
+        F.bt = ((const uint16_t *)D.beta)[at];
+      }
+    } else {
+      F.lg = F.bt = 0u;  // read by wave 0 only
     }
   };
 
@@ -2897,10 +2923,12 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
 #pragma unroll
     for (int it = 0; it < 2; it++) {
       const int idx = tid + NT * it, t = idx >> 4, d8 = (idx & 15) * 8;
-      *(uint4 *)(Kc + (t * P136 + d8) * 2) = F.k[it];
-      *(uint4 *)(Qc + (t * P136 + d8) * 2) = F.q[it];
-      const uint16_t *ke = (const uint16_t *)&F.k[it], *qe = (const uint16_t *)&F.q[it];
-      const uint16_t *ve = (const uint16_t *)&F.v[it];
+      const uint4 zero = make_uint4(0u, 0u, 0u, 0u);
+      const uint4 kv = t < n ? F.k[it] : zero, qv = t < n ? F.q[it] : zero, vv = t < n ? F.v[it] : zero;
+      *(uint4 *)(Kc + (t * P136 + d8) * 2) = kv;
+      *(uint4 *)(Qc + (t * P136 + d8) * 2) = qv;
+      const uint16_t *ke = (const uint16_t *)&kv, *qe = (const uint16_t *)&qv;
+      const uint16_t *ve = (const uint16_t *)&vv;
       float sk = 0.f, sq = 0.f;
       // rows d8 .. d8 + 7 share their swizzle (bits 3-5 of the row): one
       // base address, the rows at immediate offsets
@@ -2921,7 +2949,12 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
       }
     }
     if (w == 0) {
-      float lg = F.lg, bt = F.bt;
+      auto gate = [&](uint32_t x) {
+        if (l >= n) return 0.0f;
+        if (D.gate_dtype == SQ_F32) return __uint_as_float(x);
+        return D.gate_dtype == SQ_BF16 ? __uint_as_float(x << 16) : h2f((uint16_t)x);
+      };
+      float lg = gate(F.lg), bt = gate(F.bt);
       if (D.a_log && l < n) {
         const float u = lg + dt_h;
         const float sp = u > 20.0f ? u : __logf(1.0f + __expf(u < 20.0f ? u : 20.0f));
@@ -3132,7 +3165,9 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
         }
         if (t < n) {
           const float o4[4] = {acc[0], acc[1], acc[2], acc[3]};
-          store4(D.out, D.out_dtype, ((tb + t) * H + h) * PV + jw + 4 * q4, o4);
+          const int64_t at = ((tb + t) * H + h) * PV + jw + 4 * q4;
+          if (out_aligned) store4_aligned(D.out, D.out_dtype, at, o4);
+          else store4(D.out, D.out_dtype, at, o4);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
