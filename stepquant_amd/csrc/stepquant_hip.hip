@@ -2668,13 +2668,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KDA128_WAVE
 // (v_mfma_f32_16x16x32_bf16) with fp32 accumulation.
 //
 // For a chunk with start state S0 [K, V], Gamma_t = prod_{s<=t} g_s:
-//   A_ts  = beta_t (Gamma_t/Gamma_s) k_t.k_s  (s < t),  T = (I + A)^{-1}
-//   Delta = T R,  R = diag(beta) (V - diag(Gamma) K S0)
+//   A_ts  = beta_t (Gamma_t/Gamma_s) k_t.k_s  (s < t)
+//   Delta = (I + A)^{-1} R,  R = diag(beta) (V - diag(Gamma) K S0)
 //   O     = diag(Gamma) Q S0 + (M o Q K^T) Delta,        M_ts = Gamma_t/Gamma_s (s <= t)
 //   S_C   = Gamma_C S0 + (diag(Gamma_C/Gamma) K)^T Delta
 // (q, k L2-normalised and q scaled: the norms multiply into the products).
 // One workgroup per (sequence, head): 8 waves, chunks in order.
-// Operands with a single rounding to bf16 would lose precision (T, W, P,
+// Delta comes from 16-token blocks: D_i = T_ii (R_i - sum_{k<i} A_ik D_k),
+// T_ii = (I + A_ii)^{-1}.
+// Operands with a single rounding to bf16 would lose precision (T_ii, A, P,
 // Delta, S); they are split as x = hi + lo (two bf16) and multiplied as
 // hi*hi + hi*lo + lo*hi, leaving ~2^-16 relative error per product; q, k, v
 // are bf16 inputs and enter exactly.
@@ -2693,12 +2695,11 @@ constexpr int OFF_KC = 0;                          // bf16 [64 t][136]   k rows 
 constexpr int OFF_QC = OFF_KC + PC * P136 * 2;     // bf16 [64 t][136]   q rows
 constexpr int OFF_KT = OFF_QC + PC * P136 * 2;     // bf16 [128 d][72]   k columns (t contiguous, swizzled)
 constexpr int OFF_VT = OFF_KT + PKD * P72 * 2;     // bf16 [128 j][72]   v columns (swizzled)
-constexpr int OFF_AT = OFF_VT + PV * P72 * 2;      // f32  [64 t][68]    A, then T = (I + A)^{-1}
+constexpr int OFF_AT = OFF_VT + PV * P72 * 2;      // f32  [64 t][68]    A (diagonal blocks read)
 constexpr int OFF_P = OFF_AT + PC * PA * 4;        // bf16 2 x [64 t][72] masked, scaled Q K^T (hi, lo)
-constexpr int OFF_T = OFF_P + 2 * PC * P72 * 2;    // bf16 2 x [64 t][72] T (hi, lo)
+constexpr int OFF_T = OFF_P + 2 * PC * P72 * 2;    // bf16 2 x [64 t][72] M (hi, lo): T_ii, -A_ik (i > k), 0
 constexpr int OFF_SM = OFF_T + 2 * PC * P72 * 2;   // f32 [10][64] per-token scalars
-constexpr int OFF_R = OFF_SM + 10 * 64 * 4;        // f32 4 x [16][16] block products
-constexpr int LDS_BYTES = OFF_R + 4 * 256 * 4;
+constexpr int LDS_BYTES = OFF_SM + 10 * 64 * 4;
 constexpr int MAX_CK = 64;                          // checkpoints per sequence (one per lane)
 enum { SM_LC = 0, SM_BETA, SM_NK, SM_NQ, SM_GK, SM_QG, SM_KD, SM_KSQ, SM_QSQ };
 
@@ -2797,10 +2798,6 @@ __device__ __forceinline__ void to_operand(const f32x4 &x0, const f32x4 &x1, bf1
 __device__ __forceinline__ float row16_sum(float x) {
   x = fast::rg8_sum(x);
   return x + fast::dpp<0x140>(x);  // row_mirror
-}
-
-__device__ __forceinline__ f32x4 mfma32(float a, float b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
 // Raw inputs of one chunk, fetched into registers one chunk ahead so the
@@ -3019,7 +3016,15 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
           av[r] = s < t ? (bnt * nk4[r]) * e * aA[r] : 0.0f;
           pv[r] = s <= t ? (nqt * nk4[r]) * e * aP[r] : 0.0f;
         }
-        *(float4 *)(AT + t * PA + s0) = make_float4(av[0], av[1], av[2], av[3]);
+        if (ns == tw) {
+          *(float4 *)(AT + t * PA + s0) = make_float4(av[0], av[1], av[2], av[3]);
+        } else if (ns < tw) {  // -A of the block below the diagonal, as hi/lo
+          const float na[4] = {-av[0], -av[1], -av[2], -av[3]};
+          uint2 ah, al;
+          split4(na, ah, al);
+          *(uint2 *)(Tb + (t * P72 + s0) * 2) = ah;
+          *(uint2 *)(Tb + PC * P72 * 2 + (t * P72 + s0) * 2) = al;
+        }
         uint2 hi, lo;
         split4(pv, hi, lo);
         *(uint2 *)(Pl + (t * P72 + s0) * 2) = hi;
@@ -3070,7 +3075,7 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
     }
     lds_barrier();
 
-    // ---- T = (I + A)^{-1}: diagonal 16x16 blocks by forward substitution (waves 0-3)
+    // ---- T_ii = (I + A_ii)^{-1}: diagonal 16x16 blocks by forward substitution (waves 0-3)
     if (w < 4 && l < 16) {
       const float *blk = AT + 16 * w * PA + 16 * w;
       float x[16];
@@ -3083,67 +3088,44 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
       }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        AT[(16 * w + r) * PA + 16 * w + l] = x[r];
-        put_t(16 * w + r, 16 * w + l, x[r]);
-      }
+      for (int r = 0; r < 16; r++) put_t(16 * w + r, 16 * w + l, x[r]);
     }
     lds_barrier();
-    // off-diagonal blocks, one block row at a time (fp32 MFMA, waves 0-2):
-    // T_iw = -T_ii sum_{k=w}^{i-1} A_ik T_kw
-    {
-      float *Rs = (float *)(smem + OFF_R) + 256 * (w & 3);
-      for (int i = 1; i < 4; i++) {
-        f32x4 racc = {0.f, 0.f, 0.f, 0.f};
-        if (w < i) {
-          for (int kb = w; kb < i; kb++) {
-#pragma unroll
-            for (int kk = 0; kk < 4; kk++)
-              racc = mfma32(AT[(16 * i + c16) * PA + 16 * kb + 4 * kk + q4],
-                            AT[(16 * kb + 4 * kk + q4) * PA + 16 * w + c16], racc);
-          }
-#pragma unroll
-          for (int r = 0; r < 4; r++) Rs[(4 * q4 + r) * 16 + c16] = racc[r];
-          // Rs is this wave's own: its LDS accesses complete in order, no barrier
-          f32x4 tacc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int kk = 0; kk < 4; kk++)
-            tacc = mfma32(-AT[(16 * i + c16) * PA + 16 * i + 4 * kk + q4], Rs[(4 * kk + q4) * 16 + c16], tacc);
-#pragma unroll
-          for (int r = 0; r < 4; r++) {
-            AT[(16 * i + 4 * q4 + r) * PA + 16 * w + c16] = tacc[r];
-            put_t(16 * i + 4 * q4 + r, 16 * w + c16, tacc[r]);
-          }
-        }
-        lds_barrier();
-      }
-    }
 
-    // ---- Delta = T R and Delta' = diag(nk Gamma_C / Gamma) Delta (rows t, this wave's columns)
+    // ---- Delta by blocks of 16 tokens, in this wave's registers (no barrier):
+    // D_i = T_ii (R_i + sum_{k<i} (-A_ik) D_k), both products from M = [T_ii
+    // on the diagonal, -A_ik below it]; the B operand of a 32-token pair
+    // holds the blocks solved so far and zeros.  Delta' = diag(nk Gamma_C /
+    // Gamma) Delta.
     f32x4 dl[4], dp[4];
     {
-      bf16x8 rh[2], rl[2];
-      to_operand(R[0], R[1], rh[0], rl[0]);
-      to_operand(R[2], R[3], rh[1], rl[1]);
+      const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+      bf16x8 bh[2], bl[2];  // [D_0; D_1] (pair 0) and [D_2; 0] (pair 1) as B operands
+      auto mprod = [&](int i, int pair, bf16x8 xh, bf16x8 xl, f32x4 acc) {
+        const int o = ((16 * i + c16) * P72 + 32 * pair + 8 * q4) * 2;
+        const bf16x8 mh = ld8(Tb, o), ml = ld8(Tb, PC * P72 * 2 + o);
+        acc = mfma(mh, xh, acc);
+        acc = mfma(mh, xl, acc);
+        return mfma(ml, xh, acc);
+      };
 #pragma unroll
-      for (int tt = 0; tt < 4; tt++) {
-        const int t = 16 * tt + c16;
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kc = 0; kc < 2; kc++) {
-          const int o = (t * P72 + 32 * kc + 8 * q4) * 2;
-          const bf16x8 th = ld8(Tb, o), tl = ld8(Tb, PC * P72 * 2 + o);
-          acc = mfma(th, rh[kc], acc);
-          acc = mfma(th, rl[kc], acc);
-          acc = mfma(tl, rh[kc], acc);
-        }
-        dl[tt] = acc;
-        const float4 kd = *(const float4 *)(sm + SM_KD * 64 + 16 * tt + 4 * q4);
-        dp[tt][0] = acc[0] * kd.x;
-        dp[tt][1] = acc[1] * kd.y;
-        dp[tt][2] = acc[2] * kd.z;
-        dp[tt][3] = acc[3] * kd.w;
-        __builtin_amdgcn_sched_barrier(0);
+      for (int i = 0; i < 4; i++) {
+        f32x4 acc = R[i];
+        if (i >= 1) acc = mprod(i, 0, bh[0], bl[0], acc);
+        if (i == 3) acc = mprod(i, 1, bh[1], bl[1], acc);
+        bf16x8 xh, xl;
+        if (i & 1) to_operand(zero, acc, xh, xl);
+        else to_operand(acc, zero, xh, xl);
+        const f32x4 d = mprod(i, i >> 1, xh, xl, zero);
+        dl[i] = d;
+        const float4 kd = *(const float4 *)(sm + SM_KD * 64 + 16 * i + 4 * q4);
+        dp[i][0] = d[0] * kd.x;
+        dp[i][1] = d[1] * kd.y;
+        dp[i][2] = d[2] * kd.z;
+        dp[i][3] = d[3] * kd.w;
+        if (i == 0) to_operand(d, zero, bh[0], bl[0]);
+        if (i == 1) to_operand(dl[0], d, bh[0], bl[0]);
+        if (i == 2) to_operand(d, zero, bh[1], bl[1]);
       }
     }
     // ---- O^T = diag(nq Gamma) (S0^T Q^T) + Delta^T P^T: rows j of this wave, column t
