@@ -290,6 +290,7 @@ struct PoolDev {
   const int32_t *bits, *offsets, *rows, *columns, *head_meta;
   const float *impact;
   int H, K, V, G, kda;
+  int ng, ngsh;  // K=V=128 kernels: row-scale groups of a 2-bit row (128 / G) and its log2
   int stage;   // bytes of LDS staging per workgroup (largest head window)
   int rstage;  // bytes of LDS for one head's row scales (fast path)
   int fast;    // SQ_POOL_FAST_* bits: which K=V=128 kernel the pool qualifies for
@@ -860,6 +861,7 @@ struct StepDev {
   const void *slots;
   int64_t q_stride, k_stride, v_stride;
   int HK, qkv_dtype, gate_dtype, out_dtype, slots_dtype, normalize;
+  int hk_mul;  // K=V=128 kernels: key head of value head h = (h * hk_mul) >> 20
   float scale;
   float *s_key, *s_decay, *s_delta;
   int64_t *s_slots;
@@ -1464,7 +1466,7 @@ __device__ __forceinline__ void prologue(const PoolDev &P, const StepDev &S, con
     if (C.tid < FK) C.kraw[C.tid] = k;
     if (C.tid == FK) C.misc[1] = d;
   } else {
-    const int hk = C.h / (P.H / S.HK);
+    const int hk = (C.h * S.hk_mul) >> 20;
     const int i = C.tid & (FK - 1);  // every wave reads rows (no divergence); threads >= 128 keep them
     const int64_t qi = (int64_t)C.b * S.q_stride + (int64_t)hk * FK + i;
     const int64_t ki = (int64_t)C.b * S.k_stride + (int64_t)hk * FK + i;
@@ -1650,8 +1652,8 @@ __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx
   constexpr float ZS = W == 2 ? 2.0f : 1.0f;
   constexpr uint32_t XM = W == 8 ? 0x80808080u : W == 6 ? 0x820820u : W == 4 ? 0x8888u : 0xAAu;
   constexpr int SEG = 2 * W;                   // bytes of one row's 16-value segment
-  const int NG = W == 2 ? FV / P.G : 1;
-  const int g = W == 2 ? C.j0 / P.G : 0;
+  const int NG = W == 2 ? P.ng : 1;
+  const int g = W == 2 ? (C.j0 * P.ng) >> 7 : 0;  // j0 / G with G = 128 / NG
   const uint16_t *c16 = (const uint16_t *)C.cst;
   stage_async<W / 2>(C, 16 * NG, true);
   uint32_t vraw[4];
@@ -1781,8 +1783,9 @@ __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx
   {
     const int Geff = W == 2 ? P.G : FV;
     const int wpg = Geff / 32;  // waves per value group
+    const int ngsh = W == 2 ? P.ngsh : 0;
     for (int e = C.tid ^ FK; e < FK * NG; e += FNT) {  // rows on waves 2, 3 first
-      const int i = e / NG, gq = e % NG;
+      const int i = e >> ngsh, gq = e & (NG - 1);
       float sum = C.red[(gq * wpg) * FK + i];
       for (int w = 1; w < wpg; w++) sum += C.red[(gq * wpg + w) * FK + i];
       float m = sum / (float)Geff;
@@ -2000,8 +2003,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GDN128_WAVE
   extern __shared__ __align__(16) uint8_t smem[];
   const int H = P.H;
   Ctx C;
-  C.b = blockIdx.x / H;
-  C.h = blockIdx.x % H;
+  C.b = blockIdx.y;  // grid (heads, requests): no division
+  C.h = blockIdx.x;
   C.tid = threadIdx.x;
   C.rg = C.tid & 7;
   C.cg = C.tid >> 3;
@@ -2042,7 +2045,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GDN128_WAVE
   C.red = C.misc + MISC_FLOATS;
   C.ks = C.red + 4 * FK;
   C.qs = C.ks + FK;
-  const int ngm = P.G >= 32 ? FV / P.G : 1;
+  const int ngm = P.ng;
   C.rc = (float4 *)(C.qs + FK);
   C.iu = (float2 *)(C.rc + FK * ngm);
   switch (W) {
@@ -2526,7 +2529,7 @@ __device__ __forceinline__ void kda_prologue(const PoolDev &P, const StepDev &S,
     if (C.tid < FK) C.kraw[C.tid] = k;
     else C.gv[i] = d;
   } else {
-    const int hk = C.h / (P.H / S.HK);
+    const int hk = (C.h * S.hk_mul) >> 20;
     const int64_t qi = (int64_t)C.b * S.q_stride + (int64_t)hk * FK + i;
     const int64_t ki = (int64_t)C.b * S.k_stride + (int64_t)hk * FK + i;
     // this lane's readout column j0 + (rg >> 1) of v, raw
@@ -2595,8 +2598,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KDA128_WAVE
   extern __shared__ __align__(16) uint8_t smem[];
   const int H = P.H;
   KCtx C;
-  C.b = blockIdx.x / H;
-  C.h = blockIdx.x % H;
+  C.b = blockIdx.y;  // grid (heads, requests): no division
+  C.h = blockIdx.x;
   C.tid = threadIdx.x;
   C.rg = C.tid & 7;
   C.cg = C.tid >> 3;
@@ -3620,6 +3623,8 @@ PoolDev to_dev(const sq_pool *p) {
   d.K = p->keys;
   d.V = p->values;
   d.G = p->group > 0 ? p->group : p->values;
+  d.ng = d.G >= 32 ? 128 / d.G : 1;
+  d.ngsh = 31 - __builtin_clz((unsigned)d.ng);
   d.kda = p->kda;
   d.stage = (p->max_code_bytes + 47) & ~15;
   d.rstage = (p->max_row_bytes + 15) & ~15;
@@ -3634,6 +3639,12 @@ template <int MODE>
 int launch_step_mode(const sq_pool *pool, StepDev sd, int64_t batch, hipStream_t st) {
   PoolDev pd = to_dev(pool);
   if constexpr (MODE != MODE_DECODE) {  // the K=V=128 kernels read and step pages only
+    if (pd.fast & (SQ_POOL_FAST_GDN128 | SQ_POOL_FAST_KDA128)) {
+      // key head of value head h as (h * hk_mul) >> 20: exact for h * (H / HK) < 2^20
+      if (pool->heads > 1024 || batch > 65535) return fail(SQ_EINVAL, "step: more than 1024 heads or 65535 requests");
+      const int ratio = sd.HK > 0 ? pool->heads / sd.HK : 1;
+      sd.hk_mul = ((1 << 20) + ratio - 1) / ratio;
+    }
     if (pd.fast & SQ_POOL_FAST_GDN128) {
       const int ng_max = pool->group >= 32 ? 128 / pool->group : 1;
       // staging | rows | columns | q,k raw + w | misc | red | ks, qs | rc (float4), iu (float2) per (row, group)
@@ -3641,10 +3652,10 @@ int launch_step_mode(const sq_pool *pool, StepDev sd, int64_t batch, hipStream_t
                    (size_t)6 * 128 * ng_max * 4;
       // q, k, v element width as a compile-time choice (the writer reads fp32 only)
       if (MODE == MODE_WRITE || sd.qkv_dtype == SQ_F32)
-        hipLaunchKernelGGL((gdn128_kernel<MODE, true>), dim3((unsigned)(batch * pool->heads)), dim3(256), lds, st, pd,
+        hipLaunchKernelGGL((gdn128_kernel<MODE, true>), dim3((unsigned)pool->heads, (unsigned)batch), dim3(256), lds, st, pd,
                            sd);
       else
-        hipLaunchKernelGGL((gdn128_kernel<MODE, MODE == MODE_WRITE>), dim3((unsigned)(batch * pool->heads)), dim3(256),
+        hipLaunchKernelGGL((gdn128_kernel<MODE, MODE == MODE_WRITE>), dim3((unsigned)pool->heads, (unsigned)batch), dim3(256),
                            lds, st, pd, sd);
       return check_launch("gdn128_kernel");
     }
@@ -3657,10 +3668,10 @@ int launch_step_mode(const sq_pool *pool, StepDev sd, int64_t batch, hipStream_t
       size_t lds = (size_t)pd.stage + pd.rstage + fast::KDA_COL_STAGE + 4 * 128 * 4 + fast::MISC_FLOATS * 4 +
                    4 * 128 * 4 + 2 * 128 * 4 + 3 * 128 * 16 + 16 + 4 * 256;
       if (MODE == MODE_WRITE || sd.qkv_dtype == SQ_F32)
-        hipLaunchKernelGGL((kda128_kernel<MODE, true>), dim3((unsigned)(batch * pool->heads)), dim3(256), lds, st, pd,
+        hipLaunchKernelGGL((kda128_kernel<MODE, true>), dim3((unsigned)pool->heads, (unsigned)batch), dim3(256), lds, st, pd,
                            sd);
       else
-        hipLaunchKernelGGL((kda128_kernel<MODE, MODE == MODE_WRITE>), dim3((unsigned)(batch * pool->heads)), dim3(256),
+        hipLaunchKernelGGL((kda128_kernel<MODE, MODE == MODE_WRITE>), dim3((unsigned)pool->heads, (unsigned)batch), dim3(256),
                            lds, st, pd, sd);
       return check_launch("kda128_kernel");
     }
