@@ -328,12 +328,13 @@ __device__ __forceinline__ int colbase_of(const PoolDev &P, int h) { return P.co
 // twice rather than once per row and pass.  The operations and their order
 // are those of the general path below (the sums in PyTorch's order).
 // =====================================================================
+template <int W>
 __device__ __forceinline__ void encode_fast128(const PoolDev &P, const float *__restrict__ X, uint8_t *page,
-                                               uint8_t *smem, int h, int W) {
+                                               uint8_t *smem, int h) {
 #pragma clang fp contract(off)
   constexpr int K = 128, V = 128;
   const int tid = threadIdx.x;
-  const bool two = W == 2;
+  constexpr bool two = W == 2;
   const int NG = two ? V / 32 : 1;
   const int ngrp = two ? 32 : V;
   const int32_t *hm = P.head_meta + 4 * h;
@@ -489,9 +490,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void e
   uint8_t *page = P.data + slot * P.page_bytes;
   const float *X = state + ((int64_t)b * H + h) * 128 * 128;
   const int W = P.bits[(int64_t)h * 128];
-  if (W != 16) {
-    encode_fast128(P, X, page, smem, h, W);
-    return;
+  switch (W) {  // the width as a compile-time constant: code packing without loops or branches
+    case 2: encode_fast128<2>(P, X, page, smem, h); return;
+    case 4: encode_fast128<4>(P, X, page, smem, h); return;
+    case 6: encode_fast128<6>(P, X, page, smem, h); return;
+    case 8: encode_fast128<8>(P, X, page, smem, h); return;
+    default: break;
   }
   // pivot head: value (i, j) as a half at its tiled position
   const int code_start = P.head_meta[4 * h];
