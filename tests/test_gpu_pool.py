@@ -54,6 +54,32 @@ def test_encode_bit_exact_against_golden(golden, name):
     np.testing.assert_array_equal(dec, O.decode_page(ref, slots.cpu().numpy(), oplan, lay, V))
 
 
+@pytest.mark.parametrize("scale", [1e-35, 1e-20, 1.0, 1e20])
+def test_encode_bit_exact_extreme_magnitudes(scale):
+    """Encode stays bit-exact where the quotients by the fp16 scales leave the
+    range of the reciprocal path (|x| or |x / r| below 2^-100, exact zeros in
+    a column): those columns divide with IEEE division, the others use the
+    reciprocal with one correction."""
+    print(f"case encode scale={scale}", flush=True)
+    rng = np.random.default_rng(17)
+    H, K, V, batch = 8, 128, 128, 3
+    bits = np.repeat(np.array([2, 4, 6, 8, 2, 4, 6, 8])[:, None], K, 1)
+    oplan = make_plan("gdn", bits, seed=5)
+    x = (rng.standard_normal((batch, H, K, V)) * scale).astype(np.float32)
+    x[0, :, :, 3] = 0.0                                   # a zero column
+    x[1, :, ::7, 10] = 0.0                                # zeros inside a column
+    x[2, :, 5, :] = np.float32(scale * 1e-12)             # a row far below the others
+    x[2, :, :, 20] *= np.float32(1e-25)                   # a column far below the others
+    pool = _pool(oplan, batch + 1, V)
+    slots = torch.arange(1, batch + 1, device=dev())
+    pool.encode(torch.from_numpy(x).to(dev()), slots)
+    lay = O.layout(oplan, V)
+    ref = np.zeros((batch + 1, lay.page_bytes), np.uint8)
+    O.encode_page(x, slots.cpu().numpy(), oplan, lay, ref)
+    got = pool.data.cpu().numpy()
+    assert (got != ref).sum() == 0, f"{(got != ref).sum()} bytes differ"
+
+
 @pytest.mark.parametrize("arch,batch", [("gdn", 16), ("kda", 8)])
 def test_encode_bit_exact_full_heads(arch, batch):
     rng = np.random.default_rng(11)
