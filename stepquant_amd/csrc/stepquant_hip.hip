@@ -3642,13 +3642,15 @@ int stage_bytes(const sq_pool *p) { return (p->max_code_bytes + 47) & ~15; }
 template <int MODE>
 int launch_step_mode(const sq_pool *pool, StepDev sd, int64_t batch, hipStream_t st) {
   PoolDev pd = to_dev(pool);
+  // The K=V=128 kernels take a (heads, requests) grid and the key head of value
+  // head h as (h * hk_mul) >> 20 (exact for h * (H / HK) < 2^20): larger shapes
+  // run on the general kernels below.
+  if (pool->heads > 1024 || batch > 65535) pd.fast = 0;
+  if (pd.fast & (SQ_POOL_FAST_GDN128 | SQ_POOL_FAST_KDA128)) {
+    const int ratio = sd.HK > 0 ? pool->heads / sd.HK : 1;
+    sd.hk_mul = ((1 << 20) + ratio - 1) / ratio;
+  }
   if constexpr (MODE != MODE_DECODE) {  // the K=V=128 kernels read and step pages only
-    if (pd.fast & (SQ_POOL_FAST_GDN128 | SQ_POOL_FAST_KDA128)) {
-      // key head of value head h as (h * hk_mul) >> 20: exact for h * (H / HK) < 2^20
-      if (pool->heads > 1024 || batch > 65535) return fail(SQ_EINVAL, "step: more than 1024 heads or 65535 requests");
-      const int ratio = sd.HK > 0 ? pool->heads / sd.HK : 1;
-      sd.hk_mul = ((1 << 20) + ratio - 1) / ratio;
-    }
     if (pd.fast & SQ_POOL_FAST_GDN128) {
       const int ng_max = pool->group >= 32 ? 128 / pool->group : 1;
       // staging | rows | columns | q,k raw + w | misc | red | ks, qs | rc (float4), iu (float2) per (row, group)
