@@ -284,8 +284,10 @@ def main():
             traffic = meas.get("bytes_per_launch")
     roof = dict(bound="hbm", achieved=round(achieved, 1), peak=PEAK_GBS, unit="GB/s",
                 frac=round(achieved / PEAK_GBS, 4), traffic=traffic,
-                kernel="step_kernel (fused read+update+readout+requant+store)" if stream is None
-                else "readout + writeback kernels", algorithmic_bytes_per_launch=alg_bytes)
+                kernel=("readout + writeback kernels" if stream is not None
+                        else "format_kernel (fused step)" if a.state_format != "stepquant"
+                        else f"{a.arch}128_kernel (fused read+update+readout+requant+store)"),
+                algorithmic_bytes_per_launch=alg_bytes)
     cpu = None
     if a.cpu_sample != 0:
         sample = a.cpu_sample if a.cpu_sample > 0 else B
