@@ -138,7 +138,7 @@ def bench_prefill(a, torch):
     beta = torch.randn(tot, H, device=dev, generator=g)
     a_log = torch.zeros(H, device=dev)
     dt_bias = torch.zeros(H, device=dev)
-    cu = torch.arange(0, tot + 1, T, device=dev, dtype=torch.int32)
+    cu = torch.arange(0, tot + 1, T, dtype=torch.int32)  # sequence offsets known on the host
     init = torch.arange(1, B + 1, device=dev)
     pool.encode(torch.randn(B, H, K, V, device=dev, generator=g) * .05, init)
     # prefix slots at evenly spaced chunk boundaries, the last at the sequence end

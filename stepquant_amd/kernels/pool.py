@@ -360,14 +360,20 @@ class PackedStatePool:
         if self.plan.architecture != "gdn" or self.keys != 128 or self.values != 128:
             raise ValueError("chunked prefill handles GDN pools with K = V = 128")
         dev = self.device
-        cu = torch.as_tensor(cu_seqlens, device=dev).to(torch.int32).reshape(-1).contiguous()
+        if isinstance(cu_seqlens, torch.Tensor) and cu_seqlens.device.type != "cpu":
+            cu = cu_seqlens.to(dev, torch.int32).reshape(-1).contiguous()
+            total = int(cu[-1].item()) if cu.numel() > 1 else 0  # waits for the stream
+        else:
+            # offsets known on the host: checked here, copied without a wait
+            cu_host = torch.as_tensor(cu_seqlens).to(torch.int32).reshape(-1)
+            total = int(cu_host[-1]) if cu_host.numel() > 1 else 0
+            cu = cu_host.pin_memory().to(dev, non_blocking=True)
         batch = cu.numel() - 1
         if batch < 0:
             raise ValueError("cu_seqlens needs at least one entry")
         slots_t = _indices(slots, dev)
         if slots_t.numel() != batch:
             raise ValueError("one slot per sequence")
-        total = int(cu[-1].item()) if batch else 0
         q2 = q.reshape(-1, q.shape[-1] * (q.shape[-2] if q.dim() >= 3 else 1)) if q.dim() >= 3 else q
         k2 = k.reshape(-1, k.shape[-1] * (k.shape[-2] if k.dim() >= 3 else 1)) if k.dim() >= 3 else k
         v2 = v.reshape(-1, v.shape[-1] * (v.shape[-2] if v.dim() >= 3 else 1)) if v.dim() >= 3 else v
