@@ -1998,6 +1998,59 @@ __device__ __forceinline__ void pivot_body(const PoolDev &P, const StepDev &S, C
   stage_back_fast<8>(C, 0, false);
 }
 
+// Page -> dense fp32 of one W-bit head (decode): x = (r_i c_j) z_ij with
+// z = code - L (2-bit: 2 code - 3), the operations and order of the general
+// kernel, so both give the same bits.
+template <int W>
+__device__ __forceinline__ void decode_body(const PoolDev &P, const StepDev &S, const Ctx &C) {
+#pragma clang fp contract(off)
+  constexpr float ZS = W == 2 ? 2.0f : 1.0f;
+  constexpr uint32_t XM = W == 8 ? 0x80808080u : W == 6 ? 0x820820u : W == 4 ? 0x8888u : 0xAAu;
+  constexpr int SEG = 2 * W;
+  const int NG = W == 2 ? P.ng : 1;
+  const int g = W == 2 ? (C.j0 * P.ng) >> 7 : 0;
+  stage_async<W / 2>(C, 16 * NG, true);
+  __syncthreads();
+  const uint16_t *c16 = (const uint16_t *)C.cst, *r16 = (const uint16_t *)C.rst;
+  float cj[4];
+#pragma unroll
+  for (int c = 0; c < 4; c++) cj[c] = hw_h2f(c16[C.j0 + c]);
+  const int pos0 = code_pos0<W>(C.tid);
+  const uint32_t *w32 = (const uint32_t *)(C.code + (pos0 & ~3));
+  const uint32_t sh = (uint32_t)(pos0 & 3) * 8u;
+  float *d = S.dense + ((int64_t)C.b * P.H + C.h) * FK * FV + C.j0;
+#pragma unroll
+  for (int r = 0; r < FRPT; r++) {
+    uint32_t word;
+    if (W == 8) word = w32[r * 4 * W];
+    else if (W == 4) word = *(const uint16_t *)(C.code + pos0 + r * 8 * SEG);
+    else if (W == 2) word = C.code[pos0 + r * 8 * SEG];
+    else word = __builtin_amdgcn_alignbit(w32[r * 4 * W + 1], w32[r * 4 * W], sh);
+    word ^= XM;
+    const int i = C.rg + 8 * r;
+    const float rr = hw_h2f(r16[i * NG + g]);
+    float x[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) x[c] = (rr * cj[c]) * fmaf(ZS, (float)sfield<W>(word, c), 1.0f);
+    *(float4 *)(d + (int64_t)i * FV) = make_float4(x[0], x[1], x[2], x[3]);
+  }
+}
+
+// Page -> dense fp32 of an FP16 pivot head (decode).
+__device__ __forceinline__ void decode_pivot(const PoolDev &P, const StepDev &S, const Ctx &C) {
+  constexpr int SEG = 32, BLK = FK * SEG;
+  stage_async<8>(C, 0, false);
+  __syncthreads();
+  float *d = S.dense + ((int64_t)C.b * P.H + C.h) * FK * FV + C.j0;
+#pragma unroll
+  for (int r = 0; r < FRPT; r++) {
+    const int i = C.rg + 8 * r;
+    const uint2 hv = *(const uint2 *)(C.code + C.blk * BLK + i * SEG + C.sub * 8);
+    *(float4 *)(d + (int64_t)i * FV) =
+        make_float4(hw_h2f(hv.x & 0xffffu), hw_h2f(hv.x >> 16), hw_h2f(hv.y & 0xffffu), hw_h2f(hv.y >> 16));
+  }
+}
+
 }  // namespace fast
 
 template <int MODE, bool QW4>
@@ -2031,6 +2084,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GDN128_WAVE
   if (slot <= 0 || slot >= P.num_slots) {
     if (MODE == MODE_FUSED || MODE == MODE_READ)
       for (int j = C.tid; j < FV; j += FNT) store_val(S.out, S.out_dtype, ((int64_t)C.b * H + C.h) * FV + j, 0.0f);
+    if (MODE == MODE_DECODE) {  // masked: a zero state
+      float4 *d = (float4 *)(S.dense + ((int64_t)C.b * H + C.h) * FK * FV);
+      for (int e = C.tid; e < FK * FV / 4; e += FNT) d[e] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
     return;
   }
   C.page = P.data + slot * P.page_bytes;
@@ -2052,12 +2109,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GDN128_WAVE
   const int ngm = P.ng;
   C.rc = (float4 *)(C.qs + FK);
   C.iu = (float2 *)(C.rc + FK * ngm);
-  switch (W) {
-    case 2: int_body<2, MODE, QW4>(P, S, C); break;
-    case 4: int_body<4, MODE, QW4>(P, S, C); break;
-    case 6: int_body<6, MODE, QW4>(P, S, C); break;
-    case 8: int_body<8, MODE, QW4>(P, S, C); break;
-    default: pivot_body<MODE, QW4>(P, S, C); break;
+  if constexpr (MODE == MODE_DECODE) {
+    switch (W) {
+      case 2: decode_body<2>(P, S, C); break;
+      case 4: decode_body<4>(P, S, C); break;
+      case 6: decode_body<6>(P, S, C); break;
+      case 8: decode_body<8>(P, S, C); break;
+      default: decode_pivot(P, S, C); break;
+    }
+  } else {
+    switch (W) {
+      case 2: int_body<2, MODE, QW4>(P, S, C); break;
+      case 4: int_body<4, MODE, QW4>(P, S, C); break;
+      case 6: int_body<6, MODE, QW4>(P, S, C); break;
+      case 8: int_body<8, MODE, QW4>(P, S, C); break;
+      default: pivot_body<MODE, QW4>(P, S, C); break;
+    }
   }
 }
 
@@ -3650,7 +3717,13 @@ int launch_step_mode(const sq_pool *pool, StepDev sd, int64_t batch, hipStream_t
     const int ratio = sd.HK > 0 ? pool->heads / sd.HK : 1;
     sd.hk_mul = ((1 << 20) + ratio - 1) / ratio;
   }
-  if constexpr (MODE != MODE_DECODE) {  // the K=V=128 kernels read and step pages only
+  if (MODE == MODE_DECODE && (pd.fast & SQ_POOL_FAST_GDN128)) {
+    size_t lds = (size_t)pd.stage + pd.rstage + 2 * 128;  // staging | rows | columns
+    hipLaunchKernelGGL((gdn128_kernel<MODE_DECODE, true>), dim3((unsigned)pool->heads, (unsigned)batch), dim3(256),
+                       lds, st, pd, sd);
+    return check_launch("gdn128_kernel (decode)");
+  }
+  if constexpr (MODE != MODE_DECODE) {  // the KDA kernel reads and steps pages only
     if (pd.fast & SQ_POOL_FAST_GDN128) {
       const int ng_max = pool->group >= 32 ? 128 / pool->group : 1;
       // staging | rows | columns | q,k raw + w | misc | red | ks, qs | rc (float4), iu (float2) per (row, group)
