@@ -318,6 +318,17 @@ __device__ __forceinline__ int carrier_pos(int plane_rel, int K, int i, int j) {
 
 __device__ __forceinline__ int colbase_of(const PoolDev &P, int h) { return P.columns[h]; }
 
+// Cross-lane moves without the LDS crossbar (DPP): the value of lane i + N
+// of the same 16-lane row, and a permutation within each group of four lanes.
+template <int N>
+__device__ __forceinline__ float row_shl(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x100 + N, 0xF, 0xF, true));
+}
+template <int PERM>
+__device__ __forceinline__ uint32_t quad_perm(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, PERM, 0xF, 0xF, true);
+}
+
 // =====================================================================
 // Encode, GDN heads of one width (no FP16 pivots), K = V = 128, packed,
 // 512 threads.  Every value of the tile is loaded once per layout, in one
@@ -376,14 +387,23 @@ __device__ __forceinline__ void encode_fast128(const PoolDev &P, const float *__
 #pragma unroll
           for (int u = 0; u < 4; u++) acc += fabsf(v[p][u]);
         }
-        const float a1 = __shfl_down(acc, 1, 32), a2 = __shfl_down(acc, 2, 32), a3 = __shfl_down(acc, 3, 32);
+        // lanes 4q of each half: sl = acc(4q) + acc(4q+1) + acc(4q+2) + acc(4q+3);
+        // lane 0 of each half: total = sl(0) + sl(4) + ... + sl(28), in order
         float sl = acc;
-        sl += a1;
-        sl += a2;
-        sl += a3;
+        sl += row_shl<1>(acc);
+        sl += row_shl<2>(acc);
+        sl += row_shl<3>(acc);
+        const float up = __uint_as_float(__builtin_amdgcn_permlane16_swap(__float_as_uint(sl), __float_as_uint(sl),
+                                                                          false, false)[1]);  // lane + 16
         float total = 0.0f;
-#pragma unroll
-        for (int q = 0; q < 8; q++) total += __shfl(sl, 4 * q, 32);
+        total += sl;
+        total += row_shl<4>(sl);
+        total += row_shl<8>(sl);
+        total += row_shl<12>(sl);
+        total += up;
+        total += row_shl<4>(up);
+        total += row_shl<8>(up);
+        total += row_shl<12>(up);
         if (lane == 0) {
           float m = total / (float)ngrp;
           m = m < 1e-20f ? 1e-20f : m;
@@ -468,7 +488,7 @@ __device__ __forceinline__ void encode_fast128(const PoolDev &P, const float *__
     const int i = i0 + r;
     const float z = zq(sc[r], c);
     const uint32_t code = two ? (uint32_t)(((int)z + 3) / 2) : (uint32_t)((int)z + L);
-    const uint32_t c1 = __shfl_xor(code, 1), c2 = __shfl_xor(code, 2), c3 = __shfl_xor(code, 3);
+    const uint32_t c1 = quad_perm<0xB1>(code), c2 = quad_perm<0x4E>(code), c3 = quad_perm<0x1B>(code);  // lane ^ 1, 2, 3
     if ((tid & 3) == 0) {
       const uint32_t word = code | (c1 << W) | (c2 << (2 * W)) | (c3 << (3 * W));
       lds_put_bytes(stage, shift + group_pos(orel[i], stride, 16, j, W), word, W / 2);
