@@ -189,7 +189,7 @@ def main():
     a = parse()
     if a.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {a.gpus} is not supported (the path shards by heads "
-              "with no exchange; see DESIGN.md)", file=sys.stderr)
+              "with no exchange between GPUs)", file=sys.stderr)
         sys.exit(2)
     import torch
     if a.calibrate_copy:
