@@ -103,6 +103,12 @@ def test_encode_bit_exact_full_heads(arch, batch):
     O.encode_page(x, slots.cpu().numpy(), oplan, lay, ref)
     got = pool.data.cpu().numpy()
     assert (got != ref).sum() == 0, f"{(got != ref).sum()} bytes differ"
+    # decode (the K=V=128 kernel's decode mode for GDN) against the oracle,
+    # with masked slots (0, -1) as zero states
+    dslots = torch.cat([slots, torch.tensor([0, -1], device=dev())])
+    dec = pool.decode(dslots).cpu().numpy()
+    np.testing.assert_array_equal(dec[:batch], O.decode_page(ref, slots.cpu().numpy(), oplan, lay, V))
+    assert not dec[batch:].any()
 
 
 def _inputs(B, H, K, V, kda, seed, dtype=torch.float32):
