@@ -144,8 +144,8 @@ def bench_prefill(a, torch):
     # prefix slots at evenly spaced chunk boundaries, the last at the sequence end
     pos = [((T * (c + 1)) // NC + 63) // 64 * 64 for c in range(NC)]
     pos[-1] = T
-    ck = torch.tensor(pos, device=dev, dtype=torch.int32).repeat(B, 1)
-    ck_slots = torch.arange(B + 1, B + 1 + B * NC, device=dev).reshape(B, NC)
+    ck = torch.tensor(pos, dtype=torch.int32).repeat(B, 1)  # on the host, as the scheduler holds them
+    ck_slots = torch.arange(B + 1, B + 1 + B * NC).reshape(B, NC)
 
     def step():
         return pool.extend(q, k, v, gate, beta, init, cu, checkpoints=ck, checkpoint_slots=ck_slots,

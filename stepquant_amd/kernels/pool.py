@@ -360,6 +360,7 @@ class PackedStatePool:
         if self.plan.architecture != "gdn" or self.keys != 128 or self.values != 128:
             raise ValueError("chunked prefill handles GDN pools with K = V = 128")
         dev = self.device
+        cu_host = None
         if isinstance(cu_seqlens, torch.Tensor) and cu_seqlens.device.type != "cpu":
             cu = cu_seqlens.to(dev, torch.int32).reshape(-1).contiguous()
             total = int(cu[-1].item()) if cu.numel() > 1 else 0  # waits for the stream
@@ -398,20 +399,35 @@ class PackedStatePool:
         db = None if dt_bias is None else dt_bias.to(gate_dtype).contiguous()
         if (al is None) != (db is None):
             raise ValueError("a_log and dt_bias go together")
-        lengths = (cu[1:] - cu[:-1]).to(torch.int32)
-        if checkpoints is None:
-            ck = lengths.reshape(batch, 1)
-            ck_slots = slots_t.reshape(batch, 1)
-        else:
-            ck = torch.as_tensor(checkpoints, device=dev).to(torch.int32).reshape(batch, -1)
+        on_host = cu_host is not None and checkpoints is not None and all(
+            not isinstance(t, torch.Tensor) or t.device.type == "cpu" for t in (checkpoints, checkpoint_slots))
+        if on_host:
+            # checkpoints and their slots known on the host: masked there, copied without a wait
+            ck_h = torch.as_tensor(checkpoints).to(torch.int32).reshape(batch, -1)
             if checkpoint_slots is None:
                 raise ValueError("checkpoints need checkpoint_slots")
-            ck_slots = _indices(checkpoint_slots, dev).reshape(batch, -1)
-            if ck_slots.shape != ck.shape:
+            cs_h = torch.as_tensor(checkpoint_slots).to(torch.int64).reshape(batch, -1)
+            if cs_h.shape != ck_h.shape:
                 raise ValueError("one slot per checkpoint")
-        valid = (ck > 0) & (ck <= lengths[:, None])
-        ck_slots = torch.where(valid, ck_slots, torch.zeros_like(ck_slots)).contiguous()
-        ck = ck.contiguous()
+            lengths_h = (cu_host[1:] - cu_host[:-1]).reshape(batch, 1)
+            cs_h = torch.where((ck_h > 0) & (ck_h <= lengths_h), cs_h, torch.zeros_like(cs_h))
+            ck = ck_h.contiguous().pin_memory().to(dev, non_blocking=True)
+            ck_slots = cs_h.contiguous().pin_memory().to(dev, non_blocking=True)
+        else:
+            lengths = (cu[1:] - cu[:-1]).to(torch.int32)
+            if checkpoints is None:
+                ck = lengths.reshape(batch, 1)
+                ck_slots = slots_t.reshape(batch, 1)
+            else:
+                ck = torch.as_tensor(checkpoints, device=dev).to(torch.int32).reshape(batch, -1)
+                if checkpoint_slots is None:
+                    raise ValueError("checkpoints need checkpoint_slots")
+                ck_slots = _indices(checkpoint_slots, dev).reshape(batch, -1)
+                if ck_slots.shape != ck.shape:
+                    raise ValueError("one slot per checkpoint")
+            valid = (ck > 0) & (ck <= lengths[:, None])
+            ck_slots = torch.where(valid, ck_slots, torch.zeros_like(ck_slots)).contiguous()
+            ck = ck.contiguous()
         nc = ck.shape[1]
         init = slots_t if init_slots is None else _indices(init_slots, dev)
         out = torch.empty((total, self.heads, self.values), device=dev, dtype=q.dtype)
