@@ -126,6 +126,8 @@ STEP_CASES = {
     "gdn6_uniform": ("gdn", lambda H, K: np.full((H, K), 6), 4, 128, 128, 32),
     "gdn_mixed_pivot": ("gdn", lambda H, K: np.repeat(np.array([6, 4, 8, 16])[:, None], K, 1), 4, 128, 128, 32),
     "gdn_two_bit_g32": ("gdn", lambda H, K: np.repeat(np.array([2, 6, 2, 8])[:, None], K, 1), 4, 128, 128, 32),
+    "gdn_two_bit_g64": ("gdn", lambda H, K: np.repeat(np.array([2, 4, 2, 6])[:, None], K, 1), 4, 128, 128, 64),
+    "gdn_two_bit_g128": ("gdn", lambda H, K: np.repeat(np.array([8, 2, 2, 4])[:, None], K, 1), 4, 128, 128, 128),
     "gdn_small_v16": ("gdn", lambda H, K: np.repeat(np.array([2, 4, 6, 8, 16])[:, None], K, 1), 5, 8, 16, 4),
     "kda_mixed": ("kda", lambda H, K: np.where(np.random.default_rng(2).random((H, K)) < .03, 16,
                                                np.random.default_rng(3).choice([2, 4, 6, 8], (H, K))), 3, 128, 128, 32),
