@@ -195,6 +195,9 @@ def test_decode_step_against_oracle(name, asynchronous):
         got = pool.data.cpu().numpy()
         assert not got[0].any(), "sentinel page 0 was written"
         _check_requant(got, slots_np, oplan, lay, V, upd)
+    # the pages decode to the oracle's dequantisation, bit for bit
+    np.testing.assert_array_equal(pool.decode(slots).cpu().numpy(),
+                                  O.decode_page(pool.data.cpu().numpy(), slots_np, oplan, lay, V))
 
 
 @pytest.mark.parametrize("asynchronous", [False, True])
