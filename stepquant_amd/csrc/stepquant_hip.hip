@@ -3367,6 +3367,28 @@ __device__ __forceinline__ void fmt_write_codes(uint8_t *row, int j0, int W, uin
   for (int t = 0; t < W / 2; t++) p[t] = (uint8_t)(w >> (8 * t));
 }
 
+// x / d rounded to nearest for a divisor d that is an fp16 value (at most 11
+// significant bits), from d's correctly rounded reciprocal inv = 1 / d:
+// q0 = x inv, then one correction with the exact residual x - q0 d.  For
+// every pair of significands (x any of the 2^23, d any of the 2^10) the
+// result equals the IEEE quotient (checked exhaustively on the CPU);
+// exponents only scale it, so it is exact while x, the residual and the
+// quotient stay normal: |x| >= 2^-100 and |q0| <= 2^126 (`ok` is cleared
+// otherwise).
+__device__ __forceinline__ float div_fp16_divisor(float x, float d, float inv, bool &ok) {
+  const float q0 = x * inv;
+  const float r = fmaf(-q0, d, x);
+  const float q1 = fmaf(r, inv, q0);
+  ok = ok && fabsf(x) >= 0x1p-100f && fabsf(q0) <= 0x1p+126f;
+  return q1;
+}
+
+// compile-time switch for the two forms of a loop
+template <bool B>
+struct BoolTag {
+  static constexpr bool value = B;
+};
+
 template <int MODE, int KIND>  // KIND: the format (F.kind), fixed per instantiation
 __global__ __launch_bounds__(256) void format_kernel(FmtDev F, StepDev S) {
 #pragma clang fp contract(off)
@@ -3606,33 +3628,65 @@ __global__ __launch_bounds__(256) void format_kernel(FmtDev F, StepDev S) {
         float acc = 0.0f;
 #pragma unroll
         for (int ii = 0; ii < 4; ii++) acc += row[8 * (4 * ii + kq) + l];
-        const float a1 = __shfl_down(acc, 1, 32), a2 = __shfl_down(acc, 2, 32), a3 = __shfl_down(acc, 3, 32);
         float sl = acc;
-        sl += a1;
-        sl += a2;
-        sl += a3;
+        sl += row_shl<1>(acc);
+        sl += row_shl<2>(acc);
+        sl += row_shl<3>(acc);
+        const float up = __uint_as_float(__builtin_amdgcn_permlane16_swap(__float_as_uint(sl), __float_as_uint(sl),
+                                                                          false, false)[1]);  // lane + 16
         float total = 0.0f;
-#pragma unroll
-        for (int q = 0; q < 8; q++) total += __shfl(sl, 4 * q, 32);
+        total += sl;
+        total += row_shl<4>(sl);
+        total += row_shl<8>(sl);
+        total += row_shl<12>(sl);
+        total += up;
+        total += row_shl<4>(up);
+        total += row_shl<8>(up);
+        total += row_shl<12>(up);
         if (lane == 0) put_r(i, total);
       }
     } else {
       for (int i = tid; i < K; i += 256) put_r(i, inner_sum_lanewise(xs + i * XS, V));
     }
     __syncthreads();
-    // y = x / r; c_j = fp16(max_i |y_ij| / L)
+    // y = x / r; c_j = fp16(max_i |y_ij| / L).  The quotients by the fp16
+    // scales come from their reciprocals with one correction where that is
+    // exact for every value of the thread, else from IEEE division.
     float mx[4] = {0.f, 0.f, 0.f, 0.f};
+    float rinv[FMT_RPT];
+    bool fast = true;
+    {
+      float amin = INFINITY, amax = 0.0f, imax = 0.0f;
 #pragma unroll
-    for (int r = 0; r < FMT_RPT; r++) {
-      const int i = rg + 8 * r;
-      if (i >= K) continue;
-      const float rr = rowv[i];
+      for (int r = 0; r < FMT_RPT; r++) {
+        const int i = rg + 8 * r;
+        if (i >= K) continue;
+        rinv[r] = 1.0f / rowv[i];
+        imax = fmaxf(imax, rinv[r]);
 #pragma unroll
-      for (int c = 0; c < 4; c++) {
-        x[r][c] = x[r][c] / rr;
-        mx[c] = fmaxf(mx[c], fabsf(x[r][c]));
+        for (int c = 0; c < 4; c++) {
+          amin = fminf(amin, fabsf(x[r][c]));
+          amax = fmaxf(amax, fabsf(x[r][c]));
+        }
       }
+      fast = amin >= 0x1p-100f && amax * imax <= 0x1p+125f;
     }
+    auto scale_rows = [&](auto ieee) {
+#pragma unroll
+      for (int r = 0; r < FMT_RPT; r++) {
+        const int i = rg + 8 * r;
+        if (i >= K) continue;
+        const float rr = rowv[i];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+          bool ok = true;
+          x[r][c] = decltype(ieee)::value ? x[r][c] / rr : div_fp16_divisor(x[r][c], rr, rinv[r], ok);
+          mx[c] = fmaxf(mx[c], fabsf(x[r][c]));
+        }
+      }
+    };
+    if (fast) scale_rows(BoolTag<false>());
+    else scale_rows(BoolTag<true>());
 #pragma unroll
     for (int c = 0; c < 4; c++) {
       uint32_t hb;
@@ -3643,22 +3697,55 @@ __global__ __launch_bounds__(256) void format_kernel(FmtDev F, StepDev S) {
       }
     }
   }
-#pragma unroll
-  for (int r = 0; r < FMT_RPT; r++) {
-    const int i = rg + 8 * r;
-    if (!act || i >= K) continue;
-    uint32_t word = 0;
+  // codes: the quotients as above (reciprocal where exact for the thread)
+  float rinvq[FMT_RPT], cinvq[4];  // 1 / divisor: per row (SYMMETRIC) or per column (DSQ)
+  bool fastq;
+  {
+    float amin = INFINITY, amax = 0.0f, imax = 0.0f;
 #pragma unroll
     for (int c = 0; c < 4; c++) {
-      const float d = KIND == SQ_FMT_SYMMETRIC ? rowv[i] : div[c];
-      float q = __builtin_rintf(x[r][c] / d);
-      q = q > -Lf ? q : -Lf;
-      q = q < Lf ? q : Lf;
-      word |= (uint32_t)(int)(q + Lf) << (c * W);
+      cinvq[c] = KIND == SQ_FMT_SYMMETRIC ? 0.0f : 1.0f / div[c];
+      imax = fmaxf(imax, cinvq[c]);
     }
-    if (staged) lds_put_bytes(stg, shift + (int)(((int64_t)i * V + j0) * W / 8), word, W / 2);
-    else fmt_write_codes(page + F.offsets[(int64_t)h * K + i], j0, W, word);
+#pragma unroll
+    for (int r = 0; r < FMT_RPT; r++) {
+      const int i = rg + 8 * r;
+      rinvq[r] = 0.0f;
+      if (!act || i >= K) continue;
+      if (KIND == SQ_FMT_SYMMETRIC) {
+        rinvq[r] = 1.0f / rowv[i];
+        imax = fmaxf(imax, rinvq[r]);
+      }
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        amin = fminf(amin, fabsf(x[r][c]));
+        amax = fmaxf(amax, fabsf(x[r][c]));
+      }
+    }
+    fastq = amin >= 0x1p-100f && amax * imax <= 0x1p+125f;
   }
+  auto codes = [&](auto ieee) {
+#pragma unroll
+    for (int r = 0; r < FMT_RPT; r++) {
+      const int i = rg + 8 * r;
+      if (!act || i >= K) continue;
+      uint32_t word = 0;
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        const float d = KIND == SQ_FMT_SYMMETRIC ? rowv[i] : div[c];
+        const float dinv = KIND == SQ_FMT_SYMMETRIC ? rinvq[r] : cinvq[c];
+        bool ok = true;
+        float q = __builtin_rintf(decltype(ieee)::value ? x[r][c] / d : div_fp16_divisor(x[r][c], d, dinv, ok));
+        q = q > -Lf ? q : -Lf;
+        q = q < Lf ? q : Lf;
+        word |= (uint32_t)(int)(q + Lf) << (c * W);
+      }
+      if (staged) lds_put_bytes(stg, shift + (int)(((int64_t)i * V + j0) * W / 8), word, W / 2);
+      else fmt_write_codes(page + F.offsets[(int64_t)h * K + i], j0, W, word);
+    }
+  };
+  if (fastq) codes(BoolTag<false>());
+  else codes(BoolTag<true>());
   if (staged) {
     __syncthreads();
     stage_out(page + code_start, code_bytes, stg, tid, 256);
