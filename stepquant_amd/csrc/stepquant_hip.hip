@@ -3192,9 +3192,9 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
     // holds the blocks solved so far and zeros.  Delta' = diag(nk Gamma_C /
     // Gamma) Delta.
     f32x4 dl[4], dp[4];
+    bf16x8 bh[2], bl[2];  // [D_0; D_1] (pair 0) and [D_2; 0] (pair 1) as B operands
     {
       const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-      bf16x8 bh[2], bl[2];  // [D_0; D_1] (pair 0) and [D_2; 0] (pair 1) as B operands
       auto mprod = [&](int i, int pair, bf16x8 xh, bf16x8 xl, f32x4 acc) {
         const int o = ((16 * i + c16) * P72 + 32 * pair + 8 * q4) * 2;
         const bf16x8 mh = ld8(Tb, o), ml = ld8(Tb, PC * P72 * 2 + o);
@@ -3225,7 +3225,8 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
     // ---- O^T = diag(nq Gamma) (S0^T Q^T) + Delta^T P^T: rows j of this wave, column t
     {
       bf16x8 dh[2], dlo[2];
-      to_operand(dl[0], dl[1], dh[0], dlo[0]);
+      dh[0] = bh[0];  // [D_0; D_1], split by the block solve
+      dlo[0] = bl[0];
       to_operand(dl[2], dl[3], dh[1], dlo[1]);
 #pragma unroll
       for (int tt = 0; tt < 4; tt++) {
