@@ -1808,11 +1808,14 @@ __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx
     const int Geff = W == 2 ? P.G : FV;
     const int wpg = Geff / 32;  // waves per value group
     const int ngsh = W == 2 ? P.ngsh : 0;
+    // 1 / Geff, a power of two (Geff = 128 >> ngsh): the mean's division is
+    // this exact multiplication
+    const float ginv = __builtin_amdgcn_ldexpf(1.0f, ngsh - 7);
     for (int e = C.tid ^ FK; e < FK * NG; e += FNT) {  // rows on waves 2, 3 first
       const int i = e >> ngsh, gq = e & (NG - 1);
       float sum = C.red[(gq * wpg) * FK + i];
       for (int w = 1; w < wpg; w++) sum += C.red[(gq * wpg + w) * FK + i];
-      float m = sum / (float)Geff;
+      float m = sum * ginv;
       m = m < 1e-20f ? 1e-20f : m;
       uint32_t hb;
       const float wi = C.wv[i];
