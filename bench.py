@@ -12,6 +12,13 @@ and the state evolves from step to step.
 
 Prints one JSON line (metric, value = state-head updates/s, roofline of the
 dominant kernel, CPU baseline from the oracle on a bounded sample).
+
+Timing: the GPU clocks ramp up under load and fall back within a fraction
+of a second of idling, so steps are replayed for ``--warm-seconds`` (2 s)
+before the counted warm-up.  Decode steps are captured ``--graph-steps`` per
+graph (the largest divisor of ``--steps`` up to 16): a serving graph runs its
+layers' kernels back to back, without a host launch between them.  Every
+timed step is a whole decode step of all B requests.
 """
 import argparse
 import json
@@ -52,6 +59,15 @@ def parse():
     p.add_argument("--state-format", default="stepquant",
                    help="decode on a baseline-format pool (fp32, sym_int{4,6,8}_g128, dsq_int{4,6}) instead")
     p.add_argument("--checkpoints", type=int, default=5, help="prefill prefix slots per request")
+    p.add_argument("--warm-seconds", type=float, default=2.0,
+                   help="replay steps for this long before the counted warm-up: the GPU clocks ramp up "
+                        "under load and drop again within a fraction of a second of idling")
+    p.add_argument("--graph-steps", type=int, default=0,
+                   help="consecutive decode steps captured per graph (0: the largest divisor of --steps "
+                        "up to 16), as a serving graph runs its layers back to back")
+    p.add_argument("--cpu-threads", type=int, default=0,
+                   help="threads of the CPU baseline (0: the cores this process may use, at most 16)")
+    p.add_argument("--cpu-steps", type=int, default=4, help="full decode steps of the CPU baseline sample")
     a = p.parse_args()
     if a.batch is None:
         a.batch = 8 if a.workload == "prefill" else 256
@@ -79,17 +95,28 @@ def make_plan(torch, arch, H, K, nominal, seed=0):
     return bits, impact
 
 
-def cpu_baseline(bits, impact, arch, B, H, HK, K, V, sample, group=32):
-    """Oracle (C restatement of the reference CPU path) on a bounded sample."""
+def host_cores():
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
+def cpu_baseline(bits, impact, arch, B, H, HK, K, V, sample, steps=4, threads=0, group=32):
+    """Oracle (C restatement of the reference CPU path) on a bounded sample:
+    ``steps`` full decode steps of ``sample`` requests, the requests split
+    over ``threads`` host threads (the oracle's C calls release the GIL and
+    every (request, head) tile is independent)."""
     import numpy as np
+    from concurrent.futures import ThreadPoolExecutor
     from oracle import oracle as O
+    threads = threads or min(16, host_cores())
+    threads = max(1, min(threads, sample))
     rng = np.random.default_rng(1)
     plan = O.Plan(arch, bits.numpy(), impact.numpy(), group)
     lay = O.layout(plan, V)
     pages = np.zeros((sample + 1, lay.page_bytes), np.uint8)
     slots = np.arange(1, sample + 1)
-    x = (rng.standard_normal((sample, H, K, V)) * .05).astype(np.float32)
-    O.encode_page(x, slots, plan, lay, pages)
     q = rng.standard_normal((sample, HK * K)).astype(np.float32)
     k = rng.standard_normal((sample, HK * K)).astype(np.float32)
     v = rng.standard_normal((sample, H, V)).astype(np.float32)
@@ -97,18 +124,55 @@ def cpu_baseline(bits, impact, arch, B, H, HK, K, V, sample, group=32):
     b = rng.standard_normal((sample, H)).astype(np.float32)
     zeros_h = np.zeros(H, np.float32)
     bias = np.zeros(H * K if arch == "kda" else H, np.float32)
-    t0 = time.perf_counter()
-    state = O.decode_page(pages, slots, plan, lay, V)
-    qp, kp, ld, bt = O.prepare(q, k, a, b, H, K, arch == "kda", True, K ** -.5, zeros_h, bias)
-    out, upd = O.delta_step(state, qp, kp, v, ld, bt)
-    O.encode_page(upd, slots, plan, lay, pages)
-    dt = time.perf_counter() - t0
-    return dict(value=sample * H / dt, unit="updates/s", cores=1, kind="port",
-                sample=f"{sample} requests x {H} heads of the same workload, one step "
-                       f"(decode page, prepare, delta_step, fit_state + page store), 1 thread, {dt:.1f} s")
+    parts = [p for p in np.array_split(np.arange(sample), threads) if p.size]
+
+    def init(idx):
+        x = (np.random.default_rng(2 + int(idx[0])).standard_normal((idx.size, H, K, V)) * .05).astype(np.float32)
+        O.encode_page(x, slots[idx], plan, lay, pages)
+
+    def one(idx):
+        s = slots[idx]
+        state = O.decode_page(pages, s, plan, lay, V)
+        qp, kp, ld, bt = O.prepare(q[idx], k[idx], a[idx], b[idx], H, K, arch == "kda", True, K ** -.5,
+                                   zeros_h, bias)
+        _, upd = O.delta_step(state, qp, kp, v[idx], ld, bt)
+        O.encode_page(upd, s, plan, lay, pages)  # each thread writes only its own requests' pages
+
+    with ThreadPoolExecutor(len(parts)) as ex:
+        list(ex.map(init, parts))
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            list(ex.map(one, parts))
+        dt = time.perf_counter() - t0
+    return dict(value=steps * sample * H / dt, unit="updates/s", cores=len(parts), kind="port",
+                sample=f"{steps} decode steps of {sample} requests x {H} heads of the same workload (decode page, "
+                       f"prepare, delta_step, fit_state + page store), requests split over {len(parts)} threads, "
+                       f"{dt:.2f} s wall")
 
 
 PEAK_BF16_TFLOPS = 2500.0
+
+
+def timed_steps(torch, one, block, per_block, steps, warmup, warm_seconds):
+    """Warm by wall time, then ``warmup`` single steps, then exactly ``steps``
+    steps as ``steps / per_block`` launches of ``block``, timed with HIP
+    events on the launching stream between two synchronisations.
+    Returns (ms per step, wall seconds of the timed region)."""
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < warm_seconds:
+        block()
+    for _ in range(warmup):
+        one()
+    torch.cuda.synchronize()
+    cur = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(cur)
+    for _ in range(steps // per_block):
+        block()
+    end.record(cur)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps, time.perf_counter() - t0
 
 
 def prefill_flops(n_chunks, C=64, K=128, V=128):
@@ -151,19 +215,9 @@ def bench_prefill(a, torch):
         return pool.extend(q, k, v, gate, beta, init, cu, checkpoints=ck, checkpoint_slots=ck_slots,
                            init_slots=init, normalize=True, scale=K ** -.5, a_log=a_log, dt_bias=dt_bias)
 
-    for _ in range(max(a.warmup, 1)):
-        step()
+    step()
     torch.cuda.synchronize()
-    cur = torch.cuda.current_stream()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    start.record(cur)
-    for _ in range(a.steps):
-        step()
-    end.record(cur)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms_step = start.elapsed_time(end) / a.steps
+    ms_step, wall = timed_steps(torch, step, step, 1, a.steps, a.warmup, a.warm_seconds)
     n_chunks = B * H * ((T + 63) // 64)
     flops = prefill_flops(n_chunks)
     tflops = flops / (ms_step * 1e-3) / 1e12
@@ -175,7 +229,7 @@ def bench_prefill(a, torch):
                 vs_baseline=None, dtype="bf16", data="synthetic",
                 config=dict(workload=f"GDN prefill STEPQuant@6, B={B}, T={T}, H={H}, HK={HK}, dk=dv={K}, "
                                      f"chunk 64, bf16 q/k/v, raw gates, {NC} prefix slots per request",
-                            global_batch=B, seq_len=T, wall_s=round(wall, 3)),
+                            global_batch=B, seq_len=T, wall_s=round(wall, 3), warm_seconds=a.warm_seconds),
                 roofline=dict(bound="mfma", achieved=round(tflops, 2), peak=PEAK_BF16_TFLOPS, unit="TFLOP/s",
                               frac=round(tflops / PEAK_BF16_TFLOPS, 4), traffic=None,
                               algorithmic_flops_per_step=flops,
@@ -249,26 +303,19 @@ def main():
         step()
     torch.cuda.synchronize()
     if a.no_graph:
-        replay = step
+        one, block, per_block = step, step, 1
     else:
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
+        per_block = a.graph_steps or max(d for d in range(1, 17) if a.steps % d == 0)
+        if a.steps % per_block:
+            raise SystemExit(f"--graph-steps {per_block} must divide --steps {a.steps}")
+        single, multi = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+        with torch.cuda.graph(single):
             step()
-        replay = graph.replay
-    for _ in range(a.warmup):
-        replay()
-    torch.cuda.synchronize()
-    cur = torch.cuda.current_stream()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    start.record(cur)
-    for _ in range(a.steps):
-        replay()
-    end.record(cur)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms_total = start.elapsed_time(end)
-    ms_step = ms_total / a.steps
+        with torch.cuda.graph(multi, pool=single.pool()):
+            for _ in range(per_block):
+                step()
+        one, block = single.replay, multi.replay
+    ms_step, wall = timed_steps(torch, one, block, per_block, a.steps, a.warmup, a.warm_seconds)
     page = pool.page_bytes
     alg_bytes = 2 * B * page
     achieved = alg_bytes / (ms_step * 1e-3) / 1e9
@@ -291,16 +338,18 @@ def main():
     cpu = None
     if a.cpu_sample != 0:
         sample = a.cpu_sample if a.cpu_sample > 0 else B
-        cpu = cpu_baseline(bits, impact, a.arch, B, H, HK, K, V, sample)
+        cpu = cpu_baseline(bits, impact, a.arch, B, H, HK, K, V, sample, a.cpu_steps, a.cpu_threads)
     line = dict(metric=METRIC, value=round(updates, 1), unit="state-head updates/s", n_gpus=1, steps=a.steps,
                 warmup=a.warmup, ms_per_step=round(ms_step, 6), higher_is_better=True, scaling="weak",
                 vs_baseline=None, dtype="f32", data="synthetic",
                 config=dict(workload=(f"{a.arch.upper()} decode STEPQuant@{a.nominal}" if a.state_format == "stepquant"
                                       else f"{a.arch.upper()} decode {a.state_format} pages")
                                      + f", one layer, B={B}, H={H}, "
-                                     f"HK={HK}, dk=dv={K}, bf16 q/k/v, raw gates, graph-replayed steps"
+                                     f"HK={HK}, dk=dv={K}, bf16 q/k/v, raw gates, "
+                                     + (f"{per_block} steps per graph launch" if not a.no_graph else "eager steps")
                                      + (", async writeback" if stream is not None else ", fused writeback"),
-                            page_bytes=page, global_batch=B, wall_s=round(wall, 3)),
+                            page_bytes=page, global_batch=B, wall_s=round(wall, 3),
+                            warm_seconds=a.warm_seconds),
                 roofline=roof, cpu_baseline=cpu)
     print(json.dumps(line), flush=True)
 

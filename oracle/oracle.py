@@ -10,6 +10,8 @@ the reference repository):
 
 * ``layout``          stepquant/kernels/pool.py:19-66 (``packed_layout``)
 * ``fit_state``       stepquant/quantization.py:54-98
+* ``initial_column_scales``/``column_refit``  the column half of fit_state
+                      (quantization.py:80-98) for given row scales
 * ``encode_page``     fit_state + page stores (kernels/fused.py:62-127, 251-282;
                       kernels/bitpack.py:6-30)
 * ``decode_page``     kernels/fused.py:18-59 (``_read``), kernels/byte_codec.py:6-28
@@ -163,6 +165,63 @@ def fit_state(x, plan: Plan):
         raise ValueError(f"oracle fit_state failed ({rc})")
     r2o = r2[:, two].view(np.float16) if two.any() else None
     return z, r.view(np.float16), c.view(np.float16), r2o, recon
+
+
+def _row_constants(plan: Plan):
+    """Per key row: qmax and norm of fit_state (quantization.py:63-72)."""
+    bc = np.minimum(plan.bits, 8)
+    qmax = (2.0 ** (bc - 1) - 1).astype(np.float32)
+    norm = (2.0 ** (8 - bc) if plan.kda else np.ones_like(bc)).astype(np.float32)
+    qmax[_two_heads(plan)] = 3.0
+    return qmax, norm
+
+
+def _fp16_scale(x):
+    """quantization.py:49-51: clamp(2^-24, 65504).half().float()."""
+    return np.clip(np.asarray(x, np.float32), np.float32(2.0 ** -24), np.float32(65504)) \
+        .astype(np.float16).astype(np.float32)
+
+
+def initial_column_scales(x, r_full, plan: Plan):
+    """fit_state's c0 (quantization.py:80-82) for given row scales:
+    fp16(amax over integer key rows of |x / r| / (qmax * norm)).
+
+    x, r_full: [B, H, K, V] float32, r_full holding each value's row scale
+    (the value-group scale on 2-bit GDN heads).  Returns [B, H, V]."""
+    x = np.asarray(x, np.float32)
+    qmax, norm = _row_constants(plan)
+    t = np.abs(x / np.asarray(r_full, np.float32)) / (qmax * norm)[None, :, :, None]
+    t = np.where((plan.bits != 16)[None, :, :, None], t, np.float32(0))
+    return _fp16_scale(t.max(axis=2))
+
+
+def column_refit(x, r_full, c0, plan: Plan):
+    """The column half of fit_state (quantization.py:83-98) from given row
+    scales and initial column scales: z = encode(c0) (rounded and clamped
+    to [-qmax, qmax], or the 2-bit GDN levels +-1/+-3), then
+    c = fp16(sum_K w^2 v x / sum_K w^2 v^2) with v = r * norm * z, or c0
+    where the denominator is zero.
+
+    x, r_full: [B, H, K, V] float32; c0: [B, H, V] float32.  The key sums
+    run in float64 and are rounded once to float32, so a result can sit one
+    fp16 ulp from fit_state's, which sums in PyTorch's float32 order."""
+    x = np.asarray(x, np.float32)
+    r_full = np.asarray(r_full, np.float32)
+    c0 = np.asarray(c0, np.float32)
+    qmax, norm = _row_constants(plan)
+    qm = qmax[None, :, :, None]
+    nm = norm[None, :, :, None]
+    y = ((x / r_full) / c0[:, :, None, :]) / nm
+    two = _two_heads(plan)[None, :, None, None]
+    z = np.where(two, np.where(y >= 0, np.float32(1), np.float32(-1)) *
+                 np.where(np.abs(y) >= 2, np.float32(3), np.float32(1)),
+                 np.clip(np.rint(y), -qm, qm)).astype(np.float32)
+    wsq = (plan.impact * plan.impact * (plan.bits != 16))[None, :, :, None].astype(np.float32)
+    v = (r_full * nm) * z
+    num = ((wsq * v) * x).astype(np.float64).sum(axis=2).astype(np.float32)
+    den = (wsq * (v * v)).astype(np.float64).sum(axis=2).astype(np.float32)
+    c = np.where(den > 0, num / np.maximum(den, np.float32(1e-30)), c0)
+    return _fp16_scale(c)
 
 
 def encode_page(x, slots, plan: Plan, lay: Layout, data, storage: str = "packed"):

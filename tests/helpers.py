@@ -61,3 +61,116 @@ def scales(pages, slots, oplan, lay, V):
         rs.append(r)
         cs.append(np.stack(c))
     return rs, np.stack(cs)
+
+
+def _ordered_f16(bits):
+    """fp16 bit patterns as integers whose difference counts ulps across signs."""
+    bits = bits.astype(np.int64)
+    mag = bits & 0x7FFF
+    return np.where(bits & 0x8000, -mag, mag)
+
+
+def scale_bytes_index(oplan, lay, V):
+    """Byte offsets (within a page) of every stored scale: row scales (a
+    GDN 2-bit head stores V/group per row) then column scales, each an fp16."""
+    H, K = oplan.bits.shape
+    idx = []
+    for h in range(H):
+        two = (not oplan.kda) and oplan.bits[h, 0] == 2
+        n = V // oplan.value_group_size if two else 1
+        for i in range(K):
+            o = int(lay.rows[h * K + i])
+            if o >= 0:
+                idx.append(o + 2 * np.arange(n))
+    rows = np.concatenate(idx) if idx else np.zeros(0, np.int64)
+    cols = [int(o) + 2 * np.arange(V) for o in lay.columns if o >= 0]
+    cols = np.concatenate(cols) if cols else np.zeros(0, np.int64)
+    return rows, cols
+
+
+def scale_ulps(got_pages, ref_pages, slots, oplan, lay, V):
+    """fp16 ulp distance of the row and column scales of the live slots."""
+    live = np.asarray([s for s in slots if s > 0], np.int64)
+    out = []
+    for idx in scale_bytes_index(oplan, lay, V):
+        def read(p):
+            lo = p[live][:, idx].astype(np.uint16)
+            hi = p[live][:, idx + 1].astype(np.uint16)
+            return _ordered_f16(lo | (hi << 8))
+        out.append(np.abs(read(got_pages) - read(ref_pages)))
+    return out[0], out[1]
+
+
+def row_scales_full(pages, slots, oplan, lay, V):
+    """[B, H, K, V] float32: every value's row scale read from the pages
+    (the value-group scale on 2-bit GDN heads; 1 for pivot rows)."""
+    H, K = oplan.bits.shape
+    out = np.ones((len(slots), H, K, V), np.float32)
+    for b, s in enumerate(slots):
+        if s <= 0:
+            continue
+        for h in range(H):
+            two = (not oplan.kda) and oplan.bits[h, 0] == 2
+            n = V // oplan.value_group_size if two else 1
+            for i in range(K):
+                o = int(lay.rows[h * K + i])
+                if o >= 0:
+                    r = pages[s, o:o + 2 * n].view(np.float16).astype(np.float32)
+                    out[b, h, i] = np.repeat(r, V // n)
+    return out
+
+
+def _shift_f16(x, k):
+    return (x.astype(np.float16).view(np.int16) + k).view(np.float16).astype(np.float32)
+
+
+def explained_by_initial_scale(got_pages, slots, oplan, lay, V, updated, b, h, j):
+    """True when column j of head h (request index b) holds the least-squares
+    refit that fit_state gives for the oracle's state with the page's row
+    scales and an initial scale c0 one fp16 ulp either side (or at) the
+    oracle's c0, within one fp16 ulp."""
+    live = np.asarray(slots)[b:b + 1]
+    full = row_scales_full(got_pages, live, oplan, lay, V)[:, h:h + 1]
+    x = np.asarray(updated, np.float32)[b:b + 1, h:h + 1]
+    sub = type(oplan)(oplan.architecture, oplan.bits[h:h + 1], oplan.impact[h:h + 1], oplan.value_group_size)
+    c0 = O.initial_column_scales(x, full, sub)
+    o = int(lay.columns[h]) + 2 * j
+    got = got_pages[live[0], o:o + 2].view(np.int16).astype(np.int64)[0]
+    for k in (-1, 0, 1):
+        c = O.column_refit(x, full, _shift_f16(c0, k), sub)[0, 0, j]
+        if abs(int(np.float16(c).view(np.int16)) - got) <= 1:
+            return True
+    return False
+
+
+def check_scales(got_pages, ref_pages, slots, oplan, lay, V, budget, updated=None, c0_budget=0.01):
+    """Row and column scales equal the oracle's up to one fp16 ulp, and at
+    most a ``budget`` fraction of them differ at all.
+
+    With ``updated`` (the oracle's dense state that was requantised), a
+    column scale further off is accepted on at most a ``c0_budget`` fraction
+    of columns (rounded up), and only where it is the refit of an initial scale c0 one
+    fp16 ulp from the oracle's: c0 = fp16(max|x/r|/L) rounds the other way
+    when the step's state differs from the oracle's at the float32 ulp
+    level, and the least-squares refit of a low-width column follows the
+    codes of that c0 by several ulps.  Returns the fractions off by one ulp."""
+    rows, cols = scale_ulps(got_pages, ref_pages, slots, oplan, lay, V)
+    fr = float((rows > 0).mean()) if rows.size else 0.0
+    fc = float((cols > 0).mean()) if cols.size else 0.0
+    far = np.argwhere(cols > 1)
+    print(f"scales: rows {rows.size} max {rows.max(initial=0)} ulp, {fr:.2e} differ; "
+          f"columns {cols.size} max {cols.max(initial=0)} ulp, {fc:.2e} differ, {len(far)} beyond one ulp",
+          flush=True)
+    assert rows.max(initial=0) <= 1, f"a row scale differs by {rows.max()} fp16 ulps"
+    assert fr <= budget, f"{fr:.2e} of row scales differ"
+    assert fc <= budget, f"{fc:.2e} of column scales differ"
+    if len(far):
+        assert updated is not None, f"a column scale differs by {cols.max()} fp16 ulps"
+        live = [bi for bi, s in enumerate(slots) if s > 0]
+        heads = [h for h in range(oplan.bits.shape[0]) if lay.columns[h] >= 0]
+        for bl, idx in far:
+            b, h, j = live[bl], heads[idx // V], idx % V
+            assert explained_by_initial_scale(got_pages, slots, oplan, lay, V, updated, b, h, j), \
+                f"request {b} head {h} column {j}: scale {cols[bl, idx]} fp16 ulps off, not a c0 rounding"
+        assert len(far) <= np.ceil(c0_budget * cols.size), f"{len(far)} column scales differ by more than one fp16 ulp"
+    return fr, fc

@@ -4,14 +4,16 @@ kernels/byte_codec.py, kernels/fit.py BYTE path) on an MI355X.
 Bars as for packed pages: encode and decode bit-identical to the oracle; a
 decode step (byte pages use the writeback stream, as in the reference) within
 rtol 1e-3 / atol 1e-4 on the readout and at most one level per carrier on at
-most 0.1% of the requantised values.
+most 0.1% of the requantised values; row and column scales within one fp16
+ulp of the oracle's.
 """
 import numpy as np
 import pytest
 import torch
 
 from oracle import oracle as O
-from tests.helpers import dev, device_plan, make_plan
+from tests.helpers import check_scales, dev, device_plan, make_plan
+from tests.test_gpu_pool import SCALE_BUDGET
 
 pytestmark = pytest.mark.gpu
 
@@ -114,6 +116,7 @@ def test_byte_decode_step_against_oracle(name):
         diff = np.abs(a - b)
         assert (diff <= step).all(), "carrier differs by more than one level"
         assert (diff > 0).mean() <= 1e-3, f"{(diff > 0).mean():.2e} of carriers differ"
+        check_scales(got, ref, slots_np, oplan, lay, V, SCALE_BUDGET, upd)
         ga = O.decode_page(got, slots_np, oplan, lay, V, "byte")[live]
         gb = O.decode_page(ref, slots_np, oplan, lay, V, "byte")[live]
         assert (~np.isclose(ga, gb, rtol=1e-3, atol=1e-4)).mean() <= 1e-3

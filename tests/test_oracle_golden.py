@@ -102,3 +102,57 @@ def test_page_round_trip_equals_reconstruction(golden, name, storage):
     assert _sha(out + np.float32(0)) == _sha(recon + np.float32(0))
     masked = O.decode_page(pages, np.zeros(2, np.int64), plan, lay, V, storage)
     assert not masked.any()
+
+
+def _row_scales_full(plan, r, r2, V):
+    """[B, H, K, V] float32 row scale of every value (group scales on 2-bit GDN heads)."""
+    r = r.view(np.float16).astype(np.float32)
+    full = np.repeat(r[..., None], V, axis=-1)
+    two = (plan.bits[:, 0] == 2) & (not plan.kda)
+    if two.any():
+        g = plan.value_group_size
+        full[:, two] = np.repeat(r2.view(np.float16).astype(np.float32), g, axis=-1)
+    return full
+
+
+@pytest.mark.parametrize("name", [
+    "c_config_gdn", "c_config_gdn_uniform6", "gdn_two_bit_g32", "gdn_mixed_v16_g4", "kda_mixed_v16",
+    "kda_mixed_128", "kda_edges_v4", "kda_edges_v32", "gdn_v8_k4", "gdn_v32_k32", "zero_state",
+    "scale_extremes", "kda_pivot_a", "kda_pivot_b"])
+def test_column_refit_against_golden(golden, name):
+    """initial_column_scales + column_refit from the reference's own row
+    scales give the reference's column scales (fit_state's c) within one
+    fp16 ulp; all but a few exactly (the key sums run in another order)."""
+    data, meta = golden
+    plan = _plan(data, meta, name)
+    x = data[f"{name}/x"]
+    V = x.shape[-1]
+    r2 = data[f"{name}/r2"] if f"{name}/r2" in data else None
+    full = _row_scales_full(plan, data[f"{name}/r"], r2, V)
+    c0 = O.initial_column_scales(x, full, plan)
+    c = O.column_refit(x, full, c0, plan)
+    ref = data[f"{name}/c"].view(np.float16).astype(np.float32)
+    integer_heads = (plan.bits != 16).any(1)
+    got_bits = c.astype(np.float16).view(np.int16).astype(np.int64)[:, integer_heads]
+    ref_bits = ref.astype(np.float16).view(np.int16).astype(np.int64)[:, integer_heads]
+    ulps = np.abs(got_bits - ref_bits)
+    assert ulps.max(initial=0) <= 1
+    assert (ulps > 0).mean() <= 0.01 if ulps.size else True
+
+
+def test_column_refit_moves_with_initial_scale(golden):
+    """A one-ulp change of c0 moves the least-squares refit of low-width
+    columns by several fp16 ulps: the encode(c0) codes change by one level
+    on values near a rounding boundary and the refit follows them.  A GPU
+    step whose c0 rounds the other way (its state differs from the oracle's
+    at the float32 ulp level) therefore yields such a column scale."""
+    data, meta = golden
+    name = "c_config_gdn"
+    plan = _plan(data, meta, name)
+    x = data[f"{name}/x"]
+    full = _row_scales_full(plan, data[f"{name}/r"], None, x.shape[-1])
+    c0 = O.initial_column_scales(x, full, plan)
+    up = (c0.astype(np.float16).view(np.int16) + 1).view(np.float16).astype(np.float32)
+    a = O.column_refit(x, full, c0, plan).astype(np.float16).view(np.int16).astype(np.int64)
+    b = O.column_refit(x, full, up, plan).astype(np.float16).view(np.int16).astype(np.int64)
+    assert np.abs(a - b).max() >= 3
