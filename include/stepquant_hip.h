@@ -229,9 +229,10 @@ int sq_prefill(const sq_pool *pool, const sq_prefill_args *args, void *stream);
  * Slot operations (pool.py:358-365).  sq_clear_slots zeroes whole pages.
  * sq_copy_slots copies pages src[i] -> dst[i] through `temp`
  * ([n, page_bytes] bytes) so overlapping index sets behave like the
- * reference's gather-then-scatter.  Negative indices wrap like Python;
- * indices outside the pool are skipped.  Only data, page_bytes and num_slots
- * of `pool` are read, so format pools pass an sq_pool holding just those.
+ * reference's gather-then-scatter.  Negative indices wrap like Python; a
+ * pair whose source or destination lies outside the pool is skipped.
+ * Only data, page_bytes and num_slots of `pool` are read, so format pools
+ * pass an sq_pool holding just those.
  */
 int sq_clear_slots(const sq_pool *pool, const void *slots, int32_t slots_dtype, int64_t n,
                    void *stream);

@@ -3309,13 +3309,19 @@ __global__ void clear_kernel(uint8_t *data, int64_t page_bytes, int64_t num_slot
     p[e] = 0;
 }
 
-__global__ void gather_kernel(const uint8_t *data, int64_t page_bytes, int64_t num_slots, const void *slots,
-                              int dtype, uint8_t *temp, int scatter) {
-  int64_t s = load_slot(slots, dtype, blockIdx.y);
+// Pages src[y] -> temp[y] (scatter == 0) or temp[y] -> dst[y] (scatter == 1).
+// Negative indices wrap like Python; a pair whose source or destination
+// lies outside the pool is skipped in both passes, so a destination never
+// receives a temp page that the gather did not write.
+__global__ void gather_kernel(const uint8_t *data, int64_t page_bytes, int64_t num_slots, const void *src,
+                              const void *dst, int dtype, uint8_t *temp, int scatter) {
+  int64_t s = load_slot(src, dtype, blockIdx.y);
+  int64_t d = load_slot(dst, dtype, blockIdx.y);
   if (s < 0) s += num_slots;
-  if (s < 0 || s >= num_slots) return;
+  if (d < 0) d += num_slots;
+  if (s < 0 || s >= num_slots || d < 0 || d >= num_slots) return;
   uint8_t *t = temp + (int64_t)blockIdx.y * page_bytes;
-  uint8_t *p = (uint8_t *)data + s * page_bytes;
+  uint8_t *p = (uint8_t *)data + (scatter ? d : s) * page_bytes;
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < page_bytes;
        e += (int64_t)gridDim.x * blockDim.x) {
     if (scatter) p[e] = t[e];
@@ -3992,6 +3998,19 @@ int launch_format(const sq_format_pool *f, const FmtDev &fd, const StepDev &sd, 
   return go(format_kernel<MODE, SQ_FMT_DSQ>);
 }
 
+int launch_copy(const sq_pool *pool, const void *src, const void *dst, int32_t slots_dtype, int64_t n,
+                uint8_t *temp, hipStream_t stream) {
+  unsigned gx = (unsigned)((pool->page_bytes + 255) / 256);
+  if (gx > 1024) gx = 1024;
+  hipLaunchKernelGGL(gather_kernel, dim3(gx, (unsigned)n), dim3(256), 0, stream, pool->data,
+                     pool->page_bytes, pool->num_slots, src, dst, slots_dtype, temp, 0);
+  int rc = check_launch("gather_kernel");
+  if (rc) return rc;
+  hipLaunchKernelGGL(gather_kernel, dim3(gx, (unsigned)n), dim3(256), 0, stream, pool->data,
+                     pool->page_bytes, pool->num_slots, src, dst, slots_dtype, temp, 1);
+  return check_launch("scatter_kernel");
+}
+
 }  // namespace
 
 extern "C" {
@@ -4250,15 +4269,7 @@ int sq_copy_slots(const sq_pool *pool, const void *src, const void *dst, int32_t
   if (n == 0) return 0;
   if (!src || !dst || !temp || n < 0 || n > 65535) return fail(SQ_EINVAL, "copy: bad arguments");
   if (slots_dtype != SQ_I32 && slots_dtype != SQ_I64) return fail(SQ_EINVAL, "copy: slots dtype");
-  unsigned gx = (unsigned)((pool->page_bytes + 255) / 256);
-  if (gx > 1024) gx = 1024;
-  hipLaunchKernelGGL(gather_kernel, dim3(gx, (unsigned)n), dim3(256), 0, (hipStream_t)stream, pool->data,
-                     pool->page_bytes, pool->num_slots, src, slots_dtype, temp, 0);
-  int rc = check_launch("gather_kernel");
-  if (rc) return rc;
-  hipLaunchKernelGGL(gather_kernel, dim3(gx, (unsigned)n), dim3(256), 0, (hipStream_t)stream, pool->data,
-                     pool->page_bytes, pool->num_slots, dst, slots_dtype, temp, 1);
-  return check_launch("scatter_kernel");
+  return launch_copy(pool, src, dst, slots_dtype, n, temp, (hipStream_t)stream);
 }
 
 int sq_format_encode(const sq_format_pool *pool, const float *state, const void *slots, int32_t slots_dtype,

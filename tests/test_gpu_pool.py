@@ -305,6 +305,12 @@ def test_clear_and_overlapping_copy():
     pool.copy(torch.tensor([1, 2, 3], device=dev()), torch.tensor([2, 3, 4], device=dev()))
     assert torch.equal(pool.data[2:5], before[1:4])
     assert torch.equal(pool.data[1], before[1])
+    # a pair with a source outside the pool is skipped: its destination keeps its page
+    after = pool.data.clone()
+    pool.copy(torch.tensor([9, 2], device=dev()), torch.tensor([1, 5], device=dev()))
+    assert torch.equal(pool.data[1], after[1])
+    assert torch.equal(pool.data[5], after[2])
+    slots = torch.tensor([1, 2, 3, 4, 5], device=dev())
     pool.clear(slots)
     assert pool.decode(slots).count_nonzero() == 0
     assert pool.data.count_nonzero() == 0
