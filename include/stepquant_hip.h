@@ -240,6 +240,21 @@ int sq_copy_slots(const sq_pool *pool, const void *src, const void *dst, int32_t
                   int64_t n, uint8_t *temp, void *stream);
 
 /*
+ * No counterpart in the reference.  sq_copy_slots without the `temp`
+ * argument, for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc): the pages are staged in a static device array of
+ * SQ_COPY_STATIC_BYTES bytes that the library holds on every GPU it runs
+ * on until the process ends.  n * page_bytes above that size is rejected
+ * with SQ_EINVAL; nothing is allocated or freed.  Every call on one GPU
+ * shares that GPU's array, so calls that overlap on one GPU (concurrent
+ * streams, or host threads) race; calls ordered on one stream do not.
+ */
+#define SQ_COPY_STATIC_BYTES (16u << 20)
+int sq_copy_slots_static(const sq_pool *pool, const void *src, const void *dst, int32_t slots_dtype,
+                         int64_t n, void *stream);
+
+/*
  * Baseline state formats: one layer's pool of FormatStatePool pages
  * (reference kernels/format_pool.py:29-128; layout format_layout,
  * format_pool.py:9-25).  Every row of the pool has the same code width.

@@ -23,6 +23,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "stepquant_hip.h"
 
 namespace {
@@ -3998,6 +4000,40 @@ int launch_format(const sq_format_pool *f, const FmtDev &fd, const StepDev &sd, 
   return go(format_kernel<MODE, SQ_FMT_DSQ>);
 }
 
+// Staging of sq_copy_slots_static: a file-scope device array.  Every GPU the
+// library runs on holds its own copy at its own address until the process
+// ends.  In host code the name is only a stand-in: kernels receive the
+// device address that hipGetSymbolAddress returns for the current device.
+static __device__ __align__(256) uint8_t scratch[SQ_COPY_STATIC_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+uint8_t *g_scratch_ptr[kMaxDevices];
+
+// Device address of `scratch` on the current device, looked up once per
+// device (on the first call made with that device current).
+int static_scratch(uint8_t **out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    snprintf(g_err, sizeof(g_err), "copy_static: hipGetDevice: %s", hipGetErrorString(e));
+    return (int)e;
+  }
+  if (dev < 0 || dev >= kMaxDevices) return fail(SQ_EINVAL, "copy_static: device index out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      snprintf(g_err, sizeof(g_err), "copy_static: hipGetSymbolAddress: %s", hipGetErrorString(e));
+      return e != hipSuccess ? (int)e : SQ_EINVAL;
+    }
+    g_scratch_ptr[dev] = (uint8_t *)ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
 int launch_copy(const sq_pool *pool, const void *src, const void *dst, int32_t slots_dtype, int64_t n,
                 uint8_t *temp, hipStream_t stream) {
   unsigned gx = (unsigned)((pool->page_bytes + 255) / 256);
@@ -4269,6 +4305,25 @@ int sq_copy_slots(const sq_pool *pool, const void *src, const void *dst, int32_t
   if (n == 0) return 0;
   if (!src || !dst || !temp || n < 0 || n > 65535) return fail(SQ_EINVAL, "copy: bad arguments");
   if (slots_dtype != SQ_I32 && slots_dtype != SQ_I64) return fail(SQ_EINVAL, "copy: slots dtype");
+  return launch_copy(pool, src, dst, slots_dtype, n, temp, (hipStream_t)stream);
+}
+
+int sq_copy_slots_static(const sq_pool *pool, const void *src, const void *dst, int32_t slots_dtype, int64_t n,
+                         void *stream) {
+  if (!pool || !pool->data) return fail(SQ_EINVAL, "copy_static: null pool");
+  if (n == 0) return 0;
+  if (!src || !dst || n < 0 || n > 65535 || pool->page_bytes <= 0)
+    return fail(SQ_EINVAL, "copy_static: bad arguments");
+  if (slots_dtype != SQ_I32 && slots_dtype != SQ_I64) return fail(SQ_EINVAL, "copy_static: slots dtype");
+  if (n > (int64_t)SQ_COPY_STATIC_BYTES / pool->page_bytes) {
+    snprintf(g_err, sizeof(g_err),
+             "copy_static: %lld pages of %lld bytes exceed the static staging of %lld bytes",
+             (long long)n, (long long)pool->page_bytes, (long long)SQ_COPY_STATIC_BYTES);
+    return SQ_EINVAL;
+  }
+  uint8_t *temp = nullptr;
+  int rc = static_scratch(&temp);
+  if (rc) return rc;
   return launch_copy(pool, src, dst, slots_dtype, n, temp, (hipStream_t)stream);
 }
 
