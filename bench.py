@@ -44,7 +44,10 @@ def parse():
     p.add_argument("--arch", choices=["gdn", "kda"], default="gdn")
     p.add_argument("--nominal", type=int, choices=[4, 6], default=6)
     p.add_argument("--async-writeback", action="store_true",
-                   help="split readout (foreground) and writer (writeback stream)")
+                   help="split readout (foreground) and writer (writeback stream); under graphs the writers "
+                        "are deferred and forked at attention windows, joined at the end of the step")
+    p.add_argument("--layers", type=int, default=1,
+                   help="recurrent layers per step, each with its own pool (an attention window before each)")
     p.add_argument("--cpu-sample", type=int, default=-1,
                    help="requests in the CPU-baseline sample (-1: auto, 0: skip)")
     p.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "traffic_gdn6_b256.json"),
@@ -270,21 +273,30 @@ def main():
         spec = get_format(a.state_format)
         bits = torch.full((H, K), spec.bits, dtype=torch.long)
         impact = torch.ones(H, K)
-        pool = FormatStatePool(FormatPlan(a.arch, bits.to(dev), impact.to(dev)), B + 1, V, spec)
+        fplan = FormatPlan(a.arch, bits.to(dev), impact.to(dev))
+
+        def make_pool():
+            return FormatStatePool(fplan, B + 1, V, spec)
         stream = None
         a.cpu_sample = 0  # the CPU port restates the STEPQuant path only
     else:
         plan = QuantizationPlan(a.arch, bits.to(dev), impact.to(dev))
-        pool = PackedStatePool(plan, B + 1, V, writeback_stream=stream)
+
+        def make_pool():
+            return PackedStatePool(plan, B + 1, V, writeback_stream=stream)
+    pools = [make_pool() for _ in range(a.layers)]
+    pool = pools[0]
     g = torch.Generator(device=dev).manual_seed(0)
     slots = torch.arange(1, B + 1, device=dev, dtype=torch.int32)
-    if a.nominal == 4:
-        # key-row and value-column scales log-normal(0, 0.5)
-        r = torch.exp(torch.randn(B, H, K, 1, device=dev, generator=g) * .5)
-        c = torch.exp(torch.randn(B, H, 1, V, device=dev, generator=g) * .5)
-        pool.encode(r * torch.randn(B, H, K, V, device=dev, generator=g) * c, slots)
-    else:
-        pool.encode(torch.randn(B, H, K, V, device=dev, generator=g) * .05, slots)
+    for layer in pools:
+        if a.nominal == 4:
+            # key-row and value-column scales log-normal(0, 0.5)
+            r = torch.exp(torch.randn(B, H, K, 1, device=dev, generator=g) * .5)
+            c = torch.exp(torch.randn(B, H, 1, V, device=dev, generator=g) * .5)
+            layer.encode(r * torch.randn(B, H, K, V, device=dev, generator=g) * c, slots)
+            del r, c
+        else:
+            layer.encode(torch.randn(B, H, K, V, device=dev, generator=g) * .05, slots)
     mixed = torch.randn(B, 2 * HK * K + H * V, device=dev, generator=g).to(torch.bfloat16)
     q, k, v = mixed.split([HK * K, HK * K, H * V], -1)
     # raw gates with A_log = 0, dt_bias = 0: g = -softplus(a); KDA a = 0.5 N(0,1) per channel
@@ -294,10 +306,26 @@ def main():
     a_log = torch.zeros(H, device=dev)
     dt_bias = torch.zeros(H * K if a.arch == "kda" else H, device=dev)
 
+    from stepquant_amd.kernels.writeback import attention_window, defer_writeback
+
+    def layers():
+        outs = []
+        for layer in pools:
+            attention_window()
+            outs.append(layer.step(q, k, v, gate, beta, slots, normalize=True, scale=K ** -.5, a_log=a_log,
+                                   dt_bias=dt_bias))
+        return outs
+
     def step():
-        out = pool.step(q, k, v, gate, beta, slots, normalize=True, scale=K ** -.5, a_log=a_log, dt_bias=dt_bias)
-        pool.wait()
-        return out
+        if stream is not None and torch.cuda.is_current_stream_capturing():
+            # writers forked at attention windows, joined when the step ends
+            with defer_writeback(pools, attention_windows=True, joined=True):
+                outs = layers()
+        else:
+            outs = layers()
+        for layer in pools:
+            layer.wait()
+        return outs
 
     for _ in range(3):
         step()
@@ -317,11 +345,13 @@ def main():
         one, block = single.replay, multi.replay
     ms_step, wall = timed_steps(torch, one, block, per_block, a.steps, a.warmup, a.warm_seconds)
     page = pool.page_bytes
-    alg_bytes = 2 * B * page
+    alg_bytes = 2 * B * page * a.layers
     achieved = alg_bytes / (ms_step * 1e-3) / 1e9
-    updates = B * H / (ms_step * 1e-3)
+    updates = B * H * a.layers / (ms_step * 1e-3)
     # measured HBM bytes per launch apply only to the workload they were taken on
     key = f"{a.arch}-{a.nominal}-b{B}-h{H}-hk{HK}-{'async' if stream is not None else 'fused'}"
+    if a.layers != 1:
+        key += f"-l{a.layers}"
     if a.state_format != "stepquant":
         key = f"{a.state_format}-{a.arch}-b{B}-h{H}-hk{HK}"
     traffic = None
@@ -344,7 +374,8 @@ def main():
                 vs_baseline=None, dtype="f32", data="synthetic",
                 config=dict(workload=(f"{a.arch.upper()} decode STEPQuant@{a.nominal}" if a.state_format == "stepquant"
                                       else f"{a.arch.upper()} decode {a.state_format} pages")
-                                     + f", one layer, B={B}, H={H}, "
+                                     + (", one layer" if a.layers == 1 else f", {a.layers} layers")
+                                     + f", B={B}, H={H}, "
                                      f"HK={HK}, dk=dv={K}, bf16 q/k/v, raw gates, "
                                      + (f"{per_block} steps per graph launch" if not a.no_graph else "eager steps")
                                      + (", async writeback" if stream is not None else ", fused writeback"),

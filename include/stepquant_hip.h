@@ -323,6 +323,24 @@ int sq_pool_flags(const int32_t *bits, const int32_t *head_meta, const int32_t *
 int sq_stream_capture_id(void *stream, int32_t *capturing, uint64_t *id);
 
 /*
+ * Events that order work across graphs, the role of the reference's
+ * external events (torch.cuda.Event(external=True) and cudaEventRecordExternal
+ * / cudaEventWaitExternal nodes: pool.py:131-135, 338-355; writeback.py:43,
+ * 103, 110-116).  sq_event_record / sq_event_wait act on `stream` now when it
+ * is not capturing; on a capturing stream they add an event record / wait
+ * node to the capture's graph after the stream's current dependencies, so
+ * every replay records the event, or waits for its latest record.
+ * sq_event_query returns 0 when the event's work is done and 1 when it is
+ * not.  Events are created without timing.
+ */
+int sq_event_create(void **event);
+int sq_event_destroy(void *event);
+int sq_event_record(void *event, void *stream);
+int sq_event_wait(void *stream, void *event);
+int sq_event_query(void *event);
+int sq_event_synchronize(void *event);
+
+/*
  * A non-blocking stream restricted to `cus` compute units spread across all
  * XCDs (hipExtStreamCreateWithCUMask; 0 = unrestricted), at default priority.
  * Replaces the Green Context SM split of writeback_resources

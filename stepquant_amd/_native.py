@@ -68,7 +68,9 @@ FMT_ROWS_CONTIGUOUS = 1
 EXPORTS = ("sq_abi_version", "sq_last_error", "sq_encode", "sq_decode_dense", "sq_decode_step",
            "sq_decode_readout", "sq_writeback", "sq_clear_slots", "sq_copy_slots",
            "sq_stream_capture_id", "sq_create_cu_stream", "sq_pool_flags", "sq_prefill",
-           "sq_format_encode", "sq_format_decode", "sq_format_step", "sq_copy_slots_static")
+           "sq_format_encode", "sq_format_decode", "sq_format_step", "sq_copy_slots_static",
+           "sq_event_create", "sq_event_destroy", "sq_event_record", "sq_event_wait", "sq_event_query",
+           "sq_event_synchronize")
 COPY_STATIC_BYTES = 16 << 20
 
 _lib = None
@@ -102,6 +104,12 @@ def lib():
     L.sq_clear_slots.argtypes = [PP(Pool), _P, ctypes.c_int32, ctypes.c_int64, _P]
     L.sq_copy_slots.argtypes = [PP(Pool), _P, _P, ctypes.c_int32, ctypes.c_int64, _P, _P]
     L.sq_copy_slots_static.argtypes = [PP(Pool), _P, _P, ctypes.c_int32, ctypes.c_int64, _P]
+    L.sq_event_create.argtypes = [PP(_P)]
+    L.sq_event_destroy.argtypes = [_P]
+    L.sq_event_record.argtypes = [_P, _P]
+    L.sq_event_wait.argtypes = [_P, _P]
+    L.sq_event_query.argtypes = [_P]
+    L.sq_event_synchronize.argtypes = [_P]
     L.sq_pool_flags.argtypes = [_P, _P, _P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
                                 ctypes.c_int32, ctypes.c_int32, ctypes.c_int64]
     L.sq_stream_capture_id.argtypes = [_P, PP(ctypes.c_int32), PP(ctypes.c_uint64)]

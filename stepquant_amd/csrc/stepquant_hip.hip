@@ -4175,6 +4175,98 @@ int sq_stream_capture_id(void *stream, int32_t *capturing, uint64_t *id) {
   return 0;
 }
 
+int sq_event_create(void **event) {
+  if (!event) return fail(SQ_EINVAL, "event: null output");
+  hipEvent_t e = nullptr;
+  hipError_t rc = hipEventCreateWithFlags(&e, hipEventDisableTiming);
+  if (rc != hipSuccess) {
+    snprintf(g_err, sizeof(g_err), "hipEventCreateWithFlags: %s", hipGetErrorString(rc));
+    return (int)rc;
+  }
+  *event = (void *)e;
+  return 0;
+}
+
+int sq_event_destroy(void *event) {
+  if (!event) return 0;
+  hipError_t rc = hipEventDestroy((hipEvent_t)event);
+  if (rc != hipSuccess) {
+    snprintf(g_err, sizeof(g_err), "hipEventDestroy: %s", hipGetErrorString(rc));
+    return (int)rc;
+  }
+  return 0;
+}
+
+// Event record (wait == 0) or wait (wait == 1) on `stream`.  On a stream that
+// is capturing, the operation becomes an event node of the capture's graph,
+// placed after the stream's current capture dependencies and made the only
+// one: a record node records the event on every replay of the graph, a wait
+// node makes later captured work wait for the event's latest record.  A
+// graph can therefore order itself against eager work and other graphs
+// (hipEventRecordWithFlags with hipEventRecordExternal is refused under
+// capture on this platform; explicit nodes are not).
+static int event_op(void *event, void *stream, int wait) {
+  if (!event) return fail(SQ_EINVAL, "event: null event");
+  hipStream_t s = (hipStream_t)stream;
+  hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+  unsigned long long ident = 0;
+  hipGraph_t graph = nullptr;
+  const hipGraphNode_t *deps = nullptr;
+  size_t ndeps = 0;
+  hipError_t rc = hipStreamGetCaptureInfo_v2(s, &status, &ident, &graph, &deps, &ndeps);
+  if (rc != hipSuccess) {
+    snprintf(g_err, sizeof(g_err), "hipStreamGetCaptureInfo_v2: %s", hipGetErrorString(rc));
+    return (int)rc;
+  }
+  if (status == hipStreamCaptureStatusInvalidated) return fail(SQ_EINVAL, "event: capture was invalidated");
+  if (status == hipStreamCaptureStatusNone) {
+    rc = wait ? hipStreamWaitEvent(s, (hipEvent_t)event, 0) : hipEventRecord((hipEvent_t)event, s);
+    if (rc != hipSuccess) {
+      snprintf(g_err, sizeof(g_err), "%s: %s", wait ? "hipStreamWaitEvent" : "hipEventRecord",
+               hipGetErrorString(rc));
+      return (int)rc;
+    }
+    return 0;
+  }
+  hipGraphNode_t node = nullptr;
+  rc = wait ? hipGraphAddEventWaitNode(&node, graph, deps, ndeps, (hipEvent_t)event)
+            : hipGraphAddEventRecordNode(&node, graph, deps, ndeps, (hipEvent_t)event);
+  if (rc != hipSuccess) {
+    snprintf(g_err, sizeof(g_err), "%s: %s", wait ? "hipGraphAddEventWaitNode" : "hipGraphAddEventRecordNode",
+             hipGetErrorString(rc));
+    return (int)rc;
+  }
+  rc = hipStreamUpdateCaptureDependencies(s, &node, 1, hipStreamSetCaptureDependencies);
+  if (rc != hipSuccess) {
+    snprintf(g_err, sizeof(g_err), "hipStreamUpdateCaptureDependencies: %s", hipGetErrorString(rc));
+    return (int)rc;
+  }
+  return 0;
+}
+
+int sq_event_record(void *event, void *stream) { return event_op(event, stream, 0); }
+
+int sq_event_wait(void *stream, void *event) { return event_op(event, stream, 1); }
+
+int sq_event_query(void *event) {
+  if (!event) return fail(SQ_EINVAL, "event: null event");
+  hipError_t rc = hipEventQuery((hipEvent_t)event);
+  if (rc == hipSuccess) return 0;
+  if (rc == hipErrorNotReady) return 1;
+  snprintf(g_err, sizeof(g_err), "hipEventQuery: %s", hipGetErrorString(rc));
+  return (int)rc;
+}
+
+int sq_event_synchronize(void *event) {
+  if (!event) return fail(SQ_EINVAL, "event: null event");
+  hipError_t rc = hipEventSynchronize((hipEvent_t)event);
+  if (rc != hipSuccess) {
+    snprintf(g_err, sizeof(g_err), "hipEventSynchronize: %s", hipGetErrorString(rc));
+    return (int)rc;
+  }
+  return 0;
+}
+
 int sq_create_cu_stream(int32_t device, int32_t cus, void **stream, int32_t *actual, int32_t *total) {
   if (!stream || !actual || !total) return fail(SQ_EINVAL, "cu stream: null output");
   hipError_t e = hipSetDevice(device);

@@ -9,8 +9,11 @@ adapter can use it unchanged.  All arithmetic runs in the HIP kernels of
   tile, gated delta update, readout, requantise, store (``sq_decode_step``).
 * ``step`` with a writeback stream splits into a foreground readout
   (``sq_decode_readout``) and a writer launched on the writeback stream
-  (``sq_writeback``), ordered by events exactly as the reference's
-  ``_schedule_writeback``/``wait`` protocol (pool.py:284-356).
+  (``sq_writeback``), eagerly or as a branch of the graph being captured,
+  ordered by events with the reference's ``_schedule_writeback``/``wait``
+  protocol (pool.py:284-356): ``ready`` orders consumers in the same capture
+  or eager stream order, ``graph_ready`` (a ``GraphEvent``) consumers in
+  other graphs.
 * ``encode`` requantises dense fp32 states bit-identically to the CPU
   ``fit_state``; ``decode`` expands pages to fp32.
 """
@@ -19,6 +22,7 @@ from __future__ import annotations
 import torch
 
 from .. import _native as N
+from .events import GraphEvent, capture_id, wait_for
 
 
 def packed_layout(plan, value_dim, storage="packed"):
@@ -199,13 +203,14 @@ class PackedStatePool:
         self.consumer_dependencies = set()
         self.ready_capture = None
         self.deferred = None
-        # PyTorch-ROCm has no external (cross-graph) events: both events are
-        # ordinary, and ordering across graph replays is carried by the
-        # completion event WritebackGraph.replay records between replays.
-        self.ready = torch.cuda.Event() if writeback_stream is not None else None
-        self.graph_ready = torch.cuda.Event() if writeback_stream is not None else None
+        asynchronous = writeback_stream is not None
+        # ready: a torch event, joined by consumers in the writer's own
+        # capture (or stream order eagerly); graph_ready: a GraphEvent that
+        # consumers in other graphs wait on through a graph node.
+        self.ready = torch.cuda.Event() if asynchronous else None
+        self.graph_ready = GraphEvent() if asynchronous else None
         self.completion = self.ready
-        if self.graph_ready is not None:
+        if asynchronous:
             self.graph_ready.record(torch.cuda.current_stream(self.device))
 
     def _init_workspace(self, slots, writeback_workspace):
@@ -456,23 +461,20 @@ class PackedStatePool:
         if self.deferred is not None:
             self.deferred.append((self, update_key, decay, delta, partial, stable_slots))
             return
-        current = torch.cuda.current_stream(self.device)
-        if torch.cuda.is_current_stream_capturing():
-            # Inside a graph the writer follows the readout on the capturing
-            # stream.  A writer branch forked to the writeback stream and
-            # joined through events was observed to overlap the next queued
-            # replay on ROCm, so captures never fork.
+        here = torch.cuda.current_stream(self.device)
+        side = self.writeback_stream
+        side.wait_stream(here)
+        with torch.cuda.stream(side):
             self._finish_update(update_key, decay, delta, partial, stable_slots)
-            return
-        self.writeback_stream.wait_stream(current)
-        with torch.cuda.stream(self.writeback_stream):
-            self._finish_update(update_key, decay, delta, partial, stable_slots)
-            self.graph_ready.record()
-            self.ready.record()
+            self.graph_ready.record(side)
+            self.ready.record(side)
         for tensor in (update_key, decay, delta, partial, stable_slots):
-            tensor.record_stream(self.writeback_stream)
-        self.ready_capture = None
-        self.completion = self.ready
+            tensor.record_stream(side)
+        # Under capture the writer is a branch of the graph: consumers in the
+        # same capture join it through `ready`, consumers anywhere else wait
+        # on the graph_ready node every replay records.
+        self.ready_capture = capture_id(here) if torch.cuda.is_current_stream_capturing() else None
+        self.completion = self.graph_ready if self.ready_capture is not None else self.ready
         self.pending = True
 
     def _finish_update(self, update_key, decay, delta, partial, slots):
@@ -481,24 +483,36 @@ class PackedStatePool:
         N.check(N.lib().sq_writeback(self._desc, scratch, slots.numel(), N.stream_handle()), "writeback")
 
     def wait(self):
-        """Order the current stream after this pool's pending writer.
+        """Order the current stream after this pool's latest writer.
 
-        Eagerly this waits on the writer's completion event.  Inside a graph
-        capture the writer of a captured step already ran on the capturing
-        stream; writers of earlier replays or eager calls are ordered outside
-        the capture: torch synchronises before a capture begins, and
-        WritebackGraph.replay waits on every pool's completion before
-        replaying its forward graph.
+        Inside ``defer_writeback`` a paired capture waits on the previous
+        replay's writer of this layer (its ``graph_ready`` node); a joined
+        capture needs nothing, its replays finish their writers.  Otherwise,
+        with a writer pending: eagerly, wait on ``completion``; inside the
+        writer's own capture, join its branch; inside another capture, add a
+        wait node on ``graph_ready`` (and on a graph's completion event, kept
+        alive in ``consumer_dependencies``).  A wait orders only the stream
+        it is issued on.
         """
-        if getattr(self, "deferred", None) is not None or not self.pending:
-            return
         stream = torch.cuda.current_stream(self.device)
-        if torch.cuda.is_current_stream_capturing():
-            # writers launched inside this capture ran on the capturing
-            # stream already; earlier ones are ordered outside the graph
-            self.captured_consumers = True
+        tasks = getattr(self, "deferred", None)
+        if tasks is not None:
+            if not tasks.joined:
+                self.graph_ready.wait(stream)
             return
-        stream.wait_event(self.completion)
+        if not self.pending:
+            return
+        if not torch.cuda.is_current_stream_capturing():
+            wait_for(stream, self.completion)
+            return
+        if self.ready_capture is not None and self.ready_capture == capture_id(stream):
+            stream.wait_event(self.ready)
+            return
+        self.captured_consumers = True
+        if self.completion is not self.ready and self.completion is not self.graph_ready:
+            self.consumer_dependencies.add(self.completion)
+            wait_for(stream, self.completion)
+        self.graph_ready.wait(stream)
 
     # ------------------------------------------------------------ slot ops
     def clear(self, slots):

@@ -111,8 +111,11 @@ def test_profiles_tiers():
 @pytest.mark.parametrize("chunk", [32, 64, 128, 256, 512])
 def test_release_schedule_keeps_tail_bounded(monkeypatch, chunk):
     """Reference tests/test_writeback_schedule.py:8-23 on the same schedule."""
+    from stepquant_amd.kernels import writeback
     from stepquant_amd.kernels.writeback import CapturedWrites
-    monkeypatch.setattr(torch.cuda, "Event", lambda **kwargs: SimpleNamespace(record=lambda: None))
+    # release points record a gate event on the capturing stream: stubbed on the CPU
+    monkeypatch.setattr(writeback, "GraphEvent", lambda: SimpleNamespace(record=lambda stream: None))
+    monkeypatch.setattr(torch.cuda, "current_stream", lambda *a: None)
     tasks = CapturedWrites(attention_windows=True)
     slots = torch.arange(512)
     recurrent = [True, True, True, False] * 6 + [True, True, False]
