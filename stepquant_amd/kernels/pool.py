@@ -121,6 +121,13 @@ def _head_meta(plan, value_dim, offsets, rows, storage="packed"):
     return meta
 
 
+def _check_offsets(first, drops):
+    """Sequence offsets start at row 0 and never decrease, so every sequence's
+    rows lie inside the q/k/v/out rows (cu_seqlens[-1] of them)."""
+    if first != 0 or drops:
+        raise ValueError("cu_seqlens must start at 0 and never decrease")
+
+
 def _indices(slots, device):
     if isinstance(slots, torch.Tensor):
         t = slots.to(device)
@@ -357,9 +364,10 @@ class PackedStatePool:
         ``cu_seqlens`` ``[B+1]`` token offsets, ``slots`` ``[B]``.  Initial
         states come from ``init_slots`` (default ``slots``; ``None`` entries
         or slot <= 0 start from zero).  By default the final state is written
-        to ``slots``; ``checkpoints`` ``[B, NC]`` (token counts, ascending)
-        with ``checkpoint_slots`` ``[B, NC]`` write intermediate prefix states
-        as well.  Returns the outputs ``[T, H, V]`` in q's dtype.
+        to ``slots``; ``checkpoints`` ``[B, NC]`` (token counts, ascending;
+        checked when they are host tensors) with ``checkpoint_slots``
+        ``[B, NC]`` write intermediate prefix states as well.  ``cu_seqlens``
+        must start at 0 and never decrease (ValueError otherwise).  Returns the outputs ``[T, H, V]`` in q's dtype.
         """
         self.wait()
         if self.plan.architecture != "gdn" or self.keys != 128 or self.values != 128:
@@ -368,11 +376,17 @@ class PackedStatePool:
         cu_host = None
         if isinstance(cu_seqlens, torch.Tensor) and cu_seqlens.device.type != "cpu":
             cu = cu_seqlens.to(dev, torch.int32).reshape(-1).contiguous()
-            total = int(cu[-1].item()) if cu.numel() > 1 else 0  # waits for the stream
+            total = 0
+            if cu.numel() > 1:
+                # one wait for the stream: the row count and the offsets' validity
+                first, total, drops = torch.stack([cu[0], cu[-1], (cu[1:] < cu[:-1]).sum().to(torch.int32)]).tolist()
+                _check_offsets(first, drops)
         else:
             # offsets known on the host: checked here, copied without a wait
             cu_host = torch.as_tensor(cu_seqlens).to(torch.int32).reshape(-1)
             total = int(cu_host[-1]) if cu_host.numel() > 1 else 0
+            if cu_host.numel() > 1:
+                _check_offsets(int(cu_host[0]), int((cu_host[1:] < cu_host[:-1]).sum()))
             cu = cu_host.pin_memory().to(dev, non_blocking=True)
         batch = cu.numel() - 1
         if batch < 0:
@@ -415,7 +429,12 @@ class PackedStatePool:
             if cs_h.shape != ck_h.shape:
                 raise ValueError("one slot per checkpoint")
             lengths_h = (cu_host[1:] - cu_host[:-1]).reshape(batch, 1)
-            cs_h = torch.where((ck_h > 0) & (ck_h <= lengths_h), cs_h, torch.zeros_like(cs_h))
+            used = (ck_h > 0) & (ck_h <= lengths_h)
+            for row, mask in zip(ck_h, used):
+                kept = row[mask]
+                if (kept[1:] < kept[:-1]).any():
+                    raise ValueError("checkpoints of a sequence must be ascending")
+            cs_h = torch.where(used, cs_h, torch.zeros_like(cs_h))
             ck = ck_h.contiguous().pin_memory().to(dev, non_blocking=True)
             ck_slots = cs_h.contiguous().pin_memory().to(dev, non_blocking=True)
         else:
@@ -494,14 +513,14 @@ class PackedStatePool:
         alive in ``consumer_dependencies``).  A wait orders only the stream
         it is issued on.
         """
-        stream = torch.cuda.current_stream(self.device)
         tasks = getattr(self, "deferred", None)
         if tasks is not None:
             if not tasks.joined:
-                self.graph_ready.wait(stream)
+                self.graph_ready.wait(torch.cuda.current_stream(self.device))
             return
         if not self.pending:
             return
+        stream = torch.cuda.current_stream(self.device)
         if not torch.cuda.is_current_stream_capturing():
             wait_for(stream, self.completion)
             return

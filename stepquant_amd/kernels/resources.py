@@ -6,6 +6,14 @@ over all eight XCDs (``hipExtStreamCreateWithCUMask`` through
 ``sq_create_cu_stream``), at default priority.  A budget of 0 means an
 unrestricted stream.  Streams are cached per (device, budget) and live for
 the process, since captured graphs refer to them.
+
+Two scheduling facts of this platform matter to a caller.  A CU-masked
+stream is a blocking stream (the call takes no flags): work on the legacy
+default stream waits for it, so the foreground should run on a stream of its
+own.  And streams share the device's hardware queues (``GPU_MAX_HW_QUEUES``,
+4 here) round-robin in creation order: two streams on one queue run in
+submission order, so streams created one after the other are the ones that
+can run side by side.
 """
 from dataclasses import dataclass
 

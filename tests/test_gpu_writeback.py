@@ -48,27 +48,34 @@ def _inputs(B, arch, seed=0):
 
 
 def test_forward_completes_before_its_paired_writer(monkeypatch):
+    """The foreground and the writer run on two streams created one after the
+    other: streams share the device's few hardware queues round-robin (two
+    streams on one queue run in submission order), and work on the legacy
+    default stream waits for blocking streams, so neither is used here."""
     from stepquant_amd.kernels.writeback import WritebackGraph, defer_writeback
     print("case paired writer after forward", flush=True)
-    pool = _pool("gdn", 2)
+    foreground, side = torch.cuda.Stream(), torch.cuda.Stream()
+    pool = _pool("gdn", 2, stream=side)
     slots = torch.ones(1, device=dev(), dtype=torch.long)
     args = (*_inputs(1, "gdn"), slots)
-    pool.step(*args)
+    with torch.cuda.stream(foreground):
+        pool.step(*args)
+        torch.cuda.synchronize()
+        forward = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(forward):
+            with defer_writeback([pool]) as tasks:
+                pool.step(*args)
+        _slow_writer(monkeypatch, pool)
+        graph = WritebackGraph(forward, tasks)
+        graph.replay()
+        done = torch.cuda.Event()
+        done.record(foreground)
+        done.synchronize()
+        assert not pool.graph_ready.query(), "the forward graph waited for its writer"
+        assert not graph.completion.query()
+        pool.wait()
     torch.cuda.synchronize()
-    forward = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(forward):
-        with defer_writeback([pool]) as tasks:
-            pool.step(*args)
-    _slow_writer(monkeypatch, pool)
-    graph = WritebackGraph(forward, tasks)
-    graph.replay()
-    done = torch.cuda.Event()
-    done.record()
-    done.synchronize()
-    assert not pool.graph_ready.query(), "the forward graph waited for its writer"
-    pool.wait()
-    torch.cuda.synchronize()
-    assert pool.graph_ready.query()
+    assert pool.graph_ready.query() and graph.completion.query()
 
 
 def test_every_consumer_stream_keeps_its_dependency(monkeypatch):

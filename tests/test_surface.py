@@ -1,5 +1,6 @@
 """Host-side surface on the CPU: the C ABI exports, layout, plans, schedules."""
 import ctypes
+import os
 import re
 from types import SimpleNamespace
 
@@ -131,23 +132,6 @@ def test_release_schedule_keeps_tail_bounded(monkeypatch, chunk):
     assert sum(task.final for task in tasks) == sum(recurrent)
 
 
-def test_alias_exposes_reference_module_names():
-    import sys
-    import stepquant_amd
-    saved = {k: v for k, v in sys.modules.items() if k == "stepquant" or k.startswith("stepquant.")}
-    try:
-        stepquant_amd.install_alias("stepquant")
-        from stepquant.kernels.pool import PackedStatePool, packed_layout  # noqa: F401
-        from stepquant.kernels.writeback import defer_writeback, WritebackGraph, attention_window  # noqa: F401
-        from stepquant.formats import get_format, FormatPlan  # noqa: F401
-        from stepquant.quantization import QuantizationPlan  # noqa: F401
-        assert get_format("stepquant6").bits == 6
-    finally:
-        for k in [k for k in sys.modules if k == "stepquant" or k.startswith("stepquant.")]:
-            del sys.modules[k]
-        sys.modules.update(saved)
-
-
 @pytest.mark.parametrize("bits", [2, 4, 6, 8])
 @pytest.mark.parametrize("n", [0, 1, 7, 128, 513])
 def test_packing_matches_oracle(bits, n):
@@ -157,3 +141,42 @@ def test_packing_matches_oracle(bits, n):
     assert p.dtype == torch.uint8
     np.testing.assert_array_equal(p.numpy(), O.pack(x.numpy(), bits))
     torch.testing.assert_close(unpack(p, bits, n).long(), x)
+
+
+def _bare_gdn_pool():
+    from stepquant_amd.kernels.pool import PackedStatePool
+    pool = object.__new__(PackedStatePool)
+    pool.plan = SimpleNamespace(architecture="gdn")
+    pool.keys = pool.values = 128
+    pool.device = torch.device("cpu")
+    pool.deferred = None
+    pool.pending = False
+    return pool
+
+
+@pytest.mark.parametrize("cu", [[1, 4, 9], [0, 9, 4], [0, 4, 2, 9]])
+def test_prefill_rejects_offsets_outside_the_rows(cu):
+    """Offsets that start past row 0 or decrease would send a sequence's
+    rows outside q/k/v/out: refused on the host before any launch."""
+    pool = _bare_gdn_pool()
+    x = torch.zeros(9, 128)
+    with pytest.raises(ValueError, match="cu_seqlens must start at 0 and never decrease"):
+        pool.extend(x, x, x, torch.zeros(9, 1), torch.zeros(9, 1), [1] * (len(cu) - 1), torch.tensor(cu))
+
+
+def test_constructor_signature_matches_the_reference_order():
+    """PackedStatePool(plan, slots, value_dim=128, writeback_stream=None,
+    writeback_workspace=None, writeback_chunk=64, storage='packed')
+    (reference kernels/pool.py:70), as INTEGRATION.md documents it."""
+    import inspect
+    import re
+    from stepquant_amd.kernels.pool import PackedStatePool
+    params = list(inspect.signature(PackedStatePool.__init__).parameters.values())[1:]
+    got = [(p.name, p.default) for p in params]
+    assert got == [("plan", inspect.Parameter.empty), ("slots", inspect.Parameter.empty), ("value_dim", 128),
+                   ("writeback_stream", None), ("writeback_workspace", None), ("writeback_chunk", 64),
+                   ("storage", "packed")]
+    doc = open(os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "INTEGRATION.md")).read()
+    sig = re.search(r"PackedStatePool\(plan, slots, value_dim=128,\s+writeback_stream=None,\s+"
+                    r"writeback_workspace=None,\s+writeback_chunk=64,\s+storage=\"packed\"\)", doc)
+    assert sig, "INTEGRATION.md documents the constructor in this order"
