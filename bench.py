@@ -154,6 +154,7 @@ def cpu_baseline(bits, impact, arch, B, H, HK, K, V, sample, steps=4, threads=0,
 
 
 PEAK_BF16_TFLOPS = 2500.0
+PEAK_F32_TFLOPS = 157.3
 
 
 def timed_steps(torch, one, block, per_block, steps, warmup, warm_seconds):
@@ -164,6 +165,7 @@ def timed_steps(torch, one, block, per_block, steps, warmup, warm_seconds):
     t0 = time.perf_counter()
     while time.perf_counter() - t0 < warm_seconds:
         block()
+        torch.cuda.synchronize()  # keeps the launch queue shallow: the timed region starts from no backlog
     for _ in range(warmup):
         one()
     torch.cuda.synchronize()
@@ -193,18 +195,20 @@ def bench_prefill(a, torch):
     dev = torch.device("cuda:0")
     B, H, HK, K, V, T = a.batch, a.heads, a.key_heads, 128, 128, a.seq_len
     NC = a.checkpoints
-    bits, impact = make_plan(torch, "gdn", H, K, 6)
-    plan = QuantizationPlan("gdn", bits.to(dev), impact.to(dev))
+    kda = a.arch == "kda"
+    bits, impact = make_plan(torch, a.arch, H, K, 6)
+    plan = QuantizationPlan(a.arch, bits.to(dev), impact.to(dev))
     pool = PackedStatePool(plan, B * (NC + 1) + 1, V)
     g = torch.Generator(device=dev).manual_seed(0)
     tot = B * T
     q = torch.randn(tot, HK * K, device=dev, generator=g).to(torch.bfloat16)
     k = torch.randn(tot, HK * K, device=dev, generator=g).to(torch.bfloat16)
     v = torch.randn(tot, H * V, device=dev, generator=g).to(torch.bfloat16)
-    gate = torch.randn(tot, H, device=dev, generator=g)
+    # raw gates with A_log = 0, dt_bias = 0: g = -softplus(a); KDA a = 0.5 N(0,1) per channel
+    gate = torch.randn(tot, H, K, device=dev, generator=g) * .5 if kda else torch.randn(tot, H, device=dev, generator=g)
     beta = torch.randn(tot, H, device=dev, generator=g)
     a_log = torch.zeros(H, device=dev)
-    dt_bias = torch.zeros(H, device=dev)
+    dt_bias = torch.zeros(H * K if kda else H, device=dev)
     cu = torch.arange(0, tot + 1, T, dtype=torch.int32)  # sequence offsets known on the host
     init = torch.arange(1, B + 1, device=dev)
     pool.encode(torch.randn(B, H, K, V, device=dev, generator=g) * .05, init)
@@ -221,24 +225,35 @@ def bench_prefill(a, torch):
     step()
     torch.cuda.synchronize()
     ms_step, wall = timed_steps(torch, step, step, 1, a.steps, a.warmup, a.warm_seconds)
-    n_chunks = B * H * ((T + 63) // 64)
-    flops = prefill_flops(n_chunks)
-    tflops = flops / (ms_step * 1e-3) / 1e12
-    hbm = (3 * tot * H * K * 2 + tot * H * V * 2 + 2 * tot * H * 4 + B * pool.page_bytes
+    gate_bytes = tot * H * (K if kda else 1) * 4 + tot * H * 4
+    hbm = (2 * tot * HK * K * 2 + tot * H * V * 2 + tot * H * V * 2 + gate_bytes + B * pool.page_bytes
            + B * NC * pool.page_bytes)
-    line = dict(metric="prefill tokens/sec (chunked GDN prefill into prefix slots)",
+    workload = (f"{a.arch.upper()} prefill STEPQuant@6, B={B}, T={T}, H={H}, HK={HK}, dk=dv={K}, "
+                + ("token-by-token recurrence (per-channel decay)" if kda else "chunk 64")
+                + f", bf16 q/k/v, raw gates, {NC} prefix slots per request")
+    if kda:
+        # per token-head: decay K V multiplies, k^T S, the rank-1 update and q^T S (2 K V each)
+        flops = B * T * H * 7 * K * V
+        tflops = flops / (ms_step * 1e-3) / 1e12
+        roof = dict(bound="valu", achieved=round(tflops, 2), peak=PEAK_F32_TFLOPS, unit="TFLOP/s",
+                    frac=round(tflops / PEAK_F32_TFLOPS, 4), traffic=None, algorithmic_flops_per_step=flops,
+                    hbm_fraction=round(hbm / (ms_step * 1e-3) / 1e9 / PEAK_GBS, 4),
+                    algorithmic_bytes_per_step=hbm)
+    else:
+        n_chunks = B * H * ((T + 63) // 64)
+        flops = prefill_flops(n_chunks)
+        tflops = flops / (ms_step * 1e-3) / 1e12
+        roof = dict(bound="mfma", achieved=round(tflops, 2), peak=PEAK_BF16_TFLOPS, unit="TFLOP/s",
+                    frac=round(tflops / PEAK_BF16_TFLOPS, 4), traffic=None, algorithmic_flops_per_step=flops,
+                    hbm_fraction=round(hbm / (ms_step * 1e-3) / 1e9 / PEAK_GBS, 4),
+                    algorithmic_bytes_per_step=hbm)
+    line = dict(metric=f"prefill tokens/sec ({a.arch.upper()} prefill into prefix slots)",
                 value=round(tot / (ms_step * 1e-3), 1), unit="tokens/s", n_gpus=1, steps=a.steps,
                 warmup=a.warmup, ms_per_step=round(ms_step, 6), higher_is_better=True, scaling="weak",
                 vs_baseline=None, dtype="bf16", data="synthetic",
-                config=dict(workload=f"GDN prefill STEPQuant@6, B={B}, T={T}, H={H}, HK={HK}, dk=dv={K}, "
-                                     f"chunk 64, bf16 q/k/v, raw gates, {NC} prefix slots per request",
-                            global_batch=B, seq_len=T, wall_s=round(wall, 3), warm_seconds=a.warm_seconds),
-                roofline=dict(bound="mfma", achieved=round(tflops, 2), peak=PEAK_BF16_TFLOPS, unit="TFLOP/s",
-                              frac=round(tflops / PEAK_BF16_TFLOPS, 4), traffic=None,
-                              algorithmic_flops_per_step=flops,
-                              hbm_fraction=round(hbm / (ms_step * 1e-3) / 1e9 / PEAK_GBS, 4),
-                              algorithmic_bytes_per_step=hbm),
-                cpu_baseline=None)
+                config=dict(workload=workload, global_batch=B, seq_len=T, wall_s=round(wall, 3),
+                            warm_seconds=a.warm_seconds),
+                roofline=roof, cpu_baseline=None)
     print(json.dumps(line), flush=True)
 
 

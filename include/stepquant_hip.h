@@ -181,7 +181,8 @@ int sq_writeback(const sq_pool *pool, const sq_writeback_scratch *scratch, int64
  *   q, k      [T, HK*K] bf16 rows (row strides in elements, multiples of 8,
  *             rows 16-byte aligned); v [T, H*V] bf16; T = cu_seqlens[batch].
  *   g, beta   [T, H] log decay and write strength (raw gate a and logits b
- *             when a_log/dt_bias are given, as sq_step_args).
+ *             when a_log/dt_bias are given, as sq_step_args); KDA pools: g
+ *             [T, H, K], one log decay per key channel, dt_bias [H * K].
  *   out       [T, H, V], dtype out_dtype.
  *   cu_seqlens [batch + 1] int32 token offsets of the sequences.
  *   init_slots [batch] pages holding the initial states (slot <= 0: zero
@@ -192,7 +193,9 @@ int sq_writeback(const sq_pool *pool, const sq_writeback_scratch *scratch, int64
  *             sequence are unused and their slots must be <= 0).
  *   init_state      workspace [batch, H, K, V] f32;
  *   checkpoint_state workspace [batch * n_checkpoints, H, K, V] f32.
- * GDN pools with K = V = 128 and packed storage; chunks of 64 tokens.
+ * Pools with K = V = 128, packed or byte storage.  GDN: the chunked kernel
+ * (chunks of 64 tokens, bf16 MFMA).  KDA: a token-by-token kernel, one
+ * workgroup per (sequence, head) holding the state in registers.
  */
 typedef struct sq_prefill_args {
     const void *q;

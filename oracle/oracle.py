@@ -17,8 +17,9 @@ the reference repository):
 * ``decode_page``     kernels/fused.py:18-59 (``_read``), kernels/byte_codec.py:6-28
 * ``prepare``         kernels/fused.py:155-179 (``prepare_inputs_kernel``)
 * ``delta_step``      stepquant/core.py:5-15
-* ``prefill``         the token recurrence of core.py:5-15 (``delta_step``)
-                      applied to every token of a sequence, in float64, with
+* ``prefill``         the token recurrence of core.py:5-15 (``delta_step``,
+                      GDN or KDA) applied to every token of a sequence, in
+                      float64, with
                       the input preparation of kernels/fused.py:155-179; it is
                       the checker for the chunked prefill that replaces
                       sglang/runtime.py:193-202 (``kernel_extend``)
@@ -513,14 +514,17 @@ def _softplus20(u):
 
 def prefill(q, k, v, g, beta, state0, cu_seqlens, checkpoints=None, normalize=False, scale=1.0,
             a_log=None, dt_bias=None):
-    """Token-sequential GDN prefill in float64.
+    """Token-sequential GDN or KDA prefill in float64.
 
-    q, k: [T, HK, K]; v: [T, H, V]; g: [T, H] log decay (raw gate a when
-    a_log is given: g = -exp(a_log) softplus(a + dt_bias)); beta: [T, H]
-    (logits when a_log is given: beta = sigmoid(b)); state0: [B, H, K, V];
+    q, k: [T, HK, K]; v: [T, H, V]; g: [T, H] (GDN) or [T, H, K] (KDA,
+    per key channel) log decay, or the raw gate a when a_log is given:
+    g = -exp(a_log[h]) softplus(a + dt_bias) with dt_bias [H] (GDN) or
+    [H * K] (KDA); beta: [T, H] (logits when a_log is given: beta =
+    sigmoid(b)); state0: [B, H, K, V];
     cu_seqlens: [B + 1] token offsets; checkpoints: [B, NC] token counts
     after which the state is recorded (<= 0 or > length: unused).
-    Per token (core.py:5-15): S <- e^g S; delta = beta (v - S^T k);
+    Per token (core.py:5-15): S <- e^g S (KDA: row i scaled by e^{g_i});
+    delta = beta (v - S^T k);
     S <- S + k delta^T; o = S^T q, with q, k L2-normalised (eps 1e-6) and q
     scaled as kernels/fused.py:155-179 prepares them.
     Returns (out [T, H, V], states [B, NC, H, K, V], final [B, H, K, V]).
@@ -537,8 +541,13 @@ def prefill(q, k, v, g, beta, state0, cu_seqlens, checkpoints=None, normalize=Fa
         checkpoints = np.zeros((B, 0), np.int64)
     checkpoints = np.asarray(checkpoints).reshape(B, -1)
     NC = checkpoints.shape[1]
+    kda = g.ndim == 3
     if a_log is not None:
-        g = -np.exp(np.asarray(a_log, np.float64))[None, :] * _softplus20(g + np.asarray(dt_bias, np.float64)[None, :])
+        bias = np.asarray(dt_bias, np.float64)
+        bias = bias.reshape(H, K)[None] if kda else bias[None, :]
+        rate = np.exp(np.asarray(a_log, np.float64))
+        rate = rate[None, :, None] if kda else rate[None, :]
+        g = -rate * _softplus20(g + bias)
         beta = 1.0 / (1.0 + np.exp(-beta))
     head_of = np.arange(H) // (H // HK)
     out = np.zeros((T, H, V))
@@ -553,7 +562,7 @@ def prefill(q, k, v, g, beta, state0, cu_seqlens, checkpoints=None, normalize=Fa
                 qt = qt / np.sqrt((qt * qt).sum(-1, keepdims=True) + 1e-6)
                 kt = kt / np.sqrt((kt * kt).sum(-1, keepdims=True) + 1e-6)
             qt = qt * scale
-            S = S * np.exp(g[t])[:, None, None]
+            S = S * (np.exp(g[t])[:, :, None] if kda else np.exp(g[t])[:, None, None])
             delta = beta[t][:, None] * (v[t] - np.einsum("hk,hkv->hv", kt, S))
             S = S + kt[:, :, None] * delta[:, None, :]
             out[t] = np.einsum("hk,hkv->hv", qt, S)

@@ -3295,6 +3295,206 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
 
 }  // namespace pf
 
+// =====================================================================
+// KDA prefill (per-channel decay), token by token.  The recurrence of
+// stepquant/core.py:5-15 with the KDA log decay g_t in R^K applied to every
+// token of a sequence: S <- diag(e^{g_t}) S; delta = beta_t (v_t - S^T k_t);
+// S <- S + k_t delta^T; o_t = S^T q_t (q, k L2-normalised, q scaled), the
+// role of the upstream chunk kernel behind the reference's kernel_extend
+// (sglang/runtime.py:193-202) for Kimi-Linear pools.
+//
+// One workgroup of 512 threads per (sequence, head): thread (r, j) holds the
+// state column j for the 32 key rows 32 r .. 32 r + 31 in registers, so the
+// state never leaves the workgroup.  Tokens are staged 32 at a time into LDS
+// as fp32 rows (normalised k, q, the decays e^g and k e^g, v, beta), the next
+// block's raw inputs are fetched into registers while the current block
+// runs.  Per token: kd^T S partials over each thread's 32 rows, a barrier,
+// delta_j from the four row quarters, S = e^g S + k delta (one FMA per value
+// after the rank-1 product), q^T S partials, a barrier, one quarter writes
+// the outputs.  Every read of a token row in LDS is the same address across
+// a wave (all its lanes share r): broadcast, conflict-free.
+namespace kp {
+
+constexpr int NT = 512;
+constexpr int TB = 32;                        // tokens staged per block
+constexpr int KV = 128;                       // K = V = 128
+// LDS: per block row arrays [TB][128] f32: KD (k e^g), DC (e^g), KN (k), QN (q), VV (v);
+// BETA [TB]; partial sums [2][4][128]
+constexpr int OFF_KD = 0;
+constexpr int OFF_DC = OFF_KD + TB * KV;
+constexpr int OFF_KN = OFF_DC + TB * KV;
+constexpr int OFF_QN = OFF_KN + TB * KV;
+constexpr int OFF_VV = OFF_QN + TB * KV;
+constexpr int OFF_BT = OFF_VV + TB * KV;
+constexpr int OFF_P1 = OFF_BT + TB;
+constexpr int OFF_P2 = OFF_P1 + 4 * KV;
+constexpr int LDS_FLOATS = OFF_P2 + 4 * KV;
+constexpr int LDS_BYTES = LDS_FLOATS * 4;
+
+// Raw inputs of one staging thread for one block: token tt = tid >> 4,
+// channels c8 .. c8 + 7 (c8 = (tid & 15) * 8).
+struct Raw {
+  uint4 k, q, v;
+  float g[8];
+  float beta;
+};
+
+__device__ __forceinline__ void bf8(const uint4 &x, float o[8]) {
+  const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    o[2 * e] = __uint_as_float(w[e] << 16);
+    o[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+  }
+}
+
+// sum over the 16 lanes of a row (lanes 16 m .. 16 m + 15)
+__device__ __forceinline__ float sum16(float x) {
+  x += __shfl_xor(x, 1);
+  x += __shfl_xor(x, 2);
+  x += __shfl_xor(x, 4);
+  x += __shfl_xor(x, 8);
+  return x;
+}
+
+__global__ __launch_bounds__(NT) void kda_prefill_kernel(pf::PrefillDev D) {
+  extern __shared__ float lds[];
+  const int H = D.H;
+  const int h = blockIdx.x % H, b = blockIdx.x / H;
+  const int hk = h / (H / D.HK);
+  const int t0 = D.cu[b], len = D.cu[b + 1] - t0;
+  if (len <= 0) return;  // whole workgroup
+  const int tid = threadIdx.x;
+  const int j = tid & (KV - 1), r = tid >> 7;  // state column, row quarter (uniform per wave)
+  const int tt = tid >> 4, c8 = (tid & 15) * 8;  // staging: token of the block, first channel
+
+  float S[32];
+  {
+    const float *src = D.init + (((int64_t)b * H + h) * KV + 32 * r) * KV + j;
+#pragma unroll
+    for (int e = 0; e < 32; e++) S[e] = src[(int64_t)e * KV];
+  }
+  const float ea = D.a_log ? __expf(load_val(D.a_log, D.gate_dtype, h)) : 0.0f;
+  const uint8_t *qg = (const uint8_t *)D.q, *kg = (const uint8_t *)D.k, *vg = (const uint8_t *)D.v;
+
+  auto fetch = [&](Raw &R, int c) {  // block starting at token c; rows clamped into the sequence
+    const int tok = c + tt < len ? c + tt : len - 1;
+    const int64_t row = (int64_t)t0 + tok;
+    R.k = *(const uint4 *)(kg + (row * D.k_stride + (int64_t)hk * KV + c8) * 2);
+    R.q = *(const uint4 *)(qg + (row * D.q_stride + (int64_t)hk * KV + c8) * 2);
+    R.v = *(const uint4 *)(vg + (row * D.v_stride + (int64_t)h * KV + c8) * 2);
+    const int64_t gi = (row * H + h) * KV + c8;
+#pragma unroll
+    for (int e = 0; e < 8; e++) R.g[e] = load_val(D.g, D.gate_dtype, gi + e);
+    R.beta = load_val(D.beta, D.gate_dtype, row * H + h);
+  };
+
+  Raw R;
+  fetch(R, 0);
+  int ci = 0;  // next checkpoint index
+  for (int c0 = 0; c0 < len; c0 += TB) {
+    const int n = len - c0 < TB ? len - c0 : TB;
+    // ---- stage the fetched block (tokens past n: zero rows)
+    {
+      float kf[8], qf[8], vf[8];
+      bf8(R.k, kf);
+      bf8(R.q, qf);
+      bf8(R.v, vf);
+      float sk = 0.f, sq = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        sk = fmaf(kf[e], kf[e], sk);
+        sq = fmaf(qf[e], qf[e], sq);
+      }
+      sk = sum16(sk);
+      sq = sum16(sq);
+      const bool live = tt < n;
+      const float nk = D.normalize ? 1.0f / __builtin_sqrtf(sk + 1e-6f) : 1.0f;
+      const float nq = (D.normalize ? 1.0f / __builtin_sqrtf(sq + 1e-6f) : 1.0f) * D.scale;
+      float *kd = lds + OFF_KD + tt * KV + c8, *dc = lds + OFF_DC + tt * KV + c8;
+      float *kn = lds + OFF_KN + tt * KV + c8, *qn = lds + OFF_QN + tt * KV + c8;
+      float *vv = lds + OFF_VV + tt * KV + c8;
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        float gv = R.g[e];
+        if (D.a_log) {
+          const float u = gv + load_val(D.dt_bias, D.gate_dtype, (int64_t)h * KV + c8 + e);
+          const float sp = u > 20.0f ? u : __logf(1.0f + __expf(u < 20.0f ? u : 20.0f));
+          gv = -ea * sp;
+        }
+        const float d = __expf(gv);
+        const float k = live ? kf[e] * nk : 0.0f;
+        kd[e] = k * d;
+        dc[e] = live ? d : 1.0f;
+        kn[e] = k;
+        qn[e] = live ? qf[e] * nq : 0.0f;
+        vv[e] = live ? vf[e] : 0.0f;
+      }
+      if ((tid & 15) == 0) {
+        float bt = R.beta;
+        if (D.a_log) bt = 1.0f / (1.0f + __expf(-bt));
+        lds[OFF_BT + tt] = live ? bt : 0.0f;
+      }
+    }
+    __syncthreads();
+    if (c0 + TB < len) fetch(R, c0 + TB);  // in flight during this block's tokens
+    float *p1 = lds + OFF_P1, *p2 = lds + OFF_P2;
+    for (int u = 0; u < n; u++) {
+      const float4 *kd4 = (const float4 *)(lds + OFF_KD + u * KV + 32 * r);
+      float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const float4 w = kd4[e];
+        a0 = fmaf(w.x, S[4 * e], a0);
+        a1 = fmaf(w.y, S[4 * e + 1], a1);
+        a0 = fmaf(w.z, S[4 * e + 2], a0);
+        a1 = fmaf(w.w, S[4 * e + 3], a1);
+      }
+      p1[r * KV + j] = a0 + a1;
+      __syncthreads();
+      const float ks = (p1[j] + p1[KV + j]) + (p1[2 * KV + j] + p1[3 * KV + j]);
+      const float delta = lds[OFF_BT + u] * (lds[OFF_VV + u * KV + j] - ks);
+      const float4 *dc4 = (const float4 *)(lds + OFF_DC + u * KV + 32 * r);
+      const float4 *kn4 = (const float4 *)(lds + OFF_KN + u * KV + 32 * r);
+      const float4 *qn4 = (const float4 *)(lds + OFF_QN + u * KV + 32 * r);
+      float o0 = 0.f, o1 = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const float4 d = dc4[e], k = kn4[e], q = qn4[e];
+        S[4 * e] = fmaf(d.x, S[4 * e], k.x * delta);
+        S[4 * e + 1] = fmaf(d.y, S[4 * e + 1], k.y * delta);
+        S[4 * e + 2] = fmaf(d.z, S[4 * e + 2], k.z * delta);
+        S[4 * e + 3] = fmaf(d.w, S[4 * e + 3], k.w * delta);
+        o0 = fmaf(q.x, S[4 * e], o0);
+        o1 = fmaf(q.y, S[4 * e + 1], o1);
+        o0 = fmaf(q.z, S[4 * e + 2], o0);
+        o1 = fmaf(q.w, S[4 * e + 3], o1);
+      }
+      p2[r * KV + j] = o0 + o1;
+      __syncthreads();
+      if (r == 0) {
+        const float o = (p2[j] + p2[KV + j]) + (p2[2 * KV + j] + p2[3 * KV + j]);
+        store_val(D.out, D.out_dtype, ((int64_t)(t0 + c0 + u) * H + h) * KV + j, o);
+      }
+      // checkpoints reached after this token (token counts, ascending)
+      const int done = c0 + u + 1;
+      while (ci < D.NC) {
+        const int p = D.ckpt[(int64_t)b * D.NC + ci];
+        if (p > done && p <= len) break;
+        if (p == done) {
+          float *dst = D.ck_state + ((((int64_t)b * D.NC + ci) * H + h) * KV + 32 * r) * KV + j;
+#pragma unroll
+          for (int e = 0; e < 32; e++) dst[(int64_t)e * KV] = S[e];
+        }
+        ci++;
+      }
+    }
+    __syncthreads();  // the next block's staging overwrites the token rows
+  }
+}
+
+}  // namespace kp
+
 
 __global__ void fill_zero_kernel(float *p, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) p[i] = 0.0f;
@@ -4307,9 +4507,8 @@ int sq_prefill(const sq_pool *pool, const sq_prefill_args *a, void *stream) {
   int rc = validate_pool(pool);
   if (rc) return rc;
   if (!a) return fail(SQ_EINVAL, "prefill: null arguments");
-  if (pool->kda || pool->keys != 128 || pool->values != 128)
-    return fail(SQ_ESHAPE, "prefill: the chunked kernel handles GDN pools with K = V = 128");
-  if (pool->storage != 0) return fail(SQ_ESTORAGE, "prefill: packed storage only");
+  if (pool->keys != 128 || pool->values != 128)
+    return fail(SQ_ESHAPE, "prefill: the prefill kernels handle pools with K = V = 128");
   if (a->batch < 0 || a->n_checkpoints < 0) return fail(SQ_EINVAL, "prefill: negative batch or checkpoint count");
   if (a->batch == 0) return 0;
   if (!a->q || !a->k || !a->v || !a->g || !a->beta || !a->out || !a->cu_seqlens || !a->init_state)
@@ -4368,11 +4567,19 @@ int sq_prefill(const sq_pool *pool, const sq_prefill_args *a, void *stream) {
   D.out_dtype = a->out_dtype;
   D.normalize = a->normalize;
   D.scale = a->scale;
-  hipError_t e = hipFuncSetAttribute((const void *)pf::prefill_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                     pf::LDS_BYTES);
-  if (e != hipSuccess) return fail((int)e, "prefill: cannot raise the kernel's LDS limit");
-  hipLaunchKernelGGL(pf::prefill_kernel, dim3((unsigned)(a->batch * H)), dim3(pf::NT), pf::LDS_BYTES, st, D);
-  rc = check_launch("prefill_kernel");
+  if (pool->kda) {
+    hipError_t e = hipFuncSetAttribute((const void *)kp::kda_prefill_kernel,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, kp::LDS_BYTES);
+    if (e != hipSuccess) return fail((int)e, "prefill: cannot raise the KDA kernel's LDS limit");
+    hipLaunchKernelGGL(kp::kda_prefill_kernel, dim3((unsigned)(a->batch * H)), dim3(kp::NT), kp::LDS_BYTES, st, D);
+    rc = check_launch("kda_prefill_kernel");
+  } else {
+    hipError_t e = hipFuncSetAttribute((const void *)pf::prefill_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       pf::LDS_BYTES);
+    if (e != hipSuccess) return fail((int)e, "prefill: cannot raise the kernel's LDS limit");
+    hipLaunchKernelGGL(pf::prefill_kernel, dim3((unsigned)(a->batch * H)), dim3(pf::NT), pf::LDS_BYTES, st, D);
+    rc = check_launch("prefill_kernel");
+  }
   if (rc) return rc;
   if (a->n_checkpoints > 0)
     return sq_encode(pool, a->checkpoint_state, a->slots, a->slots_dtype, a->batch * a->n_checkpoints, stream);

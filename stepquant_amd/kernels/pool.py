@@ -19,6 +19,7 @@ adapter can use it unchanged.  All arithmetic runs in the HIP kernels of
 """
 from __future__ import annotations
 
+import numpy as np
 import torch
 
 from .. import _native as N
@@ -359,8 +360,9 @@ class PackedStatePool:
         The behaviour of the serving adapter's ``kernel_extend``
         (reference sglang/runtime.py:193-202: decode the slots' states, run
         the chunked recurrence, encode the final states back) in one call:
-        q, k ``[T, HK*K]`` (or ``[..., T, HK, K]``), v ``[T, H*V]``, g, beta
-        ``[T, H]`` (raw gate and logits with ``a_log``/``dt_bias``),
+        q, k ``[T, HK*K]`` (or ``[..., T, HK, K]``), v ``[T, H*V]``, g
+        ``[T, H]`` (KDA: ``[T, H, K]``, per key channel), beta ``[T, H]``
+        (raw gate and logits with ``a_log``/``dt_bias``),
         ``cu_seqlens`` ``[B+1]`` token offsets, ``slots`` ``[B]``.  Initial
         states come from ``init_slots`` (default ``slots``; ``None`` entries
         or slot <= 0 start from zero).  By default the final state is written
@@ -370,8 +372,9 @@ class PackedStatePool:
         must start at 0 and never decrease (ValueError otherwise).  Returns the outputs ``[T, H, V]`` in q's dtype.
         """
         self.wait()
-        if self.plan.architecture != "gdn" or self.keys != 128 or self.values != 128:
-            raise ValueError("chunked prefill handles GDN pools with K = V = 128")
+        if self.keys != 128 or self.values != 128:
+            raise ValueError("prefill handles pools with K = V = 128")
+        kda = self.plan.architecture == "kda"
         dev = self.device
         cu_host = None
         if isinstance(cu_seqlens, torch.Tensor) and cu_seqlens.device.type != "cpu":
@@ -412,12 +415,14 @@ class PackedStatePool:
             qkv.append(t)
         q2, k2, v2 = qkv
         gate_dtype = torch.float32 if g.dtype == torch.float64 else g.dtype
-        g2 = g.reshape(total, self.heads).to(gate_dtype).contiguous()
+        g2 = g.reshape(total, self.heads * (self.keys if kda else 1)).to(gate_dtype).contiguous()
         b2 = beta.reshape(total, self.heads).to(gate_dtype).contiguous()
         al = None if a_log is None else a_log.to(gate_dtype).contiguous()
         db = None if dt_bias is None else dt_bias.to(gate_dtype).contiguous()
         if (al is None) != (db is None):
             raise ValueError("a_log and dt_bias go together")
+        if al is not None and (al.numel() != self.heads or db.numel() != self.heads * (self.keys if kda else 1)):
+            raise ValueError("a_log must be [heads] and dt_bias [heads] (GDN) or [heads*key] (KDA)")
         on_host = cu_host is not None and checkpoints is not None and all(
             not isinstance(t, torch.Tensor) or t.device.type == "cpu" for t in (checkpoints, checkpoint_slots))
         if on_host:
@@ -430,10 +435,13 @@ class PackedStatePool:
                 raise ValueError("one slot per checkpoint")
             lengths_h = (cu_host[1:] - cu_host[:-1]).reshape(batch, 1)
             used = (ck_h > 0) & (ck_h <= lengths_h)
-            for row, mask in zip(ck_h, used):
-                kept = row[mask]
-                if (kept[1:] < kept[:-1]).any():
-                    raise ValueError("checkpoints of a sequence must be ascending")
+            # used positions must not decrease along a row: each one is at
+            # least the largest used position before it (numpy: host work
+            # here is on the step's critical path)
+            ck_n, used_n = ck_h.numpy(), used.numpy()
+            seen = np.maximum.accumulate(np.where(used_n, ck_n, 0), axis=1)
+            if (used_n[:, 1:] & (ck_n[:, 1:] < seen[:, :-1])).any():
+                raise ValueError("checkpoints of a sequence must be ascending")
             cs_h = torch.where(used, cs_h, torch.zeros_like(cs_h))
             ck = ck_h.contiguous().pin_memory().to(dev, non_blocking=True)
             ck_slots = cs_h.contiguous().pin_memory().to(dev, non_blocking=True)

@@ -3,7 +3,8 @@
 The reference adapter's ``kernel_extend`` (sglang/runtime.py:193-202) decodes
 the active slots into a V-first fp32 state, runs SGLang's chunk kernel on it
 and encodes the states back.  For pools whose prefill this package runs
-natively (``PackedStatePool.extend``: GDN, K = V = 128, packed pages) this hook
+natively (``PackedStatePool.extend``: GDN or KDA, K = V = 128, packed or
+byte pages) this hook
 replaces that round trip with one chunked-prefill call that reads the
 initial states from the pages and writes the final states into them; other
 pools keep the round trip.  Registering it in place of the reference's
@@ -22,8 +23,7 @@ from ..kernels.pool import PackedStatePool
 
 def fused(pool) -> bool:
     """Whether ``pool``'s prefill runs in ``PackedStatePool.extend``."""
-    return (type(pool) is PackedStatePool and pool.plan.architecture == "gdn" and pool.keys == 128
-            and pool.values == 128 and pool.storage == "packed")
+    return type(pool) is PackedStatePool and pool.keys == 128 and pool.values == 128
 
 
 def kernel_extend(original, self, q, k, v, g, beta, *, ssm_states, cache_indices, query_start_loc, **kwargs):

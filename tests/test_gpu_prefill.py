@@ -121,3 +121,74 @@ def test_extend_defaults_write_final_state_back_to_the_slots():
     got = pool.data.cpu().numpy()
     assert np.array_equal(got[slots.numpy()], ref_pages[slots.numpy()])
     assert len(lens) == 2
+
+
+@pytest.mark.parametrize("arch,storage,raw", [("kda", "packed", False), ("kda", "packed", True),
+                                              ("kda", "byte", True), ("gdn", "byte", False)])
+def test_prefill_kda_and_byte_pages(arch, storage, raw):
+    """KDA pools (per-channel decay, token-by-token kernel) and byte-carrier
+    pages go through the same extend: outputs and checkpoint states against
+    the float64 recurrence, checkpoint pages equal to the oracle encoding
+    of the kernel's states."""
+    print(f"case {arch} {storage} raw={raw}", flush=True)
+    from stepquant_amd.kernels.pool import PackedStatePool
+    H, HK, K, V = 4, 2 if arch == "gdn" else 4, 128, 128
+    lens = [97, 40, 33]
+    B = len(lens)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    T = int(cu[-1])
+    rng = np.random.default_rng(5)
+    if arch == "kda":
+        bits = np.where(rng.random((H, K)) < .03, 16, rng.choice([2, 4, 6, 8], (H, K)))
+    else:
+        bits = np.repeat(np.array([6, 2, 8, 16])[:, None], K, 1)
+    oplan = make_plan(arch, bits, seed=3)
+    stream = torch.cuda.Stream() if storage == "byte" else None
+    pool = PackedStatePool(device_plan(oplan), 12, V, writeback_stream=stream, storage=storage)
+    g = torch.Generator().manual_seed(17)
+    q = torch.randn(T, HK, K, generator=g).to(torch.bfloat16)
+    k = torch.randn(T, HK, K, generator=g).to(torch.bfloat16)
+    v = torch.randn(T, H, V, generator=g).to(torch.bfloat16)
+    gshape = (T, H, K) if arch == "kda" else (T, H)
+    if raw:
+        gate = torch.randn(gshape, generator=g) * .5
+        beta = torch.randn(T, H, generator=g)
+        a_log = torch.randn(H, generator=g) * .3
+        dt_bias = torch.randn(H * K if arch == "kda" else H, generator=g) * .3
+    else:
+        gate = -torch.nn.functional.softplus(torch.randn(gshape, generator=g) * (.5 if arch == "kda" else 1.))
+        beta = torch.sigmoid(torch.randn(T, H, generator=g))
+        a_log = dt_bias = None
+    init = torch.tensor([3, 0, 5])
+    pool.encode((torch.randn(B, H, K, V, generator=g) * .1).to(dev()), init.to(dev()))
+    pool.wait()
+    lay = O.layout(oplan, V, storage)
+    pages0 = pool.data.cpu().numpy()
+    S0 = O.decode_page(pages0, init.numpy(), oplan, lay, V, storage).astype(np.float64)
+    ck = np.array([[50, 97], [40, 0], [10, 33]])
+    ck_slots = torch.tensor([[6, 7], [8, 0], [9, 10]])
+    out = pool.extend(q.to(dev()), k.to(dev()), v.to(dev()), gate.to(dev()), beta.to(dev()),
+                      torch.tensor([3, 4, 5]), torch.from_numpy(cu), checkpoints=torch.from_numpy(ck),
+                      checkpoint_slots=ck_slots, init_slots=init, normalize=True, scale=K ** -.5,
+                      a_log=None if a_log is None else a_log.to(dev()),
+                      dt_bias=None if dt_bias is None else dt_bias.to(dev()))
+    torch.cuda.synchronize()
+    ref_out, ref_states, _ = O.prefill(q.float().numpy(), k.float().numpy(), v.float().numpy(), gate.numpy(),
+                                       beta.numpy(), S0, cu, ck, normalize=True, scale=K ** -.5,
+                                       a_log=None if a_log is None else a_log.numpy(),
+                                       dt_bias=None if dt_bias is None else dt_bias.numpy())
+    ck_state = pool._last_prefill[-1].cpu().numpy().reshape(B, 2, H, K, V)
+    for b in range(B):
+        for c in range(2):
+            if ck_slots[b, c] > 0:
+                _close(ck_state[b, c], ref_states[b, c], 1e-3, f"state b={b} c={c}")
+    assert out.dtype == torch.bfloat16
+    _close(out.float().cpu().numpy(), ref_out, 2 ** -8 + 1e-3, "bf16 outputs")
+    pages = pool.data.cpu().numpy()
+    live = ck_slots.numpy().reshape(-1)
+    ref_pages = pages0.copy()
+    O.encode_page(ck_state.reshape(B * 2, H, K, V), live, oplan, lay, ref_pages, storage)
+    for s in live[live > 0]:
+        assert np.array_equal(pages[s], ref_pages[s]), f"slot {s} page differs"
+    for s in (1, 2, 11):
+        assert not pages[s].any(), "untouched slots stay empty"

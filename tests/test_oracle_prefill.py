@@ -110,3 +110,82 @@ def test_no_write_strength_only_decays():
     S0 = rng.standard_normal((1, H, K, V))
     _, _, final = O.prefill(q, k, v, g, np.zeros_like(beta), S0, np.array([0, T]))
     np.testing.assert_allclose(final[0], S0[0] * np.exp(g.sum(0))[:, None, None], rtol=1e-12)
+
+
+def _kda_gates(rng, T, H, K):
+    return -np.log1p(np.exp(rng.standard_normal((T, H, K)) * .5))
+
+
+@pytest.mark.parametrize("raw", [False, True])
+def test_kda_single_token_equals_delta_step(raw):
+    """Per-channel decay: one token of the prefill is core.py:5-15 with the
+    KDA log decay [B, H, K] (each key row of the state decays on its own)."""
+    rng = np.random.default_rng(3)
+    H, HK, K, V, B = 4, 4, 16, 8, 3
+    q, k, v, _, beta = (x.astype(np.float32) for x in _inputs(rng, B, H, HK, K, V))
+    g = _kda_gates(rng, B, H, K).astype(np.float32)
+    state = (rng.standard_normal((B, H, K, V)) * .3).astype(np.float32)
+    a_log = rng.standard_normal(H).astype(np.float32) if raw else None
+    dt_bias = rng.standard_normal(H * K).astype(np.float32) if raw else None
+    cu = np.arange(B + 1)
+    out, _, final = O.prefill(q, k, v, g, beta, state, cu, normalize=True, scale=K ** -.5,
+                              a_log=a_log, dt_bias=dt_bias)
+    qp, kp, ld, bo = O.prepare(q.reshape(B, -1), k.reshape(B, -1), g.reshape(B, -1), beta, H, K, True, True,
+                               K ** -.5, a_log, dt_bias)
+    assert ld.shape == (B, H, K)
+    ref_out, ref_state = O.delta_step(state, qp, kp, v, ld, bo)
+    np.testing.assert_allclose(out, ref_out, rtol=2e-5, atol=2e-6)
+    np.testing.assert_allclose(final, ref_state, rtol=2e-5, atol=2e-6)
+
+
+def _kda_chunk_closed_form(q, k, v, g, beta, S0):
+    """One chunk of the KDA recurrence in closed (WY) form, written from the
+    algebra, not from the oracle: with G_t = sum_{s<=t} g_s per channel,
+    A_ts = beta_t sum_i k_ti k_si e^{G_ti - G_si} (s < t), T = (I + A)^-1,
+    Delta = T beta (V - (K o e^G) S0), S_C = e^{G_C} o S0 + (K o e^{G_C - G})^T Delta,
+    O = (Q o e^G) S0 + (M o (Q o e^G)(K o e^-G)^T) Delta, M causal incl. the diagonal.
+    q, k: [C, K]; v: [C, V]; g: [C, K]; beta: [C]; S0: [K, V]."""
+    C = q.shape[0]
+    G = np.cumsum(g, 0)
+    A = np.zeros((C, C))
+    for t in range(C):
+        for s in range(t):
+            A[t, s] = beta[t] * np.sum(k[t] * k[s] * np.exp(G[t] - G[s]))
+    Tm = np.linalg.inv(np.eye(C) + A)
+    delta = Tm @ (beta[:, None] * (v - (k * np.exp(G)) @ S0))
+    SC = np.exp(G[-1])[:, None] * S0 + (k * np.exp(G[-1] - G)).T @ delta
+    P = np.zeros((C, C))
+    for t in range(C):
+        for s in range(t + 1):
+            P[t, s] = np.sum(q[t] * k[s] * np.exp(G[t] - G[s]))
+    out = (q * np.exp(G)) @ S0 + P @ delta
+    return out, SC
+
+
+@pytest.mark.parametrize("C", [1, 5, 16])
+def test_kda_prefill_equals_closed_form_chunk(C):
+    rng = np.random.default_rng(C)
+    H, HK, K, V = 2, 2, 8, 6
+    q, k, v, _, beta = _inputs(rng, C, H, HK, K, V)
+    g = _kda_gates(rng, C, H, K)
+    S0 = rng.standard_normal((1, H, K, V)) * .3
+    out, _, final = O.prefill(q, k, v, g, beta, S0, np.array([0, C]))
+    for h in range(H):
+        ref_out, ref_S = _kda_chunk_closed_form(q[:, h], k[:, h], v[:, h], g[:, h], beta[:, h], S0[0, h])
+        np.testing.assert_allclose(out[:, h], ref_out, rtol=1e-10, atol=1e-12)
+        np.testing.assert_allclose(final[0, h], ref_S, rtol=1e-10, atol=1e-12)
+
+
+def test_kda_checkpoint_is_the_prefix_state():
+    rng = np.random.default_rng(11)
+    H, HK, K, V, T = 2, 1, 8, 4, 40
+    q, k, v, _, beta = _inputs(rng, T, H, HK, K, V)
+    g = _kda_gates(rng, T, H, K)
+    S0 = rng.standard_normal((1, H, K, V)) * .2
+    out, states, final = O.prefill(q, k, v, g, beta, S0, np.array([0, T]), checkpoints=np.array([[17, T]]))
+    o1, _, mid = O.prefill(q[:17], k[:17], v[:17], g[:17], beta[:17], S0, np.array([0, 17]))
+    o2, _, end = O.prefill(q[17:], k[17:], v[17:], g[17:], beta[17:], mid, np.array([0, T - 17]))
+    np.testing.assert_allclose(states[0, 0], mid[0], rtol=1e-12, atol=1e-14)
+    np.testing.assert_allclose(states[0, 1], final[0], rtol=1e-12, atol=1e-14)
+    np.testing.assert_allclose(end, final, rtol=1e-12, atol=1e-14)
+    np.testing.assert_allclose(np.concatenate([o1, o2]), out, rtol=1e-12, atol=1e-14)
