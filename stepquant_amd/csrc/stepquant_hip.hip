@@ -160,8 +160,8 @@ __device__ __forceinline__ int stage_in(const uint8_t *gstart, int64_t nbytes, u
 
 // Write LDS back to [gstart, gstart + nbytes): whole 16-byte chunks inside
 // the region use 16-byte stores, edge chunks store only the region's 2-byte
-// units.  `lds` is the staged window as returned by stage_in (global byte a
-// lives at lds + (a - floor16(gstart))).
+// units (from one 16-byte LDS read).  `lds` is the staged window as returned
+// by stage_in (global byte a lives at lds + (a - floor16(gstart))).
 __device__ __forceinline__ void stage_out(uint8_t *gstart, int64_t nbytes, const uint8_t *lds, int tid,
                                           int nthreads) {
   const int shift = (int)((uintptr_t)gstart & 15);
@@ -170,12 +170,15 @@ __device__ __forceinline__ void stage_out(uint8_t *gstart, int64_t nbytes, const
   const int n16 = (int)((end + 15) >> 4);
   for (int c = tid; c < n16; c += nthreads) {
     const int64_t a = 16 * (int64_t)c;
+    const uint4 v = ((const uint4 *)lds)[c];
     if (a >= shift && a + 16 <= end) {
-      *(uint4 *)(w16 + a) = ((const uint4 *)lds)[c];
+      *(uint4 *)(w16 + a) = v;
     } else {
+      const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
       for (int u = 0; u < 8; u++) {
         const int64_t b = a + 2 * u;
-        if (b >= shift && b + 2 <= end) *(uint16_t *)(w16 + b) = *(const uint16_t *)(lds + b);
+        if (b >= shift && b + 2 <= end) *(uint16_t *)(w16 + b) = (uint16_t)(wv[u >> 1] >> (16 * (u & 1)));
       }
     }
   }
@@ -2172,9 +2175,9 @@ struct KCtx {
   float *qraw, *kraw, *wv, *gv, *misc, *red, *ks, *qs;
   float4 *rc;   // per row: k*a, q*a, a, a  (zeros for pivot rows)
   float4 *rl;   // per row: L, 1/L, 1/(r' norm), w^2 r'^2 norm^2 (zeros for pivots)
-  int4 *rm;     // per row: byte position within a block, width (0: pivot), top-bit mask, tile bytes
+  int4 *rm;     // per row: byte position within a block, width w (0: pivot), 2w, 3w
+  int4 *rk;     // per row: top-bit mask, tile byte mask, L + 1/2, 2L + 1/2 (float bits; zeros for pivots)
   uint32_t *pmask;  // 128-bit mask of pivot rows
-  uint8_t *spare;   // 4 bytes per lane: target of masked-off byte stores
   int b, h, tid, rg, cg, wave, j0;
   int code_start, code_bytes, row_start, row_bytes, colbase, stride;
 };
@@ -2194,13 +2197,17 @@ __host__ __device__ __forceinline__ int block_pitch(int stride) {
 __device__ __forceinline__ void stage_blocks_async(const uint8_t *g0, int stride, int pitch, uint8_t *lds, int tid) {
   const int nc = block_chunks(stride);
   const int gmod = (int)((uintptr_t)g0 & 15);
-  const int lane = tid & 63, w = tid >> 6;
+  // the wave index in a scalar register: block addresses are wave-uniform
+  const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   for (int c0 = 0; c0 < nc; c0 += 64) {
 #pragma unroll
     for (int bb = 0; bb < 8; bb++) {
       const int blk = 8 * w + bb;
       const int off = blk * stride;
-      const uint4 *src = (const uint4 *)(g0 + (off - ((gmod + off) & 15))) + c0 + lane;
+      const uintptr_t bs = (uintptr_t)(g0 + (off - ((gmod + off) & 15)));
+      const uint8_t *block = (const uint8_t *)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(bs >> 32)) << 32) |
+                                               (uint32_t)__builtin_amdgcn_readfirstlane((int)bs));
+      const uint4 *src = (const uint4 *)(block + 16u * (uint32_t)(c0 + lane));
       if (c0 + lane < nc)
         __builtin_amdgcn_global_load_lds((gptr_t)src, (lptr_t)(lds + blk * pitch + 16 * c0), 16, 0, 0);
     }
@@ -2221,8 +2228,9 @@ __device__ __forceinline__ int stage_region_async(const uint8_t *gstart, int64_t
 }
 
 // Write the staged blocks back: per block, 16-byte chunks inside the block
-// with one store, the chunks at its two edges in 2-byte units (block bounds
-// are even; neighbouring blocks write the other units of shared chunks).
+// with one store, the chunks at its two edges in 2-byte units from one LDS
+// read (block bounds are even; neighbouring blocks write the other units of
+// shared chunks).
 __device__ __forceinline__ void stage_out_blocks(uint8_t *g0, int stride, int pitch, const uint8_t *lds, int tid) {
   const int nc = block_chunks(stride);
   const int gmod = (int)((uintptr_t)g0 & 15);
@@ -2232,16 +2240,26 @@ __device__ __forceinline__ void stage_out_blocks(uint8_t *g0, int stride, int pi
     const int sb = (gmod + off) & 15;
     uint8_t *w = g0 + (off - sb);
     const int a = 16 * ch;
-    const uint8_t *l = lds + blk * pitch + a;
+    const uint4 v = *(const uint4 *)(lds + blk * pitch + a);
     if (a >= sb && a + 16 <= sb + stride) {
-      *(uint4 *)(w + a) = *(const uint4 *)l;
+      *(uint4 *)(w + a) = v;
     } else if (a < sb + stride && a + 16 > sb) {
+      const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
       for (int u = 0; u < 8; u++) {
         const int bb = a + 2 * u;
-        if (bb >= sb && bb + 2 <= sb + stride) *(uint16_t *)(w + bb) = *(const uint16_t *)(l + 2 * u);
+        if (bb >= sb && bb + 2 <= sb + stride) *(uint16_t *)(w + bb) = (uint16_t)(wv[u >> 1] >> (16 * (u & 1)));
       }
     }
   }
+}
+
+// LDS dwords at address a and a + 4: keep the bits outside `mask`, set those of
+// `bits` (bits within mask), each dword as one atomic read-modify-write
+__device__ __forceinline__ void lds_mskor2(uint32_t a, uint64_t mask, uint64_t bits) {
+  asm volatile("ds_mskor_b32 %0, %1, %2\n\tds_mskor_b32 %0, %3, %4 offset:4" ::"v"(a), "v"((uint32_t)mask),
+               "v"((uint32_t)bits), "v"((uint32_t)(mask >> 32)), "v"((uint32_t)(bits >> 32))
+               : "memory");
 }
 
 // sign-extended field of run-time width w at bit offset o
@@ -2253,6 +2271,17 @@ __device__ __forceinline__ int sbfe(uint32_t word, uint32_t o, uint32_t w) {
 __device__ __forceinline__ uint32_t word_at(const uint8_t *lds, int p) {
   const uint32_t *w = (const uint32_t *)(lds + (p & ~3));
   return __builtin_amdgcn_alignbit(w[1], w[0], (uint32_t)(p & 3) * 8u);
+}
+
+typedef __attribute__((address_space(3))) const uint32_t lds_word_t;
+
+// LDS address of a byte of the dynamic shared window
+__device__ __forceinline__ uint32_t lds_addr(const uint8_t *p) { return (uint32_t)(uintptr_t)(lptr_t)p; }
+
+// the 32 bits starting at LDS byte address a (alignbit takes the shift mod 32)
+__device__ __forceinline__ uint32_t word_at_addr(uint32_t a) {
+  lds_word_t *w = (lds_word_t *)(uintptr_t)(a & ~3u);
+  return __builtin_amdgcn_alignbit(w[1], w[0], a << 3);
 }
 
 // Per-row constants (threads 0..127, row i = tid), the pivot-row mask and
@@ -2280,6 +2309,7 @@ __device__ __forceinline__ void row_setup(const PoolDev &P, const StepDev &S, co
       C.rc[i] = make_float4(0.f, 0.f, 0.f, 0.f);
       C.rl[i] = make_float4(0.f, 0.f, 0.f, 0.f);
       C.rm[i] = make_int4(pos, 0, 0, 0);  // width 0: no code fields
+      C.rk[i] = make_int4(0, 0, 0, 0);
     } else {
       const int L = (1 << (bi - 1)) - 1;
       const float norm = (float)(1 << (8 - bi));
@@ -2292,7 +2322,9 @@ __device__ __forceinline__ void row_setup(const PoolDev &P, const StepDev &S, co
       uint32_t xm = 0;
 #pragma unroll
       for (int c = 0; c < 4; c++) xm |= 1u << (c * bi + bi - 1);
-      C.rm[i] = make_int4(pos, bi, (int)xm, bi / 2);
+      C.rm[i] = make_int4(pos, bi, 2 * bi, 3 * bi);
+      C.rk[i] = make_int4((int)xm, (int)(0xffffffffu >> (32 - 4 * bi)), __float_as_int((float)L + 0.5f),
+                          __float_as_int(2.0f * (float)L + 0.5f));
     }
     const uint64_t pb = __ballot(piv);
     if ((i & 63) == 0) {
@@ -2351,6 +2383,7 @@ __device__ __forceinline__ void body(const PoolDev &P, const StepDev &S, KCtx &C
   const uint64_t pm_hi = ((uint64_t)__builtin_amdgcn_readfirstlane(C.pmask[3]) << 32) |
                         (uint32_t)__builtin_amdgcn_readfirstlane(C.pmask[2]);
   const int base = C.lbase;
+  const uint32_t cb = lds_addr(C.code) + (uint32_t)base;  // this lane's block
 
   // ---- foreground: signed code fields s = code - 2^(b-1) (z = s + 1)
   float cf[FRPT][4];
@@ -2360,10 +2393,12 @@ __device__ __forceinline__ void body(const PoolDev &P, const StepDev &S, KCtx &C
     if ((r % KDA_SCHED_ROWS) == KDA_SCHED_ROWS - 1) __builtin_amdgcn_sched_barrier(0);
     const int i = C.rg + 8 * r;
     const int4 m = C.rm[i];
-    const uint32_t word = word_at(C.code, m.x + base) ^ (uint32_t)m.z;
+    const uint32_t word = word_at_addr(cb + (uint32_t)m.x) ^ (uint32_t)C.rk[i].x;
     const uint32_t w = (uint32_t)m.y;
-#pragma unroll
-    for (int c = 0; c < 4; c++) cf[r][c] = (float)sbfe(word, c * w, w);
+    cf[r][0] = (float)sbfe(word, 0, w);
+    cf[r][1] = (float)sbfe(word, w, w);
+    cf[r][2] = (float)sbfe(word, (uint32_t)m.z, w);
+    cf[r][3] = (float)sbfe(word, (uint32_t)m.w, w);
     if (MODE != MODE_WRITE) {
       const float4 rc = C.rc[i];
 #pragma unroll
@@ -2373,19 +2408,29 @@ __device__ __forceinline__ void body(const PoolDev &P, const StepDev &S, KCtx &C
       }
     }
   }
+  // the readout sums (so every row's code fields) complete here: the
+  // compiler would otherwise sink the last rows' field extraction past the
+  // pivot loop and keep their code words (spilled) across it
+  if (MODE != MODE_WRITE) {
+#pragma unroll
+    for (int c = 0; c < 4; c++) asm volatile("" : "+v"(aK[c]), "+v"(aQ[c]));
+  } else {
+#pragma unroll
+    for (int r = 0; r < FRPT; r++)
+#pragma unroll
+      for (int c = 0; c < 4; c++) asm volatile("" : "+v"(cf[r][c]));
+  }
   // Per-column work runs once per column: row-group lanes 2c, 2c + 1 finish
   // column c of their four (reduce-scatter), results come back by swizzle.
   const int cl = C.rg >> 1;
   const float cjc = has_cols ? hw_h2f(*(const uint16_t *)(C.cst + C.shift_col + 2 * (C.j0 + cl))) : 1.0f;
   const bool pivots = (pm_lo | pm_hi) != 0;  // wave-uniform
-  float delta[4], dj[4];  // delta (for pivot rows) and delta / c
+  float dj[4];            // delta / c per column
+  float dlc = 0.0f;       // this lane's column delta (the pivot rows' update)
   if (MODE == MODE_WRITE) {
     const int64_t bi = ((int64_t)C.b * P.H + C.h) * FV + C.j0;
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-      delta[c] = S.s_delta[bi + c];
-      dj[c] = delta[c] * rcp(cj[c]);
-    }
+    for (int c = 0; c < 4; c++) dj[c] = S.s_delta[bi + c] * rcp(cj[c]);
   } else {
     // pivot rows owned by this lane (row % 8 == rg)
     float pK[4] = {0.f, 0.f, 0.f, 0.f}, pQ[4] = {0.f, 0.f, 0.f, 0.f};
@@ -2422,12 +2467,7 @@ __device__ __forceinline__ void body(const PoolDev &P, const StepDev &S, KCtx &C
     dj[1] = from_col<1>(djc);
     dj[2] = from_col<2>(djc);
     dj[3] = from_col<3>(djc);
-    if (pivots) {
-      delta[0] = from_col<0>(dl);
-      delta[1] = from_col<1>(dl);
-      delta[2] = from_col<2>(dl);
-      delta[3] = from_col<3>(dl);
-    }
+    dlc = dl;
   }
 
   // ---- writer: inner = x'/c = a z + k delta/c; row sums of |x'|
@@ -2472,7 +2512,7 @@ __device__ __forceinline__ void body(const PoolDev &P, const StepDev &S, KCtx &C
   if (C.tid >= FK) {  // waves 2, 3 (0 and 1 did the row set-up)
     const int i = C.tid - FK;
     const int4 m = C.rm[i];
-    if (m.w > 0) {
+    if (m.y != 0) {
       const float sum = ((C.red[i] + C.red[FK + i]) + C.red[2 * FK + i]) + C.red[3 * FK + i];
       float mean = sum / (float)FV;
       mean = mean < 1e-20f ? 1e-20f : mean;
@@ -2536,7 +2576,7 @@ __device__ __forceinline__ void body(const PoolDev &P, const StepDev &S, KCtx &C
       const float4 rc = C.rc[i];
       const float4 rl = C.rl[i];
       const float k = C.ks[i];
-      const uint32_t word = word_at(C.code, m.x + base) ^ (uint32_t)m.z;
+      const uint32_t word = word_at_addr(cb + (uint32_t)m.x) ^ (uint32_t)C.rk[i].x;
 #pragma unroll
       for (int c = 0; c < 4; c++) {
         const float s = (float)sbfe(word, c * (uint32_t)m.y, (uint32_t)m.y);
@@ -2568,26 +2608,37 @@ __device__ __forceinline__ void body(const PoolDev &P, const StepDev &S, KCtx &C
   for (int r = 0; r < FRPT; r++) {
     if ((r % KDA_SCHED_ROWS) == KDA_SCHED_ROWS - 1) __builtin_amdgcn_sched_barrier(0);
     const int i = C.rg + 8 * r;
-    const float4 rl = C.rl[i];
     const int4 m = C.rm[i];
+    const int4 k = C.rk[i];
+    const float lh = __int_as_float(k.z), top = __int_as_float(k.w);
     uint32_t code[4];
 #pragma unroll
     for (int c = 0; c < 4; c++) {
       // floor(y + L + 1/2) on [0, 2L]: the level of rint(y) + L
-      code[c] = (uint32_t)__builtin_amdgcn_fmed3f(fmaf(cf[r][c], f[c], rl.x + 0.5f), 0.0f, 2.0f * rl.x + 0.5f);
+      code[c] = (uint32_t)__builtin_amdgcn_fmed3f(fmaf(cf[r][c], f[c], lh), 0.0f, top);
     }
-    const uint32_t w = (uint32_t)m.y;
-    const uint32_t word = code[0] | (code[1] << w) | (code[2] << (2 * w)) | (code[3] << (3 * w));
-    // the tile's m.w bytes; the other byte stores go to this lane's spare
-    // dword (no branches on the per-lane width)
-    uint8_t *dst = C.code + m.x + base, *spare = C.spare + 4 * C.tid;
-    (m.w > 0 ? dst : spare)[0] = (uint8_t)word;
-    (m.w > 1 ? dst : spare)[1] = (uint8_t)(word >> 8);
-    (m.w > 2 ? dst : spare)[2] = (uint8_t)(word >> 16);
-    (m.w > 3 ? dst : spare)[3] = (uint8_t)(word >> 24);
+    const uint32_t word = code[0] | (code[1] << (uint32_t)m.y) | (code[2] << (uint32_t)m.z) | (code[3] << (uint32_t)m.w);
+    // the tile's bytes (mask k.y; none for pivot rows) merged into the two
+    // dwords they can span; neighbouring rows share those dwords
+    const uint32_t a = cb + (uint32_t)m.x;
+    const uint32_t sh = (a << 3) & 24u;
+    lds_mskor2(a & ~3u, (uint64_t)(uint32_t)k.y << sh, (uint64_t)word << sh);
   }
+  // the masked merges are not tracked by the compiler's wait counts
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   // ---- pivot rows: x' = x retention + k delta, stored as FP16
-  {
+  if (pivots) {
+    float delta[4];
+    if (MODE == MODE_WRITE) {
+      const int64_t bi = ((int64_t)C.b * P.H + C.h) * FV + C.j0;
+#pragma unroll
+      for (int c = 0; c < 4; c++) delta[c] = S.s_delta[bi + c];
+    } else {
+      delta[0] = from_col<0>(dlc);
+      delta[1] = from_col<1>(dlc);
+      delta[2] = from_col<2>(dlc);
+      delta[3] = from_col<3>(dlc);
+    }
     uint64_t lo = pm_lo, hi = pm_hi;
     for (int p = next_pivot(lo, hi); p >= 0; p = next_pivot(lo, hi)) {
       if ((p & 7) == C.rg) {
@@ -2602,8 +2653,10 @@ __device__ __forceinline__ void body(const PoolDev &P, const StepDev &S, KCtx &C
   }
   __syncthreads();
   stage_out_blocks(C.page + C.code_start, C.stride, block_pitch(C.stride), C.code, C.tid);
-  if (C.row_bytes > 0) stage_out(C.page + C.row_start, C.row_bytes, C.rst, C.tid, FNT);
-  if (has_cols) stage_out(C.page + C.colbase, 2 * FV, C.cst, C.tid, FNT);
+  // the row and column regions from waves 1 and 2 (wave 0 writes the first
+  // edge chunks of the blocks)
+  if (C.row_bytes > 0) stage_out(C.page + C.row_start, C.row_bytes, C.rst, (C.tid - 64) & (FNT - 1), FNT);
+  if (has_cols) stage_out(C.page + C.colbase, 2 * FV, C.cst, (C.tid - 128) & (FNT - 1), FNT);
 }
 
 }  // namespace kfast
@@ -2738,8 +2791,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KDA128_WAVE
   C.rc = (float4 *)(C.qs + FK);
   C.rl = C.rc + FK;
   C.rm = (int4 *)(C.rl + FK);
-  C.pmask = (uint32_t *)(C.rm + FK);
-  C.spare = (uint8_t *)(C.pmask + 4);
+  C.rk = C.rm + FK;
+  C.pmask = (uint32_t *)(C.rk + FK);
 
   // stage the head's code, row-scale and column-scale regions
   const int pitch = block_pitch(C.stride);
@@ -4062,9 +4115,9 @@ int launch_step_mode(const sq_pool *pool, StepDev sd, int64_t batch, hipStream_t
       pd.rstage = (pool->max_row_bytes + 47) & ~15;
       // code blocks in padded windows (the largest head's stride)
       pd.stage = 32 * kfast::block_pitch(pool->max_code_bytes / 32);
-      // staging | rows | columns | q,k raw, w, retention | misc | red | ks, qs | rc, rl, rm | pivot mask | spare
+      // staging | rows | columns | q,k raw, w, retention | misc | red | ks, qs | rc, rl, rm, rk | pivot mask
       size_t lds = (size_t)pd.stage + pd.rstage + fast::KDA_COL_STAGE + 4 * 128 * 4 + fast::MISC_FLOATS * 4 +
-                   4 * 128 * 4 + 2 * 128 * 4 + 3 * 128 * 16 + 16 + 4 * 256;
+                   4 * 128 * 4 + 2 * 128 * 4 + 4 * 128 * 16 + 16;
       if (MODE == MODE_WRITE || sd.qkv_dtype == SQ_F32)
         hipLaunchKernelGGL((kda128_kernel<MODE, true>), dim3((unsigned)pool->heads, (unsigned)batch), dim3(256), lds, st, pd,
                            sd);
