@@ -1269,7 +1269,7 @@ __global__ __launch_bounds__(512) void step_kernel(PoolDev P, StepDev S) {
 #define SCHED_ROWS 4  // rows between scheduling fences (bounds hoisted LDS loads)
 #endif
 #ifndef KDA_SCHED_ROWS
-#define KDA_SCHED_ROWS 2  // the KDA tile's per-row metadata loads need the tighter bound
+#define KDA_SCHED_ROWS 16  // the KDA tile: all 16 rows in one window (no spills at 4 waves per SIMD)
 #endif
 
 namespace fast {
@@ -2733,10 +2733,9 @@ __device__ __forceinline__ void kda_prologue(const PoolDev &P, const StepDev &S,
   if (C.tid >= FK) C.wv[i] = w;
 }
 
-// Four waves per SIMD (128 VGPRs) leave 14 values spilled to scratch, stored
-// once before the pivot rows and reloaded once: still faster on the K6 step
-// than three waves without spills (155 us against 164 us), because the extra
-// wave hides the tile's LDS and input latency.
+// Four waves per SIMD: the fused kernel fits 128 VGPRs with no scratch (the
+// readout sums finish before the pivot loop, one delta register is kept
+// instead of four); a fourth wave hides the tile's LDS and input latency.
 #ifndef KDA128_WAVES
 #define KDA128_WAVES 4
 #endif
