@@ -60,6 +60,14 @@ __device__ __forceinline__ uint32_t f2bf(float f) {
   return __builtin_bit_cast(uint16_t, (__bf16)f);
 }
 
+typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+typedef float f32x2_v __attribute__((ext_vector_type(2)));
+// two floats rounded to bf16 (nearest even, as f2bf) in one packed
+// conversion; a in the low half
+__device__ __forceinline__ uint32_t bf16x2_bits(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_v){a, b}, bf16x2_v));
+}
+
 __device__ __forceinline__ float load_val(const void *p, int dtype, int64_t idx) {
   if (dtype == SQ_F32) return ((const float *)p)[idx];
   if (dtype == SQ_BF16) return __uint_as_float((uint32_t)((const uint16_t *)p)[idx] << 16);
@@ -112,9 +120,16 @@ __device__ __forceinline__ void store4_aligned(void *p, int dtype, int64_t idx, 
     *(float4 *)((float *)p + idx) = make_float4(v[0], v[1], v[2], v[3]);
     return;
   }
+  if (dtype == SQ_BF16) {
+    float w[4] = {v[0], v[1], v[2], v[3]};
+#pragma unroll
+    for (int c = 0; c < 4; c++) asm("" : "+v"(w[c]));  // a separate rounding step, as for f2bf
+    *(uint2 *)((uint16_t *)p + idx) = make_uint2(bf16x2_bits(w[0], w[1]), bf16x2_bits(w[2], w[3]));
+    return;
+  }
   uint32_t e[4];
 #pragma unroll
-  for (int c = 0; c < 4; c++) e[c] = dtype == SQ_BF16 ? f2bf(v[c]) : f2h(v[c]);
+  for (int c = 0; c < 4; c++) e[c] = f2h(v[c]);
   *(uint2 *)((uint16_t *)p + idx) = make_uint2(e[0] | (e[1] << 16), e[2] | (e[3] << 16));
 }
 
@@ -2894,19 +2909,19 @@ __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
 __device__ __forceinline__ bf16x8 ld8(const uint8_t *lds, int byte) { return *(const bf16x8 *)(lds + byte); }
 __device__ __forceinline__ float bf2f(uint16_t x) { return __uint_as_float((uint32_t)x << 16); }
 
-__device__ __forceinline__ uint32_t pack2(float a, float b) {
-  return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)a) | ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)b) << 16);
+// two values rounded to bf16 (nearest even) and packed, a in the low half:
+// one v_cvt_pk_bf16_f32
+__device__ __forceinline__ uint32_t pack2(float a, float b) { return bf16x2_bits(a, b); }
+// hi/lo bf16 halves of a pair (x = hi + lo to ~2^-16 relative): the hi pair
+// is one packed conversion, its two values come back by shift and mask
+__device__ __forceinline__ void split2(float a, float b, uint32_t &hi, uint32_t &lo) {
+  hi = bf16x2_bits(a, b);
+  lo = bf16x2_bits(a - __uint_as_float(hi << 16), b - __uint_as_float(hi & 0xffff0000u));
 }
 // hi/lo halves of four values as two packed bf16 x 4
 __device__ __forceinline__ void split4(const float x[4], uint2 &hi, uint2 &lo) {
-  float h[4], r[4];
-#pragma unroll
-  for (int e = 0; e < 4; e++) {
-    h[e] = (float)(__bf16)x[e];
-    r[e] = x[e] - h[e];
-  }
-  hi = make_uint2(pack2(h[0], h[1]), pack2(h[2], h[3]));
-  lo = make_uint2(pack2(r[0], r[1]), pack2(r[2], r[3]));
+  split2(x[0], x[1], hi.x, lo.x);
+  split2(x[2], x[3], hi.y, lo.y);
 }
 
 // MFMA operand (hi and lo bf16 halves) of a 32-row chunk held as two
@@ -2921,12 +2936,8 @@ __device__ __forceinline__ void to_operand(const f32x4 &x0, const f32x4 &x1, bf1
   uint32_t h[2][2], l[2][2];  // [tile][pair]
 #pragma unroll
   for (int p = 0; p < 2; p++) {
-    const float a0 = x0[2 * p], a1 = x0[2 * p + 1], b0 = x1[2 * p], b1 = x1[2 * p + 1];
-    const float ha0 = (float)(__bf16)a0, ha1 = (float)(__bf16)a1, hb0 = (float)(__bf16)b0, hb1 = (float)(__bf16)b1;
-    h[0][p] = pack2(ha0, ha1);
-    h[1][p] = pack2(hb0, hb1);
-    l[0][p] = pack2(a0 - ha0, a1 - ha1);
-    l[1][p] = pack2(b0 - hb0, b1 - hb1);
+    split2(x0[2 * p], x0[2 * p + 1], h[0][p], l[0][p]);
+    split2(x1[2 * p], x1[2 * p + 1], h[1][p], l[1][p]);
   }
   auto conv = [](const uint32_t (&t)[2][2]) {
     uint32_t o[4];
@@ -2943,6 +2954,24 @@ __device__ __forceinline__ void to_operand(const f32x4 &x0, const f32x4 &x1, bf1
   };
   hi = conv(h);
   lo = conv(l);
+}
+
+// lane Q's value of each quad in all four of its lanes (DPP quad_perm [Q,Q,Q,Q])
+template <int Q>
+__device__ __forceinline__ float quad_bcast(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), Q * 0x55, 0xF, 0xF, false));
+}
+// step ST.. of the diagonal-block forward substitution: the quad's lane
+// ST % 4 holds x_ST (its row slot ST / 4); every lane's rows r = g + 4k take
+// -A[r][ST] x_ST (rows[4 k PA + ST] is A[g + 4k][ST])
+template <int ST>
+__device__ __forceinline__ void tsolve_step(float acc[4], const float *rows) {
+  if constexpr (ST < 16) {
+    const float xs = quad_bcast<ST & 3>(acc[ST >> 2]);
+#pragma unroll
+    for (int k = 0; k < 4; k++) acc[k] = fmaf(-rows[4 * k * PA + ST], xs, acc[k]);
+    tsolve_step<ST + 1>(acc, rows);
+  }
 }
 
 // sum over the 16 lanes of a DPP row
@@ -2995,9 +3024,9 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
   // one store per 4 output values when the output array's alignment allows
   // it (16 bytes for fp32, 8 for 16-bit values)
   const bool out_aligned = ((uintptr_t)D.out & (D.out_dtype == SQ_F32 ? 15 : 7)) == 0;
-  // T in bf16 hi/lo: blocks above the diagonal stay zero, the others are
-  // rewritten every chunk
-  for (int e = tid; e < 2 * PC * P72 / 2; e += NT) ((uint32_t *)Tb)[e] = 0u;
+  // T and P in bf16 hi/lo: blocks above the diagonal stay zero, the others
+  // are rewritten every chunk
+  for (int e = tid; e < 2 * PC * P72 / 2; e += NT) ((uint32_t *)Tb)[e] = ((uint32_t *)Pl)[e] = 0u;
   // T entry (t, s) as hi/lo bf16 next to its fp32 value
   auto put_t = [&](int t, int s, float x) {
     const __bf16 hi = (__bf16)x;
@@ -3131,29 +3160,28 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
     }
     lds_barrier();
 
-    // ---- A and P tiles (t-tile w % 4, s-tiles 2 (w / 4) and 2 (w / 4) + 1):
-    // A_ts = beta_t nk_t nk_s (Gamma_t/Gamma_s) k_t.k_s (s < t), P_ts likewise with q_t (s <= t)
+    // ---- A and P tiles (t-tile tw, s-tile ns) with ns <= tw:
+    // A_ts = beta_t nk_t nk_s (Gamma_t/Gamma_s) k_t.k_s (s < t), P_ts likewise with q_t (s <= t).
+    // The ten tiles go at most two to a wave, so that the two waves sharing a
+    // SIMD (w and w + 4) hold two or three between them; tiles above the
+    // diagonal stay zero.
     {
-      const int tw = w & 3, t = 16 * tw + c16;
-      bf16x8 bk[4], bq[4];
+      auto ap_tile = [&](int tw, int ns) {
+        const int t = 16 * tw + c16;
+        bf16x8 bk[4], bq[4];
 #pragma unroll
-      for (int ks = 0; ks < 4; ks++) {
-        bk[ks] = ld8(Kc, (t * P136 + 8 * q4 + 32 * ks) * 2);
-        bq[ks] = ld8(Qc, (t * P136 + 8 * q4 + 32 * ks) * 2);
-      }
-      const float lct = sm[SM_LC * 64 + t], bnt = sm[SM_BETA * 64 + t] * sm[SM_NK * 64 + t];
-      const float nqt = sm[SM_NQ * 64 + t];
-#pragma unroll
-      for (int u = 0; u < 2; u++) {
-        const int ns = 2 * (w >> 2) + u;
+        for (int ks = 0; ks < 4; ks++) {
+          bk[ks] = ld8(Kc, (t * P136 + 8 * q4 + 32 * ks) * 2);
+          bq[ks] = ld8(Qc, (t * P136 + 8 * q4 + 32 * ks) * 2);
+        }
+        const float lct = sm[SM_LC * 64 + t], bnt = sm[SM_BETA * 64 + t] * sm[SM_NK * 64 + t];
+        const float nqt = sm[SM_NQ * 64 + t];
         f32x4 aA = {0.f, 0.f, 0.f, 0.f}, aP = {0.f, 0.f, 0.f, 0.f};
-        if (ns <= tw) {  // wave-uniform: tiles above the diagonal are zero
 #pragma unroll
-          for (int ks = 0; ks < 4; ks++) {
-            const bf16x8 a = ld8(Kc, ((16 * ns + c16) * P136 + 8 * q4 + 32 * ks) * 2);
-            aA = mfma(a, bk[ks], aA);
-            aP = mfma(a, bq[ks], aP);
-          }
+        for (int ks = 0; ks < 4; ks++) {
+          const bf16x8 a = ld8(Kc, ((16 * ns + c16) * P136 + 8 * q4 + 32 * ks) * 2);
+          aA = mfma(a, bk[ks], aA);
+          aP = mfma(a, bq[ks], aP);
         }
         const int s0 = 16 * ns + 4 * q4;
         const float4 lcs = *(const float4 *)(sm + SM_LC * 64 + s0);
@@ -3180,6 +3208,15 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
         split4(pv, hi, lo);
         *(uint2 *)(Pl + (t * P72 + s0) * 2) = hi;
         *(uint2 *)(Pl + PC * P72 * 2 + (t * P72 + s0) * 2) = lo;
+      };
+      switch (__builtin_amdgcn_readfirstlane(w)) {
+        case 0: ap_tile(3, 0); ap_tile(3, 1); break;
+        case 1: ap_tile(3, 2); ap_tile(3, 3); break;
+        case 2: ap_tile(2, 0); ap_tile(2, 1); break;
+        case 3: ap_tile(2, 2); ap_tile(1, 0); break;
+        case 4: ap_tile(1, 1); break;
+        case 5: ap_tile(0, 0); break;
+        default: break;
       }
     }
     // ---- K S0 (rows t, this wave's columns), consumed at once by
@@ -3226,20 +3263,24 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
     }
     lds_barrier();
 
-    // ---- T_ii = (I + A_ii)^{-1}: diagonal 16x16 blocks by forward substitution (waves 0-3)
-    if (w < 4 && l < 16) {
+    // ---- T_ii = (I + A_ii)^{-1}: diagonal 16x16 blocks by forward
+    // substitution, block w on wave w (waves 0-3).  Column j of the block is
+    // solved by the four lanes 4j .. 4j + 3; lane g of them holds rows g,
+    // g + 4, g + 8, g + 12.  At step s the lane holding row s has its final
+    // x_s, which a quad broadcast (DPP) gives the other three, and every row
+    // takes its term -A_rs x_s: each row's sum runs over s in ascending order
+    // as in a row-by-row solve (A_rs = 0 for s >= r adds nothing), and the
+    // dependent chain is 16 steps instead of 120 multiply-adds.
+    if (w < 4) {
       const float *blk = AT + 16 * w * PA + 16 * w;
-      float x[16];
+      const int jc = l >> 2, g = l & 3;
+      const float *rows = blk + g * PA;  // rows g + 4 k at rows[4 k PA]
+      float acc[4];
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        float acc = r == l ? 1.0f : 0.0f;
+      for (int k = 0; k < 4; k++) acc[k] = 4 * k + g == jc ? 1.0f : 0.0f;
+      tsolve_step<0>(acc, rows);
 #pragma unroll
-        for (int s = 0; s < r; s++) acc = fmaf(-blk[r * PA + s], x[s], acc);
-        x[r] = acc;
-      }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int r = 0; r < 16; r++) put_t(16 * w + r, 16 * w + l, x[r]);
+      for (int k = 0; k < 4; k++) put_t(16 * w + 4 * k + g, 16 * w + jc, acc[k]);
     }
     lds_barrier();
 
