@@ -3013,7 +3013,8 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
   const int b = blockIdx.x / H;
   const int hk = h / (H / D.HK);
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, q4 = l >> 4, c16 = l & 15;
-  const int t0 = D.cu[b], len = D.cu[b + 1] - t0;
+  // sequence bounds as wave-uniform values (addresses formed from them stay scalar)
+  const int t0 = __builtin_amdgcn_readfirstlane(D.cu[b]), len = __builtin_amdgcn_readfirstlane(D.cu[b + 1]) - t0;
   if (len <= 0) return;  // whole workgroup: an empty sequence has no chunk and no checkpoint
   float *sm = (float *)(smem + OFF_SM);
   uint8_t *Kc = smem + OFF_KC, *Qc = smem + OFF_QC, *Kt = smem + OFF_KT, *Vt = smem + OFF_VT;
@@ -3059,14 +3060,21 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
   auto fetch = [&](Fetch &F, int c) {
     F.n = c < len ? segment(c) : 0;
     F.tb = (int64_t)t0 + c;
+    // the chunk's first row (the sequence's last past its end) as a
+    // wave-uniform base; rows within the chunk, clamped into the sequence,
+    // as 32-bit byte offsets (one 24-bit multiply-add: rows below 64, row
+    // strides below 2^23 elements)
+    const int rb = __builtin_amdgcn_readfirstlane(c < len ? c : len - 1), lim = len - 1 - rb;
+    const uint8_t *kb = (const uint8_t *)(kg + ((int64_t)t0 + rb) * D.k_stride + hk * PKD);
+    const uint8_t *qb = (const uint8_t *)(qg + ((int64_t)t0 + rb) * D.q_stride + hk * PKD);
+    const uint8_t *vb = (const uint8_t *)(vg + ((int64_t)t0 + rb) * D.v_stride + h * PV);
 #pragma unroll
     for (int it = 0; it < 2; it++) {
       const int idx = tid + NT * it, t = idx >> 4, d8 = (idx & 15) * 8;
-      const int tc = c + t < len ? c + t : len - 1;
-      const int64_t row = (int64_t)t0 + tc;
-      F.k[it] = *(const uint4 *)(kg + row * D.k_stride + hk * PKD + d8);
-      F.q[it] = *(const uint4 *)(qg + row * D.q_stride + hk * PKD + d8);
-      F.v[it] = *(const uint4 *)(vg + row * D.v_stride + h * PV + d8);
+      const uint32_t tr = (uint32_t)(t < lim ? t : lim), db = 2u * (uint32_t)d8;
+      F.k[it] = *(const uint4 *)(kb + (__umul24(tr, 2u * (uint32_t)D.k_stride) + db));
+      F.q[it] = *(const uint4 *)(qb + (__umul24(tr, 2u * (uint32_t)D.q_stride) + db));
+      F.v[it] = *(const uint4 *)(vb + (__umul24(tr, 2u * (uint32_t)D.v_stride) + db));
     }
     if (w == 0) {
       const int64_t at = ((int64_t)t0 + (c + l < len ? c + l : len - 1)) * H + h;
@@ -3340,7 +3348,10 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
         }
         if (t < n) {
           const float o4[4] = {acc[0], acc[1], acc[2], acc[3]};
-          const int64_t at = ((tb + t) * H + h) * PV + jw + 4 * q4;
+          // the chunk's first output row as a wave-uniform index, the token
+          // and column within it as a 32-bit offset
+          const int64_t ob = (tb * H + h) * PV + jw;
+          const int64_t at = ob + (int64_t)(uint32_t)(t * H * PV + 4 * q4);
           if (out_aligned) store4_aligned(D.out, D.out_dtype, at, o4);
           else store4(D.out, D.out_dtype, at, o4);
         }
@@ -4620,6 +4631,9 @@ int sq_prefill(const sq_pool *pool, const sq_prefill_args *a, void *stream) {
   if (a->q_stride % 8 || a->k_stride % 8 || a->v_stride % 8 || ((uintptr_t)a->q & 15) || ((uintptr_t)a->k & 15) ||
       ((uintptr_t)a->v & 15))
     return fail(SQ_EINVAL, "prefill: q, k, v rows must start on 16-byte boundaries (strides multiple of 8)");
+  if (a->q_stride < 0 || a->k_stride < 0 || a->v_stride < 0 || a->q_stride >= (1 << 23) || a->k_stride >= (1 << 23) ||
+      a->v_stride >= (1 << 23))
+    return fail(SQ_EINVAL, "prefill: q, k, v row strides must be below 2^23 elements");
   hipStream_t st = (hipStream_t)stream;
   const int H = pool->heads;
   const int64_t dense = a->batch * (int64_t)H * 128 * 128;

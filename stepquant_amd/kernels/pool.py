@@ -410,7 +410,8 @@ class PackedStatePool:
         qkv = []
         for t in (q2, k2, v2):
             t = t.to(torch.bfloat16)
-            if t.stride(-1) != 1 or t.stride(0) % 8 or t.data_ptr() % 16:
+            # the kernels take 16-byte aligned rows less than 2^23 elements apart
+            if t.stride(-1) != 1 or t.stride(0) % 8 or t.stride(0) >= 1 << 23 or t.data_ptr() % 16:
                 t = t.contiguous()
             qkv.append(t)
         q2, k2, v2 = qkv

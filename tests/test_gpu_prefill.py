@@ -123,6 +123,38 @@ def test_extend_defaults_write_final_state_back_to_the_slots():
     assert len(lens) == 2
 
 
+def test_prefill_rows_far_apart_match_contiguous_rows():
+    """Row strides of 2^23 elements or more (views into wide buffers) give the
+    same outputs and pages as contiguous rows."""
+    from stepquant_amd.kernels.pool import PackedStatePool
+    H, K, V, T = 2, 128, 128, 3
+    oplan = make_plan("gdn", np.full((H, K), 6), seed=3)
+    g = torch.Generator().manual_seed(4)
+    q = torch.randn(T, H * K, generator=g).to(torch.bfloat16).to(dev())
+    k = torch.randn(T, H * K, generator=g).to(torch.bfloat16).to(dev())
+    v = torch.randn(T, H * V, generator=g).to(torch.bfloat16).to(dev())
+    gate = -torch.nn.functional.softplus(torch.randn(T, H, generator=g)).to(dev())
+    beta = torch.sigmoid(torch.randn(T, H, generator=g)).to(dev())
+    init = (torch.randn(1, H, K, V, generator=g) * .1).to(dev())
+    slots = torch.tensor([1])
+    cu = torch.tensor([0, T])
+    wide = torch.zeros(T, (1 << 23) + 256, dtype=torch.bfloat16, device=dev())
+    outs, pages = [], []
+    for spread in (False, True):
+        pool = PackedStatePool(device_plan(oplan), 2, V)
+        pool.encode(init, slots.to(dev()))
+        qq = q
+        if spread:
+            wide[:, :H * K] = q
+            qq = wide[:, :H * K]
+            assert qq.stride(0) >= 1 << 23
+        outs.append(pool.extend(qq, k, v, gate, beta, slots, cu, normalize=True, scale=K ** -.5))
+        torch.cuda.synchronize()
+        pages.append(pool.data.cpu())
+    assert torch.equal(outs[0], outs[1])
+    assert torch.equal(pages[0], pages[1])
+
+
 @pytest.mark.parametrize("arch,storage,raw", [("kda", "packed", False), ("kda", "packed", True),
                                               ("kda", "byte", True), ("gdn", "byte", False)])
 def test_prefill_kda_and_byte_pages(arch, storage, raw):
