@@ -3170,9 +3170,8 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
 
     // ---- A and P tiles (t-tile tw, s-tile ns) with ns <= tw:
     // A_ts = beta_t nk_t nk_s (Gamma_t/Gamma_s) k_t.k_s (s < t), P_ts likewise with q_t (s <= t).
-    // The ten tiles go at most two to a wave, so that the two waves sharing a
-    // SIMD (w and w + 4) hold two or three between them; tiles above the
-    // diagonal stay zero.
+    // The ten tiles go at most two to a wave; tiles above the diagonal stay
+    // zero.
     {
       auto ap_tile = [&](int tw, int ns) {
         const int t = 16 * tw + c16;
@@ -3217,14 +3216,37 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
         *(uint2 *)(Pl + (t * P72 + s0) * 2) = hi;
         *(uint2 *)(Pl + PC * P72 * 2 + (t * P72 + s0) * 2) = lo;
       };
+      // T_ii = (I + A_ii)^{-1}, diagonal block i by forward substitution on
+      // the wave that computed A_ii (no barrier: the block is its own).
+      // Column j of the block is solved by the four lanes 4j .. 4j + 3; lane
+      // g of them holds rows g, g + 4, g + 8, g + 12.  At step s the lane
+      // holding row s has its final x_s, which a quad broadcast (DPP) gives
+      // the other three, and every row takes its term -A_rs x_s: each row's
+      // sum runs over s in ascending order as in a row-by-row solve
+      // (A_rs = 0 for s >= r adds nothing), and the dependent chain is 16
+      // steps instead of 120 multiply-adds.
+      auto diag_solve = [&](int i) {
+        const float *blk = AT + 16 * i * PA + 16 * i;
+        const int jc = l >> 2, g = l & 3;
+        const float *rows = blk + g * PA;  // rows g + 4 k at rows[4 k PA]
+        float acc[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) acc[k] = 4 * k + g == jc ? 1.0f : 0.0f;
+        tsolve_step<0>(acc, rows);
+#pragma unroll
+        for (int k = 0; k < 4; k++) put_t(16 * i + 4 * k + g, 16 * i + jc, acc[k]);
+      };
+      // waves 0-3: diagonal tile i = w and its T_ii; waves 4-7: the six
+      // tiles below the diagonal (w and w + 4 share a SIMD)
       switch (__builtin_amdgcn_readfirstlane(w)) {
-        case 0: ap_tile(3, 0); ap_tile(3, 1); break;
-        case 1: ap_tile(3, 2); ap_tile(3, 3); break;
-        case 2: ap_tile(2, 0); ap_tile(2, 1); break;
-        case 3: ap_tile(2, 2); ap_tile(1, 0); break;
-        case 4: ap_tile(1, 1); break;
-        case 5: ap_tile(0, 0); break;
-        default: break;
+        case 0: ap_tile(0, 0); diag_solve(0); break;
+        case 1: ap_tile(1, 1); diag_solve(1); break;
+        case 2: ap_tile(2, 2); diag_solve(2); break;
+        case 3: ap_tile(3, 3); diag_solve(3); break;
+        case 4: ap_tile(3, 0); ap_tile(3, 1); break;
+        case 5: ap_tile(3, 2); ap_tile(1, 0); break;
+        case 6: ap_tile(2, 0); break;
+        default: ap_tile(2, 1); break;
       }
     }
     // ---- K S0 (rows t, this wave's columns), consumed at once by
@@ -3268,27 +3290,6 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
         for (int r = 0; r < 4; r++) oq[tt][r] = aq[r] * qgt;
         __builtin_amdgcn_sched_barrier(0);
       }
-    }
-    lds_barrier();
-
-    // ---- T_ii = (I + A_ii)^{-1}: diagonal 16x16 blocks by forward
-    // substitution, block w on wave w (waves 0-3).  Column j of the block is
-    // solved by the four lanes 4j .. 4j + 3; lane g of them holds rows g,
-    // g + 4, g + 8, g + 12.  At step s the lane holding row s has its final
-    // x_s, which a quad broadcast (DPP) gives the other three, and every row
-    // takes its term -A_rs x_s: each row's sum runs over s in ascending order
-    // as in a row-by-row solve (A_rs = 0 for s >= r adds nothing), and the
-    // dependent chain is 16 steps instead of 120 multiply-adds.
-    if (w < 4) {
-      const float *blk = AT + 16 * w * PA + 16 * w;
-      const int jc = l >> 2, g = l & 3;
-      const float *rows = blk + g * PA;  // rows g + 4 k at rows[4 k PA]
-      float acc[4];
-#pragma unroll
-      for (int k = 0; k < 4; k++) acc[k] = 4 * k + g == jc ? 1.0f : 0.0f;
-      tsolve_step<0>(acc, rows);
-#pragma unroll
-      for (int k = 0; k < 4; k++) put_t(16 * w + 4 * k + g, 16 * w + jc, acc[k]);
     }
     lds_barrier();
 
