@@ -1736,14 +1736,28 @@ __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx
     word ^= XM;
 #pragma unroll
     for (int c = 0; c < 4; c++) cf[r][c] = (float)sfield<W>(word, c);
+    const float4 rc = rcl[r * RS8];
     if (MODE != MODE_WRITE) {
-      const float4 rc = rcl[r * RS8];
 #pragma unroll
       for (int c = 0; c < 4; c++) {
         aK[c] = fmaf(rc.x, cf[r][c], aK[c]);
         aQ[c] = fmaf(rc.y, cf[r][c], aQ[c]);
       }
     }
+    // the writer's a z = ZS a s + a, which does not wait for the readout's
+    // delta (a*z first: exact zero for z = 0; the rank-1 term comes later)
+    if (MODE != MODE_READ) {
+#pragma unroll
+      for (int c = 0; c < 4; c++) cf[r][c] = fmaf(rc.z, cf[r][c], rc.w);
+    }
+  }
+  // the whole tile completes here: the compiler would otherwise sink these
+  // products past the readout and keep the row constants live across it
+  if (MODE != MODE_READ) {
+#pragma unroll
+    for (int r = 0; r < FRPT; r++)
+#pragma unroll
+      for (int c = 0; c < 4; c++) asm volatile("" : "+v"(cf[r][c]));
   }
   // Per-column work runs once per column: the row-group lanes 2c, 2c + 1
   // finish column c of their four (reduce-scatter), and results every lane
@@ -1781,14 +1795,12 @@ __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx
 #pragma unroll
   for (int r = 0; r < FRPT; r++) {
     if ((r % SCHED_ROWS) == SCHED_ROWS - 1) __builtin_amdgcn_sched_barrier(0);
-    const float4 rc = rcl[r * RS8];
     const float k = ksl[8 * r];
     float acc = 0.f;
 #pragma unroll
     for (int c = 0; c < 4; c++) {
-      // a*z first (exact zero for z = 0), then the rank-1 term: no offset
-      // is cancelled against k*delta/c
-      const float inner = fmaf(k, dj[c], fmaf(rc.z, cf[r][c], rc.w));
+      // the rank-1 term on a z (no offset is cancelled against k*delta/c)
+      const float inner = fmaf(k, dj[c], cf[r][c]);
       cf[r][c] = inner;
       acc = fmaf(cj[c], fabsf(inner), acc);
     }
@@ -2414,22 +2426,28 @@ __device__ __forceinline__ void body(const PoolDev &P, const StepDev &S, KCtx &C
     cf[r][1] = (float)sbfe(word, w, w);
     cf[r][2] = (float)sbfe(word, (uint32_t)m.z, w);
     cf[r][3] = (float)sbfe(word, (uint32_t)m.w, w);
+    const float4 rc = C.rc[i];
     if (MODE != MODE_WRITE) {
-      const float4 rc = C.rc[i];
 #pragma unroll
       for (int c = 0; c < 4; c++) {
         aK[c] = fmaf(rc.x, cf[r][c], aK[c]);
         aQ[c] = fmaf(rc.y, cf[r][c], aQ[c]);
       }
     }
+    // the writer's a z = a s + a, which does not wait for the readout's delta
+    if (MODE != MODE_READ) {
+#pragma unroll
+      for (int c = 0; c < 4; c++) cf[r][c] = fmaf(rc.z, cf[r][c], rc.w);
+    }
   }
-  // the readout sums (so every row's code fields) complete here: the
-  // compiler would otherwise sink the last rows' field extraction past the
-  // pivot loop and keep their code words (spilled) across it
+  // the readout sums and the tile complete here: the compiler would
+  // otherwise sink the last rows' field extraction past the pivot loop and
+  // keep their code words (spilled) across it
   if (MODE != MODE_WRITE) {
 #pragma unroll
     for (int c = 0; c < 4; c++) asm volatile("" : "+v"(aK[c]), "+v"(aQ[c]));
-  } else {
+  }
+  if (MODE != MODE_READ) {
 #pragma unroll
     for (int r = 0; r < FRPT; r++)
 #pragma unroll
@@ -2491,12 +2509,11 @@ __device__ __forceinline__ void body(const PoolDev &P, const StepDev &S, KCtx &C
   for (int r = 0; r < FRPT; r++) {
     if ((r % KDA_SCHED_ROWS) == KDA_SCHED_ROWS - 1) __builtin_amdgcn_sched_barrier(0);
     const int i = C.rg + 8 * r;
-    const float4 rc = C.rc[i];
     const float k = C.ks[i];
     float acc = 0.f;
 #pragma unroll
     for (int c = 0; c < 4; c++) {
-      const float inner = fmaf(k, dj[c], fmaf(rc.z, cf[r][c], rc.w));
+      const float inner = fmaf(k, dj[c], cf[r][c]);
       cf[r][c] = inner;
       acc = fmaf(cj[c], fabsf(inner), acc);
     }
