@@ -1281,7 +1281,7 @@ __global__ __launch_bounds__(512) void step_kernel(PoolDev P, StepDev S) {
 #define GDN128_WAVES 4
 #endif
 #ifndef SCHED_ROWS
-#define SCHED_ROWS 4  // rows between scheduling fences (bounds hoisted LDS loads)
+#define SCHED_ROWS 16  // rows between scheduling fences: the whole tile (no spills at 4 waves per SIMD)
 #endif
 #ifndef KDA_SCHED_ROWS
 #define KDA_SCHED_ROWS 16  // the KDA tile: all 16 rows in one window (no spills at 4 waves per SIMD)
