@@ -1392,49 +1392,48 @@ __device__ __forceinline__ float wave_sum(float x) {
   return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
 }
 
-// Per-row constants of the integer bodies (threads 0..127, row i = tid):
-// rc[i, g] and, for the readout, the sums over rows of k*a, q*a and q*k.
+// Per-row constants of the integer bodies, row i = tid mod 128: threads
+// 0..127 write rc[i, g] (and the prepared k); for the readout, threads
+// 128..255 form the same products of their row and reduce the sums over
+// rows of k*a, q*a and q*k, in parallel with the first two waves.
 template <int MODE>
 __device__ __forceinline__ void row_setup_int(const StepDev &S, const Ctx &C, int NG, float ZS) {
-  if (C.tid < FK) {
-    const int i = C.tid;
-    float nq = 1.0f, nk = 1.0f;
-    if (MODE != MODE_WRITE && S.normalize) {
-      nq = __builtin_amdgcn_rsqf((C.misc[8] + C.misc[10]) + 1e-6f);
-      nk = __builtin_amdgcn_rsqf((C.misc[9] + C.misc[11]) + 1e-6f);
-    }
-    const float k = MODE == MODE_WRITE ? C.kraw[i] : C.kraw[i] * nk;
-    const float q = MODE == MODE_WRITE ? 0.0f : (C.qraw[i] * nq) * S.scale;
+  const bool sums = C.tid >= FK;
+  if (MODE == MODE_WRITE && sums) return;
+  const int i = C.tid & (FK - 1);
+  float nq = 1.0f, nk = 1.0f;
+  if (MODE != MODE_WRITE && S.normalize) {
+    nq = __builtin_amdgcn_rsqf((C.misc[8] + C.misc[10]) + 1e-6f);
+    nk = __builtin_amdgcn_rsqf((C.misc[9] + C.misc[11]) + 1e-6f);
+  }
+  const float k = MODE == MODE_WRITE ? C.kraw[i] : C.kraw[i] * nk;
+  const float q = MODE == MODE_WRITE ? 0.0f : (C.qraw[i] * nq) * S.scale;
+  const uint16_t *r16 = (const uint16_t *)C.rst;
+  const float retention = C.misc[1];
+  if (!sums) {
     C.ks[i] = k;
-    const uint16_t *r16 = (const uint16_t *)C.rst;
-    const float retention = C.misc[1];
-    float ska[4], sqa[4];
 #pragma unroll
     for (int g = 0; g < 4; g++) {
-      ska[g] = 0.0f;
-      sqa[g] = 0.0f;
       if (g < NG) {
         const float a = hw_h2f(r16[i * NG + g]) * retention;
-        ska[g] = k * a;
-        sqa[g] = q * a;
-        C.rc[g * FK + i] = make_float4(ska[g], sqa[g], ZS * a, a);
+        C.rc[g * FK + i] = make_float4(k * a, q * a, ZS * a, a);
       }
     }
-    if (MODE != MODE_WRITE) {
-      float* part = C.misc + 16 + 16 * (i >> 6);
+  } else if (MODE != MODE_WRITE) {
+    float *part = C.misc + 16 + 16 * (i >> 6);
 #pragma unroll
-      for (int g = 0; g < 4; g++) {
-        if (g < NG) {
-          const float s1 = wave_sum(ska[g]), s2 = wave_sum(sqa[g]);
-          if ((i & 63) == 0) {
-            part[SUM_KA + g] = s1;
-            part[SUM_QA + g] = s2;
-          }
+    for (int g = 0; g < 4; g++) {
+      if (g < NG) {
+        const float a = hw_h2f(r16[i * NG + g]) * retention;
+        const float s1 = wave_sum(k * a), s2 = wave_sum(q * a);
+        if ((i & 63) == 0) {
+          part[SUM_KA + g] = s1;
+          part[SUM_QA + g] = s2;
         }
       }
-      const float s3 = wave_sum(q * k);
-      if ((i & 63) == 0) part[SUM_QK] = s3;
     }
+    const float s3 = wave_sum(q * k);
+    if ((i & 63) == 0) part[SUM_QK] = s3;
   }
 }
 
@@ -2311,14 +2310,28 @@ __device__ __forceinline__ uint32_t word_at_addr(uint32_t a) {
   return __builtin_amdgcn_alignbit(w[1], w[0], a << 3);
 }
 
-// Per-row constants (threads 0..127, row i = tid), the pivot-row mask and
-// the readout sums over rows of k*a, q*a (integer rows) and q*k (all rows).
+// The row's plan entries (width, code offset, row-scale offset) of row
+// tid mod 128, loaded with the tile's inputs before the first barrier.
+struct RowPlan {
+  int bits, offset, row;
+};
+
+__device__ __forceinline__ RowPlan row_plan(const PoolDev &P, int h, int tid) {
+  const int64_t hi = (int64_t)h * FK + (tid & (FK - 1));
+  return RowPlan{P.bits[hi], P.offsets[hi], P.rows[hi]};
+}
+
+// Per-row constants, row i = tid mod 128: threads 0..127 write them and the
+// pivot-row mask; for the readout, threads 128..255 form the same products
+// of their row and reduce the sums over rows of k*a, q*a (integer rows) and
+// q*k (all rows), in parallel with the first two waves.
 template <int MODE>
-__device__ __forceinline__ void row_setup(const PoolDev &P, const StepDev &S, const KCtx &C) {
-  if (C.tid < FK) {
-    const int i = C.tid;
-    const int64_t hi = (int64_t)C.h * FK + i;
-    const int bi = P.bits[hi];
+__device__ __forceinline__ void row_setup(const StepDev &S, const KCtx &C, const RowPlan rp) {
+  const bool sums = C.tid >= FK;
+  if (MODE == MODE_WRITE && sums) return;
+  {
+    const int i = C.tid & (FK - 1);
+    const int bi = rp.bits;
     const bool piv = bi == 16;
     float nq = 1.0f, nk = 1.0f;
     if (MODE != MODE_WRITE && S.normalize) {
@@ -2327,11 +2340,28 @@ __device__ __forceinline__ void row_setup(const PoolDev &P, const StepDev &S, co
     }
     const float k = MODE == MODE_WRITE ? C.kraw[i] : C.kraw[i] * nk;
     const float q = MODE == MODE_WRITE ? 0.0f : (C.qraw[i] * nq) * S.scale;
+    const float retention = C.gv[i];
+    float ka = 0.f, qa = 0.f, a = 0.f;
+    if (!piv) {
+      const float norm = (float)(1 << (8 - bi));
+      const float r = hw_h2f(*(const uint16_t *)(C.rst + C.shift_r + (rp.row - C.row_start)));
+      a = (r * retention) * norm;
+      ka = k * a;
+      qa = q * a;
+    }
+    if (sums) {
+      float *part = C.misc + 16 + 16 * (i >> 6);
+      const float s1 = wave_sum(ka), s2 = wave_sum(qa), s3 = wave_sum(q * k);
+      if ((i & 63) == 0) {
+        part[SUM_KA] = s1;
+        part[SUM_QA] = s2;
+        part[SUM_QK] = s3;
+      }
+      return;
+    }
     C.ks[i] = k;
     C.qs[i] = q;
-    const float retention = C.gv[i];
-    const int pos = P.offsets[hi] - C.code_start;  // within a block
-    float ka = 0.f, qa = 0.f;
+    const int pos = rp.offset - C.code_start;  // within a block
     if (piv) {
       C.rc[i] = make_float4(0.f, 0.f, 0.f, 0.f);
       C.rl[i] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -2339,11 +2369,6 @@ __device__ __forceinline__ void row_setup(const PoolDev &P, const StepDev &S, co
       C.rk[i] = make_int4(0, 0, 0, 0);
     } else {
       const int L = (1 << (bi - 1)) - 1;
-      const float norm = (float)(1 << (8 - bi));
-      const float r = hw_h2f(*(const uint16_t *)(C.rst + C.shift_r + (P.rows[hi] - C.row_start)));
-      const float a = (r * retention) * norm;
-      ka = k * a;
-      qa = q * a;
       C.rc[i] = make_float4(ka, qa, a, a);
       C.rl[i] = make_float4((float)L, 1.0f / (float)L, 0.f, 0.f);
       uint32_t xm = 0;
@@ -2357,15 +2382,6 @@ __device__ __forceinline__ void row_setup(const PoolDev &P, const StepDev &S, co
     if ((i & 63) == 0) {
       C.pmask[2 * (i >> 6)] = (uint32_t)pb;
       C.pmask[2 * (i >> 6) + 1] = (uint32_t)(pb >> 32);
-    }
-    if (MODE != MODE_WRITE) {
-      float *part = C.misc + 16 + 16 * (i >> 6);
-      const float s1 = wave_sum(ka), s2 = wave_sum(qa), s3 = wave_sum(q * k);
-      if ((i & 63) == 0) {
-        part[SUM_KA] = s1;
-        part[SUM_QA] = s2;
-        part[SUM_QK] = s3;
-      }
     }
   }
 }
@@ -2832,6 +2848,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KDA128_WAVE
   C.shift_r = C.row_bytes > 0 ? stage_region_async(C.page + C.row_start, C.row_bytes, C.rst, C.tid) : 0;
   C.shift_col = C.colbase >= 0 ? stage_region_async(C.page + C.colbase, 2 * FV, C.cst, C.tid) : 0;
   uint32_t vraw = 0u;
+  const RowPlan rp = row_plan(P, C.h, C.tid);
   kda_prologue<MODE, QW4>(P, S, C, vraw);
   __syncthreads();
   if (MODE == MODE_READ && C.tid < FK) {
@@ -2841,7 +2858,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KDA128_WAVE
     S.s_key[bh * FK + C.tid] = C.kraw[C.tid] * nk;
     S.s_decay[bh * FK + C.tid] = C.gv[C.tid];
   }
-  row_setup<MODE>(P, S, C);
+  row_setup<MODE>(S, C, rp);
   __syncthreads();
   body<MODE, QW4>(P, S, C, vraw);
 }
