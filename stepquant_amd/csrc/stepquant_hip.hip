@@ -2199,10 +2199,11 @@ struct KCtx {
   uint8_t *page, *code, *rst, *cst;
   int lbase, shift_r, shift_col;  // lbase: this lane's block in the staged code
   float *qraw, *kraw, *wv, *gv, *misc, *red, *ks, *qs;
-  float4 *rc;   // per row: k*a, q*a, a, a  (zeros for pivot rows)
+  float4 *rc;   // per row: k*a, q*a, a, top-bit mask (float bits)  (zeros for pivot rows)
   float4 *rl;   // per row: L, 1/L, 1/(r' norm), w^2 r'^2 norm^2 (zeros for pivots)
   int4 *rm;     // per row: byte position within a block, width w (0: pivot), 2w, 3w
   int4 *rk;     // per row: top-bit mask, tile byte mask, L + 1/2, 2L + 1/2 (float bits; zeros for pivots)
+                // (the foreground reads rm and rc only: the mask rides in rc.w)
   uint32_t *pmask;  // 128-bit mask of pivot rows
   int b, h, tid, rg, cg, wave, j0;
   int code_start, code_bytes, row_start, row_bytes, colbase, stride;
@@ -2369,11 +2370,11 @@ __device__ __forceinline__ void row_setup(const StepDev &S, const KCtx &C, const
       C.rk[i] = make_int4(0, 0, 0, 0);
     } else {
       const int L = (1 << (bi - 1)) - 1;
-      C.rc[i] = make_float4(ka, qa, a, a);
-      C.rl[i] = make_float4((float)L, 1.0f / (float)L, 0.f, 0.f);
       uint32_t xm = 0;
 #pragma unroll
       for (int c = 0; c < 4; c++) xm |= 1u << (c * bi + bi - 1);
+      C.rc[i] = make_float4(ka, qa, a, __uint_as_float(xm));
+      C.rl[i] = make_float4((float)L, 1.0f / (float)L, 0.f, 0.f);
       C.rm[i] = make_int4(pos, bi, 2 * bi, 3 * bi);
       C.rk[i] = make_int4((int)xm, (int)(0xffffffffu >> (32 - 4 * bi)), __float_as_int((float)L + 0.5f),
                           __float_as_int(2.0f * (float)L + 0.5f));
@@ -2436,13 +2437,13 @@ __device__ __forceinline__ void body(const PoolDev &P, const StepDev &S, KCtx &C
     if ((r % KDA_SCHED_ROWS) == KDA_SCHED_ROWS - 1) __builtin_amdgcn_sched_barrier(0);
     const int i = C.rg + 8 * r;
     const int4 m = C.rm[i];
-    const uint32_t word = word_at_addr(cb + (uint32_t)m.x) ^ (uint32_t)C.rk[i].x;
+    const float4 rc = C.rc[i];
+    const uint32_t word = word_at_addr(cb + (uint32_t)m.x) ^ __float_as_uint(rc.w);
     const uint32_t w = (uint32_t)m.y;
     cf[r][0] = (float)sbfe(word, 0, w);
     cf[r][1] = (float)sbfe(word, w, w);
     cf[r][2] = (float)sbfe(word, (uint32_t)m.z, w);
     cf[r][3] = (float)sbfe(word, (uint32_t)m.w, w);
-    const float4 rc = C.rc[i];
     if (MODE != MODE_WRITE) {
 #pragma unroll
       for (int c = 0; c < 4; c++) {
@@ -2453,7 +2454,7 @@ __device__ __forceinline__ void body(const PoolDev &P, const StepDev &S, KCtx &C
     // the writer's a z = a s + a, which does not wait for the readout's delta
     if (MODE != MODE_READ) {
 #pragma unroll
-      for (int c = 0; c < 4; c++) cf[r][c] = fmaf(rc.z, cf[r][c], rc.w);
+      for (int c = 0; c < 4; c++) cf[r][c] = fmaf(rc.z, cf[r][c], rc.z);
     }
   }
   // the readout sums and the tile complete here: the compiler would
@@ -2624,11 +2625,11 @@ __device__ __forceinline__ void body(const PoolDev &P, const StepDev &S, KCtx &C
       const float4 rc = C.rc[i];
       const float4 rl = C.rl[i];
       const float k = C.ks[i];
-      const uint32_t word = word_at_addr(cb + (uint32_t)m.x) ^ (uint32_t)C.rk[i].x;
+      const uint32_t word = word_at_addr(cb + (uint32_t)m.x) ^ __float_as_uint(rc.w);
 #pragma unroll
       for (int c = 0; c < 4; c++) {
         const float s = (float)sbfe(word, c * (uint32_t)m.y, (uint32_t)m.y);
-        const float t = fmaf(k, dj[c], fmaf(rc.z, s, rc.w)) * rl.z;
+        const float t = fmaf(k, dj[c], fmaf(rc.z, s, rc.z)) * rl.z;
         const float z = __builtin_amdgcn_fmed3f(__builtin_rintf(t * f0[c]), -rl.x, rl.x);
         const float u = rl.w * z;
         num[c] = fmaf(u, t, num[c]);
