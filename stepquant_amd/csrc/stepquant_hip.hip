@@ -2895,8 +2895,8 @@ constexpr int P136 = 136, P72 = 72, PA = 68;  // row pitches (elements) of the L
 constexpr int OFF_KC = 0;                          // bf16 [64 t][136]   k rows (d contiguous)
 constexpr int OFF_QC = OFF_KC + PC * P136 * 2;     // bf16 [64 t][136]   q rows
 constexpr int OFF_KT = OFF_QC + PC * P136 * 2;     // bf16 [128 d][72]   k columns (t contiguous, swizzled)
-constexpr int OFF_VT = OFF_KT + PKD * P72 * 2;     // bf16 [128 j][72]   v columns (swizzled)
-constexpr int OFF_AT = OFF_VT + PV * P72 * 2;      // f32  [64 t][68]    A (diagonal blocks read)
+constexpr int OFF_VC = OFF_KT + PKD * P72 * 2;     // bf16 [64 t][136]   v rows
+constexpr int OFF_AT = OFF_VC + PC * P136 * 2;     // f32  [64 t][68]    A (diagonal blocks read)
 constexpr int OFF_P = OFF_AT + PC * PA * 4;        // bf16 2 x [64 t][72] masked, scaled Q K^T (hi, lo)
 constexpr int OFF_T = OFF_P + 2 * PC * P72 * 2;    // bf16 2 x [64 t][72] M (hi, lo): T_ii, -A_ik (i > k), 0
 constexpr int OFF_SM = OFF_T + 2 * PC * P72 * 2;   // f32 [10][64] per-token scalars
@@ -2915,12 +2915,41 @@ struct PrefillDev {
   float scale;
 };
 
-// Element (r, t) of the transposed k and v tiles sits in row r at column
-// tcol(r, t): the 8-token block index is XORed with bits 3-5 of r, so the
-// staging stores (8 consecutive rows r per lane group, one token) spread
-// over the banks instead of landing 72 elements apart in one bank; reads of
-// 8 (or 4 aligned) consecutive tokens stay contiguous.
+// Element (r, t) of the transposed k tile sits in row r at column
+// tcol(r, t): the 8-token block index is XORed with bits 3-5 of r, so rows
+// 8 apart start in different banks; runs of 4 or 8 consecutive tokens
+// (t % 4 == 0) stay contiguous.
 __device__ __forceinline__ int tcol(int r, int t) { return (((t >> 3) ^ (r >> 3)) & 7) * 8 + (t & 7); }
+
+// Four consecutive tokens of one column of a token-major bf16 tile
+// [t][P136], with gfx950's transposing LDS load (ds_read_b64_tr_b16).
+// Within each 16-lane row of the wave the instruction reads 8 bytes at
+// every lane's address, as a 16 x 4 matrix M (row i: lane i's four halves),
+// and returns to lane j the column j % 4 of rows j / 4 + 4k, k = 0..3 (lane
+// layout checked on gfx950).  Lane i addressing token t0 + i / 4 at column
+// c0 + 4 (i % 4) therefore receives column c0 + j of tokens t0 .. t0 + 3.
+typedef short tr4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ tr4_t col4(const uint8_t *tile, int t0, int c0, int lane16) {
+  const int byte = ((t0 + (lane16 >> 2)) * P136 + c0 + 4 * (lane16 & 3)) * 2;
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) tr4_t *)(uintptr_t)(fast::lptr_t)(tile + byte));
+}
+
+// 4 x 4 transpose of dwords between the four 16-lane rows of a wave: row r
+// enters with x[m] = M[r][m] and leaves with x[m] = M[m][r] (v_permlane32_swap
+// trades the upper half of its first operand with the lower half of its
+// second, v_permlane16_swap the odd rows of the first with the even rows of
+// the second)
+__device__ __forceinline__ void rows_transpose4(uint32_t x[4]) {
+  const auto s02 = __builtin_amdgcn_permlane32_swap(x[0], x[2], false, false);
+  const auto s13 = __builtin_amdgcn_permlane32_swap(x[1], x[3], false, false);
+  const auto s01 = __builtin_amdgcn_permlane16_swap(s02[0], s13[0], false, false);
+  const auto s23 = __builtin_amdgcn_permlane16_swap(s02[1], s13[1], false, false);
+  x[0] = s01[0];
+  x[1] = s01[1];
+  x[2] = s23[0];
+  x[3] = s23[1];
+}
 
 template <int CTRL, int ROWS>
 __device__ __forceinline__ float dpp0(float v) {  // DPP move, 0 where the source lane is outside the row
@@ -3052,7 +3081,7 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
   const int t0 = __builtin_amdgcn_readfirstlane(D.cu[b]), len = __builtin_amdgcn_readfirstlane(D.cu[b + 1]) - t0;
   if (len <= 0) return;  // whole workgroup: an empty sequence has no chunk and no checkpoint
   float *sm = (float *)(smem + OFF_SM);
-  uint8_t *Kc = smem + OFF_KC, *Qc = smem + OFF_QC, *Kt = smem + OFF_KT, *Vt = smem + OFF_VT;
+  uint8_t *Kc = smem + OFF_KC, *Qc = smem + OFF_QC, *Kt = smem + OFF_KT, *Vc = smem + OFF_VC;
   float *AT = (float *)(smem + OFF_AT);
   uint8_t *Pl = smem + OFF_P, *Tb = smem + OFF_T;
   const __bf16 *qg = (const __bf16 *)D.q, *kg = (const __bf16 *)D.k, *vg = (const __bf16 *)D.v;
@@ -3139,7 +3168,7 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
     // computed where used instead of being held across the loop
     const int tid = fast::opaque(threadIdx.x), l = tid & 63, q4 = l >> 4, c16 = l & 15;
 
-    // ---- stage the fetched chunk: k and q rows, k and v columns, squared norms, decays
+    // ---- stage the fetched chunk: k, q and v rows, k columns, squared norms, decays
 #pragma unroll
     for (int it = 0; it < 2; it++) {
       const int idx = tid + NT * it, t = idx >> 4, d8 = (idx & 15) * 8;
@@ -3147,19 +3176,28 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
       const uint4 kv = t < n ? F.k[it] : zero, qv = t < n ? F.q[it] : zero, vv = t < n ? F.v[it] : zero;
       *(uint4 *)(Kc + (t * P136 + d8) * 2) = kv;
       *(uint4 *)(Qc + (t * P136 + d8) * 2) = qv;
+      *(uint4 *)(Vc + (t * P136 + d8) * 2) = vv;
       const uint16_t *ke = (const uint16_t *)&kv, *qe = (const uint16_t *)&qv;
-      const uint16_t *ve = (const uint16_t *)&vv;
       float sk = 0.f, sq = 0.f;
-      // rows d8 .. d8 + 7 share their swizzle (bits 3-5 of the row): one
-      // base address, the rows at immediate offsets
-      const int cb = (d8 * P72 + tcol(d8, t)) * 2;
 #pragma unroll
       for (int e = 0; e < 8; e++) {
-        *(uint16_t *)(Kt + cb + e * P72 * 2) = ke[e];
-        *(uint16_t *)(Vt + cb + e * P72 * 2) = ve[e];
         const float fk = bf2f(ke[e]), fq = bf2f(qe[e]);
         sk = fmaf(fk, fk, sk);
         sq = fmaf(fq, fq, sq);
+      }
+      {
+        // k columns: the wave's four 16-lane rows hold tokens t0 .. t0 + 3
+        // (row r = t - t0); after the transpose row r holds value pair r
+        // (key rows d8 + 2r, d8 + 2r + 1) of all four tokens, stored as two
+        // 8-byte runs of consecutive tokens
+        const int rr = (tid >> 4) & 3, t0 = t - rr, d = d8 + 2 * rr;
+        const int o0 = (d * P72 + tcol(d, t0)) * 2;
+        uint32_t x[4] = {kv.x, kv.y, kv.z, kv.w};
+        rows_transpose4(x);
+        *(uint2 *)(Kt + o0) = make_uint2(__builtin_amdgcn_perm(x[1], x[0], 0x05040100u),
+                                         __builtin_amdgcn_perm(x[3], x[2], 0x05040100u));
+        *(uint2 *)(Kt + o0 + P72 * 2) = make_uint2(__builtin_amdgcn_perm(x[1], x[0], 0x07060302u),
+                                                   __builtin_amdgcn_perm(x[3], x[2], 0x07060302u));
       }
       sk = row16_sum(sk);
       sq = row16_sum(sq);
@@ -3301,12 +3339,12 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
           ak = mfma(kr, sh[kc], ak);
           ak = mfma(kr, sl[kc], ak);
         }
-        const int ta = 16 * tt + 4 * q4, j = jw + c16;
+        const int ta = 16 * tt + 4 * q4;
         const float4 be = *(const float4 *)(sm + SM_BETA * 64 + ta), gk = *(const float4 *)(sm + SM_GK * 64 + ta);
         const float be4[4] = {be.x, be.y, be.z, be.w}, gk4[4] = {gk.x, gk.y, gk.z, gk.w};
-        const uint2 vr = *(const uint2 *)(Vt + (j * P72 + tcol(j, ta)) * 2);
-        const float v4[4] = {__uint_as_float(vr.x << 16), __uint_as_float(vr.x & 0xffff0000u),
-                             __uint_as_float(vr.y << 16), __uint_as_float(vr.y & 0xffff0000u)};
+        const tr4_t vr = col4(Vc, ta, jw, c16);  // v of tokens ta .. ta + 3, column jw + c16
+        const float v4[4] = {bf2f((uint16_t)vr[0]), bf2f((uint16_t)vr[1]), bf2f((uint16_t)vr[2]),
+                             bf2f((uint16_t)vr[3])};
 #pragma unroll
         for (int r = 0; r < 4; r++) R[tt][r] = be4[r] * (v4[r] - gk4[r] * ak[r]);
         __builtin_amdgcn_sched_barrier(0);  // one tile's operand loads in flight at a time

@@ -390,8 +390,8 @@ class PackedStatePool:
             total = int(cu_host[-1]) if cu_host.numel() > 1 else 0
             if cu_host.numel() > 1:
                 _check_offsets(int(cu_host[0]), int((cu_host[1:] < cu_host[:-1]).sum()))
-            cu = cu_host.pin_memory().to(dev, non_blocking=True)
-        batch = cu.numel() - 1
+            cu = None  # copied below, with the checkpoints when they are host tensors too
+        batch = (cu if cu_host is None else cu_host).numel() - 1
         if batch < 0:
             raise ValueError("cu_seqlens needs at least one entry")
         slots_t = _indices(slots, dev)
@@ -444,9 +444,21 @@ class PackedStatePool:
             if (used_n[:, 1:] & (ck_n[:, 1:] < seen[:, :-1])).any():
                 raise ValueError("checkpoints of a sequence must be ascending")
             cs_h = torch.where(used, cs_h, torch.zeros_like(cs_h))
-            ck = ck_h.contiguous().pin_memory().to(dev, non_blocking=True)
-            ck_slots = cs_h.contiguous().pin_memory().to(dev, non_blocking=True)
+            # offsets, checkpoints and their slots in one pinned buffer: one copy
+            n_cs, n_ck, n_cu = cs_h.numel(), ck_h.numel(), cu_host.numel()
+            packed = torch.empty(n_cs + (n_ck + n_cu + 1) // 2, dtype=torch.int64, pin_memory=True)
+            packed[:n_cs] = cs_h.reshape(-1)
+            p32 = packed[n_cs:].view(torch.int32)
+            p32[:n_cu] = cu_host
+            p32[n_cu:n_cu + n_ck] = ck_h.reshape(-1)
+            packed = packed.to(dev, non_blocking=True)
+            ck_slots = packed[:n_cs].view(cs_h.shape)
+            d32 = packed[n_cs:].view(torch.int32)
+            cu = d32[:n_cu]
+            ck = d32[n_cu:n_cu + n_ck].view(ck_h.shape)
         else:
+            if cu is None:
+                cu = cu_host.pin_memory().to(dev, non_blocking=True)
             lengths = (cu[1:] - cu[:-1]).to(torch.int32)
             if checkpoints is None:
                 ck = lengths.reshape(batch, 1)
