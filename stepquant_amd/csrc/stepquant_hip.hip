@@ -53,6 +53,26 @@ __device__ __forceinline__ float fp16_scale(float x, uint32_t *hbits) {
   return h2f(h);
 }
 
+// x / d rounded to nearest for a divisor d that is an fp16 value (at most 11
+// significant bits), from d's correctly rounded reciprocal inv = 1 / d:
+// q0 = x inv, then one correction with the exact residual x - q0 d.  For
+// every pair of significands (x any of the 2^23, d any of the 2^10) the
+// result equals the IEEE quotient (checked exhaustively on the CPU);
+// exponents only scale it, so it is exact while x, the residual and the
+// quotient stay normal: |x| >= 2^-100 and |q0| <= 2^126.  x = 0 gives a
+// zero of either sign.
+__device__ __forceinline__ float div_half(float x, float d, float inv) {
+  const float q0 = x * inv;
+  const float r = fmaf(-q0, d, x);
+  return fmaf(r, inv, q0);
+}
+
+// compile-time switch for the two forms of a loop
+template <bool B>
+struct BoolTag {
+  static constexpr bool value = B;
+};
+
 // float -> bfloat16 bits by v_cvt_pk_bf16_f32 (round to nearest even, as
 // torch's .bfloat16() for every non-NaN input)
 __device__ __forceinline__ uint32_t f2bf(float f) {
@@ -378,7 +398,14 @@ __device__ __forceinline__ void encode_fast128(const PoolDev &P, const float *__
   int *orel = (int *)(wl + K);             // [K] row offsets within the code region
   float *cmax = (float *)(orel + K);       // [4][V]
   float *bsum = cmax + 4 * V;              // [K/16][2][V]
+  float *rinv = bsum + (K / 16) * 2 * V;   // [K][NG] 1 / row scale, correctly rounded
 
+  // The column phase divides by fp16 scales (row scales, c0, c): with their
+  // correctly rounded reciprocals, div_half gives the IEEE quotient when
+  // every value is 0 or 2^-76 <= |x| <= 2^60 (scales lie in [2^-24, 65504],
+  // so the quotients stay within [2^-92, 2^108]).  Tiles with a value
+  // outside (or a NaN or infinity) divide with IEEE division.
+  uint32_t lo_bits = 0xffffffffu, hi_bits = 0u;  // min of |x| bits - 1 (zeros wrap), max of |x| bits
   // ---- row phase
   {
     const int lane = tid & 31, l = lane >> 2, k = lane & 3, rw = tid >> 5;
@@ -393,6 +420,14 @@ __device__ __forceinline__ void encode_fast128(const PoolDev &P, const float *__
       ro[p] = P.rows[(int64_t)h * K + i];
       of[p] = P.offsets[(int64_t)h * K + i];
     }
+#pragma unroll
+    for (int p = 0; p < 8; p++)
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const uint32_t a = __float_as_uint(v[p][u]) & 0x7fffffffu;
+        lo_bits = min(lo_bits, a - 1u);
+        hi_bits = max(hi_bits, a);
+      }
 #pragma unroll
     for (int p = 0; p < 8; p++) {
       const int i = rw + 16 * p;
@@ -430,6 +465,7 @@ __device__ __forceinline__ void encode_fast128(const PoolDev &P, const float *__
           uint32_t hb;
           const float r = fp16_scale(__builtin_sqrtf(m / wi[p]), &hb);
           rsc[i * NG + g] = r;
+          rinv[i * NG + g] = 1.0f / r;
           put_page_half(page, ro[p] + 2 * g, hb);
         }
       }
@@ -445,11 +481,14 @@ __device__ __forceinline__ void encode_fast128(const PoolDev &P, const float *__
   float xs[32], sc[32];
 #pragma unroll
   for (int r = 0; r < 32; r++) xs[r] = X[(i0 + r) * V + j];
-  __syncthreads();
+  const bool ieee = __syncthreads_or(lo_bits < 0x19800000u - 1u || hi_bits > 0x5d800000u);
+  auto columns = [&](auto fast_tag) {
+  constexpr bool FAST = decltype(fast_tag)::value;
   float amax = 0.0f;
 #pragma unroll
   for (int r = 0; r < 32; r++) {
-    sc[r] = xs[r] / rsc[(i0 + r) * NG + g];
+    const int ig = (i0 + r) * NG + g;
+    sc[r] = FAST ? div_half(xs[r], rsc[ig], rinv[ig]) : xs[r] / rsc[ig];
     const float a = fabsf(sc[r]);
     amax = a > amax ? a : amax;
   }
@@ -464,8 +503,9 @@ __device__ __forceinline__ void encode_fast128(const PoolDev &P, const float *__
   const float qmax = two ? 3.0f : (float)((1 << (W - 1)) - 1);
   const float t0 = am / (qmax * 1.0f);
   const float c0 = fp16_scale(t0 > 0.0f ? t0 : 0.0f, nullptr);
-  auto zq = [&](float s, float cdiv) -> float {
-    const float y = s / cdiv;
+  const float c0inv = 1.0f / c0;
+  auto zq = [&](float s, float cdiv, float cinv) -> float {
+    const float y = FAST ? div_half(s, cdiv, cinv) : s / cdiv;
     if (two) return (y >= 0.0f ? 1.0f : -1.0f) * (fabsf(y) >= 2.0f ? 3.0f : 1.0f);
     float z = __builtin_rintf(y);
     z = z > -qmax ? z : -qmax;
@@ -480,7 +520,7 @@ __device__ __forceinline__ void encode_fast128(const PoolDev &P, const float *__
     for (int rr = 0; rr < 16; rr++) {
       const int r = 16 * mb + rr, i = i0 + r;
       const float wsq = (wl[i] * wl[i]) * 1.0f;
-      const float z = zq(sc[r], c0);
+      const float z = zq(sc[r], c0, c0inv);
       const float v = (rsc[i * NG + g] * 1.0f) * z;
       bn += (wsq * v) * xs[r];
       bd += wsq * (v * v);
@@ -499,6 +539,7 @@ __device__ __forceinline__ void encode_fast128(const PoolDev &P, const float *__
   const float denc = den < 1e-30f ? 1e-30f : den;
   uint32_t chb;
   const float c = fp16_scale(den > 0.0f ? num / denc : c0, &chb);
+  const float cinv = 1.0f / c;
   const int colbase = P.columns[h];
   if (hf == 0 && colbase >= 0) put_page_half(page, colbase + 2 * (int64_t)j, chb);
   // final codes; quads of lanes assemble each 4-value group
@@ -506,7 +547,7 @@ __device__ __forceinline__ void encode_fast128(const PoolDev &P, const float *__
 #pragma unroll
   for (int r = 0; r < 32; r++) {
     const int i = i0 + r;
-    const float z = zq(sc[r], c);
+    const float z = zq(sc[r], c, cinv);
     const uint32_t code = two ? (uint32_t)(((int)z + 3) / 2) : (uint32_t)((int)z + L);
     const uint32_t c1 = quad_perm<0xB1>(code), c2 = quad_perm<0x4E>(code), c3 = quad_perm<0x1B>(code);  // lane ^ 1, 2, 3
     if ((tid & 3) == 0) {
@@ -514,6 +555,9 @@ __device__ __forceinline__ void encode_fast128(const PoolDev &P, const float *__
       lds_put_bytes(stage, shift + group_pos(orel[i], stride, 16, j, W), word, W / 2);
     }
   }
+  };
+  if (ieee) columns(BoolTag<false>{});
+  else columns(BoolTag<true>{});
   __syncthreads();
   stage_out(page + code_start, code_bytes, stage, tid, 512);
 }
@@ -3757,27 +3801,13 @@ __device__ __forceinline__ void fmt_write_codes(uint8_t *row, int j0, int W, uin
   for (int t = 0; t < W / 2; t++) p[t] = (uint8_t)(w >> (8 * t));
 }
 
-// x / d rounded to nearest for a divisor d that is an fp16 value (at most 11
-// significant bits), from d's correctly rounded reciprocal inv = 1 / d:
-// q0 = x inv, then one correction with the exact residual x - q0 d.  For
-// every pair of significands (x any of the 2^23, d any of the 2^10) the
-// result equals the IEEE quotient (checked exhaustively on the CPU);
-// exponents only scale it, so it is exact while x, the residual and the
-// quotient stay normal: |x| >= 2^-100 and |q0| <= 2^126 (`ok` is cleared
-// otherwise).
+// div_half with its range condition: `ok` is cleared when x or the
+// quotient leaves the range where div_half equals the IEEE quotient.
 __device__ __forceinline__ float div_fp16_divisor(float x, float d, float inv, bool &ok) {
-  const float q0 = x * inv;
-  const float r = fmaf(-q0, d, x);
-  const float q1 = fmaf(r, inv, q0);
-  ok = ok && fabsf(x) >= 0x1p-100f && fabsf(q0) <= 0x1p+126f;
-  return q1;
+  ok = ok && fabsf(x) >= 0x1p-100f && fabsf(x * inv) <= 0x1p+126f;
+  return div_half(x, d, inv);
 }
 
-// compile-time switch for the two forms of a loop
-template <bool B>
-struct BoolTag {
-  static constexpr bool value = B;
-};
 
 template <int MODE, int KIND>  // KIND: the format (F.kind), fixed per instantiation
 __global__ __launch_bounds__(256) void format_kernel(FmtDev F, StepDev S) {
@@ -4451,8 +4481,8 @@ int sq_encode(const sq_pool *pool, const float *state, const void *slots, int32_
   size_t lds = (size_t)stage_bytes(pool) + (size_t)((K * NG + 3) & ~3) * 4 + 16;
   if (split > 1) lds += (size_t)split * 4 * V * 4 + (size_t)(K / 16) * 2 * V * 4;
   if (!pool->kda && pool->storage == 0 && K == 128 && V == 128 && pd.G == 32) {
-    // rows [K][4] | w [K] | row offsets [K] | column maxima [4][V] | block sums [K/16][2][V]
-    const size_t fl = (size_t)stage_bytes(pool) + (size_t)(K * 4 + 2 * K + 4 * V + (K / 16) * 2 * V) * 4;
+    // rows [K][4] | w [K] | row offsets [K] | column maxima [4][V] | block sums [K/16][2][V] | 1/rows [K][4]
+    const size_t fl = (size_t)stage_bytes(pool) + (size_t)(K * 4 + 2 * K + 4 * V + (K / 16) * 2 * V + K * 4) * 4;
     hipLaunchKernelGGL(encode128_kernel, dim3((unsigned)(batch * pool->heads)), dim3(512), fl, (hipStream_t)stream,
                        pd, state, slots, slots_dtype);
     return check_launch("encode128_kernel");
