@@ -2965,6 +2965,14 @@ struct PrefillDev {
 // (t % 4 == 0) stay contiguous.
 __device__ __forceinline__ int tcol(int r, int t) { return (((t >> 3) ^ (r >> 3)) & 7) * 8 + (t & 7); }
 
+// Position of index c (a key column of the k and q tiles, a token column of
+// the k-column, P and M tiles) within its 32-wide block: the runs c = 16 a +
+// 4 b .. + 3 are stored at 8 b + 4 a, so the 8 entries at 32 m + 8 b .. + 7
+// are indices 32 m + 4 b .. + 3 and 32 m + 16 + 4 b .. + 3 -- the k-slot
+// order in which an operand built from two accumulator tiles lists them
+// (split8), read with one 16-byte load.  Runs of 4 stay contiguous.
+__device__ __forceinline__ int pcol(int c) { return (c & ~31) + 8 * ((c >> 2) & 3) + 4 * ((c >> 4) & 1) + (c & 3); }
+
 // Four consecutive tokens of one column of a token-major bf16 tile
 // [t][P136], with gfx950's transposing LDS load (ds_read_b64_tr_b16).
 // Within each 16-lane row of the wave the instruction reads 8 bytes at
@@ -3014,7 +3022,17 @@ __device__ __forceinline__ float wave_scan(float x) {
 __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
+// 16 x 16 x 16 product: lane l holds A[l % 16][4 (l / 16) + j] and
+// B[4 (l / 16) + j][l % 16], j = 0..3, and gets D[4 (l / 16) + j][l % 16]:
+// an accumulator tile is a B operand as it is, and the A operand of its
+// transpose
+typedef short bf16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ f32x4 mfma16(bf16x4 a, bf16x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
 __device__ __forceinline__ bf16x8 ld8(const uint8_t *lds, int byte) { return *(const bf16x8 *)(lds + byte); }
+__device__ __forceinline__ bf16x4 ld4(const uint8_t *lds, int byte) { return *(const bf16x4 *)(lds + byte); }
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ float bf2f(uint16_t x) { return __uint_as_float((uint32_t)x << 16); }
 
 // two values rounded to bf16 (nearest even) and packed, a in the low half:
@@ -3031,37 +3049,33 @@ __device__ __forceinline__ void split4(const float x[4], uint2 &hi, uint2 &lo) {
   split2(x[0], x[1], hi.x, lo.x);
   split2(x[2], x[3], hi.y, lo.y);
 }
-
-// MFMA operand (hi and lo bf16 halves) of a 32-row chunk held as two
-// accumulator tiles: x0 = rows 0-15, x1 = rows 16-31, this lane's values at
-// rows 4 q4 + r, column c16.  The operand lane (c16, q4) needs rows
-// 8 q4 .. 8 q4 + 7 of column c16: as B that is B[k][c16], as A the row c16
-// of the transpose.  Packed pairs move between the 16-lane rows with
-// v_permlane32_swap (upper half of the first operand <-> lower half of the
-// second) and v_permlane16_swap (odd rows of the first <-> even rows of the
-// second); no LDS round trip.
-__device__ __forceinline__ void to_operand(const f32x4 &x0, const f32x4 &x1, bf16x8 &hi, bf16x8 &lo) {
-  uint32_t h[2][2], l[2][2];  // [tile][pair]
-#pragma unroll
-  for (int p = 0; p < 2; p++) {
-    split2(x0[2 * p], x0[2 * p + 1], h[0][p], l[0][p]);
-    split2(x1[2 * p], x1[2 * p + 1], h[1][p], l[1][p]);
-  }
-  auto conv = [](const uint32_t (&t)[2][2]) {
-    uint32_t o[4];
-#pragma unroll
-    for (int p = 0; p < 2; p++) {
-      // [t0 rows 0,1 | t1 rows 0,1] and [t0 rows 2,3 | t1 rows 2,3]
-      const auto s = __builtin_amdgcn_permlane32_swap(t[0][p], t[1][p], false, false);
-      // [t0 r0, t0 r2, t1 r0, t1 r2] and [t0 r1, t0 r3, t1 r1, t1 r3]
-      const auto u = __builtin_amdgcn_permlane16_swap(s[0], s[1], false, false);
-      o[p] = u[0];      // elements 2p, 2p + 1: rows 8 q4 + 2p, + 1
-      o[2 + p] = u[1];  // elements 4 + 2p, 5 + 2p
-    }
-    return __builtin_bit_cast(bf16x8, make_uint4(o[0], o[1], o[2], o[3]));
-  };
-  hi = conv(h);
-  lo = conv(l);
+// an accumulator tile's four values as hi/lo 16 x 16 x 16 operands
+__device__ __forceinline__ void split4x(const f32x4 &x, bf16x4 &hi, bf16x4 &lo) {
+  uint2 h, l;
+  split2(x[0], x[1], h.x, l.x);
+  split2(x[2], x[3], h.y, l.y);
+  hi = __builtin_bit_cast(bf16x4, h);
+  lo = __builtin_bit_cast(bf16x4, l);
+}
+// The 32 k-slots of a 16 x 16 x 32 product are summed in any order, so both
+// operands may list them in the same permuted order.  Here slot e of lane
+// group q4 = l / 16 is row 4 q4 + e of a 32-row block for e < 4 and row
+// 16 + 4 q4 + e - 4 for e >= 4: a block held as two accumulator tiles x0
+// (rows 0-15) and x1 (rows 16-31) is then an operand as it is (split into
+// hi/lo bf16, no lane exchange), and the other operand's LDS tile stores
+// its columns in that order (pcol).
+__device__ __forceinline__ void split8(const f32x4 &x0, const f32x4 &x1, bf16x8 &hi, bf16x8 &lo) {
+  uint32_t h[4], l[4];
+  split2(x0[0], x0[1], h[0], l[0]);
+  split2(x0[2], x0[3], h[1], l[1]);
+  split2(x1[0], x1[1], h[2], l[2]);
+  split2(x1[2], x1[3], h[3], l[3]);
+  hi = __builtin_bit_cast(bf16x8, make_uint4(h[0], h[1], h[2], h[3]));
+  lo = __builtin_bit_cast(bf16x8, make_uint4(l[0], l[1], l[2], l[3]));
+}
+__device__ __forceinline__ bf16x8 cat8(bf16x4 a, bf16x4 b) {
+  return __builtin_bit_cast(bf16x8, make_uint4(__builtin_bit_cast(uint2, a).x, __builtin_bit_cast(uint2, a).y,
+                                               __builtin_bit_cast(uint2, b).x, __builtin_bit_cast(uint2, b).y));
 }
 
 // lane Q's value of each quad in all four of its lanes (DPP quad_perm [Q,Q,Q,Q])
@@ -3117,9 +3131,18 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
 #pragma clang fp contract(off)
   extern __shared__ __align__(16) uint8_t smem[];
   const int H = D.H;
-  const int h = blockIdx.x % H;
-  const int b = blockIdx.x / H;
-  const int hk = h / (H / D.HK);
+  // Workgroups are dealt to the 8 XCDs round-robin (x mod 8).  The G value
+  // heads that share a key head read the same q and k rows, so they are
+  // placed on one XCD (x, x + 8, ..., one L2) when the grid divides evenly.
+  int x = blockIdx.x;
+  const int G = H / D.HK;
+  if (G > 1 && gridDim.x % (8 * G) == 0) {
+    const int slot = x >> 3;
+    x = ((x & 7) + 8 * (slot / G)) * G + slot % G;
+  }
+  const int h = x % H;
+  const int b = x / H;
+  const int hk = h / G;
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, q4 = l >> 4, c16 = l & 15;
   // sequence bounds as wave-uniform values (addresses formed from them stay scalar)
   const int t0 = __builtin_amdgcn_readfirstlane(D.cu[b]), len = __builtin_amdgcn_readfirstlane(D.cu[b + 1]) - t0;
@@ -3139,8 +3162,8 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
   // T entry (t, s) as hi/lo bf16 next to its fp32 value
   auto put_t = [&](int t, int s, float x) {
     const __bf16 hi = (__bf16)x;
-    ((__bf16 *)Tb)[t * P72 + s] = hi;
-    ((__bf16 *)Tb)[PC * P72 + t * P72 + s] = (__bf16)(x - (float)hi);
+    ((__bf16 *)Tb)[t * P72 + pcol(s)] = hi;
+    ((__bf16 *)Tb)[PC * P72 + t * P72 + pcol(s)] = (__bf16)(x - (float)hi);
   };
 
   // ---- state S[d][j] of this wave's columns: tile dt holds rows d = 16 dt + 4 q4 + r, column jw + c16
@@ -3218,16 +3241,23 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
       const int idx = tid + NT * it, t = idx >> 4, d8 = (idx & 15) * 8;
       const uint4 zero = make_uint4(0u, 0u, 0u, 0u);
       const uint4 kv = t < n ? F.k[it] : zero, qv = t < n ? F.q[it] : zero, vv = t < n ? F.v[it] : zero;
-      *(uint4 *)(Kc + (t * P136 + d8) * 2) = kv;
-      *(uint4 *)(Qc + (t * P136 + d8) * 2) = qv;
+      // key columns d8 .. d8 + 3 and d8 + 4 .. d8 + 7 at their permuted places
+      *(uint2 *)(Kc + (t * P136 + pcol(d8)) * 2) = make_uint2(kv.x, kv.y);
+      *(uint2 *)(Kc + (t * P136 + pcol(d8 + 4)) * 2) = make_uint2(kv.z, kv.w);
+      *(uint2 *)(Qc + (t * P136 + pcol(d8)) * 2) = make_uint2(qv.x, qv.y);
+      *(uint2 *)(Qc + (t * P136 + pcol(d8 + 4)) * 2) = make_uint2(qv.z, qv.w);
       *(uint4 *)(Vc + (t * P136 + d8) * 2) = vv;
-      const uint16_t *ke = (const uint16_t *)&kv, *qe = (const uint16_t *)&qv;
+      // squared norms of the 8 values, two bf16 products per v_dot2_f32_bf16
       float sk = 0.f, sq = 0.f;
+      {
+        const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w}, qw[4] = {qv.x, qv.y, qv.z, qv.w};
 #pragma unroll
-      for (int e = 0; e < 8; e++) {
-        const float fk = bf2f(ke[e]), fq = bf2f(qe[e]);
-        sk = fmaf(fk, fk, sk);
-        sq = fmaf(fq, fq, sq);
+        for (int e = 0; e < 4; e++) {
+          sk = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, kw[e]), __builtin_bit_cast(bf16x2, kw[e]),
+                                               sk, false);
+          sq = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, qw[e]), __builtin_bit_cast(bf16x2, qw[e]),
+                                               sq, false);
+        }
       }
       {
         // k columns: the wave's four 16-lane rows hold tokens t0 .. t0 + 3
@@ -3235,7 +3265,7 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
         // (key rows d8 + 2r, d8 + 2r + 1) of all four tokens, stored as two
         // 8-byte runs of consecutive tokens
         const int rr = (tid >> 4) & 3, t0 = t - rr, d = d8 + 2 * rr;
-        const int o0 = (d * P72 + tcol(d, t0)) * 2;
+        const int o0 = (d * P72 + tcol(d, pcol(t0))) * 2;
         uint32_t x[4] = {kv.x, kv.y, kv.z, kv.w};
         rows_transpose4(x);
         *(uint2 *)(Kt + o0) = make_uint2(__builtin_amdgcn_perm(x[1], x[0], 0x05040100u),
@@ -3261,7 +3291,7 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
         const float u = lg + dt_h;
         const float sp = u > 20.0f ? u : __logf(1.0f + __expf(u < 20.0f ? u : 20.0f));
         lg = -ea_h * sp;
-        bt = 1.0f / (1.0f + __expf(-bt));
+        bt = __builtin_amdgcn_rcpf(1.0f + __expf(-bt));
       }
       lg = wave_scan(lg);  // inclusive prefix sum of the log decays over the 64 tokens
       sm[SM_LC * 64 + l] = lg;
@@ -3273,8 +3303,8 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
     lds_barrier();
     if (tid < 64) {
       const int t = tid;
-      const float nk = D.normalize ? 1.0f / __builtin_sqrtf(sm[SM_KSQ * 64 + t] + 1e-6f) : 1.0f;
-      const float nq = (D.normalize ? 1.0f / __builtin_sqrtf(sm[SM_QSQ * 64 + t] + 1e-6f) : 1.0f) * D.scale;
+      const float nk = D.normalize ? __builtin_amdgcn_rsqf(sm[SM_KSQ * 64 + t] + 1e-6f) : 1.0f;
+      const float nq = (D.normalize ? __builtin_amdgcn_rsqf(sm[SM_QSQ * 64 + t] + 1e-6f) : 1.0f) * D.scale;
       const float lc = sm[SM_LC * 64 + t], lcC = sm[SM_LC * 64 + 63];
       const float gam = __expf(lc);
       sm[SM_NK * 64 + t] = nk;
@@ -3325,13 +3355,13 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
           const float na[4] = {-av[0], -av[1], -av[2], -av[3]};
           uint2 ah, al;
           split4(na, ah, al);
-          *(uint2 *)(Tb + (t * P72 + s0) * 2) = ah;
-          *(uint2 *)(Tb + PC * P72 * 2 + (t * P72 + s0) * 2) = al;
+          *(uint2 *)(Tb + (t * P72 + pcol(s0)) * 2) = ah;
+          *(uint2 *)(Tb + PC * P72 * 2 + (t * P72 + pcol(s0)) * 2) = al;
         }
         uint2 hi, lo;
         split4(pv, hi, lo);
-        *(uint2 *)(Pl + (t * P72 + s0) * 2) = hi;
-        *(uint2 *)(Pl + PC * P72 * 2 + (t * P72 + s0) * 2) = lo;
+        *(uint2 *)(Pl + (t * P72 + pcol(s0)) * 2) = hi;
+        *(uint2 *)(Pl + PC * P72 * 2 + (t * P72 + pcol(s0)) * 2) = lo;
       };
       // T_ii = (I + A_ii)^{-1}, diagonal block i by forward substitution on
       // the wave that computed A_ii (no barrier: the block is its own).
@@ -3368,12 +3398,13 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
     }
     // ---- K S0 (rows t, this wave's columns), consumed at once by
     // R = beta (V - Gamma nk K S0), and diag(nq Gamma) (S0^T Q^T), the first
-    // term of O^T; S0 (hi/lo) is the shared operand, k and q enter exactly
+    // term of O^T; S0 (hi/lo, key rows in the permuted slot order of split8)
+    // is the shared operand, k and q enter exactly
     f32x4 R[4], oq[4];
     {
       bf16x8 sh[4], sl[4];
 #pragma unroll
-      for (int kc = 0; kc < 4; kc++) to_operand(S[2 * kc], S[2 * kc + 1], sh[kc], sl[kc]);
+      for (int kc = 0; kc < 4; kc++) split8(S[2 * kc], S[2 * kc + 1], sh[kc], sl[kc]);
 #pragma unroll
       for (int tt = 0; tt < 4; tt++) {
         f32x4 ak = {0.f, 0.f, 0.f, 0.f};
@@ -3412,57 +3443,72 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
 
     // ---- Delta by blocks of 16 tokens, in this wave's registers (no barrier):
     // D_i = T_ii (R_i + sum_{k<i} (-A_ik) D_k), both products from M = [T_ii
-    // on the diagonal, -A_ik below it]; the B operand of a 32-token pair
-    // holds the blocks solved so far and zeros.  Delta' = diag(nk Gamma_C /
-    // Gamma) Delta.
-    f32x4 dl[4], dp[4];
-    bf16x8 bh[2], bl[2];  // [D_0; D_1] (pair 0) and [D_2; 0] (pair 1) as B operands
+    // on the diagonal, -A_ik below it].  A block that is solved is split
+    // into hi/lo bf16 once, in place: as the B operand of 16 x 16 x 16
+    // products (rows 4 q4 .. 4 q4 + 3 of column c16: the accumulator layout
+    // itself) and, paired with its neighbour, of 16 x 16 x 32 products in
+    // the permuted slot order.  Delta' = diag(nk Gamma_C / Gamma) Delta.
+    f32x4 dp[4];
+    bf16x8 ph01, pl01, ph23, pl23;  // [D_0; D_1] and [D_2; D_3] (hi, lo), permuted slots
     {
       const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-      auto mprod = [&](int i, int pair, bf16x8 xh, bf16x8 xl, f32x4 acc) {
-        const int o = ((16 * i + c16) * P72 + 32 * pair + 8 * q4) * 2;
+      bf16x4 xh[4], xl[4];
+      // acc + M[16 i .. 16 i + 15][16 k .. 16 k + 15] x (hi/lo pairs hi*hi + hi*lo + lo*hi)
+      auto mone = [&](int i, int k, bf16x4 bh, bf16x4 bl, f32x4 acc) {
+        const int o = ((16 * i + c16) * P72 + pcol(16 * k + 4 * q4)) * 2;
+        const bf16x4 mh = ld4(Tb, o), ml = ld4(Tb, PC * P72 * 2 + o);
+        acc = mfma16(mh, bh, acc);
+        acc = mfma16(mh, bl, acc);
+        return mfma16(ml, bh, acc);
+      };
+      // acc + M[16 i .. 16 i + 15][0 .. 31] [D_0; D_1]
+      auto mpair = [&](int i, f32x4 acc) {
+        const int o = ((16 * i + c16) * P72 + 8 * q4) * 2;
         const bf16x8 mh = ld8(Tb, o), ml = ld8(Tb, PC * P72 * 2 + o);
-        acc = mfma(mh, xh, acc);
-        acc = mfma(mh, xl, acc);
-        return mfma(ml, xh, acc);
+        acc = mfma(mh, ph01, acc);
+        acc = mfma(mh, pl01, acc);
+        return mfma(ml, ph01, acc);
       };
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         f32x4 acc = R[i];
-        if (i >= 1) acc = mprod(i, 0, bh[0], bl[0], acc);
-        if (i == 3) acc = mprod(i, 1, bh[1], bl[1], acc);
-        bf16x8 xh, xl;
-        if (i & 1) to_operand(zero, acc, xh, xl);
-        else to_operand(acc, zero, xh, xl);
-        const f32x4 d = mprod(i, i >> 1, xh, xl, zero);
-        dl[i] = d;
+        if (i == 1) acc = mone(1, 0, xh[0], xl[0], acc);
+        if (i >= 2) acc = mpair(i, acc);
+        if (i == 3) acc = mone(3, 2, xh[2], xl[2], acc);
+        bf16x4 ah, al;
+        split4x(acc, ah, al);
+        const f32x4 d = mone(i, i, ah, al, zero);
+        split4x(d, xh[i], xl[i]);
+        if (i == 1) {
+          ph01 = cat8(xh[0], xh[1]);
+          pl01 = cat8(xl[0], xl[1]);
+        }
+        if (i == 3) {
+          ph23 = cat8(xh[2], xh[3]);
+          pl23 = cat8(xl[2], xl[3]);
+        }
         const float4 kd = *(const float4 *)(sm + SM_KD * 64 + 16 * i + 4 * q4);
         dp[i][0] = d[0] * kd.x;
         dp[i][1] = d[1] * kd.y;
         dp[i][2] = d[2] * kd.z;
         dp[i][3] = d[3] * kd.w;
-        if (i == 0) to_operand(d, zero, bh[0], bl[0]);
-        if (i == 1) to_operand(dl[0], d, bh[0], bl[0]);
-        if (i == 2) to_operand(d, zero, bh[1], bl[1]);
       }
     }
-    // ---- O^T = diag(nq Gamma) (S0^T Q^T) + Delta^T P^T: rows j of this wave, column t
+    // ---- O^T = diag(nq Gamma) (S0^T Q^T) + Delta^T P^T: rows j of this wave,
+    // column t; a split pair [D_2kc; D_2kc+1] is the A operand of its
+    // transpose as it is, and token pairs past the tile are causal zeros
     {
-      bf16x8 dh[2], dlo[2];
-      dh[0] = bh[0];  // [D_0; D_1], split by the block solve
-      dlo[0] = bl[0];
-      to_operand(dl[2], dl[3], dh[1], dlo[1]);
 #pragma unroll
       for (int tt = 0; tt < 4; tt++) {
         const int t = 16 * tt + c16;
         f32x4 acc = oq[tt];
 #pragma unroll
-        for (int kc = 0; kc < 2; kc++) {
+        for (int kc = 0; kc <= (tt >> 1); kc++) {
           const int o = (t * P72 + 32 * kc + 8 * q4) * 2;
           const bf16x8 ph = ld8(Pl, o), pl = ld8(Pl, PC * P72 * 2 + o);
-          acc = mfma(dh[kc], ph, acc);
-          acc = mfma(dh[kc], pl, acc);
-          acc = mfma(dlo[kc], ph, acc);
+          acc = mfma(kc ? ph23 : ph01, ph, acc);
+          acc = mfma(kc ? ph23 : ph01, pl, acc);
+          acc = mfma(kc ? pl23 : pl01, ph, acc);
         }
         if (t < n) {
           const float o4[4] = {acc[0], acc[1], acc[2], acc[3]};
@@ -3476,11 +3522,12 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    // ---- S <- Gamma_C S0 + K^T Delta' (rows d, this wave's columns)
+    // ---- S <- Gamma_C S0 + K^T Delta' (rows d, this wave's columns; tokens
+    // in the permuted slot order, two 4-token runs of the k column each)
     {
       bf16x8 eh[2], el[2];
-      to_operand(dp[0], dp[1], eh[0], el[0]);
-      to_operand(dp[2], dp[3], eh[1], el[1]);
+      split8(dp[0], dp[1], eh[0], el[0]);
+      split8(dp[2], dp[3], eh[1], el[1]);
       const float gC = __expf(sm[SM_LC * 64 + 63]);
 #pragma unroll
       for (int dt = 0; dt < 8; dt++) {
