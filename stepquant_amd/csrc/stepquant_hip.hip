@@ -3315,6 +3315,7 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
     }
     lds_barrier();
 
+    f32x4 R[4], oq[4];
     // ---- A and P tiles (t-tile tw, s-tile ns) with ns <= tw:
     // A_ts = beta_t nk_t nk_s (Gamma_t/Gamma_s) k_t.k_s (s < t), P_ts likewise with q_t (s <= t).
     // The ten tiles go at most two to a wave; tiles above the diagonal stay
@@ -3383,60 +3384,61 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
 #pragma unroll
         for (int k = 0; k < 4; k++) put_t(16 * i + 4 * k + g, 16 * i + jc, acc[k]);
       };
-      // waves 0-3: diagonal tile i = w and its T_ii; waves 4-7: the six
-      // tiles below the diagonal (w and w + 4 share a SIMD)
-      switch (__builtin_amdgcn_readfirstlane(w)) {
-        case 0: ap_tile(0, 0); diag_solve(0); break;
-        case 1: ap_tile(1, 1); diag_solve(1); break;
-        case 2: ap_tile(2, 2); diag_solve(2); break;
-        case 3: ap_tile(3, 3); diag_solve(3); break;
-        case 4: ap_tile(3, 0); ap_tile(3, 1); break;
-        case 5: ap_tile(3, 2); ap_tile(1, 0); break;
-        case 6: ap_tile(2, 0); break;
-        default: ap_tile(2, 1); break;
-      }
-    }
-    // ---- K S0 (rows t, this wave's columns), consumed at once by
-    // R = beta (V - Gamma nk K S0), and diag(nq Gamma) (S0^T Q^T), the first
-    // term of O^T; S0 (hi/lo, key rows in the permuted slot order of split8)
-    // is the shared operand, k and q enter exactly
-    f32x4 R[4], oq[4];
-    {
+      // ---- K S0 (rows t, this wave's columns), consumed at once by
+      // R = beta (V - Gamma nk K S0), and diag(nq Gamma) (S0^T Q^T), the
+      // first term of O^T; S0 (hi/lo, key rows in the permuted slot order of
+      // split8) is the shared operand, k and q enter exactly.  Independent
+      // of the A/P tiles, so each wave's tiles and these products share one
+      // scheduling region and their latencies overlap.
       bf16x8 sh[4], sl[4];
 #pragma unroll
       for (int kc = 0; kc < 4; kc++) split8(S[2 * kc], S[2 * kc + 1], sh[kc], sl[kc]);
+      auto ks_part = [&]() {
 #pragma unroll
-      for (int tt = 0; tt < 4; tt++) {
-        f32x4 ak = {0.f, 0.f, 0.f, 0.f};
+        for (int tt = 0; tt < 4; tt++) {
+          f32x4 ak = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int kc = 0; kc < 4; kc++) {
-          const bf16x8 kr = ld8(Kc, ((16 * tt + c16) * P136 + 32 * kc + 8 * q4) * 2);
-          ak = mfma(kr, sh[kc], ak);
-          ak = mfma(kr, sl[kc], ak);
+          for (int kc = 0; kc < 4; kc++) {
+            const bf16x8 kr = ld8(Kc, ((16 * tt + c16) * P136 + 32 * kc + 8 * q4) * 2);
+            ak = mfma(kr, sh[kc], ak);
+            ak = mfma(kr, sl[kc], ak);
+          }
+          const int ta = 16 * tt + 4 * q4;
+          const float4 be = *(const float4 *)(sm + SM_BETA * 64 + ta), gk = *(const float4 *)(sm + SM_GK * 64 + ta);
+          const float be4[4] = {be.x, be.y, be.z, be.w}, gk4[4] = {gk.x, gk.y, gk.z, gk.w};
+          const tr4_t vr = col4(Vc, ta, jw, c16);  // v of tokens ta .. ta + 3, column jw + c16
+          const float v4[4] = {bf2f((uint16_t)vr[0]), bf2f((uint16_t)vr[1]), bf2f((uint16_t)vr[2]),
+                               bf2f((uint16_t)vr[3])};
+#pragma unroll
+          for (int r = 0; r < 4; r++) R[tt][r] = be4[r] * (v4[r] - gk4[r] * ak[r]);
         }
-        const int ta = 16 * tt + 4 * q4;
-        const float4 be = *(const float4 *)(sm + SM_BETA * 64 + ta), gk = *(const float4 *)(sm + SM_GK * 64 + ta);
-        const float be4[4] = {be.x, be.y, be.z, be.w}, gk4[4] = {gk.x, gk.y, gk.z, gk.w};
-        const tr4_t vr = col4(Vc, ta, jw, c16);  // v of tokens ta .. ta + 3, column jw + c16
-        const float v4[4] = {bf2f((uint16_t)vr[0]), bf2f((uint16_t)vr[1]), bf2f((uint16_t)vr[2]),
-                             bf2f((uint16_t)vr[3])};
+      };
+      auto qs_part = [&]() {
 #pragma unroll
-        for (int r = 0; r < 4; r++) R[tt][r] = be4[r] * (v4[r] - gk4[r] * ak[r]);
-        __builtin_amdgcn_sched_barrier(0);  // one tile's operand loads in flight at a time
-      }
+        for (int tt = 0; tt < 4; tt++) {
+          f32x4 aq = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int tt = 0; tt < 4; tt++) {
-        f32x4 aq = {0.f, 0.f, 0.f, 0.f};
+          for (int kc = 0; kc < 4; kc++) {
+            const bf16x8 qr = ld8(Qc, ((16 * tt + c16) * P136 + 32 * kc + 8 * q4) * 2);
+            aq = mfma(sh[kc], qr, aq);
+            aq = mfma(sl[kc], qr, aq);
+          }
+          const float qgt = sm[SM_QG * 64 + 16 * tt + c16];
 #pragma unroll
-        for (int kc = 0; kc < 4; kc++) {
-          const bf16x8 qr = ld8(Qc, ((16 * tt + c16) * P136 + 32 * kc + 8 * q4) * 2);
-          aq = mfma(sh[kc], qr, aq);
-          aq = mfma(sl[kc], qr, aq);
+          for (int r = 0; r < 4; r++) oq[tt][r] = aq[r] * qgt;
         }
-        const float qgt = sm[SM_QG * 64 + 16 * tt + c16];
-#pragma unroll
-        for (int r = 0; r < 4; r++) oq[tt][r] = aq[r] * qgt;
-        __builtin_amdgcn_sched_barrier(0);
+      };
+      // waves 0-3: diagonal tile i = w and its T_ii; waves 4-7: the six
+      // tiles below the diagonal (w and w + 4 share a SIMD)
+      switch (__builtin_amdgcn_readfirstlane(w)) {
+        case 0: ap_tile(0, 0); ks_part(); diag_solve(0); qs_part(); break;
+        case 1: ap_tile(1, 1); ks_part(); diag_solve(1); qs_part(); break;
+        case 2: ap_tile(2, 2); ks_part(); diag_solve(2); qs_part(); break;
+        case 3: ap_tile(3, 3); ks_part(); diag_solve(3); qs_part(); break;
+        case 4: ap_tile(3, 0); ks_part(); ap_tile(3, 1); qs_part(); break;
+        case 5: ap_tile(3, 2); ks_part(); ap_tile(1, 0); qs_part(); break;
+        case 6: ap_tile(2, 0); ks_part(); qs_part(); break;
+        default: ap_tile(2, 1); ks_part(); qs_part(); break;
       }
     }
     lds_barrier();
