@@ -3321,13 +3321,14 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
     // The ten tiles go at most two to a wave; tiles above the diagonal stay
     // zero.
     {
-      auto ap_tile = [&](int tw, int ns) {
+      // (the A or the P half alone when doA / doP is false)
+      auto ap_tile = [&](int tw, int ns, bool doA = true, bool doP = true) {
         const int t = 16 * tw + c16;
         bf16x8 bk[4], bq[4];
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
-          bk[ks] = ld8(Kc, (t * P136 + 8 * q4 + 32 * ks) * 2);
-          bq[ks] = ld8(Qc, (t * P136 + 8 * q4 + 32 * ks) * 2);
+          if (doA) bk[ks] = ld8(Kc, (t * P136 + 8 * q4 + 32 * ks) * 2);
+          if (doP) bq[ks] = ld8(Qc, (t * P136 + 8 * q4 + 32 * ks) * 2);
         }
         const float lct = sm[SM_LC * 64 + t], bnt = sm[SM_BETA * 64 + t] * sm[SM_NK * 64 + t];
         const float nqt = sm[SM_NQ * 64 + t];
@@ -3335,8 +3336,8 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
           const bf16x8 a = ld8(Kc, ((16 * ns + c16) * P136 + 8 * q4 + 32 * ks) * 2);
-          aA = mfma(a, bk[ks], aA);
-          aP = mfma(a, bq[ks], aP);
+          if (doA) aA = mfma(a, bk[ks], aA);
+          if (doP) aP = mfma(a, bq[ks], aP);
         }
         const int s0 = 16 * ns + 4 * q4;
         const float4 lcs = *(const float4 *)(sm + SM_LC * 64 + s0);
@@ -3350,19 +3351,21 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
           av[r] = s < t ? (bnt * nk4[r]) * e * aA[r] : 0.0f;
           pv[r] = s <= t ? (nqt * nk4[r]) * e * aP[r] : 0.0f;
         }
-        if (ns == tw) {
+        if (doA && ns == tw) {
           *(float4 *)(AT + t * PA + s0) = make_float4(av[0], av[1], av[2], av[3]);
-        } else if (ns < tw) {  // -A of the block below the diagonal, as hi/lo
+        } else if (doA && ns < tw) {  // -A of the block below the diagonal, as hi/lo
           const float na[4] = {-av[0], -av[1], -av[2], -av[3]};
           uint2 ah, al;
           split4(na, ah, al);
           *(uint2 *)(Tb + (t * P72 + pcol(s0)) * 2) = ah;
           *(uint2 *)(Tb + PC * P72 * 2 + (t * P72 + pcol(s0)) * 2) = al;
         }
-        uint2 hi, lo;
-        split4(pv, hi, lo);
-        *(uint2 *)(Pl + (t * P72 + pcol(s0)) * 2) = hi;
-        *(uint2 *)(Pl + PC * P72 * 2 + (t * P72 + pcol(s0)) * 2) = lo;
+        if (doP) {
+          uint2 hi, lo;
+          split4(pv, hi, lo);
+          *(uint2 *)(Pl + (t * P72 + pcol(s0)) * 2) = hi;
+          *(uint2 *)(Pl + PC * P72 * 2 + (t * P72 + pcol(s0)) * 2) = lo;
+        }
       };
       // T_ii = (I + A_ii)^{-1}, diagonal block i by forward substitution on
       // the wave that computed A_ii (no barrier: the block is its own).
@@ -3429,16 +3432,18 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
         }
       };
       // waves 0-3: diagonal tile i = w and its T_ii; waves 4-7: the six
-      // tiles below the diagonal (w and w + 4 share a SIMD)
+      // tiles below the diagonal, two of them split into their A and P
+      // halves, so that each SIMD (waves w and w + 4) holds two and a half
+      // tile pairs and one diagonal solve
       switch (__builtin_amdgcn_readfirstlane(w)) {
         case 0: ap_tile(0, 0); ks_part(); diag_solve(0); qs_part(); break;
         case 1: ap_tile(1, 1); ks_part(); diag_solve(1); qs_part(); break;
         case 2: ap_tile(2, 2); ks_part(); diag_solve(2); qs_part(); break;
         case 3: ap_tile(3, 3); ks_part(); diag_solve(3); qs_part(); break;
-        case 4: ap_tile(3, 0); ks_part(); ap_tile(3, 1); qs_part(); break;
-        case 5: ap_tile(3, 2); ks_part(); ap_tile(1, 0); qs_part(); break;
-        case 6: ap_tile(2, 0); ks_part(); qs_part(); break;
-        default: ap_tile(2, 1); ks_part(); qs_part(); break;
+        case 4: ap_tile(3, 0); ks_part(); ap_tile(3, 1, true, false); qs_part(); break;
+        case 5: ap_tile(3, 2); ks_part(); ap_tile(1, 0, true, false); qs_part(); break;
+        case 6: ap_tile(2, 0); ks_part(); ap_tile(3, 1, false, true); qs_part(); break;
+        default: ap_tile(2, 1); ks_part(); ap_tile(1, 0, false, true); qs_part(); break;
       }
     }
     lds_barrier();
