@@ -3526,7 +3526,6 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
           if (out_aligned) store4_aligned(D.out, D.out_dtype, at, o4);
           else store4(D.out, D.out_dtype, at, o4);
         }
-
       }
     }
     // ---- S <- Gamma_C S0 + K^T Delta' (rows d, this wave's columns; tokens
@@ -3549,7 +3548,6 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
           acc = mfma(a, el[kc], acc);
         }
         S[dt] = acc;
-
       }
     }
     lds_barrier();  // the next chunk's staging overwrites the shared tiles
