@@ -24,14 +24,28 @@ def _close(got, ref, tol, what):
 @pytest.mark.parametrize("raw,normalize", [(False, True), (True, True), (False, False)])
 def test_prefill_against_sequential_oracle(raw, normalize):
     print(f"case raw={raw} normalize={normalize}", flush=True)
+    _prefill_case(raw, normalize, [130, 37, 64], [[50, 130], [37, 0], [10, 64]], [[6, 7], [8, 0], [9, 10]],
+                  [3, 0, 5], [3, 4, 5], (1, 2, 11))
+
+
+def test_prefill_key_head_pairs_on_one_xcd():
+    """4 sequences x 4 value heads over 2 key heads: the grid (16 workgroups)
+    divides into groups of 8 x 2, so the two value heads of a key head run as
+    workgroups x and x + 8; ragged lengths, a one-token sequence and
+    checkpoints inside and at the end of chunks."""
+    print("case grouped heads", flush=True)
+    _prefill_case(False, True, [100, 64, 1, 150], [[64, 100], [30, 64], [1, 0], [70, 128]],
+                  [[6, 7], [8, 9], [10, 0], [11, 13]], [3, 0, 5, 12], [3, 4, 5, 12], (1, 2, 14, 15))
+
+
+def _prefill_case(raw, normalize, lens, ck, ck_slots, init, slots, untouched):
     from stepquant_amd.kernels.pool import PackedStatePool
     H, HK, K, V = 4, 2, 128, 128
-    lens = [130, 37, 64]
     B = len(lens)
     cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
     T = int(cu[-1])
     oplan = make_plan("gdn", np.repeat(np.array([6, 4, 8, 6])[:, None], K, 1), seed=3)
-    pool = PackedStatePool(device_plan(oplan), 12, V)
+    pool = PackedStatePool(device_plan(oplan), 16, V)
     rng = np.random.default_rng(7 + raw + 2 * normalize)
     g = torch.Generator().manual_seed(11)
     scale = K ** -.5 if normalize else .05
@@ -51,18 +65,18 @@ def test_prefill_against_sequential_oracle(raw, normalize):
         gate = -torch.nn.functional.softplus(torch.randn(T, H, generator=g))
         beta = torch.sigmoid(torch.randn(T, H, generator=g))
         a_log = dt_bias = None
-    init = torch.tensor([3, 0, 5])  # the second sequence starts from zero
+    init = torch.tensor(init)  # slot 0: the sequence starts from zero
     x0 = torch.randn(B, H, K, V, generator=g) * .1
     pool.encode(x0.to(dev()), init.to(dev()))
     lay = O.layout(oplan, V)
     pages0 = pool.data.cpu().numpy()
     S0 = O.decode_page(pages0, init.numpy(), oplan, lay, V).astype(np.float64)
-    ck = np.array([[50, 130], [37, 0], [10, 64]])
-    ck_slots = torch.tensor([[6, 7], [8, 0], [9, 10]])
+    ck = np.array(ck)
+    ck_slots = torch.tensor(ck_slots)
     # q as float32 holding bf16 values: the kernel reads the same bf16 inputs and
     # the outputs come back in float32, so their error is the kernel's own
     out = pool.extend(q.float().to(dev()), k.to(dev()), v.to(dev()), gate.to(dev()), beta.to(dev()),
-                      torch.tensor([3, 4, 5]), torch.from_numpy(cu), checkpoints=torch.from_numpy(ck),
+                      torch.tensor(slots), torch.from_numpy(cu), checkpoints=torch.from_numpy(ck),
                       checkpoint_slots=ck_slots, init_slots=init, normalize=normalize, scale=scale,
                       a_log=None if a_log is None else a_log.to(dev()),
                       dt_bias=None if dt_bias is None else dt_bias.to(dev()))
@@ -85,7 +99,7 @@ def test_prefill_against_sequential_oracle(raw, normalize):
     O.encode_page(ck_state.reshape(B * 2, H, K, V), live, oplan, lay, ref_pages)
     for s in live[live > 0]:
         assert np.array_equal(pages[s], ref_pages[s]), f"slot {s} page differs"
-    for s in (1, 2, 11):
+    for s in untouched:
         assert not pages[s].any(), "untouched slots stay empty"
 
 
