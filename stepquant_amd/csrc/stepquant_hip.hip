@@ -3577,33 +3577,36 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
 // role of the upstream chunk kernel behind the reference's kernel_extend
 // (sglang/runtime.py:193-202) for Kimi-Linear pools.
 //
-// One workgroup of 512 threads per (sequence, head): thread (r, j) holds the
-// state column j for the 32 key rows 32 r .. 32 r + 31 in registers, so the
-// state never leaves the workgroup.  Tokens are staged 32 at a time into LDS
-// as fp32 rows (normalised k, q, the decays e^g and k e^g, v, beta), the next
-// block's raw inputs are fetched into registers while the current block
-// runs.  Per token: kd^T S partials over each thread's 32 rows, a barrier,
-// delta_j from the four row quarters, S = e^g S + k delta (one FMA per value
-// after the rank-1 product), q^T S partials, a barrier, one quarter writes
-// the outputs.  Every read of a token row in LDS is the same address across
-// a wave (all its lanes share r): broadcast, conflict-free.
+// One workgroup of 512 threads per (sequence, head): the four lanes of a
+// quad hold one state column j for the key rows 32 r .. 32 r + 31 (r the
+// lane's place in the quad) in registers, so the state never leaves the
+// workgroup and every per-token sum over key rows is a quad sum (two DPP
+// adds, no barrier).  Tokens are staged 32 at a time into LDS as fp32 rows
+// (normalised k, q, the decays e^g and k e^g, v, beta), the next block's raw
+// inputs are fetched into registers while the current block runs.  Per
+// token: kd^T S over the lane's 32 rows, the quad sum, delta_j, S = e^g S +
+// k delta (one FMA per value after the rank-1 product), q^T S, the quad sum,
+// one lane of the quad writes the output.  The key-channel rows are stored
+// as four 32-float segments 36 floats apart, so the four row quarters a wave
+// reads at once start in different banks.
 namespace kp {
 
 constexpr int NT = 512;
 constexpr int TB = 32;                        // tokens staged per block
 constexpr int KV = 128;                       // K = V = 128
-// LDS: per block row arrays [TB][128] f32: KD (k e^g), DC (e^g), KN (k), QN (q), VV (v);
-// BETA [TB]; partial sums [2][4][128]
+constexpr int SEGP = 36, ROWP = 4 * SEGP;     // segment and row pitch (floats) of the key-channel rows
+// LDS: per block key-channel rows [TB][ROWP] f32: KD (k e^g), DC (e^g), KN (k), QN (q);
+// VV [TB][128] (v); BETA [TB]
 constexpr int OFF_KD = 0;
-constexpr int OFF_DC = OFF_KD + TB * KV;
-constexpr int OFF_KN = OFF_DC + TB * KV;
-constexpr int OFF_QN = OFF_KN + TB * KV;
-constexpr int OFF_VV = OFF_QN + TB * KV;
+constexpr int OFF_DC = OFF_KD + TB * ROWP;
+constexpr int OFF_KN = OFF_DC + TB * ROWP;
+constexpr int OFF_QN = OFF_KN + TB * ROWP;
+constexpr int OFF_VV = OFF_QN + TB * ROWP;
 constexpr int OFF_BT = OFF_VV + TB * KV;
-constexpr int OFF_P1 = OFF_BT + TB;
-constexpr int OFF_P2 = OFF_P1 + 4 * KV;
-constexpr int LDS_FLOATS = OFF_P2 + 4 * KV;
+constexpr int LDS_FLOATS = OFF_BT + TB;
 constexpr int LDS_BYTES = LDS_FLOATS * 4;
+// place of channel c in a key-channel row
+__device__ __forceinline__ int kcol(int c) { return (c >> 5) * SEGP + (c & 31); }
 
 // Raw inputs of one staging thread for one block: token tt = tid >> 4,
 // channels c8 .. c8 + 7 (c8 = (tid & 15) * 8).
@@ -3631,6 +3634,12 @@ __device__ __forceinline__ float sum16(float x) {
   return x;
 }
 
+// sum over the four lanes of a quad, (x0 + x1) + (x2 + x3) in every lane
+__device__ __forceinline__ float quad_sum(float x) {
+  x += fast::dpp<0xB1>(x);  // quad_perm [1,0,3,2]
+  return x + fast::dpp<0x4E>(x);  // quad_perm [2,3,0,1]
+}
+
 __global__ __launch_bounds__(NT) void kda_prefill_kernel(pf::PrefillDev D) {
   extern __shared__ float lds[];
   const int H = D.H;
@@ -3639,7 +3648,7 @@ __global__ __launch_bounds__(NT) void kda_prefill_kernel(pf::PrefillDev D) {
   const int t0 = D.cu[b], len = D.cu[b + 1] - t0;
   if (len <= 0) return;  // whole workgroup
   const int tid = threadIdx.x;
-  const int j = tid & (KV - 1), r = tid >> 7;  // state column, row quarter (uniform per wave)
+  const int j = 16 * (tid >> 6) + ((tid & 63) >> 2), r = tid & 3;  // state column, row quarter (lane in its quad)
   const int tt = tid >> 4, c8 = (tid & 15) * 8;  // staging: token of the block, first channel
 
   float S[32];
@@ -3685,8 +3694,9 @@ __global__ __launch_bounds__(NT) void kda_prefill_kernel(pf::PrefillDev D) {
       const bool live = tt < n;
       const float nk = D.normalize ? 1.0f / __builtin_sqrtf(sk + 1e-6f) : 1.0f;
       const float nq = (D.normalize ? 1.0f / __builtin_sqrtf(sq + 1e-6f) : 1.0f) * D.scale;
-      float *kd = lds + OFF_KD + tt * KV + c8, *dc = lds + OFF_DC + tt * KV + c8;
-      float *kn = lds + OFF_KN + tt * KV + c8, *qn = lds + OFF_QN + tt * KV + c8;
+      const int kc = tt * ROWP + kcol(c8);  // 8 channels inside one segment
+      float *kd = lds + OFF_KD + kc, *dc = lds + OFF_DC + kc;
+      float *kn = lds + OFF_KN + kc, *qn = lds + OFF_QN + kc;
       float *vv = lds + OFF_VV + tt * KV + c8;
 #pragma unroll
       for (int e = 0; e < 8; e++) {
@@ -3712,9 +3722,9 @@ __global__ __launch_bounds__(NT) void kda_prefill_kernel(pf::PrefillDev D) {
     }
     __syncthreads();
     if (c0 + TB < len) fetch(R, c0 + TB);  // in flight during this block's tokens
-    float *p1 = lds + OFF_P1, *p2 = lds + OFF_P2;
     for (int u = 0; u < n; u++) {
-      const float4 *kd4 = (const float4 *)(lds + OFF_KD + u * KV + 32 * r);
+      const int row = u * ROWP + r * SEGP;  // this lane's 32 key rows of token u
+      const float4 *kd4 = (const float4 *)(lds + OFF_KD + row);
       float a0 = 0.f, a1 = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; e++) {
@@ -3724,13 +3734,11 @@ __global__ __launch_bounds__(NT) void kda_prefill_kernel(pf::PrefillDev D) {
         a0 = fmaf(w.z, S[4 * e + 2], a0);
         a1 = fmaf(w.w, S[4 * e + 3], a1);
       }
-      p1[r * KV + j] = a0 + a1;
-      __syncthreads();
-      const float ks = (p1[j] + p1[KV + j]) + (p1[2 * KV + j] + p1[3 * KV + j]);
+      const float ks = quad_sum(a0 + a1);
       const float delta = lds[OFF_BT + u] * (lds[OFF_VV + u * KV + j] - ks);
-      const float4 *dc4 = (const float4 *)(lds + OFF_DC + u * KV + 32 * r);
-      const float4 *kn4 = (const float4 *)(lds + OFF_KN + u * KV + 32 * r);
-      const float4 *qn4 = (const float4 *)(lds + OFF_QN + u * KV + 32 * r);
+      const float4 *dc4 = (const float4 *)(lds + OFF_DC + row);
+      const float4 *kn4 = (const float4 *)(lds + OFF_KN + row);
+      const float4 *qn4 = (const float4 *)(lds + OFF_QN + row);
       float o0 = 0.f, o1 = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; e++) {
@@ -3744,12 +3752,8 @@ __global__ __launch_bounds__(NT) void kda_prefill_kernel(pf::PrefillDev D) {
         o0 = fmaf(q.z, S[4 * e + 2], o0);
         o1 = fmaf(q.w, S[4 * e + 3], o1);
       }
-      p2[r * KV + j] = o0 + o1;
-      __syncthreads();
-      if (r == 0) {
-        const float o = (p2[j] + p2[KV + j]) + (p2[2 * KV + j] + p2[3 * KV + j]);
-        store_val(D.out, D.out_dtype, ((int64_t)(t0 + c0 + u) * H + h) * KV + j, o);
-      }
+      const float o = quad_sum(o0 + o1);
+      if (r == 0) store_val(D.out, D.out_dtype, ((int64_t)(t0 + c0 + u) * H + h) * KV + j, o);
       // checkpoints reached after this token (token counts, ascending)
       const int done = c0 + u + 1;
       while (ci < D.NC) {
