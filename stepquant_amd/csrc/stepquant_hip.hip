@@ -3577,24 +3577,26 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
 // role of the upstream chunk kernel behind the reference's kernel_extend
 // (sglang/runtime.py:193-202) for Kimi-Linear pools.
 //
-// One workgroup of 512 threads per (sequence, head): the four lanes of a
-// quad hold one state column j for the key rows 32 r .. 32 r + 31 (r the
-// lane's place in the quad) in registers, so the state never leaves the
-// workgroup and every per-token sum over key rows is a quad sum (two DPP
-// adds, no barrier).  Tokens are staged 32 at a time into LDS as fp32 rows
+// One workgroup of 1024 threads per (sequence, head): eight lanes (an
+// 8-lane half-row) hold one state column j for the key rows 16 r .. 16 r +
+// 15 (r the lane's place in the eight) in registers, so the state never
+// leaves the workgroup and every per-token sum over key rows is a sum over
+// the eight lanes (three DPP adds, no barrier); 16 waves, four per SIMD,
+// overlap each other's dependent chains.  Tokens are staged 32 at a time into LDS as fp32 rows
 // (normalised k, q, the decays e^g and k e^g, v, beta), the next block's raw
 // inputs are fetched into registers while the current block runs.  Per
 // token: kd^T S over the lane's 32 rows, the quad sum, delta_j, S = e^g S +
 // k delta (one FMA per value after the rank-1 product), q^T S, the quad sum,
-// one lane of the quad writes the output.  The key-channel rows are stored
-// as four 32-float segments 36 floats apart, so the four row quarters a wave
-// reads at once start in different banks.
+// one lane of the eight writes the output.  The key-channel rows are stored
+// as eight 16-float segments 20 floats apart, so the eight row segments a
+// wave reads at once start in different banks.
 namespace kp {
 
-constexpr int NT = 512;
+constexpr int NT = 1024, NSTG = 512;          // threads; the first 512 stage the inputs
 constexpr int TB = 32;                        // tokens staged per block
 constexpr int KV = 128;                       // K = V = 128
-constexpr int SEGP = 36, ROWP = 4 * SEGP;     // segment and row pitch (floats) of the key-channel rows
+constexpr int RPL = 16;                       // key rows per lane
+constexpr int SEGP = 20, ROWP = 8 * SEGP;     // segment and row pitch (floats) of the key-channel rows
 // LDS: per block key-channel rows [TB][ROWP] f32: KD (k e^g), DC (e^g), KN (k), QN (q);
 // VV [TB][128] (v); BETA [TB]
 constexpr int OFF_KD = 0;
@@ -3606,7 +3608,7 @@ constexpr int OFF_BT = OFF_VV + TB * KV;
 constexpr int LDS_FLOATS = OFF_BT + TB;
 constexpr int LDS_BYTES = LDS_FLOATS * 4;
 // place of channel c in a key-channel row
-__device__ __forceinline__ int kcol(int c) { return (c >> 5) * SEGP + (c & 31); }
+__device__ __forceinline__ int kcol(int c) { return (c >> 4) * SEGP + (c & 15); }
 
 // Raw inputs of one staging thread for one block: token tt = tid >> 4,
 // channels c8 .. c8 + 7 (c8 = (tid & 15) * 8).
@@ -3634,11 +3636,9 @@ __device__ __forceinline__ float sum16(float x) {
   return x;
 }
 
-// sum over the four lanes of a quad, (x0 + x1) + (x2 + x3) in every lane
-__device__ __forceinline__ float quad_sum(float x) {
-  x += fast::dpp<0xB1>(x);  // quad_perm [1,0,3,2]
-  return x + fast::dpp<0x4E>(x);  // quad_perm [2,3,0,1]
-}
+// sum over the eight lanes of a half-row, ((x0 + x1) + (x2 + x3)) + ((x4 +
+// x5) + (x6 + x7)) in every lane
+__device__ __forceinline__ float sum8(float x) { return fast::rg8_sum(x); }
 
 __global__ __launch_bounds__(NT) void kda_prefill_kernel(pf::PrefillDev D) {
   extern __shared__ float lds[];
@@ -3648,14 +3648,14 @@ __global__ __launch_bounds__(NT) void kda_prefill_kernel(pf::PrefillDev D) {
   const int t0 = D.cu[b], len = D.cu[b + 1] - t0;
   if (len <= 0) return;  // whole workgroup
   const int tid = threadIdx.x;
-  const int j = 16 * (tid >> 6) + ((tid & 63) >> 2), r = tid & 3;  // state column, row quarter (lane in its quad)
+  const int j = 8 * (tid >> 6) + ((tid & 63) >> 3), r = tid & 7;  // state column, row segment (lane in its eight)
   const int tt = tid >> 4, c8 = (tid & 15) * 8;  // staging: token of the block, first channel
 
-  float S[32];
+  float S[RPL];
   {
-    const float *src = D.init + (((int64_t)b * H + h) * KV + 32 * r) * KV + j;
+    const float *src = D.init + (((int64_t)b * H + h) * KV + RPL * r) * KV + j;
 #pragma unroll
-    for (int e = 0; e < 32; e++) S[e] = src[(int64_t)e * KV];
+    for (int e = 0; e < RPL; e++) S[e] = src[(int64_t)e * KV];
   }
   const float ea = D.a_log ? __expf(load_val(D.a_log, D.gate_dtype, h)) : 0.0f;
   const uint8_t *qg = (const uint8_t *)D.q, *kg = (const uint8_t *)D.k, *vg = (const uint8_t *)D.v;
@@ -3673,12 +3673,13 @@ __global__ __launch_bounds__(NT) void kda_prefill_kernel(pf::PrefillDev D) {
   };
 
   Raw R;
-  fetch(R, 0);
+  const bool stager = tid < NSTG;
+  if (stager) fetch(R, 0);
   int ci = 0;  // next checkpoint index
   for (int c0 = 0; c0 < len; c0 += TB) {
     const int n = len - c0 < TB ? len - c0 : TB;
     // ---- stage the fetched block (tokens past n: zero rows)
-    {
+    if (stager) {
       float kf[8], qf[8], vf[8];
       bf8(R.k, kf);
       bf8(R.q, qf);
@@ -3694,7 +3695,7 @@ __global__ __launch_bounds__(NT) void kda_prefill_kernel(pf::PrefillDev D) {
       const bool live = tt < n;
       const float nk = D.normalize ? 1.0f / __builtin_sqrtf(sk + 1e-6f) : 1.0f;
       const float nq = (D.normalize ? 1.0f / __builtin_sqrtf(sq + 1e-6f) : 1.0f) * D.scale;
-      const int kc = tt * ROWP + kcol(c8);  // 8 channels inside one segment
+      const int kc = tt * ROWP + kcol(c8);  // 8 channels inside one 16-channel segment
       float *kd = lds + OFF_KD + kc, *dc = lds + OFF_DC + kc;
       float *kn = lds + OFF_KN + kc, *qn = lds + OFF_QN + kc;
       float *vv = lds + OFF_VV + tt * KV + c8;
@@ -3721,27 +3722,27 @@ __global__ __launch_bounds__(NT) void kda_prefill_kernel(pf::PrefillDev D) {
       }
     }
     __syncthreads();
-    if (c0 + TB < len) fetch(R, c0 + TB);  // in flight during this block's tokens
+    if (stager && c0 + TB < len) fetch(R, c0 + TB);  // in flight during this block's tokens
     for (int u = 0; u < n; u++) {
-      const int row = u * ROWP + r * SEGP;  // this lane's 32 key rows of token u
+      const int row = u * ROWP + r * SEGP;  // this lane's 16 key rows of token u
       const float4 *kd4 = (const float4 *)(lds + OFF_KD + row);
       float a0 = 0.f, a1 = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; e++) {
+      for (int e = 0; e < RPL / 4; e++) {
         const float4 w = kd4[e];
         a0 = fmaf(w.x, S[4 * e], a0);
         a1 = fmaf(w.y, S[4 * e + 1], a1);
         a0 = fmaf(w.z, S[4 * e + 2], a0);
         a1 = fmaf(w.w, S[4 * e + 3], a1);
       }
-      const float ks = quad_sum(a0 + a1);
+      const float ks = sum8(a0 + a1);
       const float delta = lds[OFF_BT + u] * (lds[OFF_VV + u * KV + j] - ks);
       const float4 *dc4 = (const float4 *)(lds + OFF_DC + row);
       const float4 *kn4 = (const float4 *)(lds + OFF_KN + row);
       const float4 *qn4 = (const float4 *)(lds + OFF_QN + row);
       float o0 = 0.f, o1 = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; e++) {
+      for (int e = 0; e < RPL / 4; e++) {
         const float4 d = dc4[e], k = kn4[e], q = qn4[e];
         S[4 * e] = fmaf(d.x, S[4 * e], k.x * delta);
         S[4 * e + 1] = fmaf(d.y, S[4 * e + 1], k.y * delta);
@@ -3752,7 +3753,7 @@ __global__ __launch_bounds__(NT) void kda_prefill_kernel(pf::PrefillDev D) {
         o0 = fmaf(q.z, S[4 * e + 2], o0);
         o1 = fmaf(q.w, S[4 * e + 3], o1);
       }
-      const float o = quad_sum(o0 + o1);
+      const float o = sum8(o0 + o1);
       if (r == 0) store_val(D.out, D.out_dtype, ((int64_t)(t0 + c0 + u) * H + h) * KV + j, o);
       // checkpoints reached after this token (token counts, ascending)
       const int done = c0 + u + 1;
@@ -3760,9 +3761,9 @@ __global__ __launch_bounds__(NT) void kda_prefill_kernel(pf::PrefillDev D) {
         const int p = D.ckpt[(int64_t)b * D.NC + ci];
         if (p > done && p <= len) break;
         if (p == done) {
-          float *dst = D.ck_state + ((((int64_t)b * D.NC + ci) * H + h) * KV + 32 * r) * KV + j;
+          float *dst = D.ck_state + ((((int64_t)b * D.NC + ci) * H + h) * KV + RPL * r) * KV + j;
 #pragma unroll
-          for (int e = 0; e < 32; e++) dst[(int64_t)e * KV] = S[e];
+          for (int e = 0; e < RPL; e++) dst[(int64_t)e * KV] = S[e];
         }
         ci++;
       }
