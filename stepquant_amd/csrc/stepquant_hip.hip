@@ -3582,11 +3582,11 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
 // 15 (r the lane's place in the eight) in registers, so the state never
 // leaves the workgroup and every per-token sum over key rows is a sum over
 // the eight lanes (three DPP adds, no barrier); 16 waves, four per SIMD,
-// overlap each other's dependent chains.  Tokens are staged 32 at a time into LDS as fp32 rows
-// (normalised k, q, the decays e^g and k e^g, v, beta), the next block's raw
-// inputs are fetched into registers while the current block runs.  Per
-// token: kd^T S over the lane's 32 rows, the quad sum, delta_j, S = e^g S +
-// k delta (one FMA per value after the rank-1 product), q^T S, the quad sum,
+// overlap each other's dependent chains.  Tokens are staged 32 at a time
+// into LDS as fp32 rows (normalised k, q, the decays e^g, v, beta), and the
+// next block's raw inputs are fetched into registers while the current
+// block runs.  Per token: S = e^g S, k^T S over the lane's rows and its sum
+// over the lanes of the column, delta_j, S += k delta, q^T S and its sum;
 // one lane of the eight writes the output.  The key-channel rows are stored
 // as eight 16-float segments 20 floats apart, so the eight row segments a
 // wave reads at once start in different banks.
@@ -3597,10 +3597,9 @@ constexpr int TB = 32;                        // tokens staged per block
 constexpr int KV = 128;                       // K = V = 128
 constexpr int RPL = 16;                       // key rows per lane
 constexpr int SEGP = 20, ROWP = 8 * SEGP;     // segment and row pitch (floats) of the key-channel rows
-// LDS: per block key-channel rows [TB][ROWP] f32: KD (k e^g), DC (e^g), KN (k), QN (q);
+// LDS: per block key-channel rows [TB][ROWP] f32: DC (e^g), KN (k), QN (q);
 // VV [TB][128] (v); BETA [TB]
-constexpr int OFF_KD = 0;
-constexpr int OFF_DC = OFF_KD + TB * ROWP;
+constexpr int OFF_DC = 0;
 constexpr int OFF_KN = OFF_DC + TB * ROWP;
 constexpr int OFF_QN = OFF_KN + TB * ROWP;
 constexpr int OFF_VV = OFF_QN + TB * ROWP;
@@ -3696,7 +3695,7 @@ __global__ __launch_bounds__(NT) void kda_prefill_kernel(pf::PrefillDev D) {
       const float nk = D.normalize ? 1.0f / __builtin_sqrtf(sk + 1e-6f) : 1.0f;
       const float nq = (D.normalize ? 1.0f / __builtin_sqrtf(sq + 1e-6f) : 1.0f) * D.scale;
       const int kc = tt * ROWP + kcol(c8);  // 8 channels inside one 16-channel segment
-      float *kd = lds + OFF_KD + kc, *dc = lds + OFF_DC + kc;
+      float *dc = lds + OFF_DC + kc;
       float *kn = lds + OFF_KN + kc, *qn = lds + OFF_QN + kc;
       float *vv = lds + OFF_VV + tt * KV + c8;
 #pragma unroll
@@ -3709,7 +3708,6 @@ __global__ __launch_bounds__(NT) void kda_prefill_kernel(pf::PrefillDev D) {
         }
         const float d = __expf(gv);
         const float k = live ? kf[e] * nk : 0.0f;
-        kd[e] = k * d;
         dc[e] = live ? d : 1.0f;
         kn[e] = k;
         qn[e] = live ? qf[e] * nq : 0.0f;
@@ -3724,30 +3722,40 @@ __global__ __launch_bounds__(NT) void kda_prefill_kernel(pf::PrefillDev D) {
     __syncthreads();
     if (stager && c0 + TB < len) fetch(R, c0 + TB);  // in flight during this block's tokens
     for (int u = 0; u < n; u++) {
+      // the decay first (S = e^g S), then k^T S, S += k delta, q^T S:
+      // three rows of the token read from LDS (e^g, k, q)
       const int row = u * ROWP + r * SEGP;  // this lane's 16 key rows of token u
-      const float4 *kd4 = (const float4 *)(lds + OFF_KD + row);
-      float a0 = 0.f, a1 = 0.f;
-#pragma unroll
-      for (int e = 0; e < RPL / 4; e++) {
-        const float4 w = kd4[e];
-        a0 = fmaf(w.x, S[4 * e], a0);
-        a1 = fmaf(w.y, S[4 * e + 1], a1);
-        a0 = fmaf(w.z, S[4 * e + 2], a0);
-        a1 = fmaf(w.w, S[4 * e + 3], a1);
-      }
-      const float ks = sum8(a0 + a1);
-      const float delta = lds[OFF_BT + u] * (lds[OFF_VV + u * KV + j] - ks);
       const float4 *dc4 = (const float4 *)(lds + OFF_DC + row);
       const float4 *kn4 = (const float4 *)(lds + OFF_KN + row);
       const float4 *qn4 = (const float4 *)(lds + OFF_QN + row);
+      float kk[RPL];
+      float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+      for (int e = 0; e < RPL / 4; e++) {
+        const float4 d = dc4[e], k = kn4[e];
+        S[4 * e] *= d.x;
+        S[4 * e + 1] *= d.y;
+        S[4 * e + 2] *= d.z;
+        S[4 * e + 3] *= d.w;
+        kk[4 * e] = k.x;
+        kk[4 * e + 1] = k.y;
+        kk[4 * e + 2] = k.z;
+        kk[4 * e + 3] = k.w;
+        a0 = fmaf(k.x, S[4 * e], a0);
+        a1 = fmaf(k.y, S[4 * e + 1], a1);
+        a0 = fmaf(k.z, S[4 * e + 2], a0);
+        a1 = fmaf(k.w, S[4 * e + 3], a1);
+      }
+      const float ks = sum8(a0 + a1);
+      const float delta = lds[OFF_BT + u] * (lds[OFF_VV + u * KV + j] - ks);
       float o0 = 0.f, o1 = 0.f;
 #pragma unroll
       for (int e = 0; e < RPL / 4; e++) {
-        const float4 d = dc4[e], k = kn4[e], q = qn4[e];
-        S[4 * e] = fmaf(d.x, S[4 * e], k.x * delta);
-        S[4 * e + 1] = fmaf(d.y, S[4 * e + 1], k.y * delta);
-        S[4 * e + 2] = fmaf(d.z, S[4 * e + 2], k.z * delta);
-        S[4 * e + 3] = fmaf(d.w, S[4 * e + 3], k.w * delta);
+        const float4 q = qn4[e];
+        S[4 * e] = fmaf(kk[4 * e], delta, S[4 * e]);
+        S[4 * e + 1] = fmaf(kk[4 * e + 1], delta, S[4 * e + 1]);
+        S[4 * e + 2] = fmaf(kk[4 * e + 2], delta, S[4 * e + 2]);
+        S[4 * e + 3] = fmaf(kk[4 * e + 3], delta, S[4 * e + 3]);
         o0 = fmaf(q.x, S[4 * e], o0);
         o1 = fmaf(q.y, S[4 * e + 1], o1);
         o0 = fmaf(q.z, S[4 * e + 2], o0);
