@@ -1580,11 +1580,18 @@ __device__ __forceinline__ void prologue(const PoolDev &P, const StepDev &S, con
         al = __uint_as_float(ld_uniform((const uint32_t *)S.a_log + C.h));
       }
     } else {
-      bt = load_val(S.beta, S.gate_dtype, bh);
-      gv = load_val(S.g, S.gate_dtype, bh);
-      if (S.a_log) {
-        dtb = load_val(S.dt_bias, S.gate_dtype, C.h);
-        al = load_val(S.a_log, S.gate_dtype, C.h);
+      // the raw bits of all four before any conversion: one wait covers them
+      // (without A_log, its reads fall on the gate and beta and are unused)
+      const bool has_a = S.a_log != nullptr;
+      const uint32_t br = ((const uint16_t *)S.beta)[bh], gr = ((const uint16_t *)S.g)[bh];
+      const uint32_t dr = ((const uint16_t *)(has_a ? S.dt_bias : S.g))[has_a ? (int64_t)C.h : bh];
+      const uint32_t ar = ((const uint16_t *)(has_a ? S.a_log : S.beta))[has_a ? (int64_t)C.h : bh];
+      auto cv = [&](uint32_t u) { return S.gate_dtype == SQ_BF16 ? __uint_as_float(u << 16) : hw_h2f(u); };
+      bt = cv(br);
+      gv = cv(gr);
+      if (has_a) {
+        dtb = cv(dr);
+        al = cv(ar);
       }
     }
     const float qv = QW4 ? __uint_as_float(qr) : S.qkv_dtype == SQ_BF16 ? __uint_as_float(qr << 16) : hw_h2f(qr);
@@ -2794,10 +2801,18 @@ __device__ __forceinline__ void kda_prologue(const PoolDev &P, const StepDev &S,
       bt = __uint_as_float(ld_uniform((const uint32_t *)S.beta + bh));
       if (S.a_log) al = __uint_as_float(ld_uniform((const uint32_t *)S.a_log + C.h));
     } else {
+      // The raw bits of all four 16-bit inputs before any conversion, so
+      // one wait covers them (a conversion next to its load would wait
+      // there and put a second memory round trip after the page's).
+      // Without A_log, its two reads fall on the gate and beta, unused.
+      const bool has_a = S.a_log != nullptr;
       gr = ((const uint16_t *)S.g)[bh * FK + i];
-      if (S.a_log) dr = ((const uint16_t *)S.dt_bias)[(int64_t)C.h * FK + i];
-      bt = load_val(S.beta, S.gate_dtype, bh);
-      if (S.a_log) al = load_val(S.a_log, S.gate_dtype, C.h);
+      dr = ((const uint16_t *)(has_a ? S.dt_bias : S.g))[has_a ? (int64_t)C.h * FK + i : bh * FK + i];
+      const uint32_t br = ((const uint16_t *)S.beta)[bh];
+      const uint32_t ar = ((const uint16_t *)(has_a ? S.a_log : S.beta))[has_a ? (int64_t)C.h : bh];
+      auto cv = [&](uint32_t u) { return S.gate_dtype == SQ_BF16 ? __uint_as_float(u << 16) : hw_h2f(u); };
+      bt = cv(br);
+      if (has_a) al = cv(ar);
     }
     const float qv = QW4 ? __uint_as_float(qr) : S.qkv_dtype == SQ_BF16 ? __uint_as_float(qr << 16) : hw_h2f(qr);
     const float kv = QW4 ? __uint_as_float(kr) : S.qkv_dtype == SQ_BF16 ? __uint_as_float(kr << 16) : hw_h2f(kr);
