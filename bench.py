@@ -218,13 +218,28 @@ def bench_prefill(a, torch):
     ck = torch.tensor(pos, dtype=torch.int32).repeat(B, 1)  # on the host, as the scheduler holds them
     ck_slots = torch.arange(B + 1, B + 1 + B * NC).reshape(B, NC)
 
-    def step():
+    def step(events=None):
         return pool.extend(q, k, v, gate, beta, init, cu, checkpoints=ck, checkpoint_slots=ck_slots,
-                           init_slots=init, normalize=True, scale=K ** -.5, a_log=a_log, dt_bias=dt_bias)
+                           init_slots=init, normalize=True, scale=K ** -.5, a_log=a_log, dt_bias=dt_bias,
+                           events=events)
+
+    # the recurrence kernel timed in every step on the launching stream: a
+    # ring of event pairs, one per timed step, which the timed region's steps
+    # (the last ones launched) fill completely
+    ring = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(a.steps)]
+    for e0, e1 in ring:
+        e0.record()
+        e1.record()
+    turn = [0]
+
+    def timed_step():
+        step(ring[turn[0] % len(ring)])
+        turn[0] += 1
 
     step()
     torch.cuda.synchronize()
-    ms_step, wall = timed_steps(torch, step, step, 1, a.steps, a.warmup, a.warm_seconds)
+    ms_step, wall = timed_steps(torch, step, timed_step, 1, a.steps, a.warmup, a.warm_seconds)
+    kernel_ms = sum(e0.elapsed_time(e1) for e0, e1 in ring) / len(ring) if ring else ms_step
     gate_bytes = tot * H * (K if kda else 1) * 4 + tot * H * 4
     hbm = (2 * tot * HK * K * 2 + tot * H * V * 2 + tot * H * V * 2 + gate_bytes + B * pool.page_bytes
            + B * NC * pool.page_bytes)
@@ -234,17 +249,21 @@ def bench_prefill(a, torch):
     if kda:
         # per token-head: decay K V multiplies, k^T S, the rank-1 update and q^T S (2 K V each)
         flops = B * T * H * 7 * K * V
-        tflops = flops / (ms_step * 1e-3) / 1e12
+        tflops = flops / (kernel_ms * 1e-3) / 1e12
         roof = dict(bound="valu", achieved=round(tflops, 2), peak=PEAK_F32_TFLOPS, unit="TFLOP/s",
-                    frac=round(tflops / PEAK_F32_TFLOPS, 4), traffic=None, algorithmic_flops_per_step=flops,
+                    frac=round(tflops / PEAK_F32_TFLOPS, 4), traffic=None, kernel="kp::kda_prefill_kernel",
+                    kernel_ms=round(kernel_ms, 6), step_frac=round(flops / (ms_step * 1e-3) / 1e12 / PEAK_F32_TFLOPS, 4),
+                    algorithmic_flops_per_step=flops,
                     hbm_fraction=round(hbm / (ms_step * 1e-3) / 1e9 / PEAK_GBS, 4),
                     algorithmic_bytes_per_step=hbm)
     else:
         n_chunks = B * H * ((T + 63) // 64)
         flops = prefill_flops(n_chunks)
-        tflops = flops / (ms_step * 1e-3) / 1e12
+        tflops = flops / (kernel_ms * 1e-3) / 1e12
         roof = dict(bound="mfma", achieved=round(tflops, 2), peak=PEAK_BF16_TFLOPS, unit="TFLOP/s",
-                    frac=round(tflops / PEAK_BF16_TFLOPS, 4), traffic=None, algorithmic_flops_per_step=flops,
+                    frac=round(tflops / PEAK_BF16_TFLOPS, 4), traffic=None, kernel="pf::prefill_kernel",
+                    kernel_ms=round(kernel_ms, 6), step_frac=round(flops / (ms_step * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                    algorithmic_flops_per_step=flops,
                     hbm_fraction=round(hbm / (ms_step * 1e-3) / 1e9 / PEAK_GBS, 4),
                     algorithmic_bytes_per_step=hbm)
     line = dict(metric=f"prefill tokens/sec ({a.arch.upper()} prefill into prefix slots)",

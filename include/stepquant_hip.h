@@ -193,6 +193,10 @@ int sq_writeback(const sq_pool *pool, const sq_writeback_scratch *scratch, int64
  *             sequence are unused and their slots must be <= 0).
  *   init_state      workspace [batch, H, K, V] f32;
  *   checkpoint_state workspace [batch * n_checkpoints, H, K, V] f32.
+ *   events    NULL, or two hipEvent_t recorded on the stream right before
+ *             and after the recurrence kernel (a timing hook for
+ *             benchmarks; the reference's kernel_extend has no
+ *             counterpart).
  * Pools with K = V = 128, packed or byte storage.  GDN: the chunked kernel
  * (chunks of 64 tokens, bf16 MFMA).  KDA: a token-by-token kernel, one
  * workgroup per (sequence, head) holding the state in registers.
@@ -224,6 +228,7 @@ typedef struct sq_prefill_args {
     int32_t slots_dtype;
     int32_t normalize;
     float scale;
+    void *const *events;
 } sq_prefill_args;
 
 int sq_prefill(const sq_pool *pool, const sq_prefill_args *args, void *stream);

@@ -51,7 +51,7 @@ class PrefillArgs(ctypes.Structure):
                 ("q_stride", ctypes.c_int64), ("k_stride", ctypes.c_int64), ("v_stride", ctypes.c_int64),
                 ("key_heads", ctypes.c_int32), ("n_checkpoints", ctypes.c_int32), ("qkv_dtype", ctypes.c_int32),
                 ("gate_dtype", ctypes.c_int32), ("out_dtype", ctypes.c_int32), ("slots_dtype", ctypes.c_int32),
-                ("normalize", ctypes.c_int32), ("scale", ctypes.c_float)]
+                ("normalize", ctypes.c_int32), ("scale", ctypes.c_float), ("events", _P)]
 
 
 class FormatPool(ctypes.Structure):

@@ -4862,16 +4862,24 @@ int sq_prefill(const sq_pool *pool, const sq_prefill_args *a, void *stream) {
     hipError_t e = hipFuncSetAttribute((const void *)kp::kda_prefill_kernel,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, kp::LDS_BYTES);
     if (e != hipSuccess) return fail((int)e, "prefill: cannot raise the KDA kernel's LDS limit");
+    if (a->events && (e = hipEventRecord((hipEvent_t)a->events[0], st)) != hipSuccess)
+      return fail((int)e, "prefill: hipEventRecord failed");
     hipLaunchKernelGGL(kp::kda_prefill_kernel, dim3((unsigned)(a->batch * H)), dim3(kp::NT), kp::LDS_BYTES, st, D);
     rc = check_launch("kda_prefill_kernel");
   } else {
     hipError_t e = hipFuncSetAttribute((const void *)pf::prefill_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                                        pf::LDS_BYTES);
     if (e != hipSuccess) return fail((int)e, "prefill: cannot raise the kernel's LDS limit");
+    if (a->events && (e = hipEventRecord((hipEvent_t)a->events[0], st)) != hipSuccess)
+      return fail((int)e, "prefill: hipEventRecord failed");
     hipLaunchKernelGGL(pf::prefill_kernel, dim3((unsigned)(a->batch * H)), dim3(pf::NT), pf::LDS_BYTES, st, D);
     rc = check_launch("prefill_kernel");
   }
   if (rc) return rc;
+  if (a->events) {
+    const hipError_t e = hipEventRecord((hipEvent_t)a->events[1], st);
+    if (e != hipSuccess) return fail((int)e, "prefill: hipEventRecord failed");
+  }
   if (a->n_checkpoints > 0)
     return sq_encode(pool, a->checkpoint_state, a->slots, a->slots_dtype, a->batch * a->n_checkpoints, stream);
   return 0;

@@ -19,6 +19,8 @@ adapter can use it unchanged.  All arithmetic runs in the HIP kernels of
 """
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 import torch
 
@@ -354,7 +356,7 @@ class PackedStatePool:
         return out
 
     def extend(self, q, k, v, g, beta, slots, cu_seqlens, *, checkpoints=None, checkpoint_slots=None,
-               init_slots=None, normalize=False, scale=1., a_log=None, dt_bias=None):
+               init_slots=None, normalize=False, scale=1., a_log=None, dt_bias=None, events=None):
         """Chunked prefill of whole sequences straight from and into the pool.
 
         The behaviour of the serving adapter's ``kernel_extend``
@@ -370,6 +372,9 @@ class PackedStatePool:
         checked when they are host tensors) with ``checkpoint_slots``
         ``[B, NC]`` write intermediate prefix states as well.  ``cu_seqlens``
         must start at 0 and never decrease (ValueError otherwise).  Returns the outputs ``[T, H, V]`` in q's dtype.
+        ``events`` (benchmarks): two ``torch.cuda.Event`` with timing, recorded
+        once already, that the call records on the current stream right before
+        and after the recurrence kernel.
         """
         self.wait()
         if self.keys != 128 or self.values != 128:
@@ -487,6 +492,14 @@ class PackedStatePool:
             v_stride=v2.stride(0), key_heads=hk, n_checkpoints=nc, qkv_dtype=N.BF16,
             gate_dtype=N.dtype_code(g2), out_dtype=N.dtype_code(out), slots_dtype=N.dtype_code(ck_slots),
             normalize=int(bool(normalize)), scale=float(scale))
+        if events is not None:
+            # benchmark hook: two recorded torch.cuda.Event (torch creates them
+            # at their first record) around the recurrence kernel
+            handles = [int(e.cuda_event) for e in events]
+            if len(handles) != 2 or not all(handles):
+                raise ValueError("events must be two torch.cuda.Event that have been recorded once")
+            ev = (ctypes.c_void_p * 2)(*handles)
+            args.events = ctypes.cast(ev, ctypes.c_void_p)
         if batch:
             N.check(N.lib().sq_prefill(self._desc, args, N.stream_handle()), "prefill")
         self._last_prefill = (q2, k2, v2, g2, b2, al, db, cu, ck, init, ck_slots, init_state, ck_state)

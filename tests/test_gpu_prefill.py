@@ -238,3 +238,41 @@ def test_prefill_kda_and_byte_pages(arch, storage, raw):
         assert np.array_equal(pages[s], ref_pages[s]), f"slot {s} page differs"
     for s in (1, 2, 11):
         assert not pages[s].any(), "untouched slots stay empty"
+
+
+@pytest.mark.parametrize("arch", ["gdn", "kda"])
+def test_prefill_timing_events_change_nothing(arch):
+    """The benchmark's timing hook: the two events bracket the recurrence
+    kernel (a positive interval no longer than the whole call's), and the
+    outputs and pages equal those of a call without them."""
+    from stepquant_amd.kernels.pool import PackedStatePool
+    print(f"case timing events {arch}", flush=True)
+    H, K, V, T = 2, 128, 128, 150
+    oplan = make_plan(arch, np.full((H, K), 6), seed=3)
+    pools = [PackedStatePool(device_plan(oplan), 4, V) for _ in range(2)]
+    g = torch.Generator().manual_seed(4)
+    q = torch.randn(T, H * K, generator=g).to(torch.bfloat16).to(dev())
+    k = torch.randn(T, H * K, generator=g).to(torch.bfloat16).to(dev())
+    v = torch.randn(T, H * V, generator=g).to(torch.bfloat16).to(dev())
+    gshape = (T, H, K) if arch == "kda" else (T, H)
+    gate = (-torch.nn.functional.softplus(torch.randn(gshape, generator=g))).to(dev())
+    beta = torch.sigmoid(torch.randn(T, H, generator=g)).to(dev())
+    slots = torch.tensor([2, 1])
+    x = (torch.randn(2, H, K, V, generator=g) * .1).to(dev())
+    for p in pools:
+        p.encode(x, slots.to(dev()))
+    cu = torch.tensor([0, 100, T])
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with pytest.raises(ValueError):
+        pools[0].extend(q, k, v, gate, beta, slots, cu, normalize=True, scale=K ** -.5, events=(e0, e1))
+    e0.record()
+    e1.record()
+    outer0, outer1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    outer0.record()
+    a = pools[0].extend(q, k, v, gate, beta, slots, cu, normalize=True, scale=K ** -.5, events=(e0, e1))
+    outer1.record()
+    b = pools[1].extend(q, k, v, gate, beta, slots, cu, normalize=True, scale=K ** -.5)
+    torch.cuda.synchronize()
+    assert 0 < e0.elapsed_time(e1) <= outer0.elapsed_time(outer1)
+    assert torch.equal(a, b)
+    assert torch.equal(pools[0].data, pools[1].data)

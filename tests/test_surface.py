@@ -35,7 +35,7 @@ def test_structs_match_header_layout():
     assert ctypes.sizeof(N.Pool) == 8 * 9 + 4 * 10
     assert ctypes.sizeof(N.StepArgs) == 8 * 13 + 4 * 8
     assert ctypes.sizeof(N.Scratch) == 8 * 5
-    assert ctypes.sizeof(N.PrefillArgs) == 8 * 14 + 8 * 4 + 4 * 8
+    assert ctypes.sizeof(N.PrefillArgs) == 8 * 14 + 8 * 4 + 4 * 8 + 8  # ... then the events pointer
     assert ctypes.sizeof(N.FormatPool) == 8 * 6 + 4 * 8
 
 
