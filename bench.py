@@ -8,7 +8,11 @@ beta = sigmoid(N(0,1)), L2-normalised q/k in the kernel.  Per-head widths
 {4, 6, 8} averaging 6 (page = 409,600 B).  Initial state ~ N(0, 0.05^2)
 encoded into slots 1..B.  One step = one decode step of the layer including
 the writeback of the requantised page; steps are replayed from a HIP graph
-and the state evolves from step to step.
+and the state evolves from step to step.  Consecutive steps use disjoint
+sets of B slots of one pool in turn (``--slot-sets``, 4 by default: 1,025
+pages, 420 MB), so the pages a step reads were last touched four steps
+earlier, with 315 MB of other pages read and written in between, and come
+from HBM rather than from the 256 MB Infinity Cache.
 
 Prints one JSON line (metric, value = state-head updates/s, roofline of the
 dominant kernel, CPU baseline from the oracle on a bounded sample).
@@ -46,6 +50,10 @@ def parse():
     p.add_argument("--async-writeback", action="store_true",
                    help="split readout (foreground) and writer (writeback stream); under graphs the writers "
                         "are deferred and forked at attention windows, joined at the end of the step")
+    p.add_argument("--slot-sets", type=int, default=4,
+                   help="disjoint sets of B slots in each pool, used by consecutive steps in turn, so a set's "
+                        "pages have left the 256 MB Infinity Cache before the set comes round again (4 sets: "
+                        "315 MB of other pages read and written in between)")
     p.add_argument("--layers", type=int, default=1,
                    help="recurrent layers per step, each with its own pool (an attention window before each)")
     p.add_argument("--cpu-sample", type=int, default=-1,
@@ -310,27 +318,30 @@ def main():
         fplan = FormatPlan(a.arch, bits.to(dev), impact.to(dev))
 
         def make_pool():
-            return FormatStatePool(fplan, B + 1, V, spec)
+            return FormatStatePool(fplan, a.slot_sets * B + 1, V, spec)
         stream = None
         a.cpu_sample = 0  # the CPU port restates the STEPQuant path only
     else:
         plan = QuantizationPlan(a.arch, bits.to(dev), impact.to(dev))
 
         def make_pool():
-            return PackedStatePool(plan, B + 1, V, writeback_stream=stream)
+            return PackedStatePool(plan, a.slot_sets * B + 1, V, writeback_stream=stream)
+    if a.slot_sets < 1:
+        raise SystemExit("--slot-sets must be positive")
     pools = [make_pool() for _ in range(a.layers)]
     pool = pools[0]
     g = torch.Generator(device=dev).manual_seed(0)
-    slots = torch.arange(1, B + 1, device=dev, dtype=torch.int32)
+    slot_sets = [torch.arange(1 + r * B, 1 + (r + 1) * B, device=dev, dtype=torch.int32) for r in range(a.slot_sets)]
     for layer in pools:
-        if a.nominal == 4:
-            # key-row and value-column scales log-normal(0, 0.5)
-            r = torch.exp(torch.randn(B, H, K, 1, device=dev, generator=g) * .5)
-            c = torch.exp(torch.randn(B, H, 1, V, device=dev, generator=g) * .5)
-            layer.encode(r * torch.randn(B, H, K, V, device=dev, generator=g) * c, slots)
-            del r, c
-        else:
-            layer.encode(torch.randn(B, H, K, V, device=dev, generator=g) * .05, slots)
+        for slots in slot_sets:
+            if a.nominal == 4:
+                # key-row and value-column scales log-normal(0, 0.5)
+                r = torch.exp(torch.randn(B, H, K, 1, device=dev, generator=g) * .5)
+                c = torch.exp(torch.randn(B, H, 1, V, device=dev, generator=g) * .5)
+                layer.encode(r * torch.randn(B, H, K, V, device=dev, generator=g) * c, slots)
+                del r, c
+            else:
+                layer.encode(torch.randn(B, H, K, V, device=dev, generator=g) * .05, slots)
     mixed = torch.randn(B, 2 * HK * K + H * V, device=dev, generator=g).to(torch.bfloat16)
     q, k, v = mixed.split([HK * K, HK * K, H * V], -1)
     # raw gates with A_log = 0, dt_bias = 0: g = -softplus(a); KDA a = 0.5 N(0,1) per channel
@@ -342,7 +353,7 @@ def main():
 
     from stepquant_amd.kernels.writeback import attention_window, defer_writeback
 
-    def layers():
+    def layers(slots):
         outs = []
         for layer in pools:
             attention_window()
@@ -350,13 +361,18 @@ def main():
                                    dt_bias=dt_bias))
         return outs
 
-    def step():
+    turn = [0]
+
+    def step(slots=None):
+        if slots is None:  # eager steps take the slot sets in turn
+            slots = slot_sets[turn[0] % len(slot_sets)]
+            turn[0] += 1
         if stream is not None and torch.cuda.is_current_stream_capturing():
             # writers forked at attention windows, joined when the step ends
             with defer_writeback(pools, attention_windows=True, joined=True):
-                outs = layers()
+                outs = layers(slots)
         else:
-            outs = layers()
+            outs = layers(slots)
         for layer in pools:
             layer.wait()
         return outs
@@ -370,13 +386,21 @@ def main():
         per_block = a.graph_steps or max(d for d in range(1, 17) if a.steps % d == 0)
         if a.steps % per_block:
             raise SystemExit(f"--graph-steps {per_block} must divide --steps {a.steps}")
-        single, multi = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
-        with torch.cuda.graph(single):
-            step()
-        with torch.cuda.graph(multi, pool=single.pool()):
-            for _ in range(per_block):
-                step()
-        one, block = single.replay, multi.replay
+        # a launch of the multi-step graph takes the slot sets in turn; a
+        # single-step graph per set, replayed in turn, for the warm-up steps
+        singles = [torch.cuda.CUDAGraph() for _ in slot_sets]
+        for graph, slots in zip(singles, slot_sets):
+            with torch.cuda.graph(graph, pool=singles[0].pool() if graph is not singles[0] else None):
+                step(slots)
+        multi = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(multi, pool=singles[0].pool()):
+            for i in range(per_block):
+                step(slot_sets[i % len(slot_sets)])
+
+        def one():
+            singles[turn[0] % len(singles)].replay()
+            turn[0] += 1
+        block = multi.replay
     ms_step, wall = timed_steps(torch, one, block, per_block, a.steps, a.warmup, a.warm_seconds)
     page = pool.page_bytes
     alg_bytes = 2 * B * page * a.layers
@@ -388,6 +412,7 @@ def main():
         key += f"-l{a.layers}"
     if a.state_format != "stepquant":
         key = f"{a.state_format}-{a.arch}-b{B}-h{H}-hk{HK}"
+    key += f"-sets{a.slot_sets}"
     traffic = None
     if a.traffic and os.path.exists(a.traffic):
         meas = json.load(open(a.traffic))
@@ -412,7 +437,9 @@ def main():
                                      + f", B={B}, H={H}, "
                                      f"HK={HK}, dk=dv={K}, bf16 q/k/v, raw gates, "
                                      + (f"{per_block} steps per graph launch" if not a.no_graph else "eager steps")
-                                     + (", async writeback" if stream is not None else ", fused writeback"),
+                                     + (", async writeback" if stream is not None else ", fused writeback")
+                                     + f", steps rotate over {a.slot_sets} disjoint sets of B slots "
+                                       f"({a.slot_sets * B * page * a.layers / 1e6:.0f} MB of pages)",
                             page_bytes=page, global_batch=B, wall_s=round(wall, 3),
                             warm_seconds=a.warm_seconds),
                 roofline=roof, cpu_baseline=cpu)

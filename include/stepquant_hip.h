@@ -20,7 +20,8 @@
 extern "C" {
 #endif
 
-#define SQ_ABI_VERSION 1
+/* 2: sq_prefill_args gained `events` and `beta_logits` (and a reserved word) */
+#define SQ_ABI_VERSION 2
 
 /* dtype codes for q/k/v/g/beta/out and slot indices */
 enum {
@@ -180,9 +181,15 @@ int sq_writeback(const sq_pool *pool, const sq_writeback_scratch *scratch, int64
  * kernel -> encode round trip of kernel_extend, sglang/runtime.py:193-202).
  *   q, k      [T, HK*K] bf16 rows (row strides in elements, multiples of 8,
  *             rows 16-byte aligned); v [T, H*V] bf16; T = cu_seqlens[batch].
- *   g, beta   [T, H] log decay and write strength (raw gate a and logits b
- *             when a_log/dt_bias are given, as sq_step_args); KDA pools: g
- *             [T, H, K], one log decay per key channel, dt_bias [H * K].
+ *   g, beta   [T, H] log decay and write strength.  With a_log/dt_bias, g
+ *             is the raw gate a and the log decay is
+ *             -exp(a_log[h]) * softplus(a + dt_bias) (softplus threshold 20),
+ *             as sq_step_args.  KDA pools: g [T, H, K], one value per key
+ *             channel, dt_bias [H * K].
+ *   beta_logits  1: beta holds logits b and the write strength is
+ *             sigmoid(b) (the decode hooks' convention); 0: beta is the
+ *             write strength itself (the chunk kernels' convention).
+ *             Independent of a_log.
  *   out       [T, H, V], dtype out_dtype.
  *   cu_seqlens [batch + 1] int32 token offsets of the sequences.
  *   init_slots [batch] pages holding the initial states (slot <= 0: zero
@@ -229,6 +236,8 @@ typedef struct sq_prefill_args {
     int32_t normalize;
     float scale;
     void *const *events;
+    int32_t beta_logits;
+    int32_t reserved;
 } sq_prefill_args;
 
 int sq_prefill(const sq_pool *pool, const sq_prefill_args *args, void *stream);
@@ -349,10 +358,13 @@ int sq_event_query(void *event);
 int sq_event_synchronize(void *event);
 
 /*
- * A non-blocking stream restricted to `cus` compute units spread across all
- * XCDs (hipExtStreamCreateWithCUMask; 0 = unrestricted), at default priority.
- * Replaces the Green Context SM split of writeback_resources
- * (kernels/resources.py:19-53).  The stream lives until process exit.
+ * A stream restricted to `cus` compute units spread across all XCDs
+ * (hipExtStreamCreateWithCUMask), at default priority.  A restricted stream
+ * is a blocking stream (hipExtStreamCreateWithCUMask takes no flags), so work
+ * on the legacy default stream waits for it; cus == 0 or cus equal to the
+ * device's CU count gives an unrestricted non-blocking stream.  Replaces the
+ * Green Context SM split of writeback_resources (kernels/resources.py:19-53).
+ * The stream lives until process exit.
  */
 int sq_create_cu_stream(int32_t device, int32_t cus, void **stream, int32_t *actual, int32_t *total);
 

@@ -513,14 +513,14 @@ def _softplus20(u):
 
 
 def prefill(q, k, v, g, beta, state0, cu_seqlens, checkpoints=None, normalize=False, scale=1.0,
-            a_log=None, dt_bias=None):
+            a_log=None, dt_bias=None, beta_logits=None):
     """Token-sequential GDN or KDA prefill in float64.
 
     q, k: [T, HK, K]; v: [T, H, V]; g: [T, H] (GDN) or [T, H, K] (KDA,
     per key channel) log decay, or the raw gate a when a_log is given:
     g = -exp(a_log[h]) softplus(a + dt_bias) with dt_bias [H] (GDN) or
-    [H * K] (KDA); beta: [T, H] (logits when a_log is given: beta =
-    sigmoid(b)); state0: [B, H, K, V];
+    [H * K] (KDA); beta: [T, H], logits (beta = sigmoid(b)) when
+    beta_logits is true (default: when a_log is given); state0: [B, H, K, V];
     cu_seqlens: [B + 1] token offsets; checkpoints: [B, NC] token counts
     after which the state is recorded (<= 0 or > length: unused).
     Per token (core.py:5-15): S <- e^g S (KDA: row i scaled by e^{g_i});
@@ -548,6 +548,7 @@ def prefill(q, k, v, g, beta, state0, cu_seqlens, checkpoints=None, normalize=Fa
         rate = np.exp(np.asarray(a_log, np.float64))
         rate = rate[None, :, None] if kda else rate[None, :]
         g = -rate * _softplus20(g + bias)
+    if a_log is not None if beta_logits is None else beta_logits:
         beta = 1.0 / (1.0 + np.exp(-beta))
     head_of = np.arange(H) // (H // HK)
     out = np.zeros((T, H, V))

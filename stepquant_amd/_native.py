@@ -12,7 +12,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("STEPQUANT_HIP_LIB", os.path.join(_HERE, "libstepquant_hip.so"))
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 F32, BF16, F16, I32, I64 = 0, 1, 2, 3, 4
 _DTYPES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16, torch.int32: I32, torch.int64: I64}
@@ -51,7 +51,8 @@ class PrefillArgs(ctypes.Structure):
                 ("q_stride", ctypes.c_int64), ("k_stride", ctypes.c_int64), ("v_stride", ctypes.c_int64),
                 ("key_heads", ctypes.c_int32), ("n_checkpoints", ctypes.c_int32), ("qkv_dtype", ctypes.c_int32),
                 ("gate_dtype", ctypes.c_int32), ("out_dtype", ctypes.c_int32), ("slots_dtype", ctypes.c_int32),
-                ("normalize", ctypes.c_int32), ("scale", ctypes.c_float), ("events", _P)]
+                ("normalize", ctypes.c_int32), ("scale", ctypes.c_float), ("events", _P),
+                ("beta_logits", ctypes.c_int32), ("reserved", ctypes.c_int32)]
 
 
 class FormatPool(ctypes.Structure):

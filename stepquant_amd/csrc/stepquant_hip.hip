@@ -2970,7 +2970,7 @@ struct PrefillDev {
   const float *init;
   float *ck_state;
   int64_t q_stride, k_stride, v_stride;
-  int H, HK, NC, gate_dtype, out_dtype, normalize;
+  int H, HK, NC, gate_dtype, out_dtype, normalize, beta_logits;
   float scale;
 };
 
@@ -3306,8 +3306,8 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
         const float u = lg + dt_h;
         const float sp = u > 20.0f ? u : __logf(1.0f + __expf(u < 20.0f ? u : 20.0f));
         lg = -ea_h * sp;
-        bt = __builtin_amdgcn_rcpf(1.0f + __expf(-bt));
       }
+      if (D.beta_logits && l < n) bt = __builtin_amdgcn_rcpf(1.0f + __expf(-bt));
       lg = wave_scan(lg);  // inclusive prefix sum of the log decays over the 64 tokens
       sm[SM_LC * 64 + l] = lg;
       sm[SM_BETA * 64 + l] = bt;
@@ -3730,7 +3730,7 @@ __global__ __launch_bounds__(NT) void kda_prefill_kernel(pf::PrefillDev D) {
       }
       if ((tid & 15) == 0) {
         float bt = R.beta;
-        if (D.a_log) bt = 1.0f / (1.0f + __expf(-bt));
+        if (D.beta_logits) bt = 1.0f / (1.0f + __expf(-bt));
         lds[OFF_BT + tt] = live ? bt : 0.0f;
       }
     }
@@ -4857,6 +4857,7 @@ int sq_prefill(const sq_pool *pool, const sq_prefill_args *a, void *stream) {
   D.gate_dtype = a->gate_dtype;
   D.out_dtype = a->out_dtype;
   D.normalize = a->normalize;
+  D.beta_logits = a->beta_logits != 0;
   D.scale = a->scale;
   if (pool->kda) {
     hipError_t e = hipFuncSetAttribute((const void *)kp::kda_prefill_kernel,

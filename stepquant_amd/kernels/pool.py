@@ -171,23 +171,9 @@ class PackedStatePool:
         self._pages = torch.zeros(slots * cursor + 64, device=dev, dtype=torch.uint8)
         self.data = self._pages[:slots * cursor].view(slots, cursor)
         self.bits = plan.bits.to(torch.int32).contiguous()
-        self.head_groups = []
-        if plan.architecture == "gdn":
-            widths = plan.bits[:, 0].cpu().tolist()
-            for width in sorted(set(widths)):
-                ids = [i for i, b in enumerate(widths) if b == width]
-                self.head_groups.append((width, torch.tensor(ids, device=dev, dtype=torch.int32)))
-        self.read_groups = []
-        if self.head_groups:
-            integer_ids = [i for i, b in enumerate(widths) if b != 16]
-            if integer_ids:
-                self.read_groups.append((0, torch.tensor(integer_ids, device=dev, dtype=torch.int32)))
-            self.read_groups.extend((w, ids) for w, ids in self.head_groups if w == 16)
         self.impact = plan.impact.float().contiguous().to(dev)
-        max_impact = float(self.impact.max().item())
-        self.fast_fit = self.keys * (65504. * 64 * 127 * max_impact) ** 2 < 2. ** 124
         self.coefficients = None
-        self.row_tile = min(32, value_dim, plan.value_group_size) if plan.architecture == "gdn" else min(8, value_dim)
+        self.keep_prefill_states = False
         self._desc = N.Pool(
             data=self._pages.data_ptr(), page_bytes=cursor, num_slots=slots, bits=self.bits.data_ptr(),
             offsets=self.offsets.data_ptr(), rows=self.rows.data_ptr(), columns=self.columns.data_ptr(),
@@ -263,9 +249,6 @@ class PackedStatePool:
                 tensor.record_stream(stream)
             self.writeback_stream = stream
         self.writeback_chunk = chunk
-
-    def _args(self):
-        return self.data, self.bits, self.impact, self.offsets, self.rows, self.columns
 
     # ------------------------------------------------------------- codecs
     def encode(self, state, slots):
@@ -356,7 +339,8 @@ class PackedStatePool:
         return out
 
     def extend(self, q, k, v, g, beta, slots, cu_seqlens, *, checkpoints=None, checkpoint_slots=None,
-               init_slots=None, normalize=False, scale=1., a_log=None, dt_bias=None, events=None):
+               init_slots=None, normalize=False, scale=1., a_log=None, dt_bias=None, beta_logits=None,
+               events=None, keep_states=None):
         """Chunked prefill of whole sequences straight from and into the pool.
 
         The behaviour of the serving adapter's ``kernel_extend``
@@ -364,7 +348,10 @@ class PackedStatePool:
         the chunked recurrence, encode the final states back) in one call:
         q, k ``[T, HK*K]`` (or ``[..., T, HK, K]``), v ``[T, H*V]``, g
         ``[T, H]`` (KDA: ``[T, H, K]``, per key channel), beta ``[T, H]``
-        (raw gate and logits with ``a_log``/``dt_bias``),
+        (with ``a_log``/``dt_bias``, ``g`` is the raw gate and the log decay
+        is ``-exp(a_log) * softplus(g + dt_bias)``; ``beta_logits`` says
+        whether beta holds logits, default: when ``a_log`` is given, as the
+        decode step's convention),
         ``cu_seqlens`` ``[B+1]`` token offsets, ``slots`` ``[B]``.  Initial
         states come from ``init_slots`` (default ``slots``; ``None`` entries
         or slot <= 0 start from zero).  By default the final state is written
@@ -374,7 +361,10 @@ class PackedStatePool:
         must start at 0 and never decrease (ValueError otherwise).  Returns the outputs ``[T, H, V]`` in q's dtype.
         ``events`` (benchmarks): two ``torch.cuda.Event`` with timing, recorded
         once already, that the call records on the current stream right before
-        and after the recurrence kernel.
+        and after the recurrence kernel.  ``keep_states`` (tests; default: the
+        pool's ``keep_prefill_states``, False) keeps the call's device inputs
+        and fp32 state workspaces in ``last_prefill``; otherwise the pool
+        holds no reference to them after the call.
         """
         self.wait()
         if self.keys != 128 or self.values != 128:
@@ -491,7 +481,8 @@ class PackedStatePool:
             checkpoint_state=N.ptr(ck_state), batch=batch, q_stride=q2.stride(0), k_stride=k2.stride(0),
             v_stride=v2.stride(0), key_heads=hk, n_checkpoints=nc, qkv_dtype=N.BF16,
             gate_dtype=N.dtype_code(g2), out_dtype=N.dtype_code(out), slots_dtype=N.dtype_code(ck_slots),
-            normalize=int(bool(normalize)), scale=float(scale))
+            normalize=int(bool(normalize)), scale=float(scale),
+            beta_logits=int(a_log is not None if beta_logits is None else bool(beta_logits)), reserved=0)
         if events is not None:
             # benchmark hook: two recorded torch.cuda.Event (torch creates them
             # at their first record) around the recurrence kernel
@@ -502,7 +493,8 @@ class PackedStatePool:
             args.events = ctypes.cast(ev, ctypes.c_void_p)
         if batch:
             N.check(N.lib().sq_prefill(self._desc, args, N.stream_handle()), "prefill")
-        self._last_prefill = (q2, k2, v2, g2, b2, al, db, cu, ck, init, ck_slots, init_state, ck_state)
+        if self.keep_prefill_states if keep_states is None else keep_states:
+            self.last_prefill = (q2, k2, v2, g2, b2, al, db, cu, ck, init, ck_slots, init_state, ck_state)
         return out
 
     @staticmethod

@@ -174,3 +174,84 @@ def check_scales(got_pages, ref_pages, slots, oplan, lay, V, budget, updated=Non
                 f"request {b} head {h} column {j}: scale {cols[bl, idx]} fp16 ulps off, not a c0 rounding"
         assert len(far) <= np.ceil(c0_budget * cols.size), f"{len(far)} column scales differ by more than one fp16 ulp"
     return fr, fc
+
+
+# row/column scales allowed one fp16 ulp off on at most this fraction
+SCALE_BUDGET = 0.02
+
+
+def check_requant(got_pages, slots, oplan, lay, V, updated, flip_budget=1e-3, storage="packed"):
+    """Pages requantised on the device against the oracle's encoding of the
+    oracle's own state ``updated``: integer codes at most
+    one level apart on at most ``flip_budget`` of them, pivots within
+    rtol 1e-3, row and column scales per ``check_scales``, and dequantised
+    values within rtol 1e-3 / atol 1e-4 except on at most ``flip_budget``.
+    Byte pages are held to the dequantised-value bar.  Returns the flipped
+    fraction of integer codes (of dequantised values for byte pages)."""
+    ref = np.zeros_like(got_pages)
+    O.encode_page(np.asarray(updated, np.float32), slots, oplan, lay, ref, storage)
+    live = np.broadcast_to((np.asarray(slots) > 0)[:, None, None, None], (len(slots),) + oplan.bits.shape + (V,))
+    frac = None
+    if storage == "packed":
+        a = page_codes(got_pages, slots, oplan, lay, V)
+        b = page_codes(ref, slots, oplan, lay, V)
+        integer = np.broadcast_to(oplan.bits[None, :, :, None] != 16, a.shape)
+        m = integer & live
+        diff = np.abs(a[m] - b[m])
+        assert diff.max(initial=0) <= 1, f"code differs by {diff.max()}"
+        frac = float((diff > 0).mean()) if diff.size else 0.0
+        print(f"codes: {frac:.2e} of {diff.size} flipped by one level", flush=True)
+        assert frac <= flip_budget, f"{frac:.2e} of codes flipped"
+        pv = (~integer) & live
+        if pv.any():
+            pa = a[pv].astype(np.uint16).view(np.float16).astype(np.float32)
+            pb = b[pv].astype(np.uint16).view(np.float16).astype(np.float32)
+            np.testing.assert_allclose(pa, pb, rtol=1e-3, atol=1e-5)
+        check_scales(got_pages, ref, slots, oplan, lay, V, SCALE_BUDGET, updated)
+    ga = O.decode_page(got_pages, slots, oplan, lay, V, storage)
+    gb = O.decode_page(ref, slots, oplan, lay, V, storage)
+    off = ~np.isclose(ga, gb, rtol=1e-3, atol=1e-4)
+    print(f"dequantised: {off[live].mean():.2e} beyond rtol 1e-3 / atol 1e-4", flush=True)
+    assert off[live].mean() <= flip_budget, f"{off[live].mean():.2e} of dequantised values differ"
+    return frac if frac is not None else float(off[live].mean())
+
+
+def sub_pages(pages, oplan, lay, heads, V):
+    """The packed pages restricted to ``heads``: (plan, layout, pages) of a
+    pool holding only those heads, each head's code region, row scales and
+    column scales copied to their places in the smaller layout."""
+    H, K = oplan.bits.shape
+    tile = min(4 if oplan.kda else 16, V)
+    sub = type(oplan)(oplan.architecture, oplan.bits[heads], oplan.impact[heads], oplan.value_group_size)
+    sl = O.layout(sub, V)
+    out = np.zeros((pages.shape[0], sl.page_bytes), np.uint8)
+    for n, h in enumerate(heads):
+        start, stride = int(lay.offsets[h * K]), int(lay.offsets[H * K + h])
+        dst, size = int(sl.offsets[n * K]), (V // tile) * stride
+        assert int(sl.offsets[len(heads) * K + n]) == stride
+        out[:, dst:dst + size] = pages[:, start:start + size]
+        two = (not oplan.kda) and oplan.bits[h, 0] == 2
+        nr = 2 * (V // oplan.value_group_size if two else 1)
+        for i in range(K):
+            src, to = int(lay.rows[h * K + i]), int(sl.rows[n * K + i])
+            if src >= 0:
+                out[:, to:to + nr] = pages[:, src:src + nr]
+        if lay.columns[h] >= 0:
+            src, to = int(lay.columns[h]), int(sl.columns[n])
+            out[:, to:to + 2 * V] = pages[:, src:src + 2 * V]
+    return sub, sl, out
+
+
+def check_prefill(out, ref_out, what="outputs"):
+    """Prefill outputs against the float64 recurrence: rtol 1e-3 / atol 1e-4
+    for fp32 outputs, rtol 2^-8 / atol 1e-4 for 16-bit ones (one rounding of
+    the stored value on top of the kernel's own error)."""
+    got = out.float().cpu().numpy() if isinstance(out, torch.Tensor) else np.asarray(out)
+    rtol = 1e-3 if (not isinstance(out, torch.Tensor) or out.dtype == torch.float32) else 2 ** -8
+    np.testing.assert_allclose(got, ref_out, rtol=rtol, atol=1e-4, err_msg=what)
+
+
+def check_states(got, ref, what="states"):
+    """Prefill states against the float64 recurrence, elementwise:
+    rtol 1e-3 / atol 1e-4."""
+    np.testing.assert_allclose(np.asarray(got), ref, rtol=1e-3, atol=1e-4, err_msg=what)

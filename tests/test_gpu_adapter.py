@@ -7,8 +7,10 @@ its hooks make, with the arguments they pass: slot allocation clears pages
 the page bytes after a synchronisation and loads them back after ``wait()``
 (:154-166), the temporal cache reports ``nbytes`` (TemporalPages).  The
 extend hook is this package's own (``stepquant_amd.sglang.extend``): fused
-prefill into the pages for GDN K = V = 128 packed pools, the reference's
-decode / chunk kernel / encode round trip for the others.  prefill_reduce
+prefill into the pages for GDN and KDA pools with K = V = 128 (packed or
+byte pages), with the chunk kernels' argument conventions (KDA: raw gate
+with ``A_log``/``dt_bias``, beta after the sigmoid); the reference's decode /
+chunk kernel / encode round trip for the others.  prefill_reduce
 runs on device tensors with a stand-in coordinator.
 """
 from types import SimpleNamespace
@@ -20,7 +22,7 @@ import torch
 from oracle import oracle as O
 from stepquant_amd.sglang import extend as E
 from stepquant_amd.sglang import prefill_reduce as PR
-from tests.helpers import dev
+from tests.helpers import check_prefill, check_requant, check_states, dev
 
 pytestmark = pytest.mark.gpu
 
@@ -119,20 +121,67 @@ def test_decode_calls_and_fused_extend_hook():
     ge = -torch.nn.functional.softplus(torch.randn(1, T, H, generator=g))
     be = torch.sigmoid(torch.randn(1, T, H, generator=g))
     S0 = pool_a.decode(slots).cpu().numpy().astype(np.float64)
+    pool_a.keep_prefill_states = True
     oe = E.kernel_extend(None, None, qe.to(dev()), ke.to(dev()), ve.to(dev()), ge.to(dev()), be.to(dev()),
                          ssm_states=pool_a, cache_indices=slots, query_start_loc=cu.to(dev()))
     torch.cuda.synchronize()
     ref_out, _, final = O.prefill(qe[0].float().numpy(), ke[0].float().numpy(), ve[0].float().numpy(),
                                   ge[0].numpy(), be[0].numpy(), S0, cu.numpy(), normalize=True, scale=K ** -.5)
     assert oe.shape == (1, T, H, V)
-    err = np.abs(oe[0].float().cpu().numpy() - ref_out) / (np.abs(ref_out).max(-1, keepdims=True) + 1e-30)
-    assert err.max() <= 2 ** -8 + 1e-3
-    dense = pool_a._last_prefill[-1].cpu().numpy()  # the kernel's fp32 final states
-    err = np.abs(dense - final) / (np.abs(final).max(-1, keepdims=True) + 1e-30)
-    assert err.max() <= 1e-3
+    check_prefill(oe[0], ref_out, "bf16 outputs")
+    dense = pool_a.last_prefill[-1].cpu().numpy()  # the kernel's fp32 final states
+    check_states(dense, final)
     ref = pool_a.data.cpu().numpy().copy()
     O.encode_page(dense, slots.cpu().numpy(), oplan, lay, ref)
     assert np.array_equal(pool_a.data.cpu().numpy(), ref), "final pages are the oracle encoding"
+    check_requant(pool_a.data.cpu().numpy(), slots.cpu().numpy(), oplan, lay, V, final)
+
+
+@pytest.mark.parametrize("storage", ["packed", "byte"])
+def test_fused_extend_hook_kda_reference_call_shape(storage):
+    """Kimi-Linear prefill through the hook exactly as the reference's KDA
+    call passes it (tests/test_sglang_cuda.py:30-45): q, k, v [1, T, H, K]
+    bf16, a raw per-channel gate g [1, T, H, K], beta [1, T, H] already in
+    (0, 1), A_log [H] and dt_bias [H*K] as keyword arguments, int32 offsets
+    on the device.  The log decay is -exp(A_log) softplus(g + dt_bias) and
+    beta is used as given; outputs, final states and pages against the
+    float64 recurrence."""
+    from stepquant_amd.kernels.pool import PackedStatePool
+    from stepquant_amd.quantization import QuantizationPlan
+    print(f"case kda extend hook {storage}", flush=True)
+    h, K, V = 4, 128, 128
+    rng = np.random.default_rng(54)
+    bits = np.where(rng.random((h, K)) < .02, 16, rng.choice([4, 6, 8], (h, K)))
+    oplan = O.Plan("kda", bits.astype(np.int32), np.ones((h, K), np.float32), 32)
+    plan = QuantizationPlan("kda", torch.from_numpy(bits).to(dev()), torch.ones(h, K, device=dev()))
+    stream = torch.cuda.Stream() if storage == "byte" else None
+    pool = PackedStatePool(plan, 5, V, writeback_stream=stream, storage=storage)
+    assert E.fused(pool)
+    g = torch.Generator().manual_seed(54)
+    slots = torch.tensor([3, 1], device=dev())
+    pool.encode((torch.randn(2, h, K, V, generator=g) * .1).to(dev()), slots)
+    pool.wait()
+    lay = O.layout(oplan, V, storage)
+    S0 = O.decode_page(pool.data.cpu().numpy(), slots.cpu().numpy(), oplan, lay, V, storage).astype(np.float64)
+    cu = torch.tensor([0, 8, 24], device=dev(), dtype=torch.int32)
+    q, key, val = [torch.randn(1, 24, h, K, generator=g).to(torch.bfloat16) for _ in range(3)]
+    alog = torch.randn(h, generator=g) * .3
+    bias = torch.randn(h * K, generator=g) * .3
+    graw = torch.randn(1, 24, h, K, generator=g)
+    beta = torch.rand(1, 24, h, generator=g)
+    pool.keep_prefill_states = True
+    out = E.kernel_extend(None, None, q.to(dev()), key.to(dev()), val.clone().to(dev()), graw.to(dev()),
+                          beta.to(dev()), ssm_states=pool, cache_indices=slots, query_start_loc=cu,
+                          A_log=alog.to(dev()), dt_bias=bias.to(dev()))
+    torch.cuda.synchronize()
+    ref_out, _, final = O.prefill(q[0].float().numpy(), key[0].float().numpy(), val[0].float().numpy(),
+                                  graw[0].numpy(), beta[0].numpy(), S0, cu.cpu().numpy(), normalize=True,
+                                  scale=K ** -.5, a_log=alog.numpy(), dt_bias=bias.numpy(), beta_logits=False)
+    assert out.shape == (1, 24, h, V) and out.dtype == torch.bfloat16
+    check_prefill(out[0], ref_out, "bf16 outputs")
+    check_states(pool.last_prefill[-1].cpu().numpy(), final)
+    pages = pool.data.cpu().numpy()
+    check_requant(pages, slots.cpu().numpy(), oplan, lay, V, final, storage=storage)
 
 
 def test_extend_round_trip_for_format_pools():

@@ -18,7 +18,7 @@ import pytest
 import torch
 
 from oracle import oracle as O
-from tests.helpers import check_scales, dev, device_plan, make_plan, page_codes
+from tests.helpers import SCALE_BUDGET, check_requant, check_scales, dev, device_plan, make_plan, page_codes
 
 pytestmark = pytest.mark.gpu
 
@@ -26,7 +26,6 @@ pytestmark = pytest.mark.gpu
 # from the oracle's: the step's reciprocal-based quotients and its row-sum
 # order differ from fit_state's at the float32 ulp level (observed on the
 # MI355X: at most 0.02% of row and 0.7% of column scales)
-SCALE_BUDGET = 0.02
 
 GOLDEN_GPU_CASES = ["c_config_gdn", "c_config_gdn_uniform6", "gdn_two_bit_g32", "gdn_mixed_v16_g4",
                     "kda_mixed_128", "kda_edges_v4", "kda_edges_v32", "gdn_v8_k4", "gdn_v32_k32",
@@ -148,30 +147,7 @@ STEP_CASES = {
 }
 
 
-def _check_requant(got_pages, slots, oplan, lay, V, updated, flip_budget=1e-3):
-    ref = np.zeros_like(got_pages)
-    O.encode_page(updated, slots, oplan, lay, ref)
-    a = page_codes(got_pages, slots, oplan, lay, V)
-    b = page_codes(ref, slots, oplan, lay, V)
-    integer = np.broadcast_to(oplan.bits[None, :, :, None] != 16, a.shape)
-    live = np.broadcast_to((np.asarray(slots) > 0)[:, None, None, None], a.shape)
-    m = integer & live
-    diff = np.abs(a[m] - b[m])
-    assert diff.max(initial=0) <= 1, f"code differs by {diff.max()}"
-    frac = (diff > 0).mean() if diff.size else 0.0
-    assert frac <= flip_budget, f"{frac:.2e} of codes flipped"
-    pv = (~np.broadcast_to(oplan.bits[None, :, :, None] != 16, a.shape)) & live
-    if pv.any():
-        pa = a[pv].astype(np.uint16).view(np.float16).astype(np.float32)
-        pb = b[pv].astype(np.uint16).view(np.float16).astype(np.float32)
-        np.testing.assert_allclose(pa, pb, rtol=1e-3, atol=1e-5)
-    # row scales (per value group on 2-bit GDN heads) and column scales
-    check_scales(got_pages, ref, slots, oplan, lay, V, SCALE_BUDGET, updated)
-    ga = O.decode_page(got_pages, slots, oplan, lay, V)
-    gb = O.decode_page(ref, slots, oplan, lay, V)
-    close = np.isclose(ga, gb, rtol=1e-3, atol=1e-4)
-    assert (~close).mean() <= flip_budget, f"{(~close).mean():.2e} of dequantised values differ"
-    return frac
+_check_requant = check_requant
 
 
 @pytest.mark.parametrize("name", list(STEP_CASES))

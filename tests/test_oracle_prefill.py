@@ -6,6 +6,7 @@ pinned to core.py:5-15 and kernels/fused.py:155-179); the closed-form chunked
 property of checkpoints; sequence boundaries.
 """
 import numpy as np
+import torch
 import pytest
 
 from oracle import oracle as O
@@ -136,6 +137,36 @@ def test_kda_single_token_equals_delta_step(raw):
     ref_out, ref_state = O.delta_step(state, qp, kp, v, ld, bo)
     np.testing.assert_allclose(out, ref_out, rtol=2e-5, atol=2e-6)
     np.testing.assert_allclose(final, ref_state, rtol=2e-5, atol=2e-6)
+
+
+@pytest.mark.parametrize("kda", [False, True])
+def test_raw_gate_with_post_sigmoid_beta(kda):
+    """The chunk kernels' KDA convention (raw gate with A_log/dt_bias, beta
+    already through the sigmoid): the same recurrence as the log decay
+    -exp(A_log) softplus(g + dt_bias), computed here with torch, and beta
+    taken as given; with beta_logits the sigmoid is applied."""
+    rng = np.random.default_rng(8)
+    H, HK, K, V, T = 2, 2, 8, 4, 9
+    q, k, v, _, beta = (x.astype(np.float32) for x in _inputs(rng, T, H, HK, K, V))
+    gshape = (T, H, K) if kda else (T, H)
+    raw = rng.standard_normal(gshape).astype(np.float32)
+    a_log = (rng.standard_normal(H) * .5).astype(np.float32)
+    dt_bias = (rng.standard_normal(H * K if kda else H) * .5).astype(np.float32)
+    S0 = (rng.standard_normal((1, H, K, V)) * .3).astype(np.float32)
+    cu = np.array([0, T])
+    bias = torch.from_numpy(dt_bias).double().reshape((H, K) if kda else (H,))
+    rate = torch.from_numpy(a_log).double().exp().reshape((H, 1) if kda else (H,))
+    logd = (-rate * torch.nn.functional.softplus(torch.from_numpy(raw).double() + bias)).numpy()
+    want = O.prefill(q, k, v, logd, beta, S0, cu, normalize=True, scale=.3)
+    got = O.prefill(q, k, v, raw, beta, S0, cu, normalize=True, scale=.3, a_log=a_log, dt_bias=dt_bias,
+                    beta_logits=False)
+    for a, b in zip(got, want):
+        np.testing.assert_allclose(a, b, rtol=1e-12, atol=1e-12)
+    b64 = beta.astype(np.float64)
+    logits = np.log(b64 / (1 - b64))
+    again = O.prefill(q, k, v, raw, logits, S0, cu, normalize=True, scale=.3, a_log=a_log, dt_bias=dt_bias)
+    for a, b in zip(again, want):
+        np.testing.assert_allclose(a, b, rtol=1e-9, atol=1e-9)
 
 
 def _kda_chunk_closed_form(q, k, v, g, beta, S0):

@@ -116,3 +116,40 @@ def test_far_column_scale_without_explanation_is_caught():
     got[1, o:o + 2] = np.array([wrong], np.int16).view(np.uint8)
     with pytest.raises(AssertionError, match="not a c0 rounding"):
         check_scales(got, pages, slots, oplan, lay, 128, 1.0, updated=x)
+
+
+@pytest.mark.parametrize("arch,bits", [("gdn", GDN), ("kda", None)])
+def test_sub_pages_equal_the_encoding_of_those_heads(arch, bits):
+    """sub_pages (the P6 parity check's head selection) gives exactly the
+    pages a pool of only those heads holds for the same states."""
+    from tests.helpers import sub_pages
+    if bits is None:
+        bits = np.where(np.random.default_rng(2).random((4, 128)) < .03, 16,
+                        np.random.default_rng(3).choice([2, 4, 6, 8], (4, 128)))
+    oplan = make_plan(arch, bits, seed=4)
+    H, K, V, B = 4, 128, 128, 3
+    lay = O.layout(oplan, V)
+    x = (np.random.default_rng(0).standard_normal((B, H, K, V)) * .1).astype(np.float32)
+    pages = np.zeros((B + 1, lay.page_bytes), np.uint8)
+    slots = np.arange(1, B + 1)
+    O.encode_page(x, slots, oplan, lay, pages)
+    heads = [3, 1]
+    sub, sl, got = sub_pages(pages, oplan, lay, heads, V)
+    want = np.zeros_like(got)
+    O.encode_page(x[:, heads], slots, sub, sl, want)
+    assert np.array_equal(got, want)
+
+
+def test_requant_check_catches_a_planted_code_flip_rate():
+    """check_requant passes the oracle's own pages and fails when more than
+    the budget of codes sit one level off (planted in the oracle's state)."""
+    from tests.helpers import check_requant
+    oplan, lay, pages, slots = _pages("gdn", np.full((4, 128), 8))
+    x = (np.random.default_rng(0).standard_normal((3, 4, 128, 128)) * .1).astype(np.float32)  # as _pages
+    assert check_requant(pages, slots, oplan, lay, 128, x) == 0.0
+    # move 1% of the values by about one level: their codes flip
+    rng = np.random.default_rng(1)
+    step = np.abs(x).max(axis=2, keepdims=True) / 127
+    moved = x + (rng.random(x.shape) < .01) * step * 1.01
+    with pytest.raises(AssertionError, match="code|dequantised"):
+        check_requant(pages, slots, oplan, lay, 128, moved)

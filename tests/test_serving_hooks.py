@@ -136,3 +136,41 @@ def test_fingerprint(tmp_path):
     (tmp_path / "config.json").write_text('{"a": 1}')
     (tmp_path / "model.safetensors.index.json").write_text('{"w": 2}')
     assert fingerprint(tmp_path) == hashlib.sha256(b'{"a": 1}{"w": 2}').hexdigest()
+
+
+def _registry(patched_all):
+    from stepquant_amd.sglang import extend as E
+    hooks = {"a.TritonGDNKernel.extend": [("around", E.kernel_extend, None)],
+             "b.GroupCoordinator.all_reduce": [("around", PR.all_reduce, None)],
+             "c.Unrelated.forward": [("around", len, None)]}
+    patched = set(hooks) if patched_all else {"c.Unrelated.forward", "b.GroupCoordinator.all_reduce"}
+    return SimpleNamespace(_hooks=hooks, _patched=patched)
+
+
+def test_verify_hooks_counts_this_package_hooks():
+    """The reference plugin's verify_hooks only sees hooks of its own
+    stepquant.sglang modules; this package's extend and prefill_reduce hooks
+    are counted here, and an unpatched one refuses to serve."""
+    from stepquant_amd.sglang import verify_hooks
+    assert verify_hooks(_registry(True)) == ["a.TritonGDNKernel.extend", "b.GroupCoordinator.all_reduce"]
+    with pytest.raises(RuntimeError, match="TritonGDNKernel.extend"):
+        verify_hooks(_registry(False))
+    with pytest.raises(RuntimeError, match="incomplete"):
+        verify_hooks(SimpleNamespace(_hooks={}, _patched=set()))
+
+
+def test_fused_extend_rejects_keyword_arguments_it_would_drop():
+    """The fused branch consumes A_log and dt_bias (KDA's raw gate) and
+    nothing else: any other keyword argument is an error, not dropped.  The
+    checks run before any device work, so a host stand-in of the pool is
+    enough."""
+    from stepquant_amd.kernels.pool import PackedStatePool
+    from stepquant_amd.sglang import extend as E
+    pool = object.__new__(PackedStatePool)
+    pool.keys = pool.values = 128
+    assert E.fused(pool)
+    call = dict(ssm_states=pool, cache_indices=None, query_start_loc=None)
+    with pytest.raises(TypeError, match="layer_id"):
+        E.kernel_extend(None, None, None, None, None, None, None, layer_id=3, **call)
+    with pytest.raises(TypeError, match="together"):
+        E.kernel_extend(None, None, None, None, None, None, None, A_log=torch.zeros(2), **call)

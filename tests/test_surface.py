@@ -29,14 +29,30 @@ def test_library_exports_every_declared_symbol():
     assert N.lib().sq_abi_version() == N.ABI_VERSION
 
 
-def test_structs_match_header_layout():
+def test_structs_match_header_layout(tmp_path):
+    """Every ctypes field sits at the offset gcc gives the header's struct."""
+    import subprocess
     from stepquant_amd import _native as N
-    # 8-byte pointers/int64 then int32 fields, as in include/stepquant_hip.h
-    assert ctypes.sizeof(N.Pool) == 8 * 9 + 4 * 10
-    assert ctypes.sizeof(N.StepArgs) == 8 * 13 + 4 * 8
-    assert ctypes.sizeof(N.Scratch) == 8 * 5
-    assert ctypes.sizeof(N.PrefillArgs) == 8 * 14 + 8 * 4 + 4 * 8 + 8  # ... then the events pointer
-    assert ctypes.sizeof(N.FormatPool) == 8 * 6 + 4 * 8
+    structs = {"sq_pool": N.Pool, "sq_step_args": N.StepArgs, "sq_writeback_scratch": N.Scratch,
+               "sq_prefill_args": N.PrefillArgs, "sq_format_pool": N.FormatPool}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "stepquant_hip.h"', "int main(void) {"]
+    for name, cls in structs.items():
+        lines.append(f'  printf("{name} size %zu\\n", sizeof({name}));')
+        for field, _ in cls._fields_:
+            lines.append(f'  printf("{name} {field} %zu\\n", offsetof({name}, {field}));')
+    lines.append("  return 0;\n}")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", "-I", f"{ROOT}/include", "-o", str(exe), str(src)], check=True)
+    seen = {}
+    for line in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.splitlines():
+        name, field, value = line.split()
+        seen[name, field] = int(value)
+    for name, cls in structs.items():
+        assert seen[name, "size"] == ctypes.sizeof(cls), name
+        for field, _ in cls._fields_:
+            assert seen[name, field] == getattr(cls, field).offset, (name, field)
 
 
 def test_invalid_arguments_are_reported_without_a_device():
