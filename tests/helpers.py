@@ -143,7 +143,8 @@ def explained_by_initial_scale(got_pages, slots, oplan, lay, V, updated, b, h, j
     return False
 
 
-def check_scales(got_pages, ref_pages, slots, oplan, lay, V, budget, updated=None, c0_budget=0.01):
+def check_scales(got_pages, ref_pages, slots, oplan, lay, V, budget, updated=None, c0_budget=0.01,
+                 refit_budget=None):
     """Row and column scales equal the oracle's up to one fp16 ulp, and at
     most a ``budget`` fraction of them differ at all.
 
@@ -153,7 +154,12 @@ def check_scales(got_pages, ref_pages, slots, oplan, lay, V, budget, updated=Non
     fp16 ulp from the oracle's: c0 = fp16(max|x/r|/L) rounds the other way
     when the step's state differs from the oracle's at the float32 ulp
     level, and the least-squares refit of a low-width column follows the
-    codes of that c0 by several ulps.  Returns the fractions off by one ulp."""
+    codes of that c0 by several ulps.  With ``refit_budget`` (states that
+    differ from the oracle's by more than float32 rounding, e.g. a chunked
+    recurrence against the float64 one), at most that fraction of column
+    scales may be further off: one flipped first-pass code moves the refit
+    sum Σ z² by up to 2L - 1, which is many fp16 ulps of c when the column
+    holds few large codes.  Returns the fractions off by one ulp."""
     rows, cols = scale_ulps(got_pages, ref_pages, slots, oplan, lay, V)
     fr = float((rows > 0).mean()) if rows.size else 0.0
     fc = float((cols > 0).mean()) if cols.size else 0.0
@@ -164,7 +170,10 @@ def check_scales(got_pages, ref_pages, slots, oplan, lay, V, budget, updated=Non
     assert rows.max(initial=0) <= 1, f"a row scale differs by {rows.max()} fp16 ulps"
     assert fr <= budget, f"{fr:.2e} of row scales differ"
     assert fc <= budget, f"{fc:.2e} of column scales differ"
-    if len(far):
+    if len(far) and refit_budget is not None:
+        assert len(far) <= np.ceil(refit_budget * cols.size), \
+            f"{len(far)} column scales differ by more than one fp16 ulp (max {cols.max()})"
+    elif len(far):
         assert updated is not None, f"a column scale differs by {cols.max()} fp16 ulps"
         live = [bi for bi, s in enumerate(slots) if s > 0]
         heads = [h for h in range(oplan.bits.shape[0]) if lay.columns[h] >= 0]
@@ -178,14 +187,20 @@ def check_scales(got_pages, ref_pages, slots, oplan, lay, V, budget, updated=Non
 
 # row/column scales allowed one fp16 ulp off on at most this fraction
 SCALE_BUDGET = 0.02
+# prefill pages against the oracle's encoding of the float64 recurrence's
+# states: column scales further than one fp16 ulp off on at most this
+# fraction (the refit's response to first-pass code flips; measured at P6:
+# 0.16%, max 15 ulps)
+PREFILL_REFIT_BUDGET = 0.005
 
 
-def check_requant(got_pages, slots, oplan, lay, V, updated, flip_budget=1e-3, storage="packed"):
+def check_requant(got_pages, slots, oplan, lay, V, updated, flip_budget=1e-3, storage="packed", refit_budget=None):
     """Pages requantised on the device against the oracle's encoding of the
     oracle's own state ``updated``: integer codes at most
     one level apart on at most ``flip_budget`` of them, pivots within
     rtol 1e-3, row and column scales per ``check_scales``, and dequantised
     values within rtol 1e-3 / atol 1e-4 except on at most ``flip_budget``.
+    ``refit_budget`` is passed to ``check_scales``.
     Byte pages are held to the dequantised-value bar.  Returns the flipped
     fraction of integer codes (of dequantised values for byte pages)."""
     ref = np.zeros_like(got_pages)
@@ -207,7 +222,7 @@ def check_requant(got_pages, slots, oplan, lay, V, updated, flip_budget=1e-3, st
             pa = a[pv].astype(np.uint16).view(np.float16).astype(np.float32)
             pb = b[pv].astype(np.uint16).view(np.float16).astype(np.float32)
             np.testing.assert_allclose(pa, pb, rtol=1e-3, atol=1e-5)
-        check_scales(got_pages, ref, slots, oplan, lay, V, SCALE_BUDGET, updated)
+        check_scales(got_pages, ref, slots, oplan, lay, V, SCALE_BUDGET, updated, refit_budget=refit_budget)
     ga = O.decode_page(got_pages, slots, oplan, lay, V, storage)
     gb = O.decode_page(ref, slots, oplan, lay, V, storage)
     off = ~np.isclose(ga, gb, rtol=1e-3, atol=1e-4)

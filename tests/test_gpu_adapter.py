@@ -22,7 +22,7 @@ import torch
 from oracle import oracle as O
 from stepquant_amd.sglang import extend as E
 from stepquant_amd.sglang import prefill_reduce as PR
-from tests.helpers import check_prefill, check_requant, check_states, dev
+from tests.helpers import PREFILL_REFIT_BUDGET, check_prefill, check_requant, check_states, dev
 
 pytestmark = pytest.mark.gpu
 
@@ -134,7 +134,8 @@ def test_decode_calls_and_fused_extend_hook():
     ref = pool_a.data.cpu().numpy().copy()
     O.encode_page(dense, slots.cpu().numpy(), oplan, lay, ref)
     assert np.array_equal(pool_a.data.cpu().numpy(), ref), "final pages are the oracle encoding"
-    check_requant(pool_a.data.cpu().numpy(), slots.cpu().numpy(), oplan, lay, V, final)
+    check_requant(pool_a.data.cpu().numpy(), slots.cpu().numpy(), oplan, lay, V, final,
+                  refit_budget=PREFILL_REFIT_BUDGET)
 
 
 @pytest.mark.parametrize("storage", ["packed", "byte"])
@@ -181,7 +182,8 @@ def test_fused_extend_hook_kda_reference_call_shape(storage):
     check_prefill(out[0], ref_out, "bf16 outputs")
     check_states(pool.last_prefill[-1].cpu().numpy(), final)
     pages = pool.data.cpu().numpy()
-    check_requant(pages, slots.cpu().numpy(), oplan, lay, V, final, storage=storage)
+    check_requant(pages, slots.cpu().numpy(), oplan, lay, V, final, storage=storage,
+                  refit_budget=PREFILL_REFIT_BUDGET)
 
 
 def test_extend_round_trip_for_format_pools():

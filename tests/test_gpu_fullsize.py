@@ -15,7 +15,7 @@ import torch
 
 import bench
 from oracle import oracle as O
-from tests.helpers import check_prefill, check_requant, check_states, dev, make_plan, sub_pages
+from tests.helpers import PREFILL_REFIT_BUDGET, check_prefill, check_requant, check_states, dev, make_plan, sub_pages
 from tests.test_gpu_pool import _check_requant
 
 pytestmark = pytest.mark.gpu
@@ -155,7 +155,8 @@ def _check_prefix_pages(pool, states, ref_states, ck_slots, oplan, lay, pages0, 
     bad = [int(s) for s in live if not np.array_equal(pages[s], ref_pages[s])]
     assert not bad, f"prefix pages differ from the oracle encoding of the kernel's states: slots {bad}"
     sub, sl, sp = sub_pages(pages, oplan, lay, heads, V)
-    check_requant(sp, live, sub, sl, V, ref_states.reshape(B * NC, len(heads), K, V))
+    check_requant(sp, live, sub, sl, V, ref_states.reshape(B * NC, len(heads), K, V),
+                  refit_budget=PREFILL_REFIT_BUDGET)
     return pages
 
 

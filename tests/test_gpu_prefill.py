@@ -13,7 +13,7 @@ import pytest
 import torch
 
 from oracle import oracle as O
-from tests.helpers import check_prefill, check_requant, check_states, dev, device_plan, make_plan
+from tests.helpers import PREFILL_REFIT_BUDGET, check_prefill, check_requant, check_states, dev, device_plan, make_plan
 
 pytestmark = pytest.mark.gpu
 
@@ -31,7 +31,7 @@ def _check_pages(pool, ck_state, ref_states, ck_slots, oplan, lay, pages0, stora
     for s in live[live > 0]:
         assert np.array_equal(pages[s], ref_pages[s]), f"slot {s} page differs"
     used = np.where(live[:, None, None, None] > 0, ref_states.reshape(B * NC, H, K, V), 0)
-    check_requant(pages, live, oplan, lay, V, used, storage=storage)
+    check_requant(pages, live, oplan, lay, V, used, storage=storage, refit_budget=PREFILL_REFIT_BUDGET)
     return pages
 
 
@@ -144,7 +144,7 @@ def test_extend_defaults_write_final_state_back_to_the_slots():
     O.encode_page(dense, slots.numpy(), oplan, lay, ref_pages)
     got = pool.data.cpu().numpy()
     assert np.array_equal(got[slots.numpy()], ref_pages[slots.numpy()])
-    check_requant(got, slots.numpy(), oplan, lay, V, final)
+    check_requant(got, slots.numpy(), oplan, lay, V, final, refit_budget=PREFILL_REFIT_BUDGET)
     assert len(lens) == 2
 
 

@@ -153,3 +153,15 @@ def test_requant_check_catches_a_planted_code_flip_rate():
     moved = x + (rng.random(x.shape) < .01) * step * 1.01
     with pytest.raises(AssertionError, match="code|dequantised"):
         check_requant(pages, slots, oplan, lay, 128, moved)
+
+
+def test_refit_budget_bounds_far_column_scales():
+    """The prefill bar: column scales further than one ulp off are allowed on
+    at most refit_budget of the columns, and no more."""
+    oplan, lay, pages, slots = _pages("gdn", np.full((4, 128), 4))
+    bad = pages.copy()
+    for j in (3, 50, 99):                        # 3 of 1,536 column scales 5 ulps off
+        _bump(bad, 2, lay.columns[1] + 2 * j, 5)
+    check_scales(bad, pages, slots, oplan, lay, 128, 0.01, refit_budget=0.002)
+    with pytest.raises(AssertionError, match="more than one fp16 ulp"):
+        check_scales(bad, pages, slots, oplan, lay, 128, 0.01, refit_budget=0.001)
