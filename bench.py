@@ -54,6 +54,13 @@ def parse():
                    help="disjoint sets of B slots in each pool, used by consecutive steps in turn, so a set's "
                         "pages have left the 256 MB Infinity Cache before the set comes round again (4 sets: "
                         "315 MB of other pages read and written in between)")
+    p.add_argument("--foreground-gflop", type=float, default=0.0,
+                   help="stand-in for a layer's other work (attention, MLP): a bf16 matmul [B, 4096] x "
+                        "[4096, n] of about this many GFLOP after each attention window, on the foreground "
+                        "stream; with --async-writeback the previous layer's writer can run beside it")
+    p.add_argument("--writer-cus", type=int, default=-1,
+                   help="with --async-writeback: -1 a plain stream for the writers, 0 or more the stream of "
+                        "writeback_resources (a CU-masked stream over that many compute units; 0 unrestricted)")
     p.add_argument("--layers", type=int, default=1,
                    help="recurrent layers per step, each with its own pool (an attention window before each)")
     p.add_argument("--cpu-sample", type=int, default=-1,
@@ -308,7 +315,19 @@ def main():
     dev = torch.device("cuda:0")
     B, H, HK, K, V = a.batch, a.heads, a.key_heads, 128, 128
     bits, impact = make_plan(torch, a.arch, H, K, a.nominal)
-    stream = torch.cuda.Stream() if a.async_writeback else None
+    # The foreground runs on a stream of its own, created right before the
+    # writer's: a CU-masked stream is a blocking stream (the legacy default
+    # stream would wait for it), and streams take the hardware queues in
+    # creation order, so consecutive streams can run side by side.
+    foreground = torch.cuda.Stream()
+    torch.cuda.set_stream(foreground)
+    stream = None
+    if a.async_writeback:
+        if a.writer_cus >= 0:
+            from stepquant_amd.kernels.resources import writeback_resources
+            stream = writeback_resources(dev, a.writer_cus).stream
+        else:
+            stream = torch.cuda.Stream()
     if a.state_format != "stepquant":
         from stepquant_amd.formats import FormatPlan, get_format
         from stepquant_amd.kernels.format_pool import FormatStatePool
@@ -353,10 +372,21 @@ def main():
 
     from stepquant_amd.kernels.writeback import attention_window, defer_writeback
 
+    gemm = None
+    if a.foreground_gflop > 0:
+        d = 4096
+        n = max(256, int(round(a.foreground_gflop * 1e9 / (2 * B * d) / 256)) * 256)
+        x_fg = torch.randn(B, d, device=dev, generator=g).to(torch.bfloat16)
+        w_fg = (torch.randn(d, n, device=dev, generator=g) * d ** -.5).to(torch.bfloat16)
+        y_fg = torch.empty(B, n, device=dev, dtype=torch.bfloat16)
+        gemm = (x_fg, w_fg, y_fg, 2.0 * B * d * n)
+
     def layers(slots):
         outs = []
         for layer in pools:
             attention_window()
+            if gemm is not None:
+                torch.matmul(gemm[0], gemm[1], out=gemm[2])
             outs.append(layer.step(q, k, v, gate, beta, slots, normalize=True, scale=K ** -.5, a_log=a_log,
                                    dt_bias=dt_bias))
         return outs
@@ -413,6 +443,8 @@ def main():
     if a.state_format != "stepquant":
         key = f"{a.state_format}-{a.arch}-b{B}-h{H}-hk{HK}"
     key += f"-sets{a.slot_sets}"
+    if gemm is not None:
+        key += f"-fg{a.foreground_gflop:g}"
     traffic = None
     if a.traffic and os.path.exists(a.traffic):
         meas = json.load(open(a.traffic))
@@ -439,7 +471,12 @@ def main():
                                      + (f"{per_block} steps per graph launch" if not a.no_graph else "eager steps")
                                      + (", async writeback" if stream is not None else ", fused writeback")
                                      + f", steps rotate over {a.slot_sets} disjoint sets of B slots "
-                                       f"({a.slot_sets * B * page * a.layers / 1e6:.0f} MB of pages)",
+                                       f"({a.slot_sets * B * page * a.layers / 1e6:.0f} MB of pages)"
+                                     + ("" if gemm is None else
+                                        f", a {gemm[3] / 1e9:.1f} GFLOP bf16 matmul per layer as stand-in "
+                                        f"foreground work (inside the timed step)")
+                                     + ("" if stream is None or a.writer_cus < 0 else
+                                        f", writers on a stream over {a.writer_cus or 'all'} CUs"),
                             page_bytes=page, global_batch=B, wall_s=round(wall, 3),
                             warm_seconds=a.warm_seconds),
                 roofline=roof, cpu_baseline=cpu)

@@ -379,7 +379,7 @@ __device__ __forceinline__ uint32_t quad_perm(uint32_t x) {
 // twice rather than once per row and pass.  The operations and their order
 // are those of the general path below (the sums in PyTorch's order).
 // =====================================================================
-template <int W, int XP = 128>  // XP: row pitch of X in floats (global state: 128; an LDS copy: padded)
+template <int W>
 __device__ __forceinline__ void encode_fast128(const PoolDev &P, const float *__restrict__ X, uint8_t *page,
                                                uint8_t *smem, int h) {
 #pragma clang fp contract(off)
@@ -415,7 +415,7 @@ __device__ __forceinline__ void encode_fast128(const PoolDev &P, const float *__
     for (int p = 0; p < 8; p++) {
       const int i = rw + 16 * p;
 #pragma unroll
-      for (int u = 0; u < 4; u++) v[p][u] = X[i * XP + 32 * u + 8 * k + l];
+      for (int u = 0; u < 4; u++) v[p][u] = X[i * V + 32 * u + 8 * k + l];
       wi[p] = P.impact[(int64_t)h * K + i];
       ro[p] = P.rows[(int64_t)h * K + i];
       of[p] = P.offsets[(int64_t)h * K + i];
@@ -476,17 +476,11 @@ __device__ __forceinline__ void encode_fast128(const PoolDev &P, const float *__
     }
   }
   // ---- column phase: this thread's 32 values of column j, raw and scaled
-  // (a state in LDS is read again where the raw values are needed instead
-  // of being held in registers)
-  constexpr bool reread = XP != 128;
   const int j = tid & (V - 1), hf = tid >> 7, i0 = 32 * hf;
   const int g = two ? j / 32 : 0;
-  float xs[reread ? 1 : 32], sc[32];
-  auto xval = [&](int r) -> float { return reread ? X[(i0 + r) * XP + j] : xs[reread ? 0 : r]; };
-  if (!reread) {
+  float xs[32], sc[32];
 #pragma unroll
-    for (int r = 0; r < 32; r++) xs[reread ? 0 : r] = X[(i0 + r) * XP + j];
-  }
+  for (int r = 0; r < 32; r++) xs[r] = X[(i0 + r) * V + j];
   const bool ieee = __syncthreads_or(lo_bits < 0x19800000u - 1u || hi_bits > 0x5d800000u);
   auto columns = [&](auto fast_tag) {
   constexpr bool FAST = decltype(fast_tag)::value;
@@ -494,8 +488,7 @@ __device__ __forceinline__ void encode_fast128(const PoolDev &P, const float *__
 #pragma unroll
   for (int r = 0; r < 32; r++) {
     const int ig = (i0 + r) * NG + g;
-    const float x = xval(r);
-    sc[r] = FAST ? div_half(x, rsc[ig], rinv[ig]) : x / rsc[ig];
+    sc[r] = FAST ? div_half(xs[r], rsc[ig], rinv[ig]) : xs[r] / rsc[ig];
     const float a = fabsf(sc[r]);
     amax = a > amax ? a : amax;
   }
@@ -529,7 +522,7 @@ __device__ __forceinline__ void encode_fast128(const PoolDev &P, const float *__
       const float wsq = (wl[i] * wl[i]) * 1.0f;
       const float z = zq(sc[r], c0, c0inv);
       const float v = (rsc[i * NG + g] * 1.0f) * z;
-      bn += (wsq * v) * xval(r);
+      bn += (wsq * v) * xs[r];
       bd += wsq * (v * v);
     }
     const int m = 2 * hf + mb;
@@ -2975,20 +2968,11 @@ struct PrefillDev {
   void *out;
   const int32_t *cu, *ckpt;
   const float *init;
-  float *ck_state;    // fp32 checkpoint states (NULL: not kept)
-  const void *slots;  // [batch * NC] prefix slots of the checkpoints
-  PoolDev pool;       // the pages, for checkpoints encoded in the kernel
+  float *ck_state;
   int64_t q_stride, k_stride, v_stride;
-  int H, HK, NC, gate_dtype, out_dtype, normalize, beta_logits, slots_dtype;
-  int encode;  // 1: the kernel encodes each checkpoint state into its slot (GDN packed, group 32)
+  int H, HK, NC, gate_dtype, out_dtype, normalize, beta_logits;
   float scale;
 };
-
-// LDS of the checkpoint encode, over the chunk tiles (free between chunks):
-// the state [K][XP] fp32, then the encode's own staging and tables.
-constexpr int XP = 132;  // rows 4 apart start 16 banks apart: the accumulator-layout stores do not collide
-constexpr int OFF_X = 0;
-constexpr int OFF_ENC = OFF_X + PKD * XP * 4;
 
 // Element (r, t) of the transposed k tile sits in row r at column
 // tcol(r, t): the 8-token block index is XORed with bits 3-5 of r, so rows
@@ -3158,44 +3142,6 @@ __device__ __forceinline__ void lds_barrier() {
 // k, q, v, A, T and P are shared through LDS.  Transposed products keep every
 // operand in a layout it already has: O^T = S0^T Q^T + Delta^T P^T gives
 // each lane 4 consecutive output columns for one token.
-// The checkpoint state of this workgroup's tile, held in LDS at OFF_X in row
-// layout (row pitch XP), requantised into `page`: bit-exact fit_state, as
-// sq_encode.  A call rather than inline code: the encode's registers do not
-// add to the chunk loop's (the state was stored to LDS before the call and
-// is read back after it).  Every thread of the workgroup calls it with the
-// same page.
-__device__ __noinline__ void encode_checkpoint(PoolDev P, uint8_t *page, int h, int W) {
-  extern __shared__ __align__(16) uint8_t smem[];
-  const float *X = (const float *)(smem + OFF_X);
-  uint8_t *enc = smem + OFF_ENC;
-  switch (W) {
-    case 2: encode_fast128<2, XP>(P, X, page, enc, h); break;
-    case 4: encode_fast128<4, XP>(P, X, page, enc, h); break;
-    case 6: encode_fast128<6, XP>(P, X, page, enc, h); break;
-    default: encode_fast128<8, XP>(P, X, page, enc, h); break;
-  }
-}
-
-// FP16 pivot head: the halves of this wave's columns of S at their tiled
-// places (value (i, j) at the row's offset + tile j / 16 times the head's
-// stride + 2 (j % 16)).
-__device__ __forceinline__ void store_pivot_checkpoint(const PoolDev &P, const f32x4 (&S)[8], uint8_t *page, int h,
-                                                       int jw) {
-  const int l = threadIdx.x & 63, q4 = l >> 4, c16 = l & 15;
-  const int code_start = P.head_meta[4 * h];
-  const int stride = P.offsets[(int64_t)P.H * PKD + h];
-  const int j = jw + c16;
-#pragma unroll
-  for (int dt = 0; dt < 8; dt++)
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const int i = 16 * dt + 4 * q4 + r;
-      const int off = P.offsets[(int64_t)h * PKD + i];
-      put_page_half(page, (int64_t)code_start + (off - code_start) + (j / 16) * stride + (j % 16) * 2,
-                    f2h(S[dt][r]));
-    }
-}
-
 __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
 #pragma clang fp contract(off)
   extern __shared__ __align__(16) uint8_t smem[];
@@ -3626,36 +3572,11 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
       const int p = __builtin_amdgcn_readlane(ckv, ci);
       if (p > c0 && p <= len) break;
       if (p == c0) {
-        if (D.ck_state) {
-          float *dst = D.ck_state + (((int64_t)b * D.NC + ci) * H + h) * PKD * PV + jw + c16;
+        float *dst = D.ck_state + (((int64_t)b * D.NC + ci) * H + h) * PKD * PV + jw + c16;
 #pragma unroll
-          for (int dt = 0; dt < 8; dt++)
+        for (int dt = 0; dt < 8; dt++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) dst[(int64_t)(16 * dt + 4 * q4 + r) * PV] = S[dt][r];
-        }
-        if (D.encode) {
-          const int64_t slot = load_slot_uniform(D.slots, D.slots_dtype, (int64_t)b * D.NC + ci);
-          if (slot > 0 && slot < D.pool.num_slots) {
-            uint8_t *page = D.pool.data + slot * D.pool.page_bytes;
-            const int W = ld_uniform(D.pool.bits + (int64_t)h * PKD);
-            if (W == 16) {
-              store_pivot_checkpoint(D.pool, S, page, h, jw);
-            } else {
-              float *X = (float *)(smem + OFF_X);
-#pragma unroll
-              for (int dt = 0; dt < 8; dt++)
-#pragma unroll
-                for (int r = 0; r < 4; r++) X[(16 * dt + 4 * q4 + r) * XP + jw + c16] = S[dt][r];
-              __syncthreads();
-              encode_checkpoint(D.pool, page, h, W);
-#pragma unroll
-              for (int dt = 0; dt < 8; dt++)
-#pragma unroll
-                for (int r = 0; r < 4; r++) S[dt][r] = X[(16 * dt + 4 * q4 + r) * XP + jw + c16];
-              __syncthreads();  // the next chunk's staging overwrites the encode's LDS
-            }
-          }
-        }
+          for (int r = 0; r < 4; r++) dst[(int64_t)(16 * dt + 4 * q4 + r) * PV] = S[dt][r];
       }
     }
   }
@@ -4880,12 +4801,8 @@ int sq_prefill(const sq_pool *pool, const sq_prefill_args *a, void *stream) {
   if (a->batch == 0) return 0;
   if (!a->q || !a->k || !a->v || !a->g || !a->beta || !a->out || !a->cu_seqlens || !a->init_state)
     return fail(SQ_EINVAL, "prefill: null input, output, sequence offsets or initial-state workspace");
-  // GDN packed pools (value groups of 32): the prefill kernel encodes each
-  // checkpoint state into its slot itself; other pools encode the fp32
-  // checkpoint states afterwards
-  const int encode_in_kernel = !pool->kda && pool->storage == 0 && (pool->group > 0 ? pool->group : 128) == 32;
-  if (a->n_checkpoints > 0 && (!a->checkpoints || !a->slots || (!encode_in_kernel && !a->checkpoint_state)))
-    return fail(SQ_EINVAL, "prefill: checkpoints need positions, slots and (KDA or byte pools) a state workspace");
+  if (a->n_checkpoints > 0 && (!a->checkpoints || !a->slots || !a->checkpoint_state))
+    return fail(SQ_EINVAL, "prefill: checkpoints need positions, slots and a state workspace");
   if (a->n_checkpoints > pf::MAX_CK) return fail(SQ_EINVAL, "prefill: at most 64 checkpoints per sequence");
   if (a->qkv_dtype != SQ_BF16) return fail(SQ_EINVAL, "prefill: q, k, v must be bf16 (the MFMA operand type)");
   if (a->gate_dtype != SQ_F32 && a->gate_dtype != SQ_BF16 && a->gate_dtype != SQ_F16)
@@ -4942,10 +4859,6 @@ int sq_prefill(const sq_pool *pool, const sq_prefill_args *a, void *stream) {
   D.normalize = a->normalize;
   D.beta_logits = a->beta_logits != 0;
   D.scale = a->scale;
-  D.slots = a->slots;
-  D.slots_dtype = a->slots_dtype;
-  D.pool = to_dev(pool);
-  D.encode = encode_in_kernel;
   if (pool->kda) {
     hipError_t e = hipFuncSetAttribute((const void *)kp::kda_prefill_kernel,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, kp::LDS_BYTES);
@@ -4968,7 +4881,7 @@ int sq_prefill(const sq_pool *pool, const sq_prefill_args *a, void *stream) {
     const hipError_t e = hipEventRecord((hipEvent_t)a->events[1], st);
     if (e != hipSuccess) return fail((int)e, "prefill: hipEventRecord failed");
   }
-  if (a->n_checkpoints > 0 && !encode_in_kernel)
+  if (a->n_checkpoints > 0)
     return sq_encode(pool, a->checkpoint_state, a->slots, a->slots_dtype, a->batch * a->n_checkpoints, stream);
   return 0;
 }

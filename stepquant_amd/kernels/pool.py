@@ -472,6 +472,7 @@ class PackedStatePool:
         init = slots_t if init_slots is None else _indices(init_slots, dev)
         out = torch.empty((total, self.heads, self.values), device=dev, dtype=q.dtype)
         init_state = torch.empty((batch, self.heads, self.keys, self.values), device=dev, dtype=torch.float32)
+        keep = self.keep_prefill_states if keep_states is None else keep_states
         ck_state = torch.empty((batch * nc, self.heads, self.keys, self.values), device=dev, dtype=torch.float32)
         init = init.to(ck_slots.dtype)
         args = N.PrefillArgs(
@@ -493,7 +494,7 @@ class PackedStatePool:
             args.events = ctypes.cast(ev, ctypes.c_void_p)
         if batch:
             N.check(N.lib().sq_prefill(self._desc, args, N.stream_handle()), "prefill")
-        if self.keep_prefill_states if keep_states is None else keep_states:
+        if keep:
             self.last_prefill = (q2, k2, v2, g2, b2, al, db, cu, ck, init, ck_slots, init_state, ck_state)
         return out
 
