@@ -169,7 +169,6 @@ def cpu_baseline(bits, impact, arch, B, H, HK, K, V, sample, steps=4, threads=0,
 
 
 PEAK_BF16_TFLOPS = 2500.0
-PEAK_F32_TFLOPS = 157.3
 
 
 def timed_steps(torch, one, block, per_block, steps, warmup, warm_seconds):
@@ -196,7 +195,7 @@ def timed_steps(torch, one, block, per_block, steps, warmup, warm_seconds):
 
 
 def prefill_flops(n_chunks, C=64, K=128, V=128):
-    """Algorithmic FLOPs of the chunked recurrence per chunk-head:
+    """Algorithmic FLOPs of the chunked recurrence (chunks of C tokens) per chunk-head:
     K K^T and Q K^T (2 x 2C^2K), the triangular inverse (C^3/3 x 2), W and U
     (2C^2K + 2C^2V), W S and Q S (2 x 2CKV), (M o QK^T) Delta (2C^2V) and
     K^T Delta (2CKV)."""
@@ -258,29 +257,20 @@ def bench_prefill(a, torch):
     gate_bytes = tot * H * (K if kda else 1) * 4 + tot * H * 4
     hbm = (2 * tot * HK * K * 2 + tot * H * V * 2 + tot * H * V * 2 + gate_bytes + B * pool.page_bytes
            + B * NC * pool.page_bytes)
+    chunk = 16 if kda else 64
     workload = (f"{a.arch.upper()} prefill STEPQuant@6, B={B}, T={T}, H={H}, HK={HK}, dk=dv={K}, "
-                + ("token-by-token recurrence (per-channel decay)" if kda else "chunk 64")
+                + f"chunk {chunk}" + (" (per-channel decay)" if kda else "")
                 + f", bf16 q/k/v, raw gates, {NC} prefix slots per request")
-    if kda:
-        # per token-head: decay K V multiplies, k^T S, the rank-1 update and q^T S (2 K V each)
-        flops = B * T * H * 7 * K * V
-        tflops = flops / (kernel_ms * 1e-3) / 1e12
-        roof = dict(bound="valu", achieved=round(tflops, 2), peak=PEAK_F32_TFLOPS, unit="TFLOP/s",
-                    frac=round(tflops / PEAK_F32_TFLOPS, 4), traffic=None, kernel="kp::kda_prefill_kernel",
-                    kernel_ms=round(kernel_ms, 6), step_frac=round(flops / (ms_step * 1e-3) / 1e12 / PEAK_F32_TFLOPS, 4),
-                    algorithmic_flops_per_step=flops,
-                    hbm_fraction=round(hbm / (ms_step * 1e-3) / 1e9 / PEAK_GBS, 4),
-                    algorithmic_bytes_per_step=hbm)
-    else:
-        n_chunks = B * H * ((T + 63) // 64)
-        flops = prefill_flops(n_chunks)
-        tflops = flops / (kernel_ms * 1e-3) / 1e12
-        roof = dict(bound="mfma", achieved=round(tflops, 2), peak=PEAK_BF16_TFLOPS, unit="TFLOP/s",
-                    frac=round(tflops / PEAK_BF16_TFLOPS, 4), traffic=None, kernel="pf::prefill_kernel",
-                    kernel_ms=round(kernel_ms, 6), step_frac=round(flops / (ms_step * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
-                    algorithmic_flops_per_step=flops,
-                    hbm_fraction=round(hbm / (ms_step * 1e-3) / 1e9 / PEAK_GBS, 4),
-                    algorithmic_bytes_per_step=hbm)
+    n_chunks = B * H * ((T + chunk - 1) // chunk)
+    flops = prefill_flops(n_chunks, C=chunk)
+    tflops = flops / (kernel_ms * 1e-3) / 1e12
+    roof = dict(bound="mfma", achieved=round(tflops, 2), peak=PEAK_BF16_TFLOPS, unit="TFLOP/s",
+                frac=round(tflops / PEAK_BF16_TFLOPS, 4), traffic=None,
+                kernel="kc::kda_chunk_kernel" if kda else "pf::prefill_kernel",
+                kernel_ms=round(kernel_ms, 6), step_frac=round(flops / (ms_step * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                algorithmic_flops_per_step=flops,
+                hbm_fraction=round(hbm / (ms_step * 1e-3) / 1e9 / PEAK_GBS, 4),
+                algorithmic_bytes_per_step=hbm)
     line = dict(metric=f"prefill tokens/sec ({a.arch.upper()} prefill into prefix slots)",
                 value=round(tot / (ms_step * 1e-3), 1), unit="tokens/s", n_gpus=1, steps=a.steps,
                 warmup=a.warmup, ms_per_step=round(ms_step, 6), higher_is_better=True, scaling="weak",

@@ -205,8 +205,9 @@ int sq_writeback(const sq_pool *pool, const sq_writeback_scratch *scratch, int64
  *             benchmarks; the reference's kernel_extend has no
  *             counterpart).
  * Pools with K = V = 128, packed or byte storage.  GDN: the chunked kernel
- * (chunks of 64 tokens, bf16 MFMA).  KDA: a token-by-token kernel, one
- * workgroup per (sequence, head) holding the state in registers.
+ * (chunks of 64 tokens, bf16 MFMA).  KDA: a chunked kernel with per-channel
+ * decays (chunks of 16 tokens, bf16 MFMA; in-chunk decays formed pairwise
+ * when a chunk's decay exceeds 2^96 on some channel).
  */
 typedef struct sq_prefill_args {
     const void *q;

@@ -3584,219 +3584,500 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
 
 }  // namespace pf
 
+
+
 // =====================================================================
-// KDA prefill (per-channel decay), token by token.  The recurrence of
-// stepquant/core.py:5-15 with the KDA log decay g_t in R^K applied to every
-// token of a sequence: S <- diag(e^{g_t}) S; delta = beta_t (v_t - S^T k_t);
-// S <- S + k_t delta^T; o_t = S^T q_t (q, k L2-normalised, q scaled), the
-// role of the upstream chunk kernel behind the reference's kernel_extend
-// (sglang/runtime.py:193-202) for Kimi-Linear pools.
+// Chunked KDA prefill (per-channel decay), K = V = 128, chunks of 16
+// tokens, bf16 MFMA with fp32 accumulation.  The recurrence of
+// stepquant/core.py:5-15 with the KDA log decay g_t in R^K (the role of the
+// upstream chunk kernel behind the reference's kernel_extend,
+// sglang/runtime.py:193-202, for Kimi-Linear pools).
 //
-// One workgroup of 1024 threads per (sequence, head): eight lanes (an
-// 8-lane half-row) hold one state column j for the key rows 16 r .. 16 r +
-// 15 (r the lane's place in the eight) in registers, so the state never
-// leaves the workgroup and every per-token sum over key rows is a sum over
-// the eight lanes (three DPP adds, no barrier); 16 waves, four per SIMD,
-// overlap each other's dependent chains.  Tokens are staged 32 at a time
-// into LDS as fp32 rows (normalised k, q, the decays e^g, v, beta), and the
-// next block's raw inputs are fetched into registers while the current
-// block runs.  Per token: S = e^g S, k^T S over the lane's rows and its sum
-// over the lanes of the column, delta_j, S += k delta, q^T S and its sum;
-// one lane of the eight writes the output.  The key-channel rows are stored
-// as eight 16-float segments 20 floats apart, so the eight row segments a
-// wave reads at once start in different banks.
-namespace kp {
+// For a chunk with start state S0 [K, V] and per-channel cumulative log
+// decays G_t (G_tc = sum_{s<=t} g_sc):
+//   A_ts  = beta_t sum_c k_tc k_sc e^{G_tc - G_sc}      (s < t)
+//   P_ts  = sum_c q_tc k_sc e^{G_tc - G_sc}              (s <= t)
+//   Delta = (I + A)^{-1} R,   R_t = beta_t (v_t - (k_t o e^{G_t})^T S0)
+//   O_t   = (q_t o e^{G_t})^T S0 + sum_{s<=t} P_ts Delta_s
+//   S_C   = diag(e^{G_C}) S0 + (K o e^{G_C - G})^T Delta
+// (q, k L2-normalised and q scaled: the norms multiply into the products).
+// Every decay factor above has a non-positive exponent except inside A and
+// P, where e^{G_tc - G_sc} = e^{G_tc - G_Cc} e^{G_Cc - G_sc} (G_C: the last
+// token) makes both 16 x 128 x 16 products MFMA products.  The first factor
+// grows to e^{G_0c - G_Cc}, the chunk's decay; when that exceeds 2^96 for
+// any channel the chunk forms A and P pair by pair and channel by channel
+// instead (sub, exp2, no factor that could overflow), so any gate is
+// handled exactly.  The state-side products run on MFMA with
+// every fp32 operand split into hi + lo bf16 (hi*hi + hi*lo + lo*hi, ~2^-16
+// relative): K S0 and Q S0 as 16 x 16 x 32 products (S0 in the permuted
+// k-slot order of pf::split8), Delta^T P^T and the state update as
+// 16 x 16 x 16 products whose B operands are accumulator tiles as they are.
+// Delta solves (I + A) Delta = R by forward substitution in each wave's
+// registers (fp32, tokens in ascending order; the solved token's row reaches
+// the other lane rows by v_permlane16/32_swap), so no wave waits on another
+// for an inverse.  One workgroup of 8 waves per (sequence, head); wave w owns
+// state columns 16 w .. 16 w + 15 for all 128 rows in registers
+// (accumulator layout).
+// =====================================================================
+namespace kc {
 
-constexpr int NT = 1024, NSTG = 512;          // threads; the first 512 stage the inputs
-constexpr int TB = 32;                        // tokens staged per block
-constexpr int KV = 128;                       // K = V = 128
-constexpr int RPL = 16;                       // key rows per lane
-constexpr int SEGP = 20, ROWP = 8 * SEGP;     // segment and row pitch (floats) of the key-channel rows
-// LDS: per block key-channel rows [TB][ROWP] f32: DC (e^g), KN (k), QN (q);
-// VV [TB][128] (v); BETA [TB]
-constexpr int OFF_DC = 0;
-constexpr int OFF_KN = OFF_DC + TB * ROWP;
-constexpr int OFF_QN = OFF_KN + TB * ROWP;
-constexpr int OFF_VV = OFF_QN + TB * ROWP;
-constexpr int OFF_BT = OFF_VV + TB * KV;
-constexpr int LDS_FLOATS = OFF_BT + TB;
-constexpr int LDS_BYTES = LDS_FLOATS * 4;
-// place of channel c in a key-channel row
-__device__ __forceinline__ int kcol(int c) { return (c >> 4) * SEGP + (c & 15); }
+using pf::bf16x4;
+using pf::bf16x8;
+using pf::f32x4;
 
-// Raw inputs of one staging thread for one block: token tt = tid >> 4,
-// channels c8 .. c8 + 7 (c8 = (tid & 15) * 8).
-struct Raw {
-  uint4 k, q, v;
-  float g[8];
+constexpr int C = 16;                 // tokens per chunk
+constexpr int NT = 512;               // 8 waves
+constexpr int KV = 128;               // K = V = 128
+constexpr int RP = 136;               // bf16 row pitch of token rows
+constexpr int GP = 132;               // f32 row pitch of the decay rows
+constexpr int TP = 20;                // bf16 row pitch of 16-wide tiles
+constexpr int AP = 20;                // f32 row pitch of A (rows 16-byte aligned)
+constexpr int NPAIR = C * (C - 1) / 2;  // strictly lower pairs (t, s)
+constexpr int OFF_KR = 0;                         // bf16 [C][RP] raw k
+constexpr int OFF_QR = OFF_KR + C * RP * 2;       // bf16 [C][RP] raw q
+constexpr int OFF_VR = OFF_QR + C * RP * 2;       // bf16 [C][RP] v
+constexpr int OFF_G = OFF_VR + C * RP * 2;        // f32 [C][GP] cumulative log2 decays
+constexpr int OFF_KG = OFF_G + C * GP * 4;        // bf16 2 x [C][RP] nk k e^G (hi, lo), channels in pcol order
+constexpr int OFF_QG = OFF_KG + 2 * C * RP * 2;   // bf16 2 x [C][RP] nq q e^G (hi, lo), channels in pcol order
+constexpr int OFF_KD = OFF_QG + 2 * C * RP * 2;   // bf16 2 x [KV][TP] nk k e^{G_C - G} (hi, lo), row = channel
+constexpr int OFF_A = OFF_KD + 2 * KV * TP * 2;   // f32 [C][AP] A (below the diagonal)
+constexpr int OFF_PM = OFF_A + C * AP * 4;        // bf16 2 x [C][TP] P (hi, lo)
+constexpr int OFF_SM = OFF_PM + 2 * C * TP * 2;   // f32 [4][C] beta, nk, nq; flags
+constexpr int OFF_EC = OFF_SM + 4 * C * 4;        // f32 [KV] e^{G_C}
+constexpr int OFF_KE = OFF_EC + KV * 4;           // bf16 2 x [C][RP] nk k e^{G_C - G} (hi, lo), row = token
+constexpr int OFF_KB = OFF_KE + 2 * C * RP * 2;   // bf16 2 x [C][RP] k e^{G - G_C} (hi, lo)
+constexpr int OFF_QB = OFF_KB + 2 * C * RP * 2;   // bf16 2 x [C][RP] q e^{G - G_C} (hi, lo)
+constexpr int LDS_BYTES = OFF_QB + 2 * C * RP * 2;
+enum { SM_BETA = 0, SM_NK, SM_NQ, SM_FLAG };
+// a chunk whose decay exceeds 2^GROW_MAX on some channel takes the pairwise path
+constexpr float GROW_MAX = 96.0f;
+
+// (t, s) of strictly-lower pair p, t > s, pairs ordered by t then s
+__constant__ uint8_t pair_t[NPAIR] = {1, 2, 2, 3, 3, 3, 4, 4, 4, 4, 5, 5, 5, 5, 5, 6, 6, 6, 6, 6, 6, 7, 7, 7, 7, 7, 7, 7, 8, 8, 8, 8, 8, 8, 8, 8, 9, 9, 9, 9, 9, 9, 9, 9, 9, 10, 10, 10, 10, 10, 10, 10, 10, 10, 10, 11, 11, 11, 11, 11, 11, 11, 11, 11, 11, 11, 12, 12, 12, 12, 12, 12, 12, 12, 12, 12, 12, 12, 13, 13, 13, 13, 13, 13, 13, 13, 13, 13, 13, 13, 13, 14, 14, 14, 14, 14, 14, 14, 14, 14, 14, 14, 14, 14, 14, 15, 15, 15, 15, 15, 15, 15, 15, 15, 15, 15, 15, 15, 15, 15};
+__constant__ uint8_t pair_s[NPAIR] = {0, 0, 1, 0, 1, 2, 0, 1, 2, 3, 0, 1, 2, 3, 4, 0, 1, 2, 3, 4, 5, 0, 1, 2, 3, 4, 5, 6, 0, 1, 2, 3, 4, 5, 6, 7, 0, 1, 2, 3, 4, 5, 6, 7, 8, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14};
+
+// Raw inputs of one chunk for this thread, fetched one chunk ahead: token
+// tt = tid >> 5, channels c4 .. c4 + 3 of k, q, v (bf16) and, in the decay
+// mapping (channel c = tid >> 2, tokens 4 (tid & 3) .. + 3), the raw gates.
+struct Fetch {
+  uint2 k, q, v;
+  float g[4];
   float beta;
+  int n;
 };
 
-__device__ __forceinline__ void bf8(const uint4 &x, float o[8]) {
-  const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+__device__ __forceinline__ void bf4(const uint2 &x, float o[4]) {
+  o[0] = __uint_as_float(x.x << 16);
+  o[1] = __uint_as_float(x.x & 0xffff0000u);
+  o[2] = __uint_as_float(x.y << 16);
+  o[3] = __uint_as_float(x.y & 0xffff0000u);
+}
+
+// the value of 16-lane row Q of the wave in every row (two lane-row swaps)
+template <int Q>
+__device__ __forceinline__ float row_bcast(float x) {
+  const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const uint32_t y = (Q & 1) ? s16[1] : s16[0];  // rows (x0, x0, x2, x2) or (x1, x1, x3, x3)
+  const auto s32 = __builtin_amdgcn_permlane32_swap(y, y, false, false);
+  return __uint_as_float((Q & 2) ? s32[1] : s32[0]);
+}
+
+// one step of the substitution: token S's Delta (row S / 4, register S % 4)
+// to every lane, and -A[t][S] Delta_S into every later token t of this lane
+// (a[r][S] = A[4 q4 + r][S], loaded before the first step)
+template <int S>
+__device__ __forceinline__ void delta_step(float dv[4], const float (&a)[4][C], int q4) {
+  if constexpr (S < C) {
+    const float xs = row_bcast<S / 4>(dv[S % 4]);
 #pragma unroll
-  for (int e = 0; e < 4; e++) {
-    o[2 * e] = __uint_as_float(w[e] << 16);
-    o[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+    for (int r = 0; r < 4; r++) dv[r] = 4 * q4 + r > S ? fmaf(-a[r][S], xs, dv[r]) : dv[r];
+    delta_step<S + 1>(dv, a, q4);
   }
 }
 
-// sum over the 16 lanes of a row (lanes 16 m .. 16 m + 15)
-__device__ __forceinline__ float sum16(float x) {
-  x += __shfl_xor(x, 1);
-  x += __shfl_xor(x, 2);
-  x += __shfl_xor(x, 4);
-  x += __shfl_xor(x, 8);
-  return x;
+// sum over the 32 lanes of a half wave (lanes 32 m .. 32 m + 31): the
+// 16-lane rows by DPP, then the two rows of the half with v_permlane16_swap
+__device__ __forceinline__ float sum32(float x) {
+  x = pf::row16_sum(x);
+  const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
 }
 
-// sum over the eight lanes of a half-row, ((x0 + x1) + (x2 + x3)) + ((x4 +
-// x5) + (x6 + x7)) in every lane
-__device__ __forceinline__ float sum8(float x) { return fast::rg8_sum(x); }
-
-__global__ __launch_bounds__(NT) void kda_prefill_kernel(pf::PrefillDev D) {
-  extern __shared__ float lds[];
+__global__ __launch_bounds__(NT) void kda_chunk_kernel(pf::PrefillDev D) {
+#pragma clang fp contract(off)
+  extern __shared__ __align__(16) uint8_t smem[];
   const int H = D.H;
   const int h = blockIdx.x % H, b = blockIdx.x / H;
   const int hk = h / (H / D.HK);
-  const int t0 = D.cu[b], len = D.cu[b + 1] - t0;
+  const int t0 = __builtin_amdgcn_readfirstlane(D.cu[b]);
+  const int len = __builtin_amdgcn_readfirstlane(D.cu[b + 1]) - t0;
   if (len <= 0) return;  // whole workgroup
-  const int tid = threadIdx.x;
-  const int j = 8 * (tid >> 6) + ((tid & 63) >> 3), r = tid & 7;  // state column, row segment (lane in its eight)
-  const int tt = tid >> 4, c8 = (tid & 15) * 8;  // staging: token of the block, first channel
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, q4 = l >> 4, c16 = l & 15;
+  const int jw = 16 * w;
+  uint8_t *KR = smem + OFF_KR, *QR = smem + OFF_QR, *VR = smem + OFF_VR;
+  float *G = (float *)(smem + OFF_G);
+  uint8_t *KG = smem + OFF_KG, *QG = smem + OFF_QG, *KD = smem + OFF_KD;
+  float *A = (float *)(smem + OFF_A);
+  uint8_t *PM = smem + OFF_PM;
+  float *sm = (float *)(smem + OFF_SM);
+  float *EC = (float *)(smem + OFF_EC);
+  uint8_t *KE = smem + OFF_KE, *KB = smem + OFF_KB, *QB = smem + OFF_QB;
+  constexpr float LOG2E = 1.4426950408889634f;
+  // P: entries above the diagonal stay zero (written once; the MFMA path
+  // rewrites them with zeros); the pairwise-path flags start clear
+  for (int e = tid; e < C * TP; e += NT) ((uint32_t *)PM)[e] = 0u;
+  if (tid < 2) sm[SM_FLAG * C + tid] = 0.0f;
+  pf::lds_barrier();
 
-  float S[RPL];
+  // ---- state S[d][j] of this wave's columns: tile dt holds rows d = 16 dt + 4 q4 + r, column jw + c16
+  f32x4 S[8];
   {
-    const float *src = D.init + (((int64_t)b * H + h) * KV + RPL * r) * KV + j;
+    const float *src = D.init + ((int64_t)b * H + h) * KV * KV + jw + c16;
 #pragma unroll
-    for (int e = 0; e < RPL; e++) S[e] = src[(int64_t)e * KV];
+    for (int dt = 0; dt < 8; dt++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) S[dt][r] = src[(int64_t)(16 * dt + 4 * q4 + r) * KV];
   }
+  const int ckv = l < D.NC ? D.ckpt[(int64_t)b * D.NC + l] : 0x7fffffff;
+  auto segment = [&](int c) {  // tokens of the chunk at c: up to the next checkpoint, the end, or C
+    const uint64_t m = __ballot(ckv > c && ckv <= len);
+    const int stop = m ? __builtin_amdgcn_readlane(ckv, __builtin_ctzll(m)) : len;
+    return stop - c < C ? stop - c : C;
+  };
+  // staging mapping: token tt, channels c4 .. c4 + 3; decay mapping: channel gc, tokens 4 gq .. 4 gq + 3
+  const int tt = tid >> 5, c4 = (tid & 31) * 4;
+  const int gc = tid >> 2, gq = tid & 3;
   const float ea = D.a_log ? __expf(load_val(D.a_log, D.gate_dtype, h)) : 0.0f;
+  const float dtb = D.a_log ? load_val(D.dt_bias, D.gate_dtype, (int64_t)h * KV + gc) : 0.0f;
   const uint8_t *qg = (const uint8_t *)D.q, *kg = (const uint8_t *)D.k, *vg = (const uint8_t *)D.v;
-
-  auto fetch = [&](Raw &R, int c) {  // block starting at token c; rows clamped into the sequence
-    const int tok = c + tt < len ? c + tt : len - 1;
-    const int64_t row = (int64_t)t0 + tok;
-    R.k = *(const uint4 *)(kg + (row * D.k_stride + (int64_t)hk * KV + c8) * 2);
-    R.q = *(const uint4 *)(qg + (row * D.q_stride + (int64_t)hk * KV + c8) * 2);
-    R.v = *(const uint4 *)(vg + (row * D.v_stride + (int64_t)h * KV + c8) * 2);
-    const int64_t gi = (row * H + h) * KV + c8;
+  auto fetch = [&](Fetch &F, int c) {
+    F.n = c < len ? segment(c) : 0;
+    const int last = len - 1;
+    const int64_t row = (int64_t)t0 + (c + tt < len ? c + tt : last);
+    F.k = *(const uint2 *)(kg + (row * D.k_stride + (int64_t)hk * KV + c4) * 2);
+    F.q = *(const uint2 *)(qg + (row * D.q_stride + (int64_t)hk * KV + c4) * 2);
+    F.v = *(const uint2 *)(vg + (row * D.v_stride + (int64_t)h * KV + c4) * 2);
 #pragma unroll
-    for (int e = 0; e < 8; e++) R.g[e] = load_val(D.g, D.gate_dtype, gi + e);
-    R.beta = load_val(D.beta, D.gate_dtype, row * H + h);
+    for (int i = 0; i < 4; i++) {
+      const int64_t gr = (int64_t)t0 + (c + 4 * gq + i < len ? c + 4 * gq + i : last);
+      F.g[i] = load_val(D.g, D.gate_dtype, (gr * H + h) * KV + gc);
+    }
+    const int64_t br = (int64_t)t0 + (c + (l & 15) < len ? c + (l & 15) : last);
+    F.beta = load_val(D.beta, D.gate_dtype, br * H + h);
   };
 
-  Raw R;
-  const bool stager = tid < NSTG;
-  if (stager) fetch(R, 0);
-  int ci = 0;  // next checkpoint index
-  for (int c0 = 0; c0 < len; c0 += TB) {
-    const int n = len - c0 < TB ? len - c0 : TB;
-    // ---- stage the fetched block (tokens past n: zero rows)
-    if (stager) {
-      float kf[8], qf[8], vf[8];
-      bf8(R.k, kf);
-      bf8(R.q, qf);
-      bf8(R.v, vf);
+  Fetch F;
+  fetch(F, 0);
+  int ci = 0;
+  int par = 0;  // chunk parity: which flag word this chunk uses
+  for (int c0 = 0; c0 < len; par ^= 1) {
+    const int n = F.n;
+    // ---- stage: k, q, v rows, norms, beta; cumulative decays per channel
+    {
+      float kf[4], qf[4];
+      bf4(F.k, kf);
+      bf4(F.q, qf);
+      const bool live = tt < n;
+      const uint2 z2 = make_uint2(0u, 0u);
+      *(uint2 *)(KR + (tt * RP + c4) * 2) = live ? F.k : z2;
+      *(uint2 *)(QR + (tt * RP + c4) * 2) = live ? F.q : z2;
+      *(uint2 *)(VR + (tt * RP + c4) * 2) = live ? F.v : z2;
       float sk = 0.f, sq = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; e++) {
+      for (int e = 0; e < 4; e++) {
         sk = fmaf(kf[e], kf[e], sk);
         sq = fmaf(qf[e], qf[e], sq);
       }
-      sk = sum16(sk);
-      sq = sum16(sq);
-      const bool live = tt < n;
-      const float nk = D.normalize ? 1.0f / __builtin_sqrtf(sk + 1e-6f) : 1.0f;
-      const float nq = (D.normalize ? 1.0f / __builtin_sqrtf(sq + 1e-6f) : 1.0f) * D.scale;
-      const int kc = tt * ROWP + kcol(c8);  // 8 channels inside one 16-channel segment
-      float *dc = lds + OFF_DC + kc;
-      float *kn = lds + OFF_KN + kc, *qn = lds + OFF_QN + kc;
-      float *vv = lds + OFF_VV + tt * KV + c8;
+      sk = sum32(sk);
+      sq = sum32(sq);
+      if ((tid & 31) == 0) {
+        sm[SM_NK * C + tt] = live && D.normalize ? __builtin_amdgcn_rsqf(sk + 1e-6f) : (live ? 1.0f : 0.0f);
+        sm[SM_NQ * C + tt] = live ? (D.normalize ? __builtin_amdgcn_rsqf(sq + 1e-6f) : 1.0f) * D.scale : 0.0f;
+      }
+      if (w == 0 && l < C) {
+        float bt = F.beta;
+        if (D.beta_logits) bt = __builtin_amdgcn_rcpf(1.0f + __expf(-bt));
+        sm[SM_BETA * C + l] = l < n ? bt : 0.0f;
+      }
+      // log2 decays of tokens 4 gq .. 4 gq + 3 of channel gc (0 past the
+      // chunk's tokens), then the inclusive scan over the 16 tokens: within
+      // the thread, then across the quad (lanes gq = 0..3 of the channel)
+      float gl[4];
 #pragma unroll
-      for (int e = 0; e < 8; e++) {
-        float gv = R.g[e];
+      for (int i = 0; i < 4; i++) {
+        float gv = F.g[i];
         if (D.a_log) {
-          const float u = gv + load_val(D.dt_bias, D.gate_dtype, (int64_t)h * KV + c8 + e);
+          const float u = gv + dtb;
           const float sp = u > 20.0f ? u : __logf(1.0f + __expf(u < 20.0f ? u : 20.0f));
           gv = -ea * sp;
         }
-        const float d = __expf(gv);
-        const float k = live ? kf[e] * nk : 0.0f;
-        dc[e] = live ? d : 1.0f;
-        kn[e] = k;
-        qn[e] = live ? qf[e] * nq : 0.0f;
-        vv[e] = live ? vf[e] : 0.0f;
+        gl[i] = 4 * gq + i < n ? gv * LOG2E : 0.0f;
       }
-      if ((tid & 15) == 0) {
-        float bt = R.beta;
-        if (D.beta_logits) bt = 1.0f / (1.0f + __expf(-bt));
-        lds[OFF_BT + tt] = live ? bt : 0.0f;
-      }
+      gl[1] += gl[0];
+      gl[2] += gl[1];
+      gl[3] += gl[2];
+      // exclusive prefix of the quad's totals
+      const float tot = gl[3];
+      const float t1 = pf::quad_bcast<0>(tot), t2 = pf::quad_bcast<1>(tot), t3 = pf::quad_bcast<2>(tot);
+      const float pre = gq == 0 ? 0.0f : gq == 1 ? t1 : gq == 2 ? t1 + t2 : (t1 + t2) + t3;
+#pragma unroll
+      for (int i = 0; i < 4; i++) G[(4 * gq + i) * GP + gc] = pre + gl[i];
+      // the chunk's decay of channel gc (log2): G_0 - G_C, read on lane gq = 0
+      const float gC = ((t1 + t2) + t3) + pf::quad_bcast<3>(tot);
+      if (gq == 0 && gl[0] - gC > GROW_MAX) sm[SM_FLAG * C + par] = 1.0f;
     }
-    __syncthreads();
-    if (stager && c0 + TB < len) fetch(R, c0 + TB);  // in flight during this block's tokens
-    for (int u = 0; u < n; u++) {
-      // the decay first (S = e^g S), then k^T S, S += k delta, q^T S:
-      // three rows of the token read from LDS (e^g, k, q)
-      const int row = u * ROWP + r * SEGP;  // this lane's 16 key rows of token u
-      const float4 *dc4 = (const float4 *)(lds + OFF_DC + row);
-      const float4 *kn4 = (const float4 *)(lds + OFF_KN + row);
-      const float4 *qn4 = (const float4 *)(lds + OFF_QN + row);
-      float kk[RPL];
-      float a0 = 0.f, a1 = 0.f;
+    // the next chunk's inputs are in flight while this one is computed
+    const int c_next = c0 + n;
+    fetch(F, c_next);
+    pf::lds_barrier();
+    const bool pairwise = sm[SM_FLAG * C + par] != 0.0f;  // workgroup-uniform
+    // ---- operands: nk k e^G and nq q e^G (hi/lo, pcol order), nk k e^{G_C - G}
+    // (hi/lo, transposed and row-major), e^{G_C}; for the MFMA path also
+    // k e^{G - G_C} and q e^{G - G_C} (hi/lo)
+    {
+      const float nk = sm[SM_NK * C + tt], nq = sm[SM_NQ * C + tt];
+      const float4 gt = *(const float4 *)(G + tt * GP + c4), gC = *(const float4 *)(G + (C - 1) * GP + c4);
+      const float g4[4] = {gt.x, gt.y, gt.z, gt.w}, gc4[4] = {gC.x, gC.y, gC.z, gC.w};
+      float kf[4], qf[4];
+      bf4(*(const uint2 *)(KR + (tt * RP + c4) * 2), kf);
+      bf4(*(const uint2 *)(QR + (tt * RP + c4) * 2), qf);
+      float kgv[4], qgv[4], kdv[4];
 #pragma unroll
-      for (int e = 0; e < RPL / 4; e++) {
-        const float4 d = dc4[e], k = kn4[e];
-        S[4 * e] *= d.x;
-        S[4 * e + 1] *= d.y;
-        S[4 * e + 2] *= d.z;
-        S[4 * e + 3] *= d.w;
-        kk[4 * e] = k.x;
-        kk[4 * e + 1] = k.y;
-        kk[4 * e + 2] = k.z;
-        kk[4 * e + 3] = k.w;
-        a0 = fmaf(k.x, S[4 * e], a0);
-        a1 = fmaf(k.y, S[4 * e + 1], a1);
-        a0 = fmaf(k.z, S[4 * e + 2], a0);
-        a1 = fmaf(k.w, S[4 * e + 3], a1);
+      for (int e = 0; e < 4; e++) {
+        const float eg = __builtin_amdgcn_exp2f(g4[e]);
+        kgv[e] = (nk * kf[e]) * eg;
+        qgv[e] = (nq * qf[e]) * eg;
+        kdv[e] = (nk * kf[e]) * __builtin_amdgcn_exp2f(gc4[e] - g4[e]);
       }
-      const float ks = sum8(a0 + a1);
-      const float delta = lds[OFF_BT + u] * (lds[OFF_VV + u * KV + j] - ks);
-      float o0 = 0.f, o1 = 0.f;
+      uint2 hi, lo;
+      pf::split4(kgv, hi, lo);
+      *(uint2 *)(KG + (tt * RP + pf::pcol(c4)) * 2) = hi;
+      *(uint2 *)(KG + (C * RP + tt * RP + pf::pcol(c4)) * 2) = lo;
+      pf::split4(qgv, hi, lo);
+      *(uint2 *)(QG + (tt * RP + pf::pcol(c4)) * 2) = hi;
+      *(uint2 *)(QG + (C * RP + tt * RP + pf::pcol(c4)) * 2) = lo;
+      pf::split4(kdv, hi, lo);
+      *(uint2 *)(KE + (tt * RP + c4) * 2) = hi;
+      *(uint2 *)(KE + (C * RP + tt * RP + c4) * 2) = lo;
+      if (!pairwise) {
+        float kbv[4], qbv[4];
 #pragma unroll
-      for (int e = 0; e < RPL / 4; e++) {
-        const float4 q = qn4[e];
-        S[4 * e] = fmaf(kk[4 * e], delta, S[4 * e]);
-        S[4 * e + 1] = fmaf(kk[4 * e + 1], delta, S[4 * e + 1]);
-        S[4 * e + 2] = fmaf(kk[4 * e + 2], delta, S[4 * e + 2]);
-        S[4 * e + 3] = fmaf(kk[4 * e + 3], delta, S[4 * e + 3]);
-        o0 = fmaf(q.x, S[4 * e], o0);
-        o1 = fmaf(q.y, S[4 * e + 1], o1);
-        o0 = fmaf(q.z, S[4 * e + 2], o0);
-        o1 = fmaf(q.w, S[4 * e + 3], o1);
-      }
-      const float o = sum8(o0 + o1);
-      if (r == 0) store_val(D.out, D.out_dtype, ((int64_t)(t0 + c0 + u) * H + h) * KV + j, o);
-      // checkpoints reached after this token (token counts, ascending)
-      const int done = c0 + u + 1;
-      while (ci < D.NC) {
-        const int p = D.ckpt[(int64_t)b * D.NC + ci];
-        if (p > done && p <= len) break;
-        if (p == done) {
-          float *dst = D.ck_state + ((((int64_t)b * D.NC + ci) * H + h) * KV + RPL * r) * KV + j;
-#pragma unroll
-          for (int e = 0; e < RPL; e++) dst[(int64_t)e * KV] = S[e];
+        for (int e = 0; e < 4; e++) {
+          const float eb = __builtin_amdgcn_exp2f(g4[e] - gc4[e]);
+          kbv[e] = kf[e] * eb;
+          qbv[e] = qf[e] * eb;
         }
-        ci++;
+        uint2 bh, bl;
+        pf::split4(kbv, bh, bl);
+        *(uint2 *)(KB + (tt * RP + c4) * 2) = bh;
+        *(uint2 *)(KB + (C * RP + tt * RP + c4) * 2) = bl;
+        pf::split4(qbv, bh, bl);
+        *(uint2 *)(QB + (tt * RP + c4) * 2) = bh;
+        *(uint2 *)(QB + (C * RP + tt * RP + c4) * 2) = bl;
+      }
+      const uint32_t hw[2] = {hi.x, hi.y}, lw[2] = {lo.x, lo.y};
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        ((uint16_t *)KD)[(c4 + e) * TP + tt] = (uint16_t)(hw[e >> 1] >> (16 * (e & 1)));
+        ((uint16_t *)KD)[KV * TP + (c4 + e) * TP + tt] = (uint16_t)(lw[e >> 1] >> (16 * (e & 1)));
+      }
+      if (tt == 0) *(float4 *)(EC + c4) = make_float4(__builtin_amdgcn_exp2f(gc4[0]), __builtin_amdgcn_exp2f(gc4[1]),
+                                                      __builtin_amdgcn_exp2f(gc4[2]), __builtin_amdgcn_exp2f(gc4[3]));
+    }
+    // ---- pairwise path: A and P below the diagonal, pair by pair over 32
+    // channels per lane (four lanes per pair), with the exact pairwise
+    // decays; P's diagonal from q_t . k_t
+    if (!pairwise) {
+    } else if (tid < 4 * NPAIR) {
+      const int p = tid >> 2, part = tid & 3;
+      const int t = pair_t[p], s = pair_s[p];
+      const int cb = 32 * part;
+      float a = 0.f, pp = 0.f;
+#pragma unroll
+      for (int m = 0; m < 4; m++) {
+        const int c = cb + 8 * m;
+        float kt[8], qt[8], ks[8];
+        {
+          const uint4 x = *(const uint4 *)(KR + (t * RP + c) * 2), y = *(const uint4 *)(QR + (t * RP + c) * 2),
+                      z = *(const uint4 *)(KR + (s * RP + c) * 2);
+          bf4(make_uint2(x.x, x.y), kt);
+          bf4(make_uint2(x.z, x.w), kt + 4);
+          bf4(make_uint2(y.x, y.y), qt);
+          bf4(make_uint2(y.z, y.w), qt + 4);
+          bf4(make_uint2(z.x, z.y), ks);
+          bf4(make_uint2(z.z, z.w), ks + 4);
+        }
+        const float4 ga0 = *(const float4 *)(G + t * GP + c), ga1 = *(const float4 *)(G + t * GP + c + 4);
+        const float4 gb0 = *(const float4 *)(G + s * GP + c), gb1 = *(const float4 *)(G + s * GP + c + 4);
+        const float dg[8] = {ga0.x - gb0.x, ga0.y - gb0.y, ga0.z - gb0.z, ga0.w - gb0.w,
+                             ga1.x - gb1.x, ga1.y - gb1.y, ga1.z - gb1.z, ga1.w - gb1.w};
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const float kse = ks[e] * __builtin_amdgcn_exp2f(dg[e]);
+          a = fmaf(kt[e], kse, a);
+          pp = fmaf(qt[e], kse, pp);
+        }
+      }
+      a += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(a), 0xB1, 0xF, 0xF, false));   // lane ^ 1
+      pp += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(pp), 0xB1, 0xF, 0xF, false));
+      a += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(a), 0x4E, 0xF, 0xF, false));   // lane ^ 2
+      pp += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(pp), 0x4E, 0xF, 0xF, false));
+      if (part == 0) {
+        const float nks = sm[SM_NK * C + s];
+        A[t * AP + s] = ((sm[SM_BETA * C + t] * sm[SM_NK * C + t]) * nks) * a;
+        const float pv = (sm[SM_NQ * C + t] * nks) * pp;
+        const __bf16 hi = (__bf16)pv;
+        ((__bf16 *)PM)[t * TP + s] = hi;
+        ((__bf16 *)PM)[C * TP + t * TP + s] = (__bf16)(pv - (float)hi);
+      }
+    } else if (tid < 4 * NPAIR + C) {
+      // P_tt = nq_t nk_t q_t . k_t (no decay), one lane per token
+      const int t = tid - 4 * NPAIR;
+      float d = 0.f;
+#pragma unroll 4
+      for (int c = 0; c < KV; c += 8) {
+        float kt[8], qt[8];
+        const uint4 x = *(const uint4 *)(KR + (t * RP + c) * 2), y = *(const uint4 *)(QR + (t * RP + c) * 2);
+        bf4(make_uint2(x.x, x.y), kt);
+        bf4(make_uint2(x.z, x.w), kt + 4);
+        bf4(make_uint2(y.x, y.y), qt);
+        bf4(make_uint2(y.z, y.w), qt + 4);
+#pragma unroll
+        for (int e = 0; e < 8; e++) d = fmaf(qt[e], kt[e], d);
+      }
+      const float pv = (sm[SM_NQ * C + t] * sm[SM_NK * C + t]) * d;
+      const __bf16 hi = (__bf16)pv;
+      ((__bf16 *)PM)[t * TP + t] = hi;
+      ((__bf16 *)PM)[C * TP + t * TP + t] = (__bf16)(pv - (float)hi);
+    }
+    pf::lds_barrier();
+    if (tid == 0) sm[SM_FLAG * C + par] = 0.0f;  // read by every thread before the barrier above
+    // ---- MFMA path: A (wave 0) and P (wave 1) as 16 x 128 x 16 products of
+    // the growing and the decaying factors, A_ts = beta_t nk_t (k_t e^{G_t -
+    // G_C}) . (nk_s k_s e^{G_C - G_s}) for s < t, P_ts = nq_t (q_t e^{G_t -
+    // G_C}) . (nk_s k_s e^{G_C - G_s}) for s <= t (zero above)
+    if (!pairwise && w < 2) {
+      const uint8_t *X = w == 0 ? KB : QB;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kc = 0; kc < 4; kc++) {
+        const int o = (c16 * RP + 32 * kc + 8 * q4) * 2;
+        const bf16x8 xh = pf::ld8(X, o), xl = pf::ld8(X, C * RP * 2 + o);
+        const bf16x8 eh = pf::ld8(KE, o), el = pf::ld8(KE, C * RP * 2 + o);
+        acc = pf::mfma(xh, eh, acc);
+        acc = pf::mfma(xh, el, acc);
+        acc = pf::mfma(xl, eh, acc);
+      }
+      // acc[r]: token t = 4 q4 + r, source s = c16
+      const int s0 = c16;
+      if (w == 0) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const int t = 4 * q4 + r;
+          if (s0 < t) A[t * AP + s0] = (sm[SM_BETA * C + t] * sm[SM_NK * C + t]) * acc[r];
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const int t = 4 * q4 + r;
+          const float pv = s0 <= t ? sm[SM_NQ * C + t] * acc[r] : 0.0f;
+          const __bf16 hi = (__bf16)pv;
+          ((__bf16 *)PM)[t * TP + s0] = hi;
+          ((__bf16 *)PM)[C * TP + t * TP + s0] = (__bf16)(pv - (float)hi);
+        }
       }
     }
-    __syncthreads();  // the next block's staging overwrites the token rows
+    // ---- K S0 and Q S0 for this wave's columns
+    // S0 as hi/lo operands, key rows in the permuted slot order of split8
+    bf16x8 sh[4], sl[4];
+#pragma unroll
+    for (int kc = 0; kc < 4; kc++) pf::split8(S[2 * kc], S[2 * kc + 1], sh[kc], sl[kc]);
+    f32x4 R, oq;
+    {
+      f32x4 ak = {0.f, 0.f, 0.f, 0.f}, aq = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kc = 0; kc < 4; kc++) {
+        const int o = (c16 * RP + 32 * kc + 8 * q4) * 2;
+        const bf16x8 kh = pf::ld8(KG, o), kl = pf::ld8(KG, C * RP * 2 + o);
+        const bf16x8 qh = pf::ld8(QG, o), ql = pf::ld8(QG, C * RP * 2 + o);
+        ak = pf::mfma(kh, sh[kc], ak);
+        ak = pf::mfma(kh, sl[kc], ak);
+        ak = pf::mfma(kl, sh[kc], ak);
+        aq = pf::mfma(sh[kc], qh, aq);
+        aq = pf::mfma(sl[kc], qh, aq);
+        aq = pf::mfma(sh[kc], ql, aq);
+      }
+      // R_t = beta_t (v_t - (nk k e^G)_t S0), tokens 4 q4 .. 4 q4 + 3, column jw + c16
+      const pf::tr4_t vr = pf::col4(VR, 4 * q4, jw, c16);
+      const float4 be = *(const float4 *)(sm + SM_BETA * C + 4 * q4);
+      const float be4[4] = {be.x, be.y, be.z, be.w};
+#pragma unroll
+      for (int r = 0; r < 4; r++) R[r] = be4[r] * (pf::bf2f((uint16_t)vr[r]) - ak[r]);
+      oq = aq;  // O^T first term: column 4 q4 + r, token c16
+    }
+    pf::lds_barrier();
+    // ---- (I + A) Delta = R; O^T += Delta^T P^T; S <- diag(e^{G_C}) S0 + Kd^T Delta
+    bf16x4 dh4, dl4;
+    {
+      float a[4][C];  // rows 4 q4 .. 4 q4 + 3 of A, all loads issued before the chain
+#pragma unroll
+      for (int r = 0; r < 4; r++)
+#pragma unroll
+        for (int m = 0; m < C / 4; m++) {
+          const float4 x = *(const float4 *)(A + (4 * q4 + r) * AP + 4 * m);
+          a[r][4 * m] = x.x;
+          a[r][4 * m + 1] = x.y;
+          a[r][4 * m + 2] = x.z;
+          a[r][4 * m + 3] = x.w;
+        }
+      float dv[4] = {R[0], R[1], R[2], R[3]};
+      delta_step<0>(dv, a, q4);
+      const f32x4 dl = {dv[0], dv[1], dv[2], dv[3]};
+      pf::split4x(dl, dh4, dl4);
+      const int o = (c16 * TP + 4 * q4) * 2;
+      const bf16x4 ph = pf::ld4(PM, o), plo = pf::ld4(PM, C * TP * 2 + o);
+      f32x4 acc = oq;
+      acc = pf::mfma16(dh4, ph, acc);
+      acc = pf::mfma16(dh4, plo, acc);
+      acc = pf::mfma16(dl4, ph, acc);
+      if (c16 < n) {
+        const float o4[4] = {acc[0], acc[1], acc[2], acc[3]};
+        const int64_t at = ((int64_t)(t0 + c0 + c16) * H + h) * KV + jw + 4 * q4;
+        store4(D.out, D.out_dtype, at, o4);
+      }
+    }
+#pragma unroll
+    for (int dt = 0; dt < 8; dt++) {
+      const float4 ec = *(const float4 *)(EC + 16 * dt + 4 * q4);
+      f32x4 acc;
+      acc[0] = S[dt][0] * ec.x;
+      acc[1] = S[dt][1] * ec.y;
+      acc[2] = S[dt][2] * ec.z;
+      acc[3] = S[dt][3] * ec.w;
+      const int o = ((16 * dt + c16) * TP + 4 * q4) * 2;
+      const bf16x4 kh = pf::ld4(KD, o), kl = pf::ld4(KD, KV * TP * 2 + o);
+      acc = pf::mfma16(kh, dh4, acc);
+      acc = pf::mfma16(kh, dl4, acc);
+      acc = pf::mfma16(kl, dh4, acc);
+      S[dt] = acc;
+    }
+    pf::lds_barrier();  // the next chunk's staging overwrites the shared tiles
+    c0 = c_next;
+    for (; ci < D.NC; ci++) {
+      const int p = __builtin_amdgcn_readlane(ckv, ci);
+      if (p > c0 && p <= len) break;
+      if (p == c0) {
+        float *dst = D.ck_state + (((int64_t)b * D.NC + ci) * H + h) * KV * KV + jw + c16;
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++)
+#pragma unroll
+          for (int r = 0; r < 4; r++) dst[(int64_t)(16 * dt + 4 * q4 + r) * KV] = S[dt][r];
+      }
+    }
   }
 }
 
-}  // namespace kp
-
+}  // namespace kc
 
 __global__ void fill_zero_kernel(float *p, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) p[i] = 0.0f;
@@ -4860,13 +5141,13 @@ int sq_prefill(const sq_pool *pool, const sq_prefill_args *a, void *stream) {
   D.beta_logits = a->beta_logits != 0;
   D.scale = a->scale;
   if (pool->kda) {
-    hipError_t e = hipFuncSetAttribute((const void *)kp::kda_prefill_kernel,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, kp::LDS_BYTES);
+    hipError_t e = hipFuncSetAttribute((const void *)kc::kda_chunk_kernel,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, kc::LDS_BYTES);
     if (e != hipSuccess) return fail((int)e, "prefill: cannot raise the KDA kernel's LDS limit");
     if (a->events && (e = hipEventRecord((hipEvent_t)a->events[0], st)) != hipSuccess)
       return fail((int)e, "prefill: hipEventRecord failed");
-    hipLaunchKernelGGL(kp::kda_prefill_kernel, dim3((unsigned)(a->batch * H)), dim3(kp::NT), kp::LDS_BYTES, st, D);
-    rc = check_launch("kda_prefill_kernel");
+    hipLaunchKernelGGL(kc::kda_chunk_kernel, dim3((unsigned)(a->batch * H)), dim3(kc::NT), kc::LDS_BYTES, st, D);
+    rc = check_launch("kda_chunk_kernel");
   } else {
     hipError_t e = hipFuncSetAttribute((const void *)pf::prefill_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                                        pf::LDS_BYTES);

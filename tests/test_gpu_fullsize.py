@@ -213,3 +213,54 @@ def test_prefill_at_bench_shape():
     pages = _check_prefix_pages(pool, states, ref_states, ck_slots.numpy(), oplan, lay, pages0, heads)
     # the initial slots are not overwritten (the final state goes to the last prefix slot)
     assert np.array_equal(pages[1:B + 1], pages0[1:B + 1])
+
+
+def test_kda_prefill_at_bench_shape():
+    """The KDA prefill at the P6 shape (8 sequences of 2048 tokens, 32 value
+    heads, one key head each, per-channel decays as bench.py draws them, five
+    prefix slots per sequence): four heads against the float64 recurrence
+    for every sequence; every prefix page against the oracle encoding of
+    the kernel's state."""
+    print("case KDA prefill B=8 T=2048 H=HK=32 NC=5", flush=True)
+    from stepquant_amd.kernels.pool import PackedStatePool
+    from stepquant_amd.quantization import QuantizationPlan
+    B, H, K, V, T, NC = 8, 32, 128, 128, 2048, 5
+    bits, impact = bench.make_plan(torch, "kda", H, K, 6)
+    oplan = _oracle_plan("kda", bits, impact)
+    pool = PackedStatePool(QuantizationPlan("kda", bits.to(dev()), impact.to(dev())), B * (NC + 1) + 1, V)
+    g = torch.Generator().manual_seed(23)
+    init = torch.arange(1, B + 1)
+    pool.encode((torch.randn(B, H, K, V, generator=g) * .05).to(dev()), init.to(dev()))
+    lay = O.layout(oplan, V)
+    pages0 = pool.data.cpu().numpy()
+    S0 = O.decode_page(pages0, init.numpy(), oplan, lay, V).astype(np.float64)
+    tot = B * T
+    q = torch.randn(tot, H, K, generator=g).to(torch.bfloat16)
+    k = torch.randn(tot, H, K, generator=g).to(torch.bfloat16)
+    v = torch.randn(tot, H, V, generator=g).to(torch.bfloat16)
+    gate = torch.randn(tot, H, K, generator=g) * .5
+    beta = torch.randn(tot, H, generator=g)
+    a_log = torch.zeros(H)
+    dt_bias = torch.zeros(H * K)
+    cu = np.arange(0, tot + 1, T)
+    pos = [((T * (c + 1)) // NC + 63) // 64 * 64 for c in range(NC)]
+    pos[-1] = T
+    ck = np.tile(np.array(pos), (B, 1))
+    ck_slots = torch.arange(B + 1, B + 1 + B * NC).reshape(B, NC)
+    pool.keep_prefill_states = True
+    out = pool.extend(q.to(dev()), k.to(dev()), v.to(dev()), gate.to(dev()), beta.to(dev()), init,
+                      torch.from_numpy(cu), checkpoints=torch.from_numpy(ck), checkpoint_slots=ck_slots,
+                      init_slots=init, normalize=True, scale=K ** -.5, a_log=a_log.to(dev()),
+                      dt_bias=dt_bias.to(dev()))
+    torch.cuda.synchronize()
+    states = pool.last_prefill[-1].cpu().numpy().reshape(B, NC, H, K, V)
+    assert np.isfinite(out.float().cpu().numpy()).all() and np.isfinite(states).all()
+    heads = [0, 9, 22, 31]
+    hb = np.concatenate([np.arange(h * K, (h + 1) * K) for h in heads])
+    ref_out, ref_states, _ = O.prefill(q.float().numpy()[:, heads], k.float().numpy()[:, heads],
+                                       v.float().numpy()[:, heads], gate.numpy()[:, heads],
+                                       beta.numpy()[:, heads], S0[:, heads], cu, ck, normalize=True,
+                                       scale=K ** -.5, a_log=a_log.numpy()[heads], dt_bias=dt_bias.numpy()[hb])
+    check_prefill(out[:, heads], ref_out, "bf16 outputs")
+    check_states(states[:, :, heads], ref_states)
+    _check_prefix_pages(pool, states, ref_states, ck_slots.numpy(), oplan, lay, pages0, heads)

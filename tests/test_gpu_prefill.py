@@ -183,7 +183,7 @@ def test_prefill_rows_far_apart_match_contiguous_rows():
 @pytest.mark.parametrize("arch,storage,raw", [("kda", "packed", False), ("kda", "packed", True),
                                               ("kda", "byte", True), ("gdn", "byte", False)])
 def test_prefill_kda_and_byte_pages(arch, storage, raw):
-    """KDA pools (per-channel decay, token-by-token kernel) and byte-carrier
+    """KDA pools (per-channel decay, chunks of 16 tokens) and byte-carrier
     pages go through the same extend: outputs and checkpoint states against
     the float64 recurrence, checkpoint pages equal to the oracle encoding
     of the kernel's states."""
@@ -285,3 +285,51 @@ def test_prefill_timing_events_change_nothing(arch):
     assert torch.equal(pools[0].data, pools[1].data)
     # the pools keep no reference to the call's inputs and state workspaces
     assert not any(hasattr(p, "last_prefill") for p in pools)
+
+
+@pytest.mark.parametrize("a_log", [3.0, -2.0])
+def test_kda_prefill_with_extreme_decays(a_log):
+    """KDA gates far outside the typical range: with A_log = 3 some
+    channels forget ~20-60 nats per token (hundreds over a chunk) while others
+    keep their state; with A_log = -2 every channel barely decays.  The
+    chunked kernel forms the in-chunk decays pairwise, so nothing overflows:
+    outputs and states against the float64 recurrence."""
+    from stepquant_amd.kernels.pool import PackedStatePool
+    print(f"case kda extreme decays a_log={a_log}", flush=True)
+    H, K, V = 2, 128, 128
+    lens = [75, 33]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    T = int(cu[-1])
+    oplan = make_plan("kda", np.full((H, K), 8), seed=2)
+    pool = PackedStatePool(device_plan(oplan), 6, V)
+    g = torch.Generator().manual_seed(31)
+    q = torch.randn(T, H, K, generator=g).to(torch.bfloat16)
+    k = torch.randn(T, H, K, generator=g).to(torch.bfloat16)
+    v = torch.randn(T, H, V, generator=g).to(torch.bfloat16)
+    gate = torch.randn(T, H, K, generator=g) * 2.0
+    gate[:, :, ::3] = -30.0  # a third of the channels: softplus ~ 0, almost no decay
+    beta = torch.rand(T, H, generator=g)
+    a_log_t = torch.full((H,), a_log)
+    dt_bias = torch.randn(H * K, generator=g)
+    init = torch.tensor([2, 4])
+    pool.encode((torch.randn(2, H, K, V, generator=g) * .1).to(dev()), init.to(dev()))
+    lay = O.layout(oplan, V)
+    S0 = O.decode_page(pool.data.cpu().numpy(), init.numpy(), oplan, lay, V).astype(np.float64)
+    ck = np.array([[16, 75], [20, 33]])
+    ck_slots = torch.tensor([[1, 3], [5, 0]])
+    pool.keep_prefill_states = True
+    out = pool.extend(q.to(dev()), k.to(dev()), v.to(dev()), gate.to(dev()), beta.to(dev()), init,
+                      torch.from_numpy(cu), checkpoints=torch.from_numpy(ck), checkpoint_slots=ck_slots,
+                      init_slots=init, normalize=True, scale=K ** -.5, a_log=a_log_t.to(dev()),
+                      dt_bias=dt_bias.to(dev()), beta_logits=False)
+    torch.cuda.synchronize()
+    ref_out, ref_states, _ = O.prefill(q.float().numpy(), k.float().numpy(), v.float().numpy(), gate.numpy(),
+                                       beta.numpy(), S0, cu, ck, normalize=True, scale=K ** -.5,
+                                       a_log=a_log_t.numpy(), dt_bias=dt_bias.numpy(), beta_logits=False)
+    states = pool.last_prefill[-1].cpu().numpy().reshape(2, 2, H, K, V)
+    assert np.isfinite(out.float().cpu().numpy()).all() and np.isfinite(states).all()
+    check_prefill(out, ref_out, "bf16 outputs")
+    for b in range(2):
+        for c in range(2):
+            if ck_slots[b, c] > 0:
+                check_states(states[b, c], ref_states[b, c], f"state b={b} c={c}")
