@@ -592,6 +592,228 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void e
 }
 
 // =====================================================================
+// Encode, KDA pools with K = V = 128, packed: per-row widths (2, 4, 6, 8)
+// and FP16 pivot rows, 4-value tiles, 512 threads.  The operations and
+// their order are those of encode_kernel's split path (four threads per
+// column, 16-row blocks of the refit sums), with every value of the tile
+// loaded once per layout into registers (row layout for the row scales,
+// column layout for the rest), so a tile waits for memory twice rather than
+// once per row and pass, and the divisions by fp16 scales use their
+// correctly rounded reciprocals (div_half) when the tile's values allow it.
+// =====================================================================
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void encode_kda128_kernel(
+    PoolDev P, const float *__restrict__ state, const void *slots, int slots_dtype) {
+#pragma clang fp contract(off)
+  extern __shared__ __align__(16) uint8_t smem[];
+  constexpr int K = 128, V = 128;
+  const int H = P.H;
+  const int b = blockIdx.x / H, h = blockIdx.x % H;
+  const int tid = threadIdx.x;
+  const int64_t slot = load_slot(slots, slots_dtype, b);
+  if (slot <= 0 || slot >= P.num_slots) return;  // masked (or outside the pool)
+  uint8_t *page = P.data + slot * P.page_bytes;
+  const float *X = state + ((int64_t)b * H + h) * K * V;
+  const int32_t *hm = P.head_meta + 4 * h;
+  const int code_start = hm[0], code_bytes = hm[1];
+  const int stride = P.offsets[(int64_t)H * K + h];
+  const int shift = (int)((uintptr_t)(page + code_start) & 15);
+  uint8_t *stage = smem;
+  float *rsc = (float *)(smem + P.stage);  // [K] row scales (1 for pivots)
+  float *rinv = rsc + K;                   // [K] 1 / row scale
+  float *wl = rinv + K;                    // [K] fit weights
+  int *bl = (int *)(wl + K);               // [K] widths
+  int *orel = bl + K;                      // [K] row offsets within the code region
+  float *cmax = (float *)(orel + K);       // [4 parts][4 widths][V]
+  float *bsum = cmax + 16 * V;             // [K/16][2][V]
+  uint32_t lo_bits = 0xffffffffu, hi_bits = 0u;  // min of |x| bits - 1 (zeros wrap), max of |x| bits
+  // ---- row phase: r = fp16(sqrt(max(mean|x|, 1e-20) / w)) in PyTorch's
+  // summation order (as encode_fast128); pivot rows as halves
+  {
+    const int lane = tid & 31, l = lane >> 2, k = lane & 3, rw = tid >> 5;
+    float v[8][4], wi[8];
+    int ro[8], of[8], bi[8];
+#pragma unroll
+    for (int p = 0; p < 8; p++) {
+      const int i = rw + 16 * p;
+#pragma unroll
+      for (int u = 0; u < 4; u++) v[p][u] = X[i * V + 32 * u + 8 * k + l];
+      wi[p] = P.impact[(int64_t)h * K + i];
+      ro[p] = P.rows[(int64_t)h * K + i];
+      of[p] = P.offsets[(int64_t)h * K + i];
+      bi[p] = P.bits[(int64_t)h * K + i];
+    }
+    // the existing code region (padding bytes before pivot rows keep their
+    // contents, as in encode_kernel), staged after the tile's loads
+    stage_in(page + code_start, code_bytes, stage, tid, 512);
+    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < 8; p++)
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const uint32_t a = __float_as_uint(v[p][u]) & 0x7fffffffu;
+        lo_bits = min(lo_bits, a - 1u);
+        hi_bits = max(hi_bits, a);
+      }
+#pragma unroll
+    for (int p = 0; p < 8; p++) {
+      const int i = rw + 16 * p;
+      const int off_rel = of[p] - code_start;
+      if (bi[p] == 16) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+          const int j = 32 * u + 8 * k + l;
+          const int pos = shift + group_pos(off_rel, stride, 4, j, 16);
+          const uint32_t hb = f2h(v[p][u]);
+          stage[pos] = (uint8_t)hb;
+          stage[pos + 1] = (uint8_t)(hb >> 8);
+        }
+      }
+      float acc = 0.0f;
+#pragma unroll
+      for (int u = 0; u < 4; u++) acc += fabsf(v[p][u]);
+      float sl = acc;
+      sl += row_shl<1>(acc);
+      sl += row_shl<2>(acc);
+      sl += row_shl<3>(acc);
+      const float up = __uint_as_float(
+          __builtin_amdgcn_permlane16_swap(__float_as_uint(sl), __float_as_uint(sl), false, false)[1]);
+      float total = 0.0f;
+      total += sl;
+      total += row_shl<4>(sl);
+      total += row_shl<8>(sl);
+      total += row_shl<12>(sl);
+      total += up;
+      total += row_shl<4>(up);
+      total += row_shl<8>(up);
+      total += row_shl<12>(up);
+      if (lane == 0) {
+        if (bi[p] == 16) {
+          rsc[i] = 1.0f;
+          rinv[i] = 1.0f;
+        } else {
+          float m = total / (float)V;
+          m = m < 1e-20f ? 1e-20f : m;
+          uint32_t hb;
+          const float r = fp16_scale(__builtin_sqrtf(m / wi[p]), &hb);
+          rsc[i] = r;
+          rinv[i] = 1.0f / r;
+          put_page_half(page, ro[p], hb);
+        }
+        wl[i] = wi[p];
+        bl[i] = bi[p];
+        orel[i] = off_rel;
+      }
+    }
+  }
+  // ---- column phase: this thread's 32 values of column j (rows 32 hf ..)
+  const int j = tid & (V - 1), hf = tid >> 7, i0 = 32 * hf;
+  float xs[32], sc[32];
+#pragma unroll
+  for (int r = 0; r < 32; r++) xs[r] = X[(i0 + r) * V + j];
+  const bool ieee = __syncthreads_or(lo_bits < 0x19800000u - 1u || hi_bits > 0x5d800000u);
+  auto columns = [&](auto fast_tag) {
+    constexpr bool FAST = decltype(fast_tag)::value;
+    float amax[4] = {0.f, 0.f, 0.f, 0.f};  // widths 2, 4, 6, 8
+#pragma unroll
+    for (int r = 0; r < 32; r++) {
+      const int i = i0 + r;
+      sc[r] = FAST ? div_half(xs[r], rsc[i], rinv[i]) : xs[r] / rsc[i];
+      const int w = bl[i];
+      if (w == 16) continue;
+      const float a = fabsf(sc[r]);
+      const int wsel = (w < 8 ? w : 8) / 2 - 1;
+#pragma unroll
+      for (int q = 0; q < 4; q++)
+        if (q == wsel) amax[q] = a > amax[q] ? a : amax[q];
+    }
+#pragma unroll
+    for (int q = 0; q < 4; q++) cmax[(hf * 4 + q) * V + j] = amax[q];
+    __syncthreads();
+    float mx = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      float am = 0.0f;
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const float a = cmax[(u * 4 + q) * V + j];
+        am = a > am ? a : am;
+      }
+      const int bc = 2 * q + 2;
+      const float qmax = (float)((1 << (bc - 1)) - 1);
+      const float norm = (float)(1 << (8 - bc));
+      const float t = am / (qmax * norm);
+      mx = t > mx ? t : mx;
+    }
+    const float c0 = fp16_scale(mx, nullptr);
+    const float c0inv = 1.0f / c0;
+    auto zq = [&](int r, float cdiv, float cinv) -> float {
+      const int w = bl[i0 + r];
+      const int bc = w < 8 ? w : 8;
+      const float qmax = (float)((1 << (bc - 1)) - 1);
+      const float norm = (float)(1 << (8 - bc));
+      float y = FAST ? div_half(sc[r], cdiv, cinv) : sc[r] / cdiv;
+      y = y * (1.0f / norm);  // exact: norm is a power of two
+      float z = __builtin_rintf(y);
+      z = z > -qmax ? z : -qmax;
+      z = z < qmax ? z : qmax;
+      return z;
+    };
+#pragma unroll
+    for (int mb = 0; mb < 2; mb++) {
+      float bn = 0.0f, bd = 0.0f;
+#pragma unroll
+      for (int rr = 0; rr < 16; rr++) {
+        const int r = 16 * mb + rr, i = i0 + r;
+        const int w = bl[i];
+        const int bc = w < 8 ? w : 8;
+        const float norm = (float)(1 << (8 - bc));
+        const float wsq = (wl[i] * wl[i]) * (w != 16 ? 1.0f : 0.0f);
+        const float z = zq(r, c0, c0inv);
+        const float v = (rsc[i] * norm) * z;
+        bn += (wsq * v) * xs[r];
+        bd += wsq * (v * v);
+      }
+      const int m = 2 * hf + mb;
+      bsum[(2 * m) * V + j] = bn;
+      bsum[(2 * m + 1) * V + j] = bd;
+    }
+    __syncthreads();
+    float num = 0.0f, den = 0.0f;
+#pragma unroll
+    for (int m = 0; m < K / 16; m++) {
+      num += bsum[(2 * m) * V + j];
+      den += bsum[(2 * m + 1) * V + j];
+    }
+    const float denc = den < 1e-30f ? 1e-30f : den;
+    uint32_t chb;
+    const float c = fp16_scale(den > 0.0f ? num / denc : c0, &chb);
+    const float cinv = 1.0f / c;
+    const int colbase = P.columns[h];
+    if (hf == 0 && colbase >= 0) put_page_half(page, colbase + 2 * (int64_t)j, chb);
+    // final codes; quads of lanes assemble each row's 4-value tile
+#pragma unroll
+    for (int r = 0; r < 32; r++) {
+      const int i = i0 + r;
+      const int w = bl[i];
+      uint32_t code = 0;
+      if (w != 16) {
+        const int bc = w < 8 ? w : 8;
+        code = (uint32_t)((int)zq(r, c, cinv) + ((1 << (bc - 1)) - 1));
+      }
+      const uint32_t c1 = quad_perm<0xB1>(code), c2 = quad_perm<0x4E>(code), c3 = quad_perm<0x1B>(code);
+      if (w != 16 && (tid & 3) == 0) {
+        const uint32_t word = code | (c1 << w) | (c2 << (2 * w)) | (c3 << (3 * w));
+        lds_put_bytes(stage, shift + group_pos(orel[i], stride, 4, j, w), word, w / 2);
+      }
+    }
+  };
+  if (ieee) columns(BoolTag<false>{});
+  else columns(BoolTag<true>{});
+  __syncthreads();
+  stage_out(page + code_start, code_bytes, stage, tid, 512);
+}
+
+// =====================================================================
 // Encode: dense fp32 -> page, bit-exact fit_state.  Thread j owns column j
 // (NT >= V); rows are processed by thread i in the row phase.
 // =====================================================================
@@ -3683,15 +3905,16 @@ __device__ __forceinline__ float row_bcast(float x) {
 }
 
 // one step of the substitution: token S's Delta (row S / 4, register S % 4)
-// to every lane, and -A[t][S] Delta_S into every later token t of this lane
-// (a[r][S] = A[4 q4 + r][S], loaded before the first step)
+// to every lane, and -A[t][S] Delta_S into every token t of this lane
+// (a[r][S] = A[4 q4 + r][S], loaded before the first step; A is zero on and
+// above the diagonal, so earlier tokens take exact zeros)
 template <int S>
-__device__ __forceinline__ void delta_step(float dv[4], const float (&a)[4][C], int q4) {
+__device__ __forceinline__ void delta_step(float dv[4], const float (&a)[4][C]) {
   if constexpr (S < C) {
     const float xs = row_bcast<S / 4>(dv[S % 4]);
 #pragma unroll
-    for (int r = 0; r < 4; r++) dv[r] = 4 * q4 + r > S ? fmaf(-a[r][S], xs, dv[r]) : dv[r];
-    delta_step<S + 1>(dv, a, q4);
+    for (int r = 0; r < 4; r++) dv[r] = fmaf(-a[r][S], xs, dv[r]);
+    delta_step<S + 1>(dv, a);
   }
 }
 
@@ -3723,9 +3946,11 @@ __global__ __launch_bounds__(NT) void kda_chunk_kernel(pf::PrefillDev D) {
   float *EC = (float *)(smem + OFF_EC);
   uint8_t *KE = smem + OFF_KE, *KB = smem + OFF_KB, *QB = smem + OFF_QB;
   constexpr float LOG2E = 1.4426950408889634f;
-  // P: entries above the diagonal stay zero (written once; the MFMA path
-  // rewrites them with zeros); the pairwise-path flags start clear
+  // P and A: entries above (A: on and above) the diagonal stay zero
+  // (written once; the MFMA path rewrites them with zeros); the
+  // pairwise-path flags start clear
   for (int e = tid; e < C * TP; e += NT) ((uint32_t *)PM)[e] = 0u;
+  for (int e = tid; e < C * AP; e += NT) A[e] = 0.0f;
   if (tid < 2) sm[SM_FLAG * C + tid] = 0.0f;
   pf::lds_barrier();
 
@@ -3974,7 +4199,7 @@ __global__ __launch_bounds__(NT) void kda_chunk_kernel(pf::PrefillDev D) {
 #pragma unroll
         for (int r = 0; r < 4; r++) {
           const int t = 4 * q4 + r;
-          if (s0 < t) A[t * AP + s0] = (sm[SM_BETA * C + t] * sm[SM_NK * C + t]) * acc[r];
+          A[t * AP + s0] = s0 < t ? (sm[SM_BETA * C + t] * sm[SM_NK * C + t]) * acc[r] : 0.0f;
         }
       } else {
 #pragma unroll
@@ -4031,7 +4256,7 @@ __global__ __launch_bounds__(NT) void kda_chunk_kernel(pf::PrefillDev D) {
           a[r][4 * m + 3] = x.w;
         }
       float dv[4] = {R[0], R[1], R[2], R[3]};
-      delta_step<0>(dv, a, q4);
+      delta_step<0>(dv, a);
       const f32x4 dl = {dv[0], dv[1], dv[2], dv[3]};
       pf::split4x(dl, dh4, dl4);
       const int o = (c16 * TP + 4 * q4) * 2;
@@ -4841,6 +5066,13 @@ int sq_encode(const sq_pool *pool, const float *state, const void *slots, int32_
   const int NT = split > 1 ? split * V : (V < 64 ? 64 : V);  // lanes per value column
   size_t lds = (size_t)stage_bytes(pool) + (size_t)((K * NG + 3) & ~3) * 4 + 16;
   if (split > 1) lds += (size_t)split * 4 * V * 4 + (size_t)(K / 16) * 2 * V * 4;
+  if (pool->kda && pool->storage == 0 && K == 128 && V == 128) {
+    // rows, 1 / rows, w, widths, row offsets [K] | column maxima [4][4][V] | block sums [K/16][2][V]
+    const size_t fl = (size_t)stage_bytes(pool) + (size_t)(5 * K + 16 * V + (K / 16) * 2 * V) * 4;
+    hipLaunchKernelGGL(encode_kda128_kernel, dim3((unsigned)(batch * pool->heads)), dim3(512), fl,
+                       (hipStream_t)stream, pd, state, slots, slots_dtype);
+    return check_launch("encode_kda128_kernel");
+  }
   if (!pool->kda && pool->storage == 0 && K == 128 && V == 128 && pd.G == 32) {
     // rows [K][4] | w [K] | row offsets [K] | column maxima [4][V] | block sums [K/16][2][V] | 1/rows [K][4]
     const size_t fl = (size_t)stage_bytes(pool) + (size_t)(K * 4 + 2 * K + 4 * V + (K / 16) * 2 * V + K * 4) * 4;
