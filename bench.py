@@ -257,7 +257,7 @@ def bench_prefill(a, torch):
     gate_bytes = tot * H * (K if kda else 1) * 4 + tot * H * 4
     hbm = (2 * tot * HK * K * 2 + tot * H * V * 2 + tot * H * V * 2 + gate_bytes + B * pool.page_bytes
            + B * NC * pool.page_bytes)
-    chunk = 16 if kda else 64
+    chunk = 32 if kda else 64
     workload = (f"{a.arch.upper()} prefill STEPQuant@6, B={B}, T={T}, H={H}, HK={HK}, dk=dv={K}, "
                 + f"chunk {chunk}" + (" (per-channel decay)" if kda else "")
                 + f", bf16 q/k/v, raw gates, {NC} prefix slots per request")

@@ -3847,52 +3847,63 @@ using pf::bf16x4;
 using pf::bf16x8;
 using pf::f32x4;
 
-constexpr int C = 16;                 // tokens per chunk
-constexpr int NT = 512;               // 8 waves
-constexpr int KV = 128;               // K = V = 128
-constexpr int RP = 136;               // bf16 row pitch of token rows
-constexpr int GP = 132;               // f32 row pitch of the decay rows
-constexpr int TP = 20;                // bf16 row pitch of 16-wide tiles
-constexpr int AP = 20;                // f32 row pitch of A (rows 16-byte aligned)
+constexpr int C = 32;                   // tokens per chunk: two blocks of 16
+constexpr int NT = 512;                 // 8 waves
+constexpr int KV = 128;                 // K = V = 128
+constexpr int RP = 136;                 // bf16 row pitch of token rows
+constexpr int GP = 132;                 // f32 row pitch of the decay rows
+constexpr int AP = 36;                  // f32 row pitch of A (rows 16-byte aligned)
+constexpr int PP = 40;                  // bf16 row pitch of P and of -A10
 constexpr int NPAIR = C * (C - 1) / 2;  // strictly lower pairs (t, s)
-constexpr int OFF_KR = 0;                         // bf16 [C][RP] raw k
-constexpr int OFF_QR = OFF_KR + C * RP * 2;       // bf16 [C][RP] raw q
-constexpr int OFF_VR = OFF_QR + C * RP * 2;       // bf16 [C][RP] v
+// LDS.  The hi planes of KB and QB hold the raw k and q rows from the
+// staging until each thread replaces its own entries by the scaled operand.
+constexpr int OFF_VR = 0;                         // bf16 [C][RP] v
 constexpr int OFF_G = OFF_VR + C * RP * 2;        // f32 [C][GP] cumulative log2 decays
 constexpr int OFF_KG = OFF_G + C * GP * 4;        // bf16 2 x [C][RP] nk k e^G (hi, lo), channels in pcol order
 constexpr int OFF_QG = OFF_KG + 2 * C * RP * 2;   // bf16 2 x [C][RP] nq q e^G (hi, lo), channels in pcol order
-constexpr int OFF_KD = OFF_QG + 2 * C * RP * 2;   // bf16 2 x [KV][TP] nk k e^{G_C - G} (hi, lo), row = channel
-constexpr int OFF_A = OFF_KD + 2 * KV * TP * 2;   // f32 [C][AP] A (below the diagonal)
-constexpr int OFF_PM = OFF_A + C * AP * 4;        // bf16 2 x [C][TP] P (hi, lo)
-constexpr int OFF_SM = OFF_PM + 2 * C * TP * 2;   // f32 [4][C] beta, nk, nq; flags
+constexpr int OFF_KE = OFF_QG + 2 * C * RP * 2;   // bf16 2 x [C][RP] nk k e^{G_C - G} (hi, lo)
+constexpr int OFF_KB = OFF_KE + 2 * C * RP * 2;   // bf16 2 x [C][RP] k e^{G - G_C} (hi, lo); raw k first
+constexpr int OFF_QB = OFF_KB + 2 * C * RP * 2;   // bf16 2 x [C][RP] q e^{G - G_C} (hi, lo); raw q first
+constexpr int OFF_A = OFF_QB + 2 * C * RP * 2;   // f32 [C][AP] A (zero on and above the diagonal)
+constexpr int OFF_M = OFF_A + C * AP * 4;         // bf16 2 x [16][PP] -A10 (hi, lo): rows 16.., columns 0..15
+constexpr int OFF_PM = OFF_M + 2 * 16 * PP * 2;   // bf16 2 x [C][PP] P (hi, lo), zero above the diagonal
+constexpr int OFF_SM = OFF_PM + 2 * C * PP * 2;   // f32 [4][C] beta, nk, nq; flags
 constexpr int OFF_EC = OFF_SM + 4 * C * 4;        // f32 [KV] e^{G_C}
-constexpr int OFF_KE = OFF_EC + KV * 4;           // bf16 2 x [C][RP] nk k e^{G_C - G} (hi, lo), row = token
-constexpr int OFF_KB = OFF_KE + 2 * C * RP * 2;   // bf16 2 x [C][RP] k e^{G - G_C} (hi, lo)
-constexpr int OFF_QB = OFF_KB + 2 * C * RP * 2;   // bf16 2 x [C][RP] q e^{G - G_C} (hi, lo)
-constexpr int LDS_BYTES = OFF_QB + 2 * C * RP * 2;
+constexpr int LDS_BYTES = OFF_EC + KV * 4;
+static_assert(LDS_BYTES <= 160 * 1024, "LDS of the KDA chunk kernel");
 enum { SM_BETA = 0, SM_NK, SM_NQ, SM_FLAG };
 // a chunk whose decay exceeds 2^GROW_MAX on some channel takes the pairwise path
 constexpr float GROW_MAX = 96.0f;
 
 // (t, s) of strictly-lower pair p, t > s, pairs ordered by t then s
-__constant__ uint8_t pair_t[NPAIR] = {1, 2, 2, 3, 3, 3, 4, 4, 4, 4, 5, 5, 5, 5, 5, 6, 6, 6, 6, 6, 6, 7, 7, 7, 7, 7, 7, 7, 8, 8, 8, 8, 8, 8, 8, 8, 9, 9, 9, 9, 9, 9, 9, 9, 9, 10, 10, 10, 10, 10, 10, 10, 10, 10, 10, 11, 11, 11, 11, 11, 11, 11, 11, 11, 11, 11, 12, 12, 12, 12, 12, 12, 12, 12, 12, 12, 12, 12, 13, 13, 13, 13, 13, 13, 13, 13, 13, 13, 13, 13, 13, 14, 14, 14, 14, 14, 14, 14, 14, 14, 14, 14, 14, 14, 14, 15, 15, 15, 15, 15, 15, 15, 15, 15, 15, 15, 15, 15, 15, 15};
-__constant__ uint8_t pair_s[NPAIR] = {0, 0, 1, 0, 1, 2, 0, 1, 2, 3, 0, 1, 2, 3, 4, 0, 1, 2, 3, 4, 5, 0, 1, 2, 3, 4, 5, 6, 0, 1, 2, 3, 4, 5, 6, 7, 0, 1, 2, 3, 4, 5, 6, 7, 8, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14};
+__constant__ uint8_t pair_t[NPAIR] = {1, 2, 2, 3, 3, 3, 4, 4, 4, 4, 5, 5, 5, 5, 5, 6, 6, 6, 6, 6, 6, 7, 7, 7, 7, 7, 7, 7, 8, 8, 8, 8, 8, 8, 8, 8, 9, 9, 9, 9, 9, 9, 9, 9, 9, 10, 10, 10, 10, 10, 10, 10, 10, 10, 10, 11, 11, 11, 11, 11, 11, 11, 11, 11, 11, 11, 12, 12, 12, 12, 12, 12, 12, 12, 12, 12, 12, 12, 13, 13, 13, 13, 13, 13, 13, 13, 13, 13, 13, 13, 13, 14, 14, 14, 14, 14, 14, 14, 14, 14, 14, 14, 14, 14, 14, 15, 15, 15, 15, 15, 15, 15, 15, 15, 15, 15, 15, 15, 15, 15, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 17, 17, 17, 17, 17, 17, 17, 17, 17, 17, 17, 17, 17, 17, 17, 17, 17, 18, 18, 18, 18, 18, 18, 18, 18, 18, 18, 18, 18, 18, 18, 18, 18, 18, 18, 19, 19, 19, 19, 19, 19, 19, 19, 19, 19, 19, 19, 19, 19, 19, 19, 19, 19, 19, 20, 20, 20, 20, 20, 20, 20, 20, 20, 20, 20, 20, 20, 20, 20, 20, 20, 20, 20, 20, 21, 21, 21, 21, 21, 21, 21, 21, 21, 21, 21, 21, 21, 21, 21, 21, 21, 21, 21, 21, 21, 22, 22, 22, 22, 22, 22, 22, 22, 22, 22, 22, 22, 22, 22, 22, 22, 22, 22, 22, 22, 22, 22, 23, 23, 23, 23, 23, 23, 23, 23, 23, 23, 23, 23, 23, 23, 23, 23, 23, 23, 23, 23, 23, 23, 23, 24, 24, 24, 24, 24, 24, 24, 24, 24, 24, 24, 24, 24, 24, 24, 24, 24, 24, 24, 24, 24, 24, 24, 24, 25, 25, 25, 25, 25, 25, 25, 25, 25, 25, 25, 25, 25, 25, 25, 25, 25, 25, 25, 25, 25, 25, 25, 25, 25, 26, 26, 26, 26, 26, 26, 26, 26, 26, 26, 26, 26, 26, 26, 26, 26, 26, 26, 26, 26, 26, 26, 26, 26, 26, 26, 27, 27, 27, 27, 27, 27, 27, 27, 27, 27, 27, 27, 27, 27, 27, 27, 27, 27, 27, 27, 27, 27, 27, 27, 27, 27, 27, 28, 28, 28, 28, 28, 28, 28, 28, 28, 28, 28, 28, 28, 28, 28, 28, 28, 28, 28, 28, 28, 28, 28, 28, 28, 28, 28, 28, 29, 29, 29, 29, 29, 29, 29, 29, 29, 29, 29, 29, 29, 29, 29, 29, 29, 29, 29, 29, 29, 29, 29, 29, 29, 29, 29, 29, 29, 30, 30, 30, 30, 30, 30, 30, 30, 30, 30, 30, 30, 30, 30, 30, 30, 30, 30, 30, 30, 30, 30, 30, 30, 30, 30, 30, 30, 30, 30, 31, 31, 31, 31, 31, 31, 31, 31, 31, 31, 31, 31, 31, 31, 31, 31, 31, 31, 31, 31, 31, 31, 31, 31, 31, 31, 31, 31, 31, 31, 31};
+__constant__ uint8_t pair_s[NPAIR] = {0, 0, 1, 0, 1, 2, 0, 1, 2, 3, 0, 1, 2, 3, 4, 0, 1, 2, 3, 4, 5, 0, 1, 2, 3, 4, 5, 6, 0, 1, 2, 3, 4, 5, 6, 7, 0, 1, 2, 3, 4, 5, 6, 7, 8, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16, 17, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18, 19, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18, 19, 20, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18, 19, 20, 21, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18, 19, 20, 21, 22, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18, 19, 20, 21, 22, 23, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18, 19, 20, 21, 22, 23, 24, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18, 19, 20, 21, 22, 23, 24, 25, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18, 19, 20, 21, 22, 23, 24, 25, 26, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18, 19, 20, 21, 22, 23, 24, 25, 26, 27, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18, 19, 20, 21, 22, 23, 24, 25, 26, 27, 28, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18, 19, 20, 21, 22, 23, 24, 25, 26, 27, 28, 29, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18, 19, 20, 21, 22, 23, 24, 25, 26, 27, 28, 29, 30};
 
 // Raw inputs of one chunk for this thread, fetched one chunk ahead: token
-// tt = tid >> 5, channels c4 .. c4 + 3 of k, q, v (bf16) and, in the decay
-// mapping (channel c = tid >> 2, tokens 4 (tid & 3) .. + 3), the raw gates.
+// tid >> 4, channels 8 (tid & 15) .. + 7 of k, q, v (bf16) and, in the
+// decay mapping (channel tid >> 2, tokens 8 (tid & 3) .. + 7), the raw gates.
 struct Fetch {
-  uint2 k, q, v;
-  float g[4];
+  uint4 k, q, v;
+  float g[8];
   float beta;
   int n;
 };
 
-__device__ __forceinline__ void bf4(const uint2 &x, float o[4]) {
-  o[0] = __uint_as_float(x.x << 16);
-  o[1] = __uint_as_float(x.x & 0xffff0000u);
-  o[2] = __uint_as_float(x.y << 16);
-  o[3] = __uint_as_float(x.y & 0xffff0000u);
+__device__ __forceinline__ void bf8(const uint4 &x, float o[8]) {
+  const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    o[2 * e] = __uint_as_float(w[e] << 16);
+    o[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+  }
+}
+
+// hi/lo halves of eight values as two packed bf16 x 8 (natural order)
+__device__ __forceinline__ void split8v(const float x[8], uint4 &hi, uint4 &lo) {
+  pf::split2(x[0], x[1], hi.x, lo.x);
+  pf::split2(x[2], x[3], hi.y, lo.y);
+  pf::split2(x[4], x[5], hi.z, lo.z);
+  pf::split2(x[6], x[7], hi.w, lo.w);
 }
 
 // the value of 16-lane row Q of the wave in every row (two lane-row swaps)
@@ -3904,13 +3915,14 @@ __device__ __forceinline__ float row_bcast(float x) {
   return __uint_as_float((Q & 2) ? s32[1] : s32[0]);
 }
 
-// one step of the substitution: token S's Delta (row S / 4, register S % 4)
-// to every lane, and -A[t][S] Delta_S into every token t of this lane
-// (a[r][S] = A[4 q4 + r][S], loaded before the first step; A is zero on and
-// above the diagonal, so earlier tokens take exact zeros)
+// one step of a 16-token block's substitution: token S's Delta (row S / 4,
+// register S % 4) to every lane, and -A[t][S] Delta_S into every token t of
+// this lane (a[r][S]: the block's A row of the lane's token r, loaded before
+// the first step; A is zero on and above the diagonal, so earlier tokens
+// take exact zeros)
 template <int S>
-__device__ __forceinline__ void delta_step(float dv[4], const float (&a)[4][C]) {
-  if constexpr (S < C) {
+__device__ __forceinline__ void delta_step(float dv[4], const float (&a)[4][16]) {
+  if constexpr (S < 16) {
     const float xs = row_bcast<S / 4>(dv[S % 4]);
 #pragma unroll
     for (int r = 0; r < 4; r++) dv[r] = fmaf(-a[r][S], xs, dv[r]);
@@ -3918,12 +3930,42 @@ __device__ __forceinline__ void delta_step(float dv[4], const float (&a)[4][C]) 
   }
 }
 
-// sum over the 32 lanes of a half wave (lanes 32 m .. 32 m + 31): the
-// 16-lane rows by DPP, then the two rows of the half with v_permlane16_swap
-__device__ __forceinline__ float sum32(float x) {
-  x = pf::row16_sum(x);
-  const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+// Delta of one 16-token block from its right-hand side: rows t0 + 4 q4 + r
+// of A, columns c0 .. c0 + 15
+__device__ __forceinline__ f32x4 block_solve(const float *A, int t0, int c0, int q4, const f32x4 &rhs) {
+  float a[4][16];  // all loads issued before the chain
+#pragma unroll
+  for (int r = 0; r < 4; r++)
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+      const float4 x = *(const float4 *)(A + (t0 + 4 * q4 + r) * AP + c0 + 4 * m);
+      a[r][4 * m] = x.x;
+      a[r][4 * m + 1] = x.y;
+      a[r][4 * m + 2] = x.z;
+      a[r][4 * m + 3] = x.w;
+    }
+  float dv[4] = {rhs[0], rhs[1], rhs[2], rhs[3]};
+  delta_step<0>(dv, a);
+  const f32x4 d = {dv[0], dv[1], dv[2], dv[3]};
+  return d;
+}
+
+// acc + (16 x 16 hi/lo matrix at byte offset o of `tile`, lo plane `lo`
+// bytes further) x (the hi/lo B operand xh, xl)
+__device__ __forceinline__ f32x4 mm16(const uint8_t *tile, int o, int lo, bf16x4 xh, bf16x4 xl, f32x4 acc) {
+  const bf16x4 mh = pf::ld4(tile, o), ml = pf::ld4(tile, lo + o);
+  acc = pf::mfma16(mh, xh, acc);
+  acc = pf::mfma16(mh, xl, acc);
+  return pf::mfma16(ml, xh, acc);
+}
+
+// acc + (the hi/lo A operand xh, xl) x (16 x 16 hi/lo matrix at byte offset o
+// of `tile`, lo plane `lo` bytes further, as the B operand)
+__device__ __forceinline__ f32x4 mm16t(const uint8_t *tile, int o, int lo, bf16x4 xh, bf16x4 xl, f32x4 acc) {
+  const bf16x4 mh = pf::ld4(tile, o), ml = pf::ld4(tile, lo + o);
+  acc = pf::mfma16(xh, mh, acc);
+  acc = pf::mfma16(xh, ml, acc);
+  return pf::mfma16(xl, mh, acc);
 }
 
 __global__ __launch_bounds__(NT) void kda_chunk_kernel(pf::PrefillDev D) {
@@ -3937,19 +3979,18 @@ __global__ __launch_bounds__(NT) void kda_chunk_kernel(pf::PrefillDev D) {
   if (len <= 0) return;  // whole workgroup
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, q4 = l >> 4, c16 = l & 15;
   const int jw = 16 * w;
-  uint8_t *KR = smem + OFF_KR, *QR = smem + OFF_QR, *VR = smem + OFF_VR;
+  uint8_t *VR = smem + OFF_VR;
   float *G = (float *)(smem + OFF_G);
-  uint8_t *KG = smem + OFF_KG, *QG = smem + OFF_QG, *KD = smem + OFF_KD;
+  uint8_t *KG = smem + OFF_KG, *QG = smem + OFF_QG, *KE = smem + OFF_KE, *KB = smem + OFF_KB, *QB = smem + OFF_QB;
+  uint8_t *M = smem + OFF_M, *PM = smem + OFF_PM;
   float *A = (float *)(smem + OFF_A);
-  uint8_t *PM = smem + OFF_PM;
   float *sm = (float *)(smem + OFF_SM);
   float *EC = (float *)(smem + OFF_EC);
-  uint8_t *KE = smem + OFF_KE, *KB = smem + OFF_KB, *QB = smem + OFF_QB;
   constexpr float LOG2E = 1.4426950408889634f;
-  // P and A: entries above (A: on and above) the diagonal stay zero
-  // (written once; the MFMA path rewrites them with zeros); the
-  // pairwise-path flags start clear
-  for (int e = tid; e < C * TP; e += NT) ((uint32_t *)PM)[e] = 0u;
+  constexpr int KB_LO = C * RP * 2, PLO = C * PP * 2, MLO = 16 * PP * 2;
+  // A and P: entries on / above the diagonal stay zero (written once; the
+  // MFMA path rewrites them with zeros); the pairwise-path flags start clear
+  for (int e = tid; e < C * PP; e += NT) ((uint32_t *)PM)[e] = 0u;
   for (int e = tid; e < C * AP; e += NT) A[e] = 0.0f;
   if (tid < 2) sm[SM_FLAG * C + tid] = 0.0f;
   pf::lds_barrier();
@@ -3969,8 +4010,8 @@ __global__ __launch_bounds__(NT) void kda_chunk_kernel(pf::PrefillDev D) {
     const int stop = m ? __builtin_amdgcn_readlane(ckv, __builtin_ctzll(m)) : len;
     return stop - c < C ? stop - c : C;
   };
-  // staging mapping: token tt, channels c4 .. c4 + 3; decay mapping: channel gc, tokens 4 gq .. 4 gq + 3
-  const int tt = tid >> 5, c4 = (tid & 31) * 4;
+  // staging mapping: token tt, channels c8 .. c8 + 7; decay mapping: channel gc, tokens 8 gq .. 8 gq + 7
+  const int tt = tid >> 4, c8 = (tid & 15) * 8;
   const int gc = tid >> 2, gq = tid & 3;
   const float ea = D.a_log ? __expf(load_val(D.a_log, D.gate_dtype, h)) : 0.0f;
   const float dtb = D.a_log ? load_val(D.dt_bias, D.gate_dtype, (int64_t)h * KV + gc) : 0.0f;
@@ -3979,15 +4020,15 @@ __global__ __launch_bounds__(NT) void kda_chunk_kernel(pf::PrefillDev D) {
     F.n = c < len ? segment(c) : 0;
     const int last = len - 1;
     const int64_t row = (int64_t)t0 + (c + tt < len ? c + tt : last);
-    F.k = *(const uint2 *)(kg + (row * D.k_stride + (int64_t)hk * KV + c4) * 2);
-    F.q = *(const uint2 *)(qg + (row * D.q_stride + (int64_t)hk * KV + c4) * 2);
-    F.v = *(const uint2 *)(vg + (row * D.v_stride + (int64_t)h * KV + c4) * 2);
+    F.k = *(const uint4 *)(kg + (row * D.k_stride + (int64_t)hk * KV + c8) * 2);
+    F.q = *(const uint4 *)(qg + (row * D.q_stride + (int64_t)hk * KV + c8) * 2);
+    F.v = *(const uint4 *)(vg + (row * D.v_stride + (int64_t)h * KV + c8) * 2);
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int64_t gr = (int64_t)t0 + (c + 4 * gq + i < len ? c + 4 * gq + i : last);
+    for (int i = 0; i < 8; i++) {
+      const int64_t gr = (int64_t)t0 + (c + 8 * gq + i < len ? c + 8 * gq + i : last);
       F.g[i] = load_val(D.g, D.gate_dtype, (gr * H + h) * KV + gc);
     }
-    const int64_t br = (int64_t)t0 + (c + (l & 15) < len ? c + (l & 15) : last);
+    const int64_t br = (int64_t)t0 + (c + (l & 31) < len ? c + (l & 31) : last);
     F.beta = load_val(D.beta, D.gate_dtype, br * H + h);
   };
 
@@ -3997,25 +4038,25 @@ __global__ __launch_bounds__(NT) void kda_chunk_kernel(pf::PrefillDev D) {
   int par = 0;  // chunk parity: which flag word this chunk uses
   for (int c0 = 0; c0 < len; par ^= 1) {
     const int n = F.n;
-    // ---- stage: k, q, v rows, norms, beta; cumulative decays per channel
+    // ---- stage: v rows, raw k and q rows, norms, beta; cumulative decays per channel
     {
-      float kf[4], qf[4];
-      bf4(F.k, kf);
-      bf4(F.q, qf);
+      float kf[8], qf[8];
+      bf8(F.k, kf);
+      bf8(F.q, qf);
       const bool live = tt < n;
-      const uint2 z2 = make_uint2(0u, 0u);
-      *(uint2 *)(KR + (tt * RP + c4) * 2) = live ? F.k : z2;
-      *(uint2 *)(QR + (tt * RP + c4) * 2) = live ? F.q : z2;
-      *(uint2 *)(VR + (tt * RP + c4) * 2) = live ? F.v : z2;
+      const uint32_t mk = live ? 0xffffffffu : 0u;  // tokens past the chunk's: zero rows
+      *(uint4 *)(KB + (tt * RP + c8) * 2) = make_uint4(F.k.x & mk, F.k.y & mk, F.k.z & mk, F.k.w & mk);
+      *(uint4 *)(QB + (tt * RP + c8) * 2) = make_uint4(F.q.x & mk, F.q.y & mk, F.q.z & mk, F.q.w & mk);
+      *(uint4 *)(VR + (tt * RP + c8) * 2) = make_uint4(F.v.x & mk, F.v.y & mk, F.v.z & mk, F.v.w & mk);
       float sk = 0.f, sq = 0.f;
 #pragma unroll
-      for (int e = 0; e < 4; e++) {
+      for (int e = 0; e < 8; e++) {
         sk = fmaf(kf[e], kf[e], sk);
         sq = fmaf(qf[e], qf[e], sq);
       }
-      sk = sum32(sk);
-      sq = sum32(sq);
-      if ((tid & 31) == 0) {
+      sk = pf::row16_sum(sk);
+      sq = pf::row16_sum(sq);
+      if ((tid & 15) == 0) {
         sm[SM_NK * C + tt] = live && D.normalize ? __builtin_amdgcn_rsqf(sk + 1e-6f) : (live ? 1.0f : 0.0f);
         sm[SM_NQ * C + tt] = live ? (D.normalize ? __builtin_amdgcn_rsqf(sq + 1e-6f) : 1.0f) * D.scale : 0.0f;
       }
@@ -4024,29 +4065,27 @@ __global__ __launch_bounds__(NT) void kda_chunk_kernel(pf::PrefillDev D) {
         if (D.beta_logits) bt = __builtin_amdgcn_rcpf(1.0f + __expf(-bt));
         sm[SM_BETA * C + l] = l < n ? bt : 0.0f;
       }
-      // log2 decays of tokens 4 gq .. 4 gq + 3 of channel gc (0 past the
-      // chunk's tokens), then the inclusive scan over the 16 tokens: within
+      // log2 decays of tokens 8 gq .. 8 gq + 7 of channel gc (0 past the
+      // chunk's tokens), then the inclusive scan over the 32 tokens: within
       // the thread, then across the quad (lanes gq = 0..3 of the channel)
-      float gl[4];
+      float gl[8];
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
+      for (int i = 0; i < 8; i++) {
         float gv = F.g[i];
         if (D.a_log) {
           const float u = gv + dtb;
           const float sp = u > 20.0f ? u : __logf(1.0f + __expf(u < 20.0f ? u : 20.0f));
           gv = -ea * sp;
         }
-        gl[i] = 4 * gq + i < n ? gv * LOG2E : 0.0f;
+        gl[i] = 8 * gq + i < n ? gv * LOG2E : 0.0f;
       }
-      gl[1] += gl[0];
-      gl[2] += gl[1];
-      gl[3] += gl[2];
-      // exclusive prefix of the quad's totals
-      const float tot = gl[3];
+#pragma unroll
+      for (int i = 1; i < 8; i++) gl[i] += gl[i - 1];
+      const float tot = gl[7];
       const float t1 = pf::quad_bcast<0>(tot), t2 = pf::quad_bcast<1>(tot), t3 = pf::quad_bcast<2>(tot);
       const float pre = gq == 0 ? 0.0f : gq == 1 ? t1 : gq == 2 ? t1 + t2 : (t1 + t2) + t3;
 #pragma unroll
-      for (int i = 0; i < 4; i++) G[(4 * gq + i) * GP + gc] = pre + gl[i];
+      for (int i = 0; i < 8; i++) G[(8 * gq + i) * GP + gc] = pre + gl[i];
       // the chunk's decay of channel gc (log2): G_0 - G_C, read on lane gq = 0
       const float gC = ((t1 + t2) + t3) + pf::quad_bcast<3>(tot);
       if (gq == 0 && gl[0] - gC > GROW_MAX) sm[SM_FLAG * C + par] = 1.0f;
@@ -4056,175 +4095,198 @@ __global__ __launch_bounds__(NT) void kda_chunk_kernel(pf::PrefillDev D) {
     fetch(F, c_next);
     pf::lds_barrier();
     const bool pairwise = sm[SM_FLAG * C + par] != 0.0f;  // workgroup-uniform
-    // ---- operands: nk k e^G and nq q e^G (hi/lo, pcol order), nk k e^{G_C - G}
-    // (hi/lo, transposed and row-major), e^{G_C}; for the MFMA path also
-    // k e^{G - G_C} and q e^{G - G_C} (hi/lo)
+    // ---- operands of token tt, channels c8 .. c8 + 7: nk k e^G and nq q e^G
+    // (hi/lo, pcol order), nk k e^{G_C - G} (hi/lo), e^{G_C}; for the MFMA path
+    // k e^{G - G_C} and q e^{G - G_C} (hi/lo) in place of the raw rows
     {
       const float nk = sm[SM_NK * C + tt], nq = sm[SM_NQ * C + tt];
-      const float4 gt = *(const float4 *)(G + tt * GP + c4), gC = *(const float4 *)(G + (C - 1) * GP + c4);
-      const float g4[4] = {gt.x, gt.y, gt.z, gt.w}, gc4[4] = {gC.x, gC.y, gC.z, gC.w};
-      float kf[4], qf[4];
-      bf4(*(const uint2 *)(KR + (tt * RP + c4) * 2), kf);
-      bf4(*(const uint2 *)(QR + (tt * RP + c4) * 2), qf);
-      float kgv[4], qgv[4], kdv[4];
+      float g8[8], gc8[8];
+      {
+        const float4 a0 = *(const float4 *)(G + tt * GP + c8), a1 = *(const float4 *)(G + tt * GP + c8 + 4);
+        const float4 e0 = *(const float4 *)(G + (C - 1) * GP + c8), e1 = *(const float4 *)(G + (C - 1) * GP + c8 + 4);
+        const float ga[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+        const float ge[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
 #pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const float eg = __builtin_amdgcn_exp2f(g4[e]);
+        for (int e = 0; e < 8; e++) {
+          g8[e] = ga[e];
+          gc8[e] = ge[e];
+        }
+      }
+      float kf[8], qf[8];
+      bf8(*(const uint4 *)(KB + (tt * RP + c8) * 2), kf);
+      bf8(*(const uint4 *)(QB + (tt * RP + c8) * 2), qf);
+      float kgv[8], qgv[8], kdv[8];
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const float eg = __builtin_amdgcn_exp2f(g8[e]);
         kgv[e] = (nk * kf[e]) * eg;
         qgv[e] = (nq * qf[e]) * eg;
-        kdv[e] = (nk * kf[e]) * __builtin_amdgcn_exp2f(gc4[e] - g4[e]);
+        kdv[e] = (nk * kf[e]) * __builtin_amdgcn_exp2f(gc8[e] - g8[e]);
       }
-      uint2 hi, lo;
-      pf::split4(kgv, hi, lo);
-      *(uint2 *)(KG + (tt * RP + pf::pcol(c4)) * 2) = hi;
-      *(uint2 *)(KG + (C * RP + tt * RP + pf::pcol(c4)) * 2) = lo;
-      pf::split4(qgv, hi, lo);
-      *(uint2 *)(QG + (tt * RP + pf::pcol(c4)) * 2) = hi;
-      *(uint2 *)(QG + (C * RP + tt * RP + pf::pcol(c4)) * 2) = lo;
-      pf::split4(kdv, hi, lo);
-      *(uint2 *)(KE + (tt * RP + c4) * 2) = hi;
-      *(uint2 *)(KE + (C * RP + tt * RP + c4) * 2) = lo;
+      {
+        // channels c8 .. c8 + 3 and c8 + 4 .. c8 + 7 at their permuted places
+        uint4 kh8, kl8, qh8, ql8;
+        split8v(kgv, kh8, kl8);
+        split8v(qgv, qh8, ql8);
+        const int p0 = pf::pcol(c8), p1 = pf::pcol(c8 + 4);
+        *(uint2 *)(KG + (tt * RP + p0) * 2) = make_uint2(kh8.x, kh8.y);
+        *(uint2 *)(KG + (tt * RP + p1) * 2) = make_uint2(kh8.z, kh8.w);
+        *(uint2 *)(KG + KB_LO + (tt * RP + p0) * 2) = make_uint2(kl8.x, kl8.y);
+        *(uint2 *)(KG + KB_LO + (tt * RP + p1) * 2) = make_uint2(kl8.z, kl8.w);
+        *(uint2 *)(QG + (tt * RP + p0) * 2) = make_uint2(qh8.x, qh8.y);
+        *(uint2 *)(QG + (tt * RP + p1) * 2) = make_uint2(qh8.z, qh8.w);
+        *(uint2 *)(QG + KB_LO + (tt * RP + p0) * 2) = make_uint2(ql8.x, ql8.y);
+        *(uint2 *)(QG + KB_LO + (tt * RP + p1) * 2) = make_uint2(ql8.z, ql8.w);
+      }
+      uint4 h4, l4;
+      split8v(kdv, h4, l4);
+      *(uint4 *)(KE + (tt * RP + c8) * 2) = h4;
+      *(uint4 *)(KE + KB_LO + (tt * RP + c8) * 2) = l4;
       if (!pairwise) {
-        float kbv[4], qbv[4];
+        float kbv[8], qbv[8];
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const float eb = __builtin_amdgcn_exp2f(g4[e] - gc4[e]);
+        for (int e = 0; e < 8; e++) {
+          const float eb = __builtin_amdgcn_exp2f(g8[e] - gc8[e]);
           kbv[e] = kf[e] * eb;
           qbv[e] = qf[e] * eb;
         }
-        uint2 bh, bl;
-        pf::split4(kbv, bh, bl);
-        *(uint2 *)(KB + (tt * RP + c4) * 2) = bh;
-        *(uint2 *)(KB + (C * RP + tt * RP + c4) * 2) = bl;
-        pf::split4(qbv, bh, bl);
-        *(uint2 *)(QB + (tt * RP + c4) * 2) = bh;
-        *(uint2 *)(QB + (C * RP + tt * RP + c4) * 2) = bl;
+        split8v(kbv, h4, l4);
+        *(uint4 *)(KB + (tt * RP + c8) * 2) = h4;  // over this thread's own raw entries
+        *(uint4 *)(KB + KB_LO + (tt * RP + c8) * 2) = l4;
+        split8v(qbv, h4, l4);
+        *(uint4 *)(QB + (tt * RP + c8) * 2) = h4;
+        *(uint4 *)(QB + KB_LO + (tt * RP + c8) * 2) = l4;
       }
-      const uint32_t hw[2] = {hi.x, hi.y}, lw[2] = {lo.x, lo.y};
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        ((uint16_t *)KD)[(c4 + e) * TP + tt] = (uint16_t)(hw[e >> 1] >> (16 * (e & 1)));
-        ((uint16_t *)KD)[KV * TP + (c4 + e) * TP + tt] = (uint16_t)(lw[e >> 1] >> (16 * (e & 1)));
+      if (tt == 0) {
+        *(float4 *)(EC + c8) = make_float4(__builtin_amdgcn_exp2f(gc8[0]), __builtin_amdgcn_exp2f(gc8[1]),
+                                           __builtin_amdgcn_exp2f(gc8[2]), __builtin_amdgcn_exp2f(gc8[3]));
+        *(float4 *)(EC + c8 + 4) = make_float4(__builtin_amdgcn_exp2f(gc8[4]), __builtin_amdgcn_exp2f(gc8[5]),
+                                               __builtin_amdgcn_exp2f(gc8[6]), __builtin_amdgcn_exp2f(gc8[7]));
       }
-      if (tt == 0) *(float4 *)(EC + c4) = make_float4(__builtin_amdgcn_exp2f(gc4[0]), __builtin_amdgcn_exp2f(gc4[1]),
-                                                      __builtin_amdgcn_exp2f(gc4[2]), __builtin_amdgcn_exp2f(gc4[3]));
     }
     // ---- pairwise path: A and P below the diagonal, pair by pair over 32
-    // channels per lane (four lanes per pair), with the exact pairwise
-    // decays; P's diagonal from q_t . k_t
-    if (!pairwise) {
-    } else if (tid < 4 * NPAIR) {
-      const int p = tid >> 2, part = tid & 3;
-      const int t = pair_t[p], s = pair_s[p];
-      const int cb = 32 * part;
-      float a = 0.f, pp = 0.f;
+    // channels per lane (four lanes per pair) with the exact pairwise decays
+    // from the raw rows; P's diagonal from q_t . k_t
+    if (pairwise) {
+      for (int task = tid; task < 4 * NPAIR + C; task += NT) {
+        if (task < 4 * NPAIR) {
+          const int p = task >> 2, part = task & 3;
+          const int t = pair_t[p], s = pair_s[p];
+          const int cb = 32 * part;
+          float a = 0.f, pp = 0.f;
 #pragma unroll
-      for (int m = 0; m < 4; m++) {
-        const int c = cb + 8 * m;
-        float kt[8], qt[8], ks[8];
-        {
-          const uint4 x = *(const uint4 *)(KR + (t * RP + c) * 2), y = *(const uint4 *)(QR + (t * RP + c) * 2),
-                      z = *(const uint4 *)(KR + (s * RP + c) * 2);
-          bf4(make_uint2(x.x, x.y), kt);
-          bf4(make_uint2(x.z, x.w), kt + 4);
-          bf4(make_uint2(y.x, y.y), qt);
-          bf4(make_uint2(y.z, y.w), qt + 4);
-          bf4(make_uint2(z.x, z.y), ks);
-          bf4(make_uint2(z.z, z.w), ks + 4);
-        }
-        const float4 ga0 = *(const float4 *)(G + t * GP + c), ga1 = *(const float4 *)(G + t * GP + c + 4);
-        const float4 gb0 = *(const float4 *)(G + s * GP + c), gb1 = *(const float4 *)(G + s * GP + c + 4);
-        const float dg[8] = {ga0.x - gb0.x, ga0.y - gb0.y, ga0.z - gb0.z, ga0.w - gb0.w,
-                             ga1.x - gb1.x, ga1.y - gb1.y, ga1.z - gb1.z, ga1.w - gb1.w};
+          for (int m = 0; m < 4; m++) {
+            const int c = cb + 8 * m;
+            float kt[8], qt[8], ks[8];
+            bf8(*(const uint4 *)(KB + (t * RP + c) * 2), kt);
+            bf8(*(const uint4 *)(QB + (t * RP + c) * 2), qt);
+            bf8(*(const uint4 *)(KB + (s * RP + c) * 2), ks);
+            const float4 ga0 = *(const float4 *)(G + t * GP + c), ga1 = *(const float4 *)(G + t * GP + c + 4);
+            const float4 gb0 = *(const float4 *)(G + s * GP + c), gb1 = *(const float4 *)(G + s * GP + c + 4);
+            const float dg[8] = {ga0.x - gb0.x, ga0.y - gb0.y, ga0.z - gb0.z, ga0.w - gb0.w,
+                                 ga1.x - gb1.x, ga1.y - gb1.y, ga1.z - gb1.z, ga1.w - gb1.w};
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-          const float kse = ks[e] * __builtin_amdgcn_exp2f(dg[e]);
-          a = fmaf(kt[e], kse, a);
-          pp = fmaf(qt[e], kse, pp);
-        }
-      }
-      a += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(a), 0xB1, 0xF, 0xF, false));   // lane ^ 1
-      pp += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(pp), 0xB1, 0xF, 0xF, false));
-      a += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(a), 0x4E, 0xF, 0xF, false));   // lane ^ 2
-      pp += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(pp), 0x4E, 0xF, 0xF, false));
-      if (part == 0) {
-        const float nks = sm[SM_NK * C + s];
-        A[t * AP + s] = ((sm[SM_BETA * C + t] * sm[SM_NK * C + t]) * nks) * a;
-        const float pv = (sm[SM_NQ * C + t] * nks) * pp;
-        const __bf16 hi = (__bf16)pv;
-        ((__bf16 *)PM)[t * TP + s] = hi;
-        ((__bf16 *)PM)[C * TP + t * TP + s] = (__bf16)(pv - (float)hi);
-      }
-    } else if (tid < 4 * NPAIR + C) {
-      // P_tt = nq_t nk_t q_t . k_t (no decay), one lane per token
-      const int t = tid - 4 * NPAIR;
-      float d = 0.f;
+            for (int e = 0; e < 8; e++) {
+              const float kse = ks[e] * __builtin_amdgcn_exp2f(dg[e]);
+              a = fmaf(kt[e], kse, a);
+              pp = fmaf(qt[e], kse, pp);
+            }
+          }
+          a += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(a), 0xB1, 0xF, 0xF, false));   // lane ^ 1
+          pp += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(pp), 0xB1, 0xF, 0xF, false));
+          a += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(a), 0x4E, 0xF, 0xF, false));   // lane ^ 2
+          pp += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(pp), 0x4E, 0xF, 0xF, false));
+          if (part == 0) {
+            const float nks = sm[SM_NK * C + s];
+            const float av = ((sm[SM_BETA * C + t] * sm[SM_NK * C + t]) * nks) * a;
+            A[t * AP + s] = av;
+            if (t >= 16 && s < 16) {  // -A10 for the second block's right-hand side
+              const __bf16 hi = (__bf16)(-av);
+              ((__bf16 *)M)[(t - 16) * PP + s] = hi;
+              ((__bf16 *)M)[16 * PP + (t - 16) * PP + s] = (__bf16)(-av - (float)hi);
+            }
+            const float pv = (sm[SM_NQ * C + t] * nks) * pp;
+            const __bf16 hi = (__bf16)pv;
+            ((__bf16 *)PM)[t * PP + s] = hi;
+            ((__bf16 *)PM)[C * PP + t * PP + s] = (__bf16)(pv - (float)hi);
+          }
+        } else {
+          const int t = task - 4 * NPAIR;
+          float d = 0.f;
 #pragma unroll 4
-      for (int c = 0; c < KV; c += 8) {
-        float kt[8], qt[8];
-        const uint4 x = *(const uint4 *)(KR + (t * RP + c) * 2), y = *(const uint4 *)(QR + (t * RP + c) * 2);
-        bf4(make_uint2(x.x, x.y), kt);
-        bf4(make_uint2(x.z, x.w), kt + 4);
-        bf4(make_uint2(y.x, y.y), qt);
-        bf4(make_uint2(y.z, y.w), qt + 4);
+          for (int c = 0; c < KV; c += 8) {
+            float kt[8], qt[8];
+            bf8(*(const uint4 *)(KB + (t * RP + c) * 2), kt);
+            bf8(*(const uint4 *)(QB + (t * RP + c) * 2), qt);
 #pragma unroll
-        for (int e = 0; e < 8; e++) d = fmaf(qt[e], kt[e], d);
+            for (int e = 0; e < 8; e++) d = fmaf(qt[e], kt[e], d);
+          }
+          const float pv = (sm[SM_NQ * C + t] * sm[SM_NK * C + t]) * d;
+          const __bf16 hi = (__bf16)pv;
+          ((__bf16 *)PM)[t * PP + t] = hi;
+          ((__bf16 *)PM)[C * PP + t * PP + t] = (__bf16)(pv - (float)hi);
+        }
       }
-      const float pv = (sm[SM_NQ * C + t] * sm[SM_NK * C + t]) * d;
-      const __bf16 hi = (__bf16)pv;
-      ((__bf16 *)PM)[t * TP + t] = hi;
-      ((__bf16 *)PM)[C * TP + t * TP + t] = (__bf16)(pv - (float)hi);
     }
     pf::lds_barrier();
     if (tid == 0) sm[SM_FLAG * C + par] = 0.0f;  // read by every thread before the barrier above
-    // ---- MFMA path: A (wave 0) and P (wave 1) as 16 x 128 x 16 products of
-    // the growing and the decaying factors, A_ts = beta_t nk_t (k_t e^{G_t -
+    // ---- MFMA path: the three A blocks (waves 0-2) and three P blocks
+    // (waves 3-5) below or on the diagonal as 16 x 128 x 16 products of the
+    // growing and the decaying factors: A_ts = beta_t nk_t (k_t e^{G_t -
     // G_C}) . (nk_s k_s e^{G_C - G_s}) for s < t, P_ts = nq_t (q_t e^{G_t -
     // G_C}) . (nk_s k_s e^{G_C - G_s}) for s <= t (zero above)
-    if (!pairwise && w < 2) {
-      const uint8_t *X = w == 0 ? KB : QB;
+    if (!pairwise && w < 6) {
+      const int blk = w < 3 ? w : w - 3;
+      const int ti = blk == 0 ? 0 : 1, si = blk == 2 ? 1 : 0;
+      const uint8_t *X = w < 3 ? KB : QB;
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kc = 0; kc < 4; kc++) {
-        const int o = (c16 * RP + 32 * kc + 8 * q4) * 2;
-        const bf16x8 xh = pf::ld8(X, o), xl = pf::ld8(X, C * RP * 2 + o);
-        const bf16x8 eh = pf::ld8(KE, o), el = pf::ld8(KE, C * RP * 2 + o);
+        const int ox = ((16 * ti + c16) * RP + 32 * kc + 8 * q4) * 2, oe = ((16 * si + c16) * RP + 32 * kc + 8 * q4) * 2;
+        const bf16x8 xh = pf::ld8(X, ox), xl = pf::ld8(X, KB_LO + ox);
+        const bf16x8 eh = pf::ld8(KE, oe), el = pf::ld8(KE, KB_LO + oe);
         acc = pf::mfma(xh, eh, acc);
         acc = pf::mfma(xh, el, acc);
         acc = pf::mfma(xl, eh, acc);
       }
-      // acc[r]: token t = 4 q4 + r, source s = c16
-      const int s0 = c16;
-      if (w == 0) {
+      // acc[r]: token t = 16 ti + 4 q4 + r, source s = 16 si + c16
+      const int s0 = 16 * si + c16;
+      if (w < 3) {
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-          const int t = 4 * q4 + r;
-          A[t * AP + s0] = s0 < t ? (sm[SM_BETA * C + t] * sm[SM_NK * C + t]) * acc[r] : 0.0f;
+          const int t = 16 * ti + 4 * q4 + r;
+          const float av = s0 < t ? (sm[SM_BETA * C + t] * sm[SM_NK * C + t]) * acc[r] : 0.0f;
+          A[t * AP + s0] = av;
+          if (blk == 1) {
+            const __bf16 hi = (__bf16)(-av);
+            ((__bf16 *)M)[(t - 16) * PP + s0] = hi;
+            ((__bf16 *)M)[16 * PP + (t - 16) * PP + s0] = (__bf16)(-av - (float)hi);
+          }
         }
       } else {
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-          const int t = 4 * q4 + r;
+          const int t = 16 * ti + 4 * q4 + r;
           const float pv = s0 <= t ? sm[SM_NQ * C + t] * acc[r] : 0.0f;
           const __bf16 hi = (__bf16)pv;
-          ((__bf16 *)PM)[t * TP + s0] = hi;
-          ((__bf16 *)PM)[C * TP + t * TP + s0] = (__bf16)(pv - (float)hi);
+          ((__bf16 *)PM)[t * PP + s0] = hi;
+          ((__bf16 *)PM)[C * PP + t * PP + s0] = (__bf16)(pv - (float)hi);
         }
       }
     }
-    // ---- K S0 and Q S0 for this wave's columns
-    // S0 as hi/lo operands, key rows in the permuted slot order of split8
+    // ---- K S0 and Q S0 for this wave's columns, two 16-token tiles
     bf16x8 sh[4], sl[4];
 #pragma unroll
     for (int kc = 0; kc < 4; kc++) pf::split8(S[2 * kc], S[2 * kc + 1], sh[kc], sl[kc]);
-    f32x4 R, oq;
-    {
+    f32x4 R[2], oq[2];
+#pragma unroll
+    for (int tb = 0; tb < 2; tb++) {
       f32x4 ak = {0.f, 0.f, 0.f, 0.f}, aq = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kc = 0; kc < 4; kc++) {
-        const int o = (c16 * RP + 32 * kc + 8 * q4) * 2;
-        const bf16x8 kh = pf::ld8(KG, o), kl = pf::ld8(KG, C * RP * 2 + o);
-        const bf16x8 qh = pf::ld8(QG, o), ql = pf::ld8(QG, C * RP * 2 + o);
+        const int o = ((16 * tb + c16) * RP + 32 * kc + 8 * q4) * 2;
+        const bf16x8 kh = pf::ld8(KG, o), kl = pf::ld8(KG, KB_LO + o);
+        const bf16x8 qh = pf::ld8(QG, o), ql = pf::ld8(QG, KB_LO + o);
         ak = pf::mfma(kh, sh[kc], ak);
         ak = pf::mfma(kh, sl[kc], ak);
         ak = pf::mfma(kl, sh[kc], ak);
@@ -4232,59 +4294,59 @@ __global__ __launch_bounds__(NT) void kda_chunk_kernel(pf::PrefillDev D) {
         aq = pf::mfma(sl[kc], qh, aq);
         aq = pf::mfma(sh[kc], ql, aq);
       }
-      // R_t = beta_t (v_t - (nk k e^G)_t S0), tokens 4 q4 .. 4 q4 + 3, column jw + c16
-      const pf::tr4_t vr = pf::col4(VR, 4 * q4, jw, c16);
-      const float4 be = *(const float4 *)(sm + SM_BETA * C + 4 * q4);
+      // R_t = beta_t (v_t - (nk k e^G)_t S0), tokens 16 tb + 4 q4 .. + 3, column jw + c16
+      const pf::tr4_t vr = pf::col4(VR, 16 * tb + 4 * q4, jw, c16);
+      const float4 be = *(const float4 *)(sm + SM_BETA * C + 16 * tb + 4 * q4);
       const float be4[4] = {be.x, be.y, be.z, be.w};
 #pragma unroll
-      for (int r = 0; r < 4; r++) R[r] = be4[r] * (pf::bf2f((uint16_t)vr[r]) - ak[r]);
-      oq = aq;  // O^T first term: column 4 q4 + r, token c16
+      for (int r = 0; r < 4; r++) R[tb][r] = be4[r] * (pf::bf2f((uint16_t)vr[r]) - ak[r]);
+      oq[tb] = aq;  // O^T first term: column 4 q4 + r, token 16 tb + c16
     }
     pf::lds_barrier();
-    // ---- (I + A) Delta = R; O^T += Delta^T P^T; S <- diag(e^{G_C}) S0 + Kd^T Delta
-    bf16x4 dh4, dl4;
-    {
-      float a[4][C];  // rows 4 q4 .. 4 q4 + 3 of A, all loads issued before the chain
+    // ---- (I + A) Delta = R by blocks: Delta_0 from block 0, then block 1's
+    // right-hand side less A10 Delta_0 (M holds -A10); O^T += Delta^T P^T;
+    // S <- diag(e^{G_C}) S0 + Kd^T Delta over the 32 tokens
+    const f32x4 d0 = block_solve(A, 0, 0, q4, R[0]);
+    bf16x4 d0h, d0l;
+    pf::split4x(d0, d0h, d0l);
+    const f32x4 d1 = block_solve(A, 16, 16, q4, mm16(M, (c16 * PP + 4 * q4) * 2, MLO, d0h, d0l, R[1]));
+    bf16x4 d1h, d1l;
+    pf::split4x(d1, d1h, d1l);
 #pragma unroll
-      for (int r = 0; r < 4; r++)
-#pragma unroll
-        for (int m = 0; m < C / 4; m++) {
-          const float4 x = *(const float4 *)(A + (4 * q4 + r) * AP + 4 * m);
-          a[r][4 * m] = x.x;
-          a[r][4 * m + 1] = x.y;
-          a[r][4 * m + 2] = x.z;
-          a[r][4 * m + 3] = x.w;
-        }
-      float dv[4] = {R[0], R[1], R[2], R[3]};
-      delta_step<0>(dv, a);
-      const f32x4 dl = {dv[0], dv[1], dv[2], dv[3]};
-      pf::split4x(dl, dh4, dl4);
-      const int o = (c16 * TP + 4 * q4) * 2;
-      const bf16x4 ph = pf::ld4(PM, o), plo = pf::ld4(PM, C * TP * 2 + o);
-      f32x4 acc = oq;
-      acc = pf::mfma16(dh4, ph, acc);
-      acc = pf::mfma16(dh4, plo, acc);
-      acc = pf::mfma16(dl4, ph, acc);
-      if (c16 < n) {
+    for (int tb = 0; tb < 2; tb++) {
+      // rows of P for tokens 16 tb + c16: the blocks of source tokens 0-15 and (tb = 1) 16-31
+      const int o = ((16 * tb + c16) * PP + 4 * q4) * 2;
+      f32x4 acc = oq[tb];
+      acc = mm16t(PM, o, PLO, d0h, d0l, acc);
+      if (tb == 1) acc = mm16t(PM, o + 32, PLO, d1h, d1l, acc);
+      const int t = 16 * tb + c16;
+      if (t < n) {
         const float o4[4] = {acc[0], acc[1], acc[2], acc[3]};
-        const int64_t at = ((int64_t)(t0 + c0 + c16) * H + h) * KV + jw + 4 * q4;
+        const int64_t at = ((int64_t)(t0 + c0 + t) * H + h) * KV + jw + 4 * q4;
         store4(D.out, D.out_dtype, at, o4);
       }
     }
+    {
+      bf16x8 eh, el;
+      pf::split8(d0, d1, eh, el);  // the 32 tokens in the permuted slot order (pcol)
 #pragma unroll
-    for (int dt = 0; dt < 8; dt++) {
-      const float4 ec = *(const float4 *)(EC + 16 * dt + 4 * q4);
-      f32x4 acc;
-      acc[0] = S[dt][0] * ec.x;
-      acc[1] = S[dt][1] * ec.y;
-      acc[2] = S[dt][2] * ec.z;
-      acc[3] = S[dt][3] * ec.w;
-      const int o = ((16 * dt + c16) * TP + 4 * q4) * 2;
-      const bf16x4 kh = pf::ld4(KD, o), kl = pf::ld4(KD, KV * TP * 2 + o);
-      acc = pf::mfma16(kh, dh4, acc);
-      acc = pf::mfma16(kh, dl4, acc);
-      acc = pf::mfma16(kl, dh4, acc);
-      S[dt] = acc;
+      for (int dt = 0; dt < 8; dt++) {
+        const float4 ec = *(const float4 *)(EC + 16 * dt + 4 * q4);
+        f32x4 acc;
+        acc[0] = S[dt][0] * ec.x;
+        acc[1] = S[dt][1] * ec.y;
+        acc[2] = S[dt][2] * ec.z;
+        acc[3] = S[dt][3] * ec.w;
+        // Kd rows 16 dt + c16 (channels) over the 32 tokens in the slot order
+        // of split8: transposing loads of tokens 4 q4 .. + 3 and 16 + 4 q4 .. + 3
+        const bf16x8 kh = pf::cat8(pf::col4(KE, 4 * q4, 16 * dt, c16), pf::col4(KE, 16 + 4 * q4, 16 * dt, c16));
+        const bf16x8 kl = pf::cat8(pf::col4(KE + KB_LO, 4 * q4, 16 * dt, c16),
+                                   pf::col4(KE + KB_LO, 16 + 4 * q4, 16 * dt, c16));
+        acc = pf::mfma(kh, eh, acc);
+        acc = pf::mfma(kh, el, acc);
+        acc = pf::mfma(kl, eh, acc);
+        S[dt] = acc;
+      }
     }
     pf::lds_barrier();  // the next chunk's staging overwrites the shared tiles
     c0 = c_next;
