@@ -206,7 +206,7 @@ int sq_writeback(const sq_pool *pool, const sq_writeback_scratch *scratch, int64
  *             counterpart).
  * Pools with K = V = 128, packed or byte storage.  GDN: the chunked kernel
  * (chunks of 64 tokens, bf16 MFMA).  KDA: a chunked kernel with per-channel
- * decays (chunks of 16 tokens, bf16 MFMA; in-chunk decays formed pairwise
+ * decays (chunks of 32 tokens, bf16 MFMA; in-chunk decays formed pairwise
  * when a chunk's decay exceeds 2^96 on some channel).
  */
 typedef struct sq_prefill_args {

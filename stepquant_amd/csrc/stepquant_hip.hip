@@ -3809,8 +3809,8 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
 
 
 // =====================================================================
-// Chunked KDA prefill (per-channel decay), K = V = 128, chunks of 16
-// tokens, bf16 MFMA with fp32 accumulation.  The recurrence of
+// Chunked KDA prefill (per-channel decay), K = V = 128, chunks of 32
+// tokens solved as two blocks of 16, bf16 MFMA with fp32 accumulation.  The recurrence of
 // stepquant/core.py:5-15 with the KDA log decay g_t in R^K (the role of the
 // upstream chunk kernel behind the reference's kernel_extend,
 // sglang/runtime.py:193-202, for Kimi-Linear pools).
@@ -3825,7 +3825,8 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
 // (q, k L2-normalised and q scaled: the norms multiply into the products).
 // Every decay factor above has a non-positive exponent except inside A and
 // P, where e^{G_tc - G_sc} = e^{G_tc - G_Cc} e^{G_Cc - G_sc} (G_C: the last
-// token) makes both 16 x 128 x 16 products MFMA products.  The first factor
+// token) makes A and P MFMA products (each three 16 x 128 x 16 blocks on or
+// below the diagonal).  The first factor
 // grows to e^{G_0c - G_Cc}, the chunk's decay; when that exceeds 2^96 for
 // any channel the chunk forms A and P pair by pair and channel by channel
 // instead (sub, exp2, no factor that could overflow), so any gate is
@@ -3833,11 +3834,13 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
 // every fp32 operand split into hi + lo bf16 (hi*hi + hi*lo + lo*hi, ~2^-16
 // relative): K S0 and Q S0 as 16 x 16 x 32 products (S0 in the permuted
 // k-slot order of pf::split8), Delta^T P^T and the state update as
-// 16 x 16 x 16 products whose B operands are accumulator tiles as they are.
-// Delta solves (I + A) Delta = R by forward substitution in each wave's
-// registers (fp32, tokens in ascending order; the solved token's row reaches
-// the other lane rows by v_permlane16/32_swap), so no wave waits on another
-// for an inverse.  One workgroup of 8 waves per (sequence, head); wave w owns
+// 16 x 16 x 16 products whose B operands are accumulator tiles as they are
+// (the update's k operand read from the token-major tile by transposing LDS
+// loads).  Delta solves (I + A) Delta = R block by block by forward
+// substitution in each wave's registers (fp32, tokens in ascending order; the
+// solved token's row reaches the other lane rows by v_permlane16/32_swap;
+// block 1's right-hand side less A10 Delta_0 as one MFMA product), so no
+// wave waits on another for an inverse.  One workgroup of 8 waves per (sequence, head); wave w owns
 // state columns 16 w .. 16 w + 15 for all 128 rows in registers
 // (accumulator layout).
 // =====================================================================
