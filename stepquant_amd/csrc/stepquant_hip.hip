@@ -3633,16 +3633,25 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
       bf16x8 sh[4], sl[4];
 #pragma unroll
       for (int kc = 0; kc < 4; kc++) split8(S[2 * kc], S[2 * kc + 1], sh[kc], sl[kc]);
+      // key-slot blocks outermost: the four token tiles' accumulators are
+      // independent, so each block's loads are in flight while the previous
+      // block's products run
       auto ks_part = [&]() {
+        f32x4 ak[4];
+#pragma unroll
+        for (int tt = 0; tt < 4; tt++) ak[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kc = 0; kc < 4; kc++) {
+          bf16x8 kr[4];
+#pragma unroll
+          for (int tt = 0; tt < 4; tt++) kr[tt] = ld8(Kc, ((16 * tt + c16) * P136 + 32 * kc + 8 * q4) * 2);
+#pragma unroll
+          for (int tt = 0; tt < 4; tt++) ak[tt] = mfma(kr[tt], sh[kc], ak[tt]);
+#pragma unroll
+          for (int tt = 0; tt < 4; tt++) ak[tt] = mfma(kr[tt], sl[kc], ak[tt]);
+        }
 #pragma unroll
         for (int tt = 0; tt < 4; tt++) {
-          f32x4 ak = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int kc = 0; kc < 4; kc++) {
-            const bf16x8 kr = ld8(Kc, ((16 * tt + c16) * P136 + 32 * kc + 8 * q4) * 2);
-            ak = mfma(kr, sh[kc], ak);
-            ak = mfma(kr, sl[kc], ak);
-          }
           const int ta = 16 * tt + 4 * q4;
           const float4 be = *(const float4 *)(sm + SM_BETA * 64 + ta), gk = *(const float4 *)(sm + SM_GK * 64 + ta);
           const float be4[4] = {be.x, be.y, be.z, be.w}, gk4[4] = {gk.x, gk.y, gk.z, gk.w};
@@ -3650,22 +3659,28 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
           const float v4[4] = {bf2f((uint16_t)vr[0]), bf2f((uint16_t)vr[1]), bf2f((uint16_t)vr[2]),
                                bf2f((uint16_t)vr[3])};
 #pragma unroll
-          for (int r = 0; r < 4; r++) R[tt][r] = be4[r] * (v4[r] - gk4[r] * ak[r]);
+          for (int r = 0; r < 4; r++) R[tt][r] = be4[r] * (v4[r] - gk4[r] * ak[tt][r]);
         }
       };
       auto qs_part = [&]() {
+        f32x4 aq[4];
+#pragma unroll
+        for (int tt = 0; tt < 4; tt++) aq[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kc = 0; kc < 4; kc++) {
+          bf16x8 qr[4];
+#pragma unroll
+          for (int tt = 0; tt < 4; tt++) qr[tt] = ld8(Qc, ((16 * tt + c16) * P136 + 32 * kc + 8 * q4) * 2);
+#pragma unroll
+          for (int tt = 0; tt < 4; tt++) aq[tt] = mfma(sh[kc], qr[tt], aq[tt]);
+#pragma unroll
+          for (int tt = 0; tt < 4; tt++) aq[tt] = mfma(sl[kc], qr[tt], aq[tt]);
+        }
 #pragma unroll
         for (int tt = 0; tt < 4; tt++) {
-          f32x4 aq = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int kc = 0; kc < 4; kc++) {
-            const bf16x8 qr = ld8(Qc, ((16 * tt + c16) * P136 + 32 * kc + 8 * q4) * 2);
-            aq = mfma(sh[kc], qr, aq);
-            aq = mfma(sl[kc], qr, aq);
-          }
           const float qgt = sm[SM_QG * 64 + 16 * tt + c16];
 #pragma unroll
-          for (int r = 0; r < 4; r++) oq[tt][r] = aq[r] * qgt;
+          for (int r = 0; r < 4; r++) oq[tt][r] = aq[tt][r] * qgt;
         }
       };
       // waves 0-3: diagonal tile i = w and its T_ii; waves 4-7: the six
@@ -3741,21 +3756,33 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
     // ---- O^T = diag(nq Gamma) (S0^T Q^T) + Delta^T P^T: rows j of this wave,
     // column t; a split pair [D_2kc; D_2kc+1] is the A operand of its
     // transpose as it is, and token pairs past the tile are causal zeros
+    // (the six tile pairs' loads first, then their products interleaved
+    // across the four independent token tiles)
     {
+      bf16x8 ph[6], pl[6];
+#pragma unroll
+      for (int e = 0; e < 6; e++) {
+        const int tt = e < 2 ? e : 2 + ((e - 2) >> 1), kc = e < 2 ? 0 : (e - 2) & 1;
+        const int o = ((16 * tt + c16) * P72 + 32 * kc + 8 * q4) * 2;
+        ph[e] = ld8(Pl, o);
+        pl[e] = ld8(Pl, PC * P72 * 2 + o);
+      }
+      f32x4 acc[4] = {oq[0], oq[1], oq[2], oq[3]};
+#pragma unroll
+      for (int pass = 0; pass < 3; pass++)
+#pragma unroll
+        for (int kc = 0; kc < 2; kc++)
+#pragma unroll
+          for (int tt = 2 * kc; tt < 4; tt++) {
+            const int e = tt < 2 ? tt : 2 + 2 * (tt - 2) + kc;
+            const bf16x8 x = pass < 2 ? (kc ? ph23 : ph01) : (kc ? pl23 : pl01);
+            acc[tt] = mfma(x, pass == 1 ? pl[e] : ph[e], acc[tt]);
+          }
 #pragma unroll
       for (int tt = 0; tt < 4; tt++) {
         const int t = 16 * tt + c16;
-        f32x4 acc = oq[tt];
-#pragma unroll
-        for (int kc = 0; kc <= (tt >> 1); kc++) {
-          const int o = (t * P72 + 32 * kc + 8 * q4) * 2;
-          const bf16x8 ph = ld8(Pl, o), pl = ld8(Pl, PC * P72 * 2 + o);
-          acc = mfma(kc ? ph23 : ph01, ph, acc);
-          acc = mfma(kc ? ph23 : ph01, pl, acc);
-          acc = mfma(kc ? pl23 : pl01, ph, acc);
-        }
         if (t < n) {
-          const float o4[4] = {acc[0], acc[1], acc[2], acc[3]};
+          const float o4[4] = {acc[tt][0], acc[tt][1], acc[tt][2], acc[tt][3]};
           // the chunk's first output row as a wave-uniform index, the token
           // and column within it as a 32-bit offset
           const int64_t ob = (tb * H + h) * PV + jw;
@@ -3772,19 +3799,26 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
       split8(dp[0], dp[1], eh[0], el[0]);
       split8(dp[2], dp[3], eh[1], el[1]);
       const float gC = __expf(sm[SM_LC * 64 + 63]);
+      // four row tiles at a time: their eight loads first, then the
+      // products interleaved across the four independent accumulators
 #pragma unroll
-      for (int dt = 0; dt < 8; dt++) {
-        const int d = 16 * dt + c16;
-        f32x4 acc;
+      for (int d4 = 0; d4 < 8; d4 += 4) {
+        bf16x8 a[4][2];
 #pragma unroll
-        for (int r = 0; r < 4; r++) acc[r] = S[dt][r] * gC;
+        for (int dt = d4; dt < d4 + 4; dt++) {
+          const int d = 16 * dt + c16;
+#pragma unroll
+          for (int kc = 0; kc < 2; kc++) a[dt - d4][kc] = ld8(Kt, (d * P72 + tcol(d, 32 * kc + 8 * q4)) * 2);
+#pragma unroll
+          for (int r = 0; r < 4; r++) S[dt][r] = S[dt][r] * gC;
+        }
 #pragma unroll
         for (int kc = 0; kc < 2; kc++) {
-          const bf16x8 a = ld8(Kt, (d * P72 + tcol(d, 32 * kc + 8 * q4)) * 2);
-          acc = mfma(a, eh[kc], acc);
-          acc = mfma(a, el[kc], acc);
+#pragma unroll
+          for (int dt = d4; dt < d4 + 4; dt++) S[dt] = mfma(a[dt - d4][kc], eh[kc], S[dt]);
+#pragma unroll
+          for (int dt = d4; dt < d4 + 4; dt++) S[dt] = mfma(a[dt - d4][kc], el[kc], S[dt]);
         }
-        S[dt] = acc;
       }
     }
     lds_barrier();  // the next chunk's staging overwrites the shared tiles
