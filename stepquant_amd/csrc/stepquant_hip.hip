@@ -4316,28 +4316,47 @@ __global__ __launch_bounds__(NT) void kda_chunk_kernel(pf::PrefillDev D) {
 #pragma unroll
     for (int kc = 0; kc < 4; kc++) pf::split8(S[2 * kc], S[2 * kc + 1], sh[kc], sl[kc]);
     f32x4 R[2], oq[2];
+    // key-slot blocks outermost: the four accumulators (k and q, two token
+    // tiles) are independent, and each product pass runs over all four
+    f32x4 ak[2], aq[2];
+#pragma unroll
+    for (int tb = 0; tb < 2; tb++) ak[tb] = aq[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kc = 0; kc < 4; kc++) {
+      bf16x8 kh[2], kl[2], qh[2], ql[2];
+#pragma unroll
+      for (int tb = 0; tb < 2; tb++) {
+        const int o = ((16 * tb + c16) * RP + 32 * kc + 8 * q4) * 2;
+        kh[tb] = pf::ld8(KG, o);
+        kl[tb] = pf::ld8(KG, KB_LO + o);
+        qh[tb] = pf::ld8(QG, o);
+        ql[tb] = pf::ld8(QG, KB_LO + o);
+      }
+#pragma unroll
+      for (int tb = 0; tb < 2; tb++) {
+        ak[tb] = pf::mfma(kh[tb], sh[kc], ak[tb]);
+        aq[tb] = pf::mfma(sh[kc], qh[tb], aq[tb]);
+      }
+#pragma unroll
+      for (int tb = 0; tb < 2; tb++) {
+        ak[tb] = pf::mfma(kh[tb], sl[kc], ak[tb]);
+        aq[tb] = pf::mfma(sl[kc], qh[tb], aq[tb]);
+      }
+#pragma unroll
+      for (int tb = 0; tb < 2; tb++) {
+        ak[tb] = pf::mfma(kl[tb], sh[kc], ak[tb]);
+        aq[tb] = pf::mfma(sh[kc], ql[tb], aq[tb]);
+      }
+    }
 #pragma unroll
     for (int tb = 0; tb < 2; tb++) {
-      f32x4 ak = {0.f, 0.f, 0.f, 0.f}, aq = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kc = 0; kc < 4; kc++) {
-        const int o = ((16 * tb + c16) * RP + 32 * kc + 8 * q4) * 2;
-        const bf16x8 kh = pf::ld8(KG, o), kl = pf::ld8(KG, KB_LO + o);
-        const bf16x8 qh = pf::ld8(QG, o), ql = pf::ld8(QG, KB_LO + o);
-        ak = pf::mfma(kh, sh[kc], ak);
-        ak = pf::mfma(kh, sl[kc], ak);
-        ak = pf::mfma(kl, sh[kc], ak);
-        aq = pf::mfma(sh[kc], qh, aq);
-        aq = pf::mfma(sl[kc], qh, aq);
-        aq = pf::mfma(sh[kc], ql, aq);
-      }
       // R_t = beta_t (v_t - (nk k e^G)_t S0), tokens 16 tb + 4 q4 .. + 3, column jw + c16
       const pf::tr4_t vr = pf::col4(VR, 16 * tb + 4 * q4, jw, c16);
       const float4 be = *(const float4 *)(sm + SM_BETA * C + 16 * tb + 4 * q4);
       const float be4[4] = {be.x, be.y, be.z, be.w};
 #pragma unroll
-      for (int r = 0; r < 4; r++) R[tb][r] = be4[r] * (pf::bf2f((uint16_t)vr[r]) - ak[r]);
-      oq[tb] = aq;  // O^T first term: column 4 q4 + r, token 16 tb + c16
+      for (int r = 0; r < 4; r++) R[tb][r] = be4[r] * (pf::bf2f((uint16_t)vr[r]) - ak[tb][r]);
+      oq[tb] = aq[tb];  // O^T first term: column 4 q4 + r, token 16 tb + c16
     }
     pf::lds_barrier();
     // ---- (I + A) Delta = R by blocks: Delta_0 from block 0, then block 1's
@@ -4366,23 +4385,30 @@ __global__ __launch_bounds__(NT) void kda_chunk_kernel(pf::PrefillDev D) {
     {
       bf16x8 eh, el;
       pf::split8(d0, d1, eh, el);  // the 32 tokens in the permuted slot order (pcol)
+      // four row tiles at a time: their loads first, then each product pass
+      // over the four independent accumulators
 #pragma unroll
-      for (int dt = 0; dt < 8; dt++) {
-        const float4 ec = *(const float4 *)(EC + 16 * dt + 4 * q4);
-        f32x4 acc;
-        acc[0] = S[dt][0] * ec.x;
-        acc[1] = S[dt][1] * ec.y;
-        acc[2] = S[dt][2] * ec.z;
-        acc[3] = S[dt][3] * ec.w;
-        // Kd rows 16 dt + c16 (channels) over the 32 tokens in the slot order
-        // of split8: transposing loads of tokens 4 q4 .. + 3 and 16 + 4 q4 .. + 3
-        const bf16x8 kh = pf::cat8(pf::col4(KE, 4 * q4, 16 * dt, c16), pf::col4(KE, 16 + 4 * q4, 16 * dt, c16));
-        const bf16x8 kl = pf::cat8(pf::col4(KE + KB_LO, 4 * q4, 16 * dt, c16),
-                                   pf::col4(KE + KB_LO, 16 + 4 * q4, 16 * dt, c16));
-        acc = pf::mfma(kh, eh, acc);
-        acc = pf::mfma(kh, el, acc);
-        acc = pf::mfma(kl, eh, acc);
-        S[dt] = acc;
+      for (int d4 = 0; d4 < 8; d4 += 4) {
+        bf16x8 kh[4], kl[4];
+#pragma unroll
+        for (int dt = d4; dt < d4 + 4; dt++) {
+          // Kd rows 16 dt + c16 (channels) over the 32 tokens in the slot order
+          // of split8: transposing loads of tokens 4 q4 .. + 3 and 16 + 4 q4 .. + 3
+          kh[dt - d4] = pf::cat8(pf::col4(KE, 4 * q4, 16 * dt, c16), pf::col4(KE, 16 + 4 * q4, 16 * dt, c16));
+          kl[dt - d4] = pf::cat8(pf::col4(KE + KB_LO, 4 * q4, 16 * dt, c16),
+                                 pf::col4(KE + KB_LO, 16 + 4 * q4, 16 * dt, c16));
+          const float4 ec = *(const float4 *)(EC + 16 * dt + 4 * q4);
+          S[dt][0] = S[dt][0] * ec.x;
+          S[dt][1] = S[dt][1] * ec.y;
+          S[dt][2] = S[dt][2] * ec.z;
+          S[dt][3] = S[dt][3] * ec.w;
+        }
+#pragma unroll
+        for (int dt = d4; dt < d4 + 4; dt++) S[dt] = pf::mfma(kh[dt - d4], eh, S[dt]);
+#pragma unroll
+        for (int dt = d4; dt < d4 + 4; dt++) S[dt] = pf::mfma(kh[dt - d4], el, S[dt]);
+#pragma unroll
+        for (int dt = d4; dt < d4 + 4; dt++) S[dt] = pf::mfma(kl[dt - d4], eh, S[dt]);
       }
     }
     pf::lds_barrier();  // the next chunk's staging overwrites the shared tiles
