@@ -625,6 +625,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void e
   int *orel = bl + K;                      // [K] row offsets within the code region
   float *cmax = (float *)(orel + K);       // [4 parts][4 widths][V]
   float *bsum = cmax + 16 * V;             // [K/16][2][V]
+  // per row: qmax, 1 / norm, r norm, w^2 (0 for pivots) | width, L, row offset, width class
+  float4 *rowc = (float4 *)(bsum + (K / 16) * 2 * V);
+  int4 *rowi = (int4 *)(rowc + K);
   uint32_t lo_bits = 0xffffffffu, hi_bits = 0u;  // min of |x| bits - 1 (zeros wrap), max of |x| bits
   // ---- row phase: r = fp16(sqrt(max(mean|x|, 1e-20) / w)) in PyTorch's
   // summation order (as encode_fast128); pivot rows as halves
@@ -687,6 +690,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void e
       total += row_shl<8>(up);
       total += row_shl<12>(up);
       if (lane == 0) {
+        float r = 1.0f;
         if (bi[p] == 16) {
           rsc[i] = 1.0f;
           rinv[i] = 1.0f;
@@ -694,7 +698,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void e
           float m = total / (float)V;
           m = m < 1e-20f ? 1e-20f : m;
           uint32_t hb;
-          const float r = fp16_scale(__builtin_sqrtf(m / wi[p]), &hb);
+          r = fp16_scale(__builtin_sqrtf(m / wi[p]), &hb);
           rsc[i] = r;
           rinv[i] = 1.0f / r;
           put_page_half(page, ro[p], hb);
@@ -702,6 +706,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void e
         wl[i] = wi[p];
         bl[i] = bi[p];
         orel[i] = off_rel;
+        // the column phase's per-row factors, formed as it would form them
+        const int bc = bi[p] < 8 ? bi[p] : 8;
+        const float norm = (float)(1 << (8 - bc));
+        rowc[i] = make_float4((float)((1 << (bc - 1)) - 1), 1.0f / norm, r * norm,
+                              (wi[p] * wi[p]) * (bi[p] != 16 ? 1.0f : 0.0f));
+        rowi[i] = make_int4(bi[p], (1 << (bc - 1)) - 1, off_rel, bc / 2 - 1);
       }
     }
   }
@@ -711,14 +721,20 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void e
 #pragma unroll
   for (int r = 0; r < 32; r++) xs[r] = X[(i0 + r) * V + j];
   const bool ieee = __syncthreads_or(lo_bits < 0x19800000u - 1u || hi_bits > 0x5d800000u);
+  // Every lane of a wave works on the same row at a time (rows i0 + r, i0
+  // wave-uniform), so a row's factors are read into scalar registers: the
+  // width-dependent choices become scalar branches and the per-value work
+  // is the arithmetic alone.
+  auto ufl = [](float x) { return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, x))); };
   auto columns = [&](auto fast_tag) {
     constexpr bool FAST = decltype(fast_tag)::value;
     float amax[4] = {0.f, 0.f, 0.f, 0.f};  // widths 2, 4, 6, 8
 #pragma unroll
     for (int r = 0; r < 32; r++) {
+      if (r % 8 == 0) __builtin_amdgcn_sched_barrier(0);  // row factors loaded 8 rows at a time
       const int i = i0 + r;
-      sc[r] = FAST ? div_half(xs[r], rsc[i], rinv[i]) : xs[r] / rsc[i];
-      const int w = bl[i];
+      sc[r] = FAST ? div_half(xs[r], ufl(rsc[i]), ufl(rinv[i])) : xs[r] / ufl(rsc[i]);
+      const int w = __builtin_amdgcn_readfirstlane(rowi[i].x);
       if (w == 16) continue;
       const float a = fabsf(sc[r]);
       const int wsel = (w < 8 ? w : 8) / 2 - 1;
@@ -746,13 +762,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void e
     }
     const float c0 = fp16_scale(mx, nullptr);
     const float c0inv = 1.0f / c0;
-    auto zq = [&](int r, float cdiv, float cinv) -> float {
-      const int w = bl[i0 + r];
-      const int bc = w < 8 ? w : 8;
-      const float qmax = (float)((1 << (bc - 1)) - 1);
-      const float norm = (float)(1 << (8 - bc));
-      float y = FAST ? div_half(sc[r], cdiv, cinv) : sc[r] / cdiv;
-      y = y * (1.0f / norm);  // exact: norm is a power of two
+    // level of a scaled value in a row of quantisation range qmax (1 / norm: the row's power of two)
+    auto zq = [&](float s, float cdiv, float cinv, float qmax, float inv_norm) -> float {
+      float y = FAST ? div_half(s, cdiv, cinv) : s / cdiv;
+      y = y * inv_norm;  // exact: norm is a power of two
       float z = __builtin_rintf(y);
       z = z > -qmax ? z : -qmax;
       z = z < qmax ? z : qmax;
@@ -764,12 +777,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void e
 #pragma unroll
       for (int rr = 0; rr < 16; rr++) {
         const int r = 16 * mb + rr, i = i0 + r;
-        const int w = bl[i];
-        const int bc = w < 8 ? w : 8;
-        const float norm = (float)(1 << (8 - bc));
-        const float wsq = (wl[i] * wl[i]) * (w != 16 ? 1.0f : 0.0f);
-        const float z = zq(r, c0, c0inv);
-        const float v = (rsc[i] * norm) * z;
+        if (rr % 8 == 0) __builtin_amdgcn_sched_barrier(0);
+        const float wsq = ufl(rowc[i].w);
+        const float z = zq(sc[r], c0, c0inv, ufl(rowc[i].x), ufl(rowc[i].y));
+        const float v = ufl(rowc[i].z) * z;
         bn += (wsq * v) * xs[r];
         bd += wsq * (v * v);
       }
@@ -793,17 +804,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void e
     // final codes; quads of lanes assemble each row's 4-value tile
 #pragma unroll
     for (int r = 0; r < 32; r++) {
+      if (r % 8 == 0) __builtin_amdgcn_sched_barrier(0);
       const int i = i0 + r;
-      const int w = bl[i];
-      uint32_t code = 0;
-      if (w != 16) {
-        const int bc = w < 8 ? w : 8;
-        code = (uint32_t)((int)zq(r, c, cinv) + ((1 << (bc - 1)) - 1));
-      }
+      const int w = __builtin_amdgcn_readfirstlane(rowi[i].x);
+      if (w == 16) continue;
+      const uint32_t code = (uint32_t)((int)zq(sc[r], c, cinv, ufl(rowc[i].x), ufl(rowc[i].y)) +
+                                       __builtin_amdgcn_readfirstlane(rowi[i].y));
       const uint32_t c1 = quad_perm<0xB1>(code), c2 = quad_perm<0x4E>(code), c3 = quad_perm<0x1B>(code);
-      if (w != 16 && (tid & 3) == 0) {
+      if ((tid & 3) == 0) {
         const uint32_t word = code | (c1 << w) | (c2 << (2 * w)) | (c3 << (3 * w));
-        lds_put_bytes(stage, shift + group_pos(orel[i], stride, 4, j, w), word, w / 2);
+        lds_put_bytes(stage, shift + group_pos(__builtin_amdgcn_readfirstlane(rowi[i].z), stride, 4, j, w), word, w / 2);
       }
     }
   };
@@ -5192,8 +5202,9 @@ int sq_encode(const sq_pool *pool, const float *state, const void *slots, int32_
   size_t lds = (size_t)stage_bytes(pool) + (size_t)((K * NG + 3) & ~3) * 4 + 16;
   if (split > 1) lds += (size_t)split * 4 * V * 4 + (size_t)(K / 16) * 2 * V * 4;
   if (pool->kda && pool->storage == 0 && K == 128 && V == 128) {
-    // rows, 1 / rows, w, widths, row offsets [K] | column maxima [4][4][V] | block sums [K/16][2][V]
-    const size_t fl = (size_t)stage_bytes(pool) + (size_t)(5 * K + 16 * V + (K / 16) * 2 * V) * 4;
+    // rows, 1 / rows, w, widths, row offsets [K] | column maxima [4][4][V] | block sums [K/16][2][V] |
+    // per-row factors [K] float4 + int4
+    const size_t fl = (size_t)stage_bytes(pool) + (size_t)(5 * K + 16 * V + (K / 16) * 2 * V + 8 * K) * 4;
     hipLaunchKernelGGL(encode_kda128_kernel, dim3((unsigned)(batch * pool->heads)), dim3(512), fl,
                        (hipStream_t)stream, pd, state, slots, slots_dtype);
     return check_launch("encode_kda128_kernel");
