@@ -406,19 +406,22 @@ __device__ __forceinline__ void encode_fast128(const PoolDev &P, const float *__
   // so the quotients stay within [2^-92, 2^108]).  Tiles with a value
   // outside (or a NaN or infinity) divide with IEEE division.
   uint32_t lo_bits = 0xffffffffu, hi_bits = 0u;  // min of |x| bits - 1 (zeros wrap), max of |x| bits
-  // ---- row phase
+  // ---- row phase.  Each 32-lane half takes rows rw + 16 p; its row sums
+  // (in PyTorch's order) land in lane 0 and go through LDS to lane p NG + g,
+  // so the scale arithmetic of the half's 8 NG (row, group) pairs runs once,
+  // side by side, instead of once per pair on lane 0.
   {
     const int lane = tid & 31, l = lane >> 2, k = lane & 3, rw = tid >> 5;
-    float v[8][4], wi[8];
-    int ro[8], of[8];
+    float v[8][4];
+    // lane e < 8 NG: the inputs of pair (p, g) = (e / NG, e % NG)
+    const int pe = lane / NG, ge = lane % NG, ie = rw + 16 * (pe & 7);
+    const float wie = P.impact[(int64_t)h * K + ie];
+    const int roe = P.rows[(int64_t)h * K + ie], ofe = P.offsets[(int64_t)h * K + ie];
 #pragma unroll
     for (int p = 0; p < 8; p++) {
       const int i = rw + 16 * p;
 #pragma unroll
       for (int u = 0; u < 4; u++) v[p][u] = X[i * V + 32 * u + 8 * k + l];
-      wi[p] = P.impact[(int64_t)h * K + i];
-      ro[p] = P.rows[(int64_t)h * K + i];
-      of[p] = P.offsets[(int64_t)h * K + i];
     }
 #pragma unroll
     for (int p = 0; p < 8; p++)
@@ -428,9 +431,9 @@ __device__ __forceinline__ void encode_fast128(const PoolDev &P, const float *__
         lo_bits = min(lo_bits, a - 1u);
         hi_bits = max(hi_bits, a);
       }
+    float *tot = cmax + 32 * rw;  // the half's row sums (cmax is free until the column phase)
 #pragma unroll
     for (int p = 0; p < 8; p++) {
-      const int i = rw + 16 * p;
 #pragma unroll
       for (int g = 0; g < 4; g++) {
         if (g >= NG) break;
@@ -459,19 +462,22 @@ __device__ __forceinline__ void encode_fast128(const PoolDev &P, const float *__
         total += row_shl<4>(up);
         total += row_shl<8>(up);
         total += row_shl<12>(up);
-        if (lane == 0) {
-          float m = total / (float)ngrp;
-          m = m < 1e-20f ? 1e-20f : m;
-          uint32_t hb;
-          const float r = fp16_scale(__builtin_sqrtf(m / wi[p]), &hb);
-          rsc[i * NG + g] = r;
-          rinv[i * NG + g] = 1.0f / r;
-          put_page_half(page, ro[p] + 2 * g, hb);
-        }
+        if (lane == 0) tot[p * NG + g] = total;
       }
-      if (lane == 0) {
-        wl[i] = wi[p];
-        orel[i] = of[p] - code_start;
+    }
+    // (the LDS accesses of one wave complete in order: lane e reads what lane 0 wrote)
+    if (lane < 8 * NG) {
+      const int i = ie, g = ge;
+      float m = tot[lane] / (float)ngrp;
+      m = m < 1e-20f ? 1e-20f : m;
+      uint32_t hb;
+      const float r = fp16_scale(__builtin_sqrtf(m / wie), &hb);
+      rsc[i * NG + g] = r;
+      rinv[i * NG + g] = 1.0f / r;
+      put_page_half(page, roe + 2 * g, hb);
+      if (g == 0) {
+        wl[i] = wie;
+        orel[i] = ofe - code_start;
       }
     }
   }
@@ -630,18 +636,21 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void e
   int4 *rowi = (int4 *)(rowc + K);
   uint32_t lo_bits = 0xffffffffu, hi_bits = 0u;  // min of |x| bits - 1 (zeros wrap), max of |x| bits
   // ---- row phase: r = fp16(sqrt(max(mean|x|, 1e-20) / w)) in PyTorch's
-  // summation order (as encode_fast128); pivot rows as halves
+  // summation order (as encode_fast128); pivot rows as halves.  Each 32-lane
+  // half takes rows rw + 16 p; lane 0's row sums reach lane p through LDS,
+  // and the scale arithmetic of the half's 8 rows runs side by side.
   {
     const int lane = tid & 31, l = lane >> 2, k = lane & 3, rw = tid >> 5;
-    float v[8][4], wi[8];
-    int ro[8], of[8], bi[8];
+    float v[8][4];
+    int of[8], bi[8];
+    const int ie = rw + 16 * (lane & 7);  // lane p < 8: row rw + 16 p
+    const float wie = P.impact[(int64_t)h * K + ie];
+    const int roe = P.rows[(int64_t)h * K + ie];
 #pragma unroll
     for (int p = 0; p < 8; p++) {
       const int i = rw + 16 * p;
 #pragma unroll
       for (int u = 0; u < 4; u++) v[p][u] = X[i * V + 32 * u + 8 * k + l];
-      wi[p] = P.impact[(int64_t)h * K + i];
-      ro[p] = P.rows[(int64_t)h * K + i];
       of[p] = P.offsets[(int64_t)h * K + i];
       bi[p] = P.bits[(int64_t)h * K + i];
     }
@@ -657,9 +666,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void e
         lo_bits = min(lo_bits, a - 1u);
         hi_bits = max(hi_bits, a);
       }
+    float *tot = cmax + 8 * rw;  // the half's row sums (cmax is free until the column phase)
 #pragma unroll
     for (int p = 0; p < 8; p++) {
-      const int i = rw + 16 * p;
       const int off_rel = of[p] - code_start;
       if (bi[p] == 16) {
 #pragma unroll
@@ -689,30 +698,33 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void e
       total += row_shl<4>(up);
       total += row_shl<8>(up);
       total += row_shl<12>(up);
-      if (lane == 0) {
-        float r = 1.0f;
-        if (bi[p] == 16) {
-          rsc[i] = 1.0f;
-          rinv[i] = 1.0f;
-        } else {
-          float m = total / (float)V;
-          m = m < 1e-20f ? 1e-20f : m;
-          uint32_t hb;
-          r = fp16_scale(__builtin_sqrtf(m / wi[p]), &hb);
-          rsc[i] = r;
-          rinv[i] = 1.0f / r;
-          put_page_half(page, ro[p], hb);
-        }
-        wl[i] = wi[p];
-        bl[i] = bi[p];
-        orel[i] = off_rel;
-        // the column phase's per-row factors, formed as it would form them
-        const int bc = bi[p] < 8 ? bi[p] : 8;
-        const float norm = (float)(1 << (8 - bc));
-        rowc[i] = make_float4((float)((1 << (bc - 1)) - 1), 1.0f / norm, r * norm,
-                              (wi[p] * wi[p]) * (bi[p] != 16 ? 1.0f : 0.0f));
-        rowi[i] = make_int4(bi[p], (1 << (bc - 1)) - 1, off_rel, bc / 2 - 1);
+      if (lane == 0) tot[p] = total;
+    }
+    // (the LDS accesses of one wave complete in order: lane p reads what lane 0 wrote)
+    if (lane < 8) {
+      const int i = ie, bw = P.bits[(int64_t)h * K + i];
+      const int off_rel = P.offsets[(int64_t)h * K + i] - code_start;
+      float r = 1.0f;
+      if (bw == 16) {
+        rsc[i] = 1.0f;
+        rinv[i] = 1.0f;
+      } else {
+        float m = tot[lane] / (float)V;
+        m = m < 1e-20f ? 1e-20f : m;
+        uint32_t hb;
+        r = fp16_scale(__builtin_sqrtf(m / wie), &hb);
+        rsc[i] = r;
+        rinv[i] = 1.0f / r;
+        put_page_half(page, roe, hb);
       }
+      wl[i] = wie;
+      bl[i] = bw;
+      orel[i] = off_rel;
+      // the column phase's per-row factors, formed as it would form them
+      const int bc = bw < 8 ? bw : 8;
+      const float norm = (float)(1 << (8 - bc));
+      rowc[i] = make_float4((float)((1 << (bc - 1)) - 1), 1.0f / norm, r * norm, (wie * wie) * (bw != 16 ? 1.0f : 0.0f));
+      rowi[i] = make_int4(bw, (1 << (bc - 1)) - 1, off_rel, bc / 2 - 1);
     }
   }
   // ---- column phase: this thread's 32 values of column j (rows 32 hf ..)
