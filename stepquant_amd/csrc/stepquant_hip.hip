@@ -3003,6 +3003,57 @@ __device__ __forceinline__ void body(const PoolDev &P, const StepDev &S, KCtx &C
   if (has_cols) stage_out(C.page + C.colbase, 2 * FV, C.cst, (C.tid - 128) & (FNT - 1), FNT);
 }
 
+// Page -> dense fp32 (decode): per-row tables of the rows this workgroup
+// stages (threads 0..127, row i = tid: the code field layout, r, and 2^(8-b)
+// of integer rows; width 0 marks pivot rows), then x = (r c) ((code - L) 2^(8-b))
+// per value, FP16 halves for pivot rows: the operations of the general
+// kernel's decode mode.
+__device__ __forceinline__ void decode_rows(const KCtx &C, const RowPlan rp) {
+  if (C.tid >= FK) return;
+  const int i = C.tid, bi = rp.bits;
+  const int pos = rp.offset - C.code_start;  // within a block
+  if (bi == 16) {
+    C.rm[i] = make_int4(pos, 0, 0, 0);
+    C.rc[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    return;
+  }
+  const float r = hw_h2f(*(const uint16_t *)(C.rst + C.shift_r + (rp.row - C.row_start)));
+  uint32_t xm = 0;
+#pragma unroll
+  for (int c = 0; c < 4; c++) xm |= 1u << (c * bi + bi - 1);
+  C.rm[i] = make_int4(pos, bi, 2 * bi, 3 * bi);
+  C.rc[i] = make_float4(r, (float)(1 << (8 - bi)), 0.f, __uint_as_float(xm));
+}
+
+__device__ __forceinline__ void decode_body(const PoolDev &P, const StepDev &S, const KCtx &C) {
+#pragma clang fp contract(off)
+  const bool has_cols = C.colbase >= 0;
+  float cj[4];
+#pragma unroll
+  for (int c = 0; c < 4; c++)
+    cj[c] = has_cols ? hw_h2f(*(const uint16_t *)(C.cst + C.shift_col + 2 * (C.j0 + c))) : 1.0f;
+  const uint32_t cb = lds_addr(C.code) + (uint32_t)C.lbase;  // this lane's block
+  float *d = S.dense + ((int64_t)C.b * P.H + C.h) * FK * FV + C.j0;
+#pragma unroll 4
+  for (int r = 0; r < FRPT; r++) {
+    const int i = C.rg + 8 * r;
+    const int4 m = C.rm[i];
+    float x[4];
+    if (m.y == 0) {
+      pivot_load(C, i, 1.0f, x);
+    } else {
+      const float4 rc = C.rc[i];
+      const uint32_t word = word_at_addr(cb + (uint32_t)m.x) ^ __float_as_uint(rc.w);
+      const uint32_t w = (uint32_t)m.y;
+      // signed fields s = code - 2^(b-1), so code - L = s + 1
+      const int s[4] = {sbfe(word, 0, w), sbfe(word, w, w), sbfe(word, (uint32_t)m.z, w), sbfe(word, (uint32_t)m.w, w)};
+#pragma unroll
+      for (int c = 0; c < 4; c++) x[c] = (rc.x * cj[c]) * ((float)(s[c] + 1) * rc.y);
+    }
+    *(float4 *)(d + (int64_t)i * FV) = make_float4(x[0], x[1], x[2], x[3]);
+  }
+}
+
 }  // namespace kfast
 
 // Per-head inputs of the KDA kernel into LDS: raw q, k rows and their squared
@@ -3119,6 +3170,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KDA128_WAVE
   if (slot <= 0 || slot >= P.num_slots) {
     if (MODE == MODE_FUSED || MODE == MODE_READ)
       for (int j = C.tid; j < FV; j += FNT) store_val(S.out, S.out_dtype, ((int64_t)C.b * H + C.h) * FV + j, 0.0f);
+    if (MODE == MODE_DECODE) {  // masked: a zero state
+      float4 *d = (float4 *)(S.dense + ((int64_t)C.b * H + C.h) * FK * FV);
+      for (int e = C.tid; e < FK * FV / 4; e += FNT) d[e] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
     return;
   }
   C.page = P.data + slot * P.page_bytes;
@@ -3153,6 +3208,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KDA128_WAVE
   C.shift_col = C.colbase >= 0 ? stage_region_async(C.page + C.colbase, 2 * FV, C.cst, C.tid) : 0;
   uint32_t vraw = 0u;
   const RowPlan rp = row_plan(P, C.h, C.tid);
+  if constexpr (MODE == MODE_DECODE) {
+    __syncthreads();
+    decode_rows(C, rp);
+    __syncthreads();
+    decode_body(P, S, C);
+    return;
+  }
   kda_prologue<MODE, QW4>(P, S, C, vraw);
   __syncthreads();
   if (MODE == MODE_READ && C.tid < FK) {
@@ -4983,7 +5045,19 @@ int launch_step_mode(const sq_pool *pool, StepDev sd, int64_t batch, hipStream_t
                        lds, st, pd, sd);
     return check_launch("gdn128_kernel (decode)");
   }
-  if constexpr (MODE != MODE_DECODE) {  // the KDA kernel reads and steps pages only
+  if (MODE == MODE_DECODE && (pd.fast & SQ_POOL_FAST_KDA128)) {
+    // row-scale regions may start at any even byte: room for the alignment shift
+    pd.rstage = (pool->max_row_bytes + 47) & ~15;
+    // code blocks in padded windows (the largest head's stride)
+    pd.stage = 32 * kfast::block_pitch(pool->max_code_bytes / 32);
+    // the step's layout (staging | rows | columns | ... | rc, rl, rm, rk | pivot mask)
+    size_t lds = (size_t)pd.stage + pd.rstage + fast::KDA_COL_STAGE + 4 * 128 * 4 + fast::MISC_FLOATS * 4 +
+                 4 * 128 * 4 + 2 * 128 * 4 + 4 * 128 * 16 + 16;
+    hipLaunchKernelGGL((kda128_kernel<MODE_DECODE, true>), dim3((unsigned)pool->heads, (unsigned)batch), dim3(256),
+                       lds, st, pd, sd);
+    return check_launch("kda128_kernel (decode)");
+  }
+  if constexpr (MODE != MODE_DECODE) {
     if (pd.fast & SQ_POOL_FAST_GDN128) {
       const int ng_max = pool->group >= 32 ? 128 / pool->group : 1;
       // staging | rows | columns | q,k raw + w | misc | red | ks, qs | rc (float4), iu (float2) per (row, group)
