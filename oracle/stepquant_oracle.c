@@ -21,7 +21,9 @@
  * the value axis, :131-132 sums over the key axis).  The order is that of
  * aten/src/ATen/native/cpu/SumKernel.cpp (cascade_sum): 8-wide float vectors,
  * 4 interleaved accumulators, 16-element cascade levels.  It is pinned by
- * tests/test_oracle_trees.py against torch itself and by the golden vectors.
+ * tests/test_oracle_math.py (test_inner_sum_tree_matches_torch,
+ * test_outer_sum_tree_matches_torch, test_tree_differs_from_naive_order)
+ * against torch itself and by the golden vectors.
  *
  * Compile with -ffp-contract=off: every multiply and add rounds separately,
  * as the reference's PyTorch elementwise ops do.
