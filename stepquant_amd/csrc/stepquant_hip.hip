@@ -335,6 +335,7 @@ struct PoolDev {
   int rstage;  // bytes of LDS for one head's row scales (fast path)
   int fast;    // SQ_POOL_FAST_* bits: which K=V=128 kernel the pool qualifies for
   int storage; // 0: packed codes; 1: int8 carriers, plane value (i, j) at base + i + j*K
+  int hrot;    // K=V=128 step kernels: H - 1 when H is a power of two (head of block (x, y) is (x + y) & hrot), else 0
 };
 
 __device__ __forceinline__ int tile_of(const PoolDev &P) { return P.kda ? (P.V < 4 ? P.V : 4) : (P.V < 16 ? P.V : 16); }
@@ -2410,7 +2411,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GDN128_WAVE
   const int H = P.H;
   Ctx C;
   C.b = blockIdx.y;  // grid (heads, requests): no division
-  C.h = blockIdx.x;
+  // The dispatcher deals consecutive blocks to the 8 XCDs in turn, so with
+  // heads in block order an XCD would run the same H/8 heads for every
+  // request (and their widths set its load); rotating the head by the request
+  // gives every XCD every head.
+  C.h = P.hrot ? (int)((blockIdx.x + blockIdx.y) & (unsigned)P.hrot) : (int)blockIdx.x;
   C.tid = threadIdx.x;
   C.rg = C.tid & 7;
   C.cg = C.tid >> 3;
@@ -3150,7 +3155,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KDA128_WAVE
   const int H = P.H;
   KCtx C;
   C.b = blockIdx.y;  // grid (heads, requests): no division
-  C.h = blockIdx.x;
+  // The dispatcher deals consecutive blocks to the 8 XCDs in turn, so with
+  // heads in block order an XCD would run the same H/8 heads for every
+  // request (and their widths set its load); rotating the head by the request
+  // gives every XCD every head.
+  C.h = P.hrot ? (int)((blockIdx.x + blockIdx.y) & (unsigned)P.hrot) : (int)blockIdx.x;
   C.tid = threadIdx.x;
   C.rg = C.tid & 7;
   C.cg = C.tid >> 3;
@@ -5023,6 +5032,7 @@ PoolDev to_dev(const sq_pool *p) {
   d.rstage = (p->max_row_bytes + 15) & ~15;
   d.fast = p->flags & (SQ_POOL_FAST_GDN128 | SQ_POOL_FAST_KDA128);
   d.storage = p->storage;
+  d.hrot = (p->heads & (p->heads - 1)) == 0 ? p->heads - 1 : 0;
   return d;
 }
 
