@@ -15,6 +15,8 @@ LIB_PATH = os.environ.get("STEPQUANT_HIP_LIB", os.path.join(_HERE, "libstepquant
 ABI_VERSION = 2
 
 F32, BF16, F16, I32, I64 = 0, 1, 2, 3, 4
+# sq_pool.flags bits (SQ_POOL_FAST_*)
+POOL_FAST_GDN128, POOL_FAST_KDA128 = 1, 2
 _DTYPES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16, torch.int32: I32, torch.int64: I64}
 
 _P = ctypes.c_void_p

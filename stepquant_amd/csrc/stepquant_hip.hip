@@ -3278,15 +3278,26 @@ constexpr int LDS_BYTES = OFF_SM + 10 * 64 * 4;
 constexpr int MAX_CK = 64;                          // checkpoints per sequence (one per lane)
 enum { SM_LC = 0, SM_BETA, SM_NK, SM_NQ, SM_GK, SM_QG, SM_KD, SM_KSQ, SM_QSQ };
 
+// The pool's pages, for a kernel that reads the initial states itself.
+struct PageInit {
+  const uint8_t *data;
+  int64_t page_bytes, num_slots;
+  const int32_t *bits, *head_meta, *columns;
+  const void *slots;  // [batch] initial slots
+  int slots_dtype, ng;
+};
+
 struct PrefillDev {
   const void *q, *k, *v, *g, *beta, *a_log, *dt_bias;
   void *out;
   const int32_t *cu, *ckpt;
-  const float *init;
+  const float *init;  // dense initial states, unless page_init
   float *ck_state;
   int64_t q_stride, k_stride, v_stride;
   int H, HK, NC, gate_dtype, out_dtype, normalize, beta_logits;
   float scale;
+  int page_init;  // 1: initial states decoded from the pages of pi.slots inside the kernel
+  PageInit pi;
 };
 
 // Element (r, t) of the transposed k tile sits in row r at column
@@ -3450,6 +3461,87 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// Initial state of one (sequence, head) read from its page, for GDN pools
+// with K = V = 128, one width per head and 16-byte aligned regions (the
+// pools the K = V = 128 decode kernels take).  The head's code, row-scale
+// and column-scale regions are copied into LDS (the chunk tiles' space,
+// unused until the first chunk); each lane then decodes the 32 values of its
+// column j = 16 w + c16 (code block w) with the page decode's operations in
+// its order, x = (r_d c_j)(ZS s + 1) with s the field with its top bit
+// flipped, sign-extended (2-bit heads: z = 2 s + 1 and the row scale of j's
+// value group), so the state is the dense decode's to the bit.
+constexpr int INIT_ROWS = 32768, INIT_COLS = INIT_ROWS + 1024;  // LDS offsets of the staged scale regions
+static_assert(INIT_COLS + 2 * PV <= OFF_P, "the staged page must not overlap the T and P tiles cleared at the start");
+
+template <int W>
+__device__ __forceinline__ void init_from_codes(const uint8_t *lds, int w, int q4, int c16, int ng, f32x4 S[8]) {
+#pragma clang fp contract(off)
+  constexpr float ZS = W == 2 ? 2.0f : 1.0f;
+  constexpr int SEG = 2 * W;  // bytes of a row's 16-value segment
+  const int j = 16 * w + c16;
+  const float cj = fast::hw_h2f(((const uint16_t *)(lds + INIT_COLS))[j]);
+  const uint16_t *rows = (const uint16_t *)(lds + INIT_ROWS);
+  const int NG = W == 2 ? ng : 1;  // row scales per row: the value groups of a 2-bit head
+  const int g = W == 2 ? (j * ng) >> 7 : 0;
+  const int bit = c16 * W, sh = bit & 7;
+  const uint8_t *base = lds + w * (PKD * SEG) + (bit >> 3);
+#pragma unroll
+  for (int dt = 0; dt < 8; dt++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int d = 16 * dt + 4 * q4 + r;
+      const uint8_t *p = base + d * SEG;
+      uint32_t u = p[0];
+      if (sh + W > 8) u |= (uint32_t)p[1] << 8;  // a 6-bit field across two bytes
+      const uint32_t f = ((u >> sh) & ((1u << W) - 1u)) ^ (1u << (W - 1));
+      const int sv = (int)(f << (32 - W)) >> (32 - W);
+      const float rr = fast::hw_h2f(rows[d * NG + g]);
+      S[dt][r] = (rr * cj) * fmaf(ZS, (float)sv, 1.0f);
+    }
+}
+
+// FP16 pivot head: row d's 16-value segment of block w holds fp16 values
+__device__ __forceinline__ void init_from_pivots(const uint8_t *lds, int w, int q4, int c16, f32x4 S[8]) {
+#pragma unroll
+  for (int dt = 0; dt < 8; dt++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int d = 16 * dt + 4 * q4 + r;
+      S[dt][r] = fast::hw_h2f(((const uint16_t *)(lds + w * (PKD * 32) + d * 32))[c16]);
+    }
+}
+
+__device__ __forceinline__ void init_from_page(const PageInit &pi, int b, int h, uint8_t *lds, int tid, f32x4 S[8]) {
+  const int w = tid >> 6, q4 = (tid >> 4) & 3, c16 = tid & 15;
+  const int64_t slot = pi.slots_dtype == SQ_I64 ? ld_uniform((const int64_t *)pi.slots + b)
+                                                 : (int64_t)ld_uniform((const int32_t *)pi.slots + b);
+  if (slot <= 0 || slot >= pi.num_slots) {  // whole workgroup: a zero state
+#pragma unroll
+    for (int dt = 0; dt < 8; dt++) S[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    return;
+  }
+  const int W = ld_uniform(pi.bits + (int64_t)h * PKD);
+  const int32_t *hm = pi.head_meta + 4 * h;
+  const int code_start = ld_uniform(hm), code_bytes = ld_uniform(hm + 1);
+  const int row_start = ld_uniform(hm + 2), row_bytes = ld_uniform(hm + 3);
+  const uint8_t *page = pi.data + slot * pi.page_bytes;
+  for (int e = tid; e < code_bytes / 16; e += NT) ((uint4 *)lds)[e] = ((const uint4 *)(page + code_start))[e];
+  if (W != 16) {
+    for (int e = tid; e < row_bytes / 16; e += NT)
+      ((uint4 *)(lds + INIT_ROWS))[e] = ((const uint4 *)(page + row_start))[e];
+    if (tid < 2 * PV / 16)
+      ((uint4 *)(lds + INIT_COLS))[tid] = ((const uint4 *)(page + ld_uniform(pi.columns + h)))[tid];
+  }
+  __syncthreads();
+  switch (W) {
+    case 2: init_from_codes<2>(lds, w, q4, c16, pi.ng, S); break;
+    case 4: init_from_codes<4>(lds, w, q4, c16, pi.ng, S); break;
+    case 6: init_from_codes<6>(lds, w, q4, c16, pi.ng, S); break;
+    case 8: init_from_codes<8>(lds, w, q4, c16, pi.ng, S); break;
+    default: init_from_pivots(lds, w, q4, c16, S); break;
+  }
+}
+
 // One workgroup of 8 waves per (sequence, head), chunks in order.  Wave w
 // owns the 16 state columns j = 16 w .. 16 w + 15 for all 128 rows d (in
 // registers, accumulator layout); R, Delta and Delta' of its columns stay in
@@ -3498,7 +3590,10 @@ __global__ __launch_bounds__(NT) void prefill_kernel(PrefillDev D) {
 
   // ---- state S[d][j] of this wave's columns: tile dt holds rows d = 16 dt + 4 q4 + r, column jw + c16
   f32x4 S[8];
-  {
+  if (D.page_init) {
+    init_from_page(D.pi, b, h, smem, tid, S);
+    __syncthreads();  // the staged page is read before the first chunk's tiles overwrite it
+  } else {
     const float *src = D.init + ((int64_t)b * H + h) * PKD * PV + jw + c16;
 #pragma unroll
     for (int dt = 0; dt < 8; dt++)
@@ -5544,7 +5639,10 @@ int sq_prefill(const sq_pool *pool, const sq_prefill_args *a, void *stream) {
     return fail(SQ_ESHAPE, "prefill: the prefill kernels handle pools with K = V = 128");
   if (a->batch < 0 || a->n_checkpoints < 0) return fail(SQ_EINVAL, "prefill: negative batch or checkpoint count");
   if (a->batch == 0) return 0;
-  if (!a->q || !a->k || !a->v || !a->g || !a->beta || !a->out || !a->cu_seqlens || !a->init_state)
+  // GDN pools that the K = V = 128 decode kernels take: the recurrence kernel
+  // reads the initial pages itself (no dense initial state in between)
+  const bool page_init = a->init_slots && (pool->flags & SQ_POOL_FAST_GDN128) && !pool->kda && pool->storage == 0;
+  if (!a->q || !a->k || !a->v || !a->g || !a->beta || !a->out || !a->cu_seqlens || (!a->init_state && !page_init))
     return fail(SQ_EINVAL, "prefill: null input, output, sequence offsets or initial-state workspace");
   if (a->n_checkpoints > 0 && (!a->checkpoints || !a->slots || !a->checkpoint_state))
     return fail(SQ_EINVAL, "prefill: checkpoints need positions, slots and a state workspace");
@@ -5566,8 +5664,9 @@ int sq_prefill(const sq_pool *pool, const sq_prefill_args *a, void *stream) {
   hipStream_t st = (hipStream_t)stream;
   const int H = pool->heads;
   const int64_t dense = a->batch * (int64_t)H * 128 * 128;
-  if (a->init_slots) {
-    if (a->slots_dtype != SQ_I32 && a->slots_dtype != SQ_I64) return fail(SQ_EINVAL, "prefill: slots dtype");
+  if (page_init) {
+    // decoded inside the recurrence kernel
+  } else if (a->init_slots) {
     StepDev sd;
     memset(&sd, 0, sizeof(sd));
     sd.slots = a->init_slots;
@@ -5604,6 +5703,16 @@ int sq_prefill(const sq_pool *pool, const sq_prefill_args *a, void *stream) {
   D.normalize = a->normalize;
   D.beta_logits = a->beta_logits != 0;
   D.scale = a->scale;
+  D.page_init = page_init ? 1 : 0;
+  D.pi.data = pool->data;
+  D.pi.page_bytes = pool->page_bytes;
+  D.pi.num_slots = pool->num_slots;
+  D.pi.bits = pool->bits;
+  D.pi.head_meta = pool->head_meta;
+  D.pi.columns = pool->columns;
+  D.pi.slots = a->init_slots;
+  D.pi.slots_dtype = a->slots_dtype;
+  D.pi.ng = pool->group >= 32 ? 128 / pool->group : 1;
   if (pool->kda) {
     hipError_t e = hipFuncSetAttribute((const void *)kc::kda_chunk_kernel,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, kc::LDS_BYTES);

@@ -247,6 +247,50 @@ def test_prefill_kda_and_byte_pages(arch, storage, raw):
         assert not pages[s].any(), "untouched slots stay empty"
 
 
+def test_prefill_reads_initial_pages_in_kernel():
+    """GDN pools that the K = V = 128 kernels take have their initial pages
+    decoded inside the recurrence kernel; the same pages in a pool whose
+    fast flags are cleared go through the dense decode (the general step
+    kernel's decode mode) first.  Outputs, checkpoint states and pages agree
+    bit for bit, for 2-bit (four value groups), 4-, 6-, 8-bit and FP16
+    pivot heads, a zero slot and ragged sequences."""
+    print("case in-kernel initial pages", flush=True)
+    from stepquant_amd.kernels.pool import PackedStatePool
+    from stepquant_amd import _native as N
+    H, HK, K, V = 5, 5, 128, 128
+    lens = [70, 1, 129]
+    B = len(lens)
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]).astype(np.int64))
+    T = int(cu[-1])
+    oplan = make_plan("gdn", np.repeat(np.array([2, 4, 6, 8, 16])[:, None], K, 1), seed=4)
+    pools = [PackedStatePool(device_plan(oplan), 12, V) for _ in range(2)]
+    assert pools[0]._desc.flags & N.POOL_FAST_GDN128
+    pools[1]._desc.flags = 0  # the dense decode path
+    g = torch.Generator().manual_seed(23)
+    init = torch.tensor([3, 0, 5])
+    pools[0].encode((torch.randn(B, H, K, V, generator=g) * .1).to(dev()), init.to(dev()))
+    pools[1].data.copy_(pools[0].data)
+    q = torch.randn(T, HK, K, generator=g).to(torch.bfloat16).to(dev())
+    k = torch.randn(T, HK, K, generator=g).to(torch.bfloat16).to(dev())
+    v = torch.randn(T, H, V, generator=g).to(torch.bfloat16).to(dev())
+    gate = (-torch.nn.functional.softplus(torch.randn(T, H, generator=g))).to(dev())
+    beta = torch.sigmoid(torch.randn(T, H, generator=g)).to(dev())
+    ck = torch.tensor([[64, 70], [1, 0], [100, 129]], dtype=torch.int32)
+    ck_slots = torch.tensor([[6, 7], [8, 0], [9, 10]])
+    outs, states = [], []
+    for pool in pools:
+        pool.keep_prefill_states = True
+        outs.append(pool.extend(q, k, v, gate, beta, torch.tensor([3, 4, 5]), cu, checkpoints=ck,
+                                checkpoint_slots=ck_slots, init_slots=init, normalize=True, scale=K ** -.5))
+        states.append(pool.last_prefill[-1])
+    torch.cuda.synchronize()
+    assert pools[0].last_prefill[-2] is None and pools[1].last_prefill[-2] is not None
+    used = (ck_slots.reshape(-1) > 0).to(dev())  # unused checkpoints leave their workspace entry unwritten
+    assert torch.equal(states[0][used], states[1][used]), "checkpoint states differ between the two initial-state paths"
+    assert torch.equal(outs[0], outs[1]), "outputs differ between the two initial-state paths"
+    assert torch.equal(pools[0].data, pools[1].data), "pages differ between the two initial-state paths"
+
+
 @pytest.mark.parametrize("arch", ["gdn", "kda"])
 def test_prefill_timing_events_change_nothing(arch):
     """The benchmark's timing hook: the two events bracket the recurrence
