@@ -372,15 +372,34 @@ __device__ __forceinline__ uint32_t quad_perm(uint32_t x) {
 
 // =====================================================================
 // Encode, GDN heads of one width (no FP16 pivots), K = V = 128, packed,
-// 512 threads.  Every value of the tile is loaded once per layout, in one
-// batch of independent loads: row layout for the row scales (row group
-// tid / 32 takes rows rw + 16p, lane (l, k) = (lane / 4, lane % 4) the values
-// 32u + 8k + l), column layout (thread j + 128 hf: rows 32 hf .. 32 hf + 31 of
-// column j) for the column scales and codes.  A tile then waits for memory
-// twice rather than once per row and pass.  The operations and their order
-// are those of the general path below (the sums in PyTorch's order).
+// NTH threads (512: 16 row groups of 32 lanes, 4 threads per column).
+// Every value of the tile is loaded once per layout, both batches issued
+// together before any arithmetic: row layout for the row scales (row group
+// rw = tid / 32 takes rows rw + (NTH / 32) p, lane (l, k) = (lane / 4,
+// lane % 4) the values 32u + 8k + l), column layout (thread j + 128 hf: rows
+// CR hf .. CR hf + CR - 1 of column j, CR = 128 * 128 / NTH) for the column
+// scales and codes.  The operations and their order are those of the
+// general path below (the sums in PyTorch's order).
 // =====================================================================
+// Four codes b0..b3 (< 2^W), one per byte of x, as consecutive W-bit
+// fields (b0 lowest): the packed 4-value group of a row.
 template <int W>
+__device__ __forceinline__ uint32_t pack_bytes(uint32_t x) {
+  if (W == 8) return x;
+  if (W == 4) return __builtin_amdgcn_perm(0u, x | (x >> 4), 0x0c0c0200u);  // bytes 0 and 2 of b0|b1<<4, b2|b3<<4
+  if (W == 2) {
+    const uint32_t y = x | (x >> 6);  // byte 0: b0 | b1 << 2, byte 2: b2 | b3 << 2
+    return (y & 0xfu) | ((y >> 12) & 0xf0u);
+  }
+  // W == 6: b0, b1 at bits 0 and 6, b2, b3 at bits 16 and 22, then bits
+  // [16, 28) moved down to [12, 24) by one bitfield insert
+  const uint32_t y = (x & 0x003f003fu) | ((x >> 2) & 0x0fc00fc0u);
+  uint32_t w;
+  __asm__("v_bfi_b32 %0, %1, %2, %3" : "=v"(w) : "s"(0xfffu), "v"(y), "v"(y >> 4));
+  return w;
+}
+
+template <int W, int NTH>
 __device__ __forceinline__ void encode_fast128(const PoolDev &P, const float *__restrict__ X, uint8_t *page,
                                                uint8_t *smem, int h) {
 #pragma clang fp contract(off)
@@ -395,10 +414,13 @@ __device__ __forceinline__ void encode_fast128(const PoolDev &P, const float *__
   const int shift = (int)((uintptr_t)(page + code_start) & 15);
   uint8_t *stage = smem;
   float *rsc = (float *)(smem + P.stage);  // [K][NG]
-  float *wl = rsc + K * 4;                 // [K] fit weights
+  float *wl = rsc + K * 4;                 // [K] squared fit weights w^2
   int *orel = (int *)(wl + K);             // [K] row offsets within the code region
-  float *cmax = (float *)(orel + K);       // [4][V]
-  float *bsum = cmax + 4 * V;              // [K/16][2][V]
+  constexpr int HALVES = NTH / 32, RP = K / HALVES;  // 32-lane row groups, rows per group
+  constexpr int CT = NTH / V, CR = K / CT;             // threads per column, rows per thread
+  static_assert(RP * 4 <= 32 && CR % 16 == 0, "row groups hold at most 8 rows, columns whole 16-row blocks");
+  float *cmax = (float *)(orel + K);       // [CT][V]
+  float *bsum = cmax + CT * V;             // [K/16][2][V]
   float *rinv = bsum + (K / 16) * 2 * V;   // [K][NG] 1 / row scale, correctly rounded
 
   // The column phase divides by fp16 scales (row scales, c0, c): with their
@@ -407,25 +429,31 @@ __device__ __forceinline__ void encode_fast128(const PoolDev &P, const float *__
   // so the quotients stay within [2^-92, 2^108]).  Tiles with a value
   // outside (or a NaN or infinity) divide with IEEE division.
   uint32_t lo_bits = 0xffffffffu, hi_bits = 0u;  // min of |x| bits - 1 (zeros wrap), max of |x| bits
-  // ---- row phase.  Each 32-lane half takes rows rw + 16 p; its row sums
-  // (in PyTorch's order) land in lane 0 and go through LDS to lane p NG + g,
-  // so the scale arithmetic of the half's 8 NG (row, group) pairs runs once,
-  // side by side, instead of once per pair on lane 0.
+  // this thread's CR values of column j (the column phase's layout), loaded
+  // together with the row layout's values below: one wait for memory
+  const int j = tid & (V - 1), hf = tid >> 7, i0 = CR * hf;
+  float xs[CR], sc[CR];
+#pragma unroll
+  for (int r = 0; r < CR; r++) xs[r] = X[(i0 + r) * V + j];
+  // ---- row phase.  Each 32-lane half takes rows rw + HALVES p; its row
+  // sums (in PyTorch's order) land in lane 0 and go through LDS to lane
+  // p NG + g, so the scale arithmetic of the half's RP NG (row, group) pairs
+  // runs once, side by side, instead of once per pair on lane 0.
   {
     const int lane = tid & 31, l = lane >> 2, k = lane & 3, rw = tid >> 5;
-    float v[8][4];
-    // lane e < 8 NG: the inputs of pair (p, g) = (e / NG, e % NG)
-    const int pe = lane / NG, ge = lane % NG, ie = rw + 16 * (pe & 7);
+    float v[RP][4];
+    // lane e < RP NG: the inputs of pair (p, g) = (e / NG, e % NG)
+    const int pe = lane / NG, ge = lane % NG, ie = rw + HALVES * (pe & (RP - 1));
     const float wie = P.impact[(int64_t)h * K + ie];
     const int roe = P.rows[(int64_t)h * K + ie], ofe = P.offsets[(int64_t)h * K + ie];
 #pragma unroll
-    for (int p = 0; p < 8; p++) {
-      const int i = rw + 16 * p;
+    for (int p = 0; p < RP; p++) {
+      const int i = rw + HALVES * p;
 #pragma unroll
       for (int u = 0; u < 4; u++) v[p][u] = X[i * V + 32 * u + 8 * k + l];
     }
 #pragma unroll
-    for (int p = 0; p < 8; p++)
+    for (int p = 0; p < RP; p++)
 #pragma unroll
       for (int u = 0; u < 4; u++) {
         const uint32_t a = __float_as_uint(v[p][u]) & 0x7fffffffu;
@@ -434,7 +462,7 @@ __device__ __forceinline__ void encode_fast128(const PoolDev &P, const float *__
       }
     float *tot = cmax + 32 * rw;  // the half's row sums (cmax is free until the column phase)
 #pragma unroll
-    for (int p = 0; p < 8; p++) {
+    for (int p = 0; p < RP; p++) {
 #pragma unroll
       for (int g = 0; g < 4; g++) {
         if (g >= NG) break;
@@ -467,7 +495,7 @@ __device__ __forceinline__ void encode_fast128(const PoolDev &P, const float *__
       }
     }
     // (the LDS accesses of one wave complete in order: lane e reads what lane 0 wrote)
-    if (lane < 8 * NG) {
+    if (lane < RP * NG) {
       const int i = ie, g = ge;
       float m = tot[lane] / (float)ngrp;
       m = m < 1e-20f ? 1e-20f : m;
@@ -477,23 +505,19 @@ __device__ __forceinline__ void encode_fast128(const PoolDev &P, const float *__
       rinv[i * NG + g] = 1.0f / r;
       put_page_half(page, roe + 2 * g, hb);
       if (g == 0) {
-        wl[i] = wie;
+        wl[i] = wie * wie;
         orel[i] = ofe - code_start;
       }
     }
   }
-  // ---- column phase: this thread's 32 values of column j, raw and scaled
-  const int j = tid & (V - 1), hf = tid >> 7, i0 = 32 * hf;
+  // ---- column phase: the thread's values of column j, raw and scaled
   const int g = two ? j / 32 : 0;
-  float xs[32], sc[32];
-#pragma unroll
-  for (int r = 0; r < 32; r++) xs[r] = X[(i0 + r) * V + j];
   const bool ieee = __syncthreads_or(lo_bits < 0x19800000u - 1u || hi_bits > 0x5d800000u);
   auto columns = [&](auto fast_tag) {
   constexpr bool FAST = decltype(fast_tag)::value;
   float amax = 0.0f;
 #pragma unroll
-  for (int r = 0; r < 32; r++) {
+  for (int r = 0; r < CR; r++) {
     const int ig = (i0 + r) * NG + g;
     sc[r] = FAST ? div_half(xs[r], rsc[ig], rinv[ig]) : xs[r] / rsc[ig];
     const float a = fabsf(sc[r]);
@@ -503,7 +527,7 @@ __device__ __forceinline__ void encode_fast128(const PoolDev &P, const float *__
   __syncthreads();
   float am = 0.0f;
 #pragma unroll
-  for (int u = 0; u < 4; u++) {
+  for (int u = 0; u < CT; u++) {
     const float a = cmax[u * V + j];
     am = a > am ? a : am;
   }
@@ -514,25 +538,22 @@ __device__ __forceinline__ void encode_fast128(const PoolDev &P, const float *__
   auto zq = [&](float s, float cdiv, float cinv) -> float {
     const float y = FAST ? div_half(s, cdiv, cinv) : s / cdiv;
     if (two) return (y >= 0.0f ? 1.0f : -1.0f) * (fabsf(y) >= 2.0f ? 3.0f : 1.0f);
-    float z = __builtin_rintf(y);
-    z = z > -qmax ? z : -qmax;
-    z = z < qmax ? z : qmax;
-    return z;
+    return __builtin_amdgcn_fmed3f(__builtin_rintf(y), -qmax, qmax);
   };
-  // refit sums: two 16-row blocks per thread, each from zero
+  // refit sums: CR / 16 blocks of 16 rows per thread, each from zero
 #pragma unroll
-  for (int mb = 0; mb < 2; mb++) {
+  for (int mb = 0; mb < CR / 16; mb++) {
     float bn = 0.0f, bd = 0.0f;
 #pragma unroll
     for (int rr = 0; rr < 16; rr++) {
       const int r = 16 * mb + rr, i = i0 + r;
-      const float wsq = (wl[i] * wl[i]) * 1.0f;
+      const float wsq = wl[i];  // (w w) 1 of integer rows: the factor 1 is exact
       const float z = zq(sc[r], c0, c0inv);
       const float v = (rsc[i * NG + g] * 1.0f) * z;
       bn += (wsq * v) * xs[r];
       bd += wsq * (v * v);
     }
-    const int m = 2 * hf + mb;
+    const int m = (CR / 16) * hf + mb;
     bsum[(2 * m) * V + j] = bn;
     bsum[(2 * m + 1) * V + j] = bd;
   }
@@ -549,30 +570,50 @@ __device__ __forceinline__ void encode_fast128(const PoolDev &P, const float *__
   const float cinv = 1.0f / c;
   const int colbase = P.columns[h];
   if (hf == 0 && colbase >= 0) put_page_half(page, colbase + 2 * (int64_t)j, chb);
-  // final codes; quads of lanes assemble each 4-value group
-  const int L = two ? 3 : (1 << (W - 1)) - 1;
+  // final codes: each lane converts its column's codes of rows 4t .. 4t + 3
+  // into the bytes of one dword; a 4 x 4 byte transpose within the quad of
+  // lanes j & ~3 .. j | 3 (two lane exchanges, two byte permutes) leaves lane
+  // q with the four codes of row 4t + q in the quad's 4-value group, which it
+  // packs into W-bit fields and stores (the rows of a head of one width
+  // follow each other 2W bytes apart)
+  const float L = two ? 3.0f : (float)((1 << (W - 1)) - 1);
+  const int q = j & 3;
+  const uint32_t sel1 = (q & 1) ? 0x03070105u : 0x06020400u;  // [nb1 own1 nb3 own3] / [own0 nb0 own2 nb2]
+  const uint32_t sel2 = (q & 2) ? 0x03020706u : 0x05040100u;  // [nb2 nb3 own2 own3] / [own0 own1 nb0 nb1]
+  const int pos0 = shift + group_pos(orel[i0], stride, 16, j & ~3, W) + q * 2 * W;
 #pragma unroll
-  for (int r = 0; r < 32; r++) {
-    const int i = i0 + r;
-    const float z = zq(sc[r], c, cinv);
-    const uint32_t code = two ? (uint32_t)(((int)z + 3) / 2) : (uint32_t)((int)z + L);
-    const uint32_t c1 = quad_perm<0xB1>(code), c2 = quad_perm<0x4E>(code), c3 = quad_perm<0x1B>(code);  // lane ^ 1, 2, 3
-    if ((tid & 3) == 0) {
-      const uint32_t word = code | (c1 << W) | (c2 << (2 * W)) | (c3 << (3 * W));
-      lds_put_bytes(stage, shift + group_pos(orel[i], stride, 16, j, W), word, W / 2);
+  for (int t = 0; t < CR / 4; t++) {
+    uint32_t w4 = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const float z = zq(sc[4 * t + k], c, cinv);
+      const float code = two ? (z + 3.0f) * 0.5f : z + L;  // an exact small integer
+      w4 = __builtin_amdgcn_cvt_pk_u8_f32(code, k, w4);
     }
+    w4 = __builtin_amdgcn_perm(quad_perm<0xB1>(w4), w4, sel1);  // lane ^ 1
+    w4 = __builtin_amdgcn_perm(quad_perm<0x4E>(w4), w4, sel2);  // lane ^ 2
+    lds_put_bytes(stage, pos0 + 4 * t * 2 * W, pack_bytes<W>(w4), W / 2);
   }
   };
   if (ieee) columns(BoolTag<false>{});
   else columns(BoolTag<true>{});
   __syncthreads();
-  stage_out(page + code_start, code_bytes, stage, tid, 512);
+  stage_out(page + code_start, code_bytes, stage, tid, NTH);
 }
 
 // GDN pools with K = V = 128 (packed, 2-bit groups of 32): the fast form
 // above, FP16 pivot heads as halves of every value.
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void encode128_kernel(
+// 512 threads per tile, 4 waves per SIMD (1024 threads at 8 waves per SIMD
+// measured the same)
+#ifndef ENC128_NT
+#define ENC128_NT 512
+#endif
+#ifndef ENC128_WAVES
+#define ENC128_WAVES 4
+#endif
+__global__ __launch_bounds__(ENC128_NT) __attribute__((amdgpu_waves_per_eu(ENC128_WAVES))) void encode128_kernel(
     PoolDev P, const float *__restrict__ state, const void *slots, int slots_dtype) {
+  constexpr int NTH = ENC128_NT;
   extern __shared__ __align__(16) uint8_t smem[];
   const int H = P.H;
   const int b = blockIdx.x / H, h = blockIdx.x % H;
@@ -582,16 +623,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void e
   const float *X = state + ((int64_t)b * H + h) * 128 * 128;
   const int W = P.bits[(int64_t)h * 128];
   switch (W) {  // the width as a compile-time constant: code packing without loops or branches
-    case 2: encode_fast128<2>(P, X, page, smem, h); return;
-    case 4: encode_fast128<4>(P, X, page, smem, h); return;
-    case 6: encode_fast128<6>(P, X, page, smem, h); return;
-    case 8: encode_fast128<8>(P, X, page, smem, h); return;
+    case 2: encode_fast128<2, NTH>(P, X, page, smem, h); return;
+    case 4: encode_fast128<4, NTH>(P, X, page, smem, h); return;
+    case 6: encode_fast128<6, NTH>(P, X, page, smem, h); return;
+    case 8: encode_fast128<8, NTH>(P, X, page, smem, h); return;
     default: break;
   }
   // pivot head: value (i, j) as a half at its tiled position
   const int code_start = P.head_meta[4 * h];
   const int stride = P.offsets[(int64_t)H * 128 + h];
-  for (int e = threadIdx.x; e < 128 * 128; e += 512) {
+  for (int e = threadIdx.x; e < 128 * 128; e += NTH) {
     const int i = e >> 7, j = e & 127;
     const int off = P.offsets[(int64_t)h * 128 + i];
     put_page_half(page, (int64_t)code_start + (off - code_start) + (j / 16) * stride + (j % 16) * 2, f2h(X[e]));
@@ -5401,10 +5442,11 @@ int sq_encode(const sq_pool *pool, const float *state, const void *slots, int32_
     return check_launch("encode_kda128_kernel");
   }
   if (!pool->kda && pool->storage == 0 && K == 128 && V == 128 && pd.G == 32) {
-    // rows [K][4] | w [K] | row offsets [K] | column maxima [4][V] | block sums [K/16][2][V] | 1/rows [K][4]
-    const size_t fl = (size_t)stage_bytes(pool) + (size_t)(K * 4 + 2 * K + 4 * V + (K / 16) * 2 * V + K * 4) * 4;
-    hipLaunchKernelGGL(encode128_kernel, dim3((unsigned)(batch * pool->heads)), dim3(512), fl, (hipStream_t)stream,
-                       pd, state, slots, slots_dtype);
+    // rows [K][4] | w [K] | row offsets [K] | column maxima [NT/V][V] | block sums [K/16][2][V] | 1/rows [K][4]
+    const size_t fl =
+        (size_t)stage_bytes(pool) + (size_t)(K * 4 + 2 * K + (ENC128_NT / V) * V + (K / 16) * 2 * V + K * 4) * 4;
+    hipLaunchKernelGGL(encode128_kernel, dim3((unsigned)(batch * pool->heads)), dim3(ENC128_NT), fl,
+                       (hipStream_t)stream, pd, state, slots, slots_dtype);
     return check_launch("encode128_kernel");
   }
   hipLaunchKernelGGL(encode_kernel, dim3((unsigned)(batch * pool->heads)), dim3(NT), lds, (hipStream_t)stream, pd,
