@@ -855,19 +855,39 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void e
     const float cinv = 1.0f / c;
     const int colbase = P.columns[h];
     if (hf == 0 && colbase >= 0) put_page_half(page, colbase + 2 * (int64_t)j, chb);
-    // final codes; quads of lanes assemble each row's 4-value tile
+    // final codes: each lane converts its column's codes of rows 4t .. 4t + 3
+    // into the bytes of one dword; a 4 x 4 byte transpose within the quad of
+    // lanes j & ~3 .. j | 3 (two lane exchanges, two byte permutes) leaves
+    // lane q with the four codes of row 4t + q in the quad's 4-value tile,
+    // which it packs with that row's width and stores (pivot rows: nothing)
+    const int q = j & 3;
+    const uint32_t sel1 = (q & 1) ? 0x03070105u : 0x06020400u;  // [nb1 own1 nb3 own3] / [own0 nb0 own2 nb2]
+    const uint32_t sel2 = (q & 2) ? 0x03020706u : 0x05040100u;  // [nb2 nb3 own2 own3] / [own0 own1 nb0 nb1]
+    const int blk = shift + (j >> 2) * stride;
 #pragma unroll
-    for (int r = 0; r < 32; r++) {
-      if (r % 8 == 0) __builtin_amdgcn_sched_barrier(0);
-      const int i = i0 + r;
-      const int w = __builtin_amdgcn_readfirstlane(rowi[i].x);
-      if (w == 16) continue;
-      const uint32_t code = (uint32_t)((int)zq(sc[r], c, cinv, ufl(rowc[i].x), ufl(rowc[i].y)) +
-                                       __builtin_amdgcn_readfirstlane(rowi[i].y));
-      const uint32_t c1 = quad_perm<0xB1>(code), c2 = quad_perm<0x4E>(code), c3 = quad_perm<0x1B>(code);
-      if ((tid & 3) == 0) {
-        const uint32_t word = code | (c1 << w) | (c2 << (2 * w)) | (c3 << (3 * w));
-        lds_put_bytes(stage, shift + group_pos(__builtin_amdgcn_readfirstlane(rowi[i].z), stride, 4, j, w), word, w / 2);
+    for (int t = 0; t < 8; t++) {
+      if (t % 2 == 0) __builtin_amdgcn_sched_barrier(0);
+      uint32_t w4 = 0;
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const int r = 4 * t + k, i = i0 + r;
+        // pivot rows give an unused byte (their lane stores nothing)
+        const float z = zq(sc[r], c, cinv, ufl(rowc[i].x), ufl(rowc[i].y));
+        const float code = z + (float)__builtin_amdgcn_readfirstlane(rowi[i].y);
+        w4 = __builtin_amdgcn_cvt_pk_u8_f32(code, k, w4);  // code >= 0: z + L with z in [-L, L]
+      }
+      w4 = __builtin_amdgcn_perm(quad_perm<0xB1>(w4), w4, sel1);  // lane ^ 1
+      w4 = __builtin_amdgcn_perm(quad_perm<0x4E>(w4), w4, sel2);  // lane ^ 2
+      const int4 ri = rowi[i0 + 4 * t + q];  // this lane's row: width, L, row offset, width class
+      const int w = ri.x;
+      if (w != 16) {
+        const uint32_t word = (w4 & 0xffu) | (((w4 >> 8) & 0xffu) << w) | (((w4 >> 16) & 0xffu) << (2 * w)) |
+                              ((w4 >> 24) << (3 * w));
+        uint8_t *dst = stage + blk + ri.z;
+        dst[0] = (uint8_t)word;
+        if (w >= 4) dst[1] = (uint8_t)(word >> 8);
+        if (w >= 6) dst[2] = (uint8_t)(word >> 16);
+        if (w == 8) dst[3] = (uint8_t)(word >> 24);
       }
     }
   };
