@@ -199,9 +199,10 @@ int sq_writeback(const sq_pool *pool, const sq_writeback_scratch *scratch, int64
  *             slots[b * n_checkpoints + c] (positions <= 0 or beyond the
  *             sequence are unused and their slots must be <= 0).
  *   init_state      workspace [batch, H, K, V] f32 for the decoded initial
- *             states; pools flagged SQ_POOL_FAST_GDN128 are decoded inside
- *             the recurrence kernel from init_slots' pages (to the same
- *             bits), leave it untouched and accept NULL;
+ *             states; pools flagged SQ_POOL_FAST_GDN128 or
+ *             SQ_POOL_FAST_KDA128 are decoded inside the recurrence kernel
+ *             from init_slots' pages (to the same bits), leave it untouched
+ *             and accept NULL;
  *   checkpoint_state workspace [batch * n_checkpoints, H, K, V] f32.
  *   events    NULL, or two hipEvent_t recorded on the stream right before
  *             and after the recurrence kernel (a timing hook for

@@ -3343,7 +3343,7 @@ enum { SM_LC = 0, SM_BETA, SM_NK, SM_NQ, SM_GK, SM_QG, SM_KD, SM_KSQ, SM_QSQ };
 struct PageInit {
   const uint8_t *data;
   int64_t page_bytes, num_slots;
-  const int32_t *bits, *head_meta, *columns;
+  const int32_t *bits, *head_meta, *columns, *offsets, *rows;
   const void *slots;  // [batch] initial slots
   int slots_dtype, ng;
 };
@@ -4254,6 +4254,78 @@ __device__ __forceinline__ f32x4 mm16t(const uint8_t *tile, int o, int lo, bf16x
   return pf::mfma16(xl, mh, acc);
 }
 
+// Initial state of one (sequence, head) of a KDA pool with K = V = 128
+// (per-row widths, FP16 pivot rows, 4-value tiles), read from its page: the
+// head's code, row-scale and column-scale regions and its rows' plan entries
+// are copied into LDS (the chunk tiles' space, unused until the first
+// chunk), then each lane decodes the 32 values of its column j = 16 w + c16
+// (block j / 4, field j % 4) with the KDA page decode's operations in its
+// order, x = (r c_j)((s + 1) 2^(8-b)) with s the field with its top bit
+// flipped, sign-extended, and the stored half for pivot rows, so the state
+// is the dense decode's to the bit.
+constexpr int KI_ROWS = 33024, KI_COLS = KI_ROWS + 288, KI_TAB = KI_COLS + 288;  // LDS offsets past the code
+static_assert(KI_TAB + 3 * KV * 4 <= OFF_A, "the staged page must not overlap A, which is cleared at the start");
+
+__device__ __forceinline__ void kda_init_from_page(const pf::PageInit &pi, int b, int h, int H, uint8_t *lds, int tid,
+                                                   pf::f32x4 S[8]) {
+#pragma clang fp contract(off)
+  const int w = tid >> 6, q4 = (tid >> 4) & 3, c16 = tid & 15;
+  const int64_t slot = pi.slots_dtype == SQ_I64 ? ld_uniform((const int64_t *)pi.slots + b)
+                                                 : (int64_t)ld_uniform((const int32_t *)pi.slots + b);
+  if (slot <= 0 || slot >= pi.num_slots) {  // whole workgroup: a zero state
+#pragma unroll
+    for (int dt = 0; dt < 8; dt++) S[dt] = pf::f32x4{0.f, 0.f, 0.f, 0.f};
+    return;
+  }
+  const int32_t *hm = pi.head_meta + 4 * h;
+  const int code_start = ld_uniform(hm), code_bytes = ld_uniform(hm + 1);
+  const int row_start = ld_uniform(hm + 2), row_bytes = ld_uniform(hm + 3);
+  const int colbase = ld_uniform(pi.columns + h);
+  const int stride = ld_uniform(pi.offsets + (int64_t)H * KV + h);
+  const uint8_t *page = pi.data + slot * pi.page_bytes;
+  // 16-byte windows around each region (pages may start on any even byte)
+  auto stage = [&](const uint8_t *g, int nbytes, uint8_t *dst) {
+    const int sh = (int)((uintptr_t)g & 15);
+    const uint4 *src = (const uint4 *)(g - sh);
+    for (int e = tid; e < (sh + nbytes + 15) >> 4; e += NT) ((uint4 *)dst)[e] = src[e];
+    return sh;
+  };
+  const int shc = stage(page + code_start, code_bytes, lds);
+  const int shr = row_bytes > 0 ? stage(page + row_start, row_bytes, lds + KI_ROWS) : 0;
+  const int shk = colbase >= 0 ? stage(page + colbase, 2 * KV, lds + KI_COLS) : 0;
+  int *tab = (int *)(lds + KI_TAB);  // per row: width, code offset within a block, row-scale offset
+  if (tid < KV) {
+    const int64_t e = (int64_t)h * KV + tid;
+    tab[tid] = pi.bits[e];
+    tab[KV + tid] = pi.offsets[e] - code_start;
+    tab[2 * KV + tid] = pi.rows[e] - row_start;
+  }
+  __syncthreads();
+  const int j = 16 * w + c16, f = j & 3;
+  const float cj = colbase >= 0 ? fast::hw_h2f(*(const uint16_t *)(lds + KI_COLS + shk + 2 * j)) : 1.0f;
+  const int blk = shc + (j >> 2) * stride;  // this column's block within the staged window (an even byte)
+#pragma unroll
+  for (int dt = 0; dt < 8; dt++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int d = 16 * dt + 4 * q4 + r;
+      const int bw = tab[d], pos = blk + tab[KV + d];
+      float x;
+      if (bw == 16) {
+        x = fast::hw_h2f(*(const uint16_t *)(lds + pos + 2 * f)) * 1.0f;
+      } else {
+        const float rr = fast::hw_h2f(*(const uint16_t *)(lds + KI_ROWS + shr + tab[2 * KV + d]));
+        uint32_t xm = 0;
+#pragma unroll
+        for (int c = 0; c < 4; c++) xm |= 1u << (c * bw + bw - 1);
+        const uint32_t word = kfast::word_at(lds, pos) ^ xm;
+        const int sv = kfast::sbfe(word, (uint32_t)(f * bw), (uint32_t)bw);
+        x = (rr * cj) * ((float)(sv + 1) * (float)(1 << (8 - bw)));
+      }
+      S[dt][r] = x;
+    }
+}
+
 __global__ __launch_bounds__(NT) void kda_chunk_kernel(pf::PrefillDev D) {
 #pragma clang fp contract(off)
   extern __shared__ __align__(16) uint8_t smem[];
@@ -4283,7 +4355,10 @@ __global__ __launch_bounds__(NT) void kda_chunk_kernel(pf::PrefillDev D) {
 
   // ---- state S[d][j] of this wave's columns: tile dt holds rows d = 16 dt + 4 q4 + r, column jw + c16
   f32x4 S[8];
-  {
+  if (D.page_init) {
+    kda_init_from_page(D.pi, b, h, H, smem, tid, S);
+    __syncthreads();  // the staged page is read before the first chunk's tiles overwrite it
+  } else {
     const float *src = D.init + ((int64_t)b * H + h) * KV * KV + jw + c16;
 #pragma unroll
     for (int dt = 0; dt < 8; dt++)
@@ -5701,9 +5776,10 @@ int sq_prefill(const sq_pool *pool, const sq_prefill_args *a, void *stream) {
     return fail(SQ_ESHAPE, "prefill: the prefill kernels handle pools with K = V = 128");
   if (a->batch < 0 || a->n_checkpoints < 0) return fail(SQ_EINVAL, "prefill: negative batch or checkpoint count");
   if (a->batch == 0) return 0;
-  // GDN pools that the K = V = 128 decode kernels take: the recurrence kernel
-  // reads the initial pages itself (no dense initial state in between)
-  const bool page_init = a->init_slots && (pool->flags & SQ_POOL_FAST_GDN128) && !pool->kda && pool->storage == 0;
+  // packed pools that the K = V = 128 decode kernels take: the recurrence
+  // kernel reads the initial pages itself (no dense initial state in between)
+  const bool page_init = a->init_slots && pool->storage == 0 &&
+                         (pool->flags & (pool->kda ? SQ_POOL_FAST_KDA128 : SQ_POOL_FAST_GDN128));
   if (!a->q || !a->k || !a->v || !a->g || !a->beta || !a->out || !a->cu_seqlens || (!a->init_state && !page_init))
     return fail(SQ_EINVAL, "prefill: null input, output, sequence offsets or initial-state workspace");
   if (a->n_checkpoints > 0 && (!a->checkpoints || !a->slots || !a->checkpoint_state))
@@ -5772,6 +5848,8 @@ int sq_prefill(const sq_pool *pool, const sq_prefill_args *a, void *stream) {
   D.pi.bits = pool->bits;
   D.pi.head_meta = pool->head_meta;
   D.pi.columns = pool->columns;
+  D.pi.offsets = pool->offsets;
+  D.pi.rows = pool->rows;
   D.pi.slots = a->init_slots;
   D.pi.slots_dtype = a->slots_dtype;
   D.pi.ng = pool->group >= 32 ? 128 / pool->group : 1;

@@ -471,9 +471,9 @@ class PackedStatePool:
         nc = ck.shape[1]
         init = slots_t if init_slots is None else _indices(init_slots, dev)
         out = torch.empty((total, self.heads, self.values), device=dev, dtype=q.dtype)
-        # GDN pools that the K = V = 128 kernels take are decoded inside the
-        # recurrence kernel: no dense initial-state workspace
-        page_init = bool(self._desc.flags & N.POOL_FAST_GDN128)
+        # packed pools that the K = V = 128 kernels take are decoded inside
+        # the recurrence kernel: no dense initial-state workspace
+        page_init = bool(self._desc.flags & (N.POOL_FAST_GDN128 | N.POOL_FAST_KDA128))
         init_state = None if page_init else \
             torch.empty((batch, self.heads, self.keys, self.values), device=dev, dtype=torch.float32)
         keep = self.keep_prefill_states if keep_states is None else keep_states

@@ -247,14 +247,16 @@ def test_prefill_kda_and_byte_pages(arch, storage, raw):
         assert not pages[s].any(), "untouched slots stay empty"
 
 
-def test_prefill_reads_initial_pages_in_kernel():
-    """GDN pools that the K = V = 128 kernels take have their initial pages
-    decoded inside the recurrence kernel; the same pages in a pool whose
-    fast flags are cleared go through the dense decode (the general step
-    kernel's decode mode) first.  Outputs, checkpoint states and pages agree
-    bit for bit, for 2-bit (four value groups), 4-, 6-, 8-bit and FP16
-    pivot heads, a zero slot and ragged sequences."""
-    print("case in-kernel initial pages", flush=True)
+@pytest.mark.parametrize("arch", ["gdn", "kda"])
+def test_prefill_reads_initial_pages_in_kernel(arch):
+    """Packed pools that the K = V = 128 kernels take have their initial
+    pages decoded inside the recurrence kernel; the same pages in a pool
+    whose fast flags are cleared go through the dense decode (the general
+    step kernel's decode mode) first.  Outputs, checkpoint states and pages
+    agree bit for bit: GDN 2-bit (four value groups), 4-, 6-, 8-bit and FP16
+    pivot heads; KDA rows of every width with FP16 pivot rows (odd tile
+    offsets); a zero slot and ragged sequences."""
+    print(f"case in-kernel initial pages {arch}", flush=True)
     from stepquant_amd.kernels.pool import PackedStatePool
     from stepquant_amd import _native as N
     H, HK, K, V = 5, 5, 128, 128
@@ -262,9 +264,15 @@ def test_prefill_reads_initial_pages_in_kernel():
     B = len(lens)
     cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]).astype(np.int64))
     T = int(cu[-1])
-    oplan = make_plan("gdn", np.repeat(np.array([2, 4, 6, 8, 16])[:, None], K, 1), seed=4)
+    if arch == "gdn":
+        bits = np.repeat(np.array([2, 4, 6, 8, 16])[:, None], K, 1)
+    else:
+        rng = np.random.default_rng(8)
+        bits = np.where(rng.random((H, K)) < .05, 16, rng.choice([2, 4, 6, 8], (H, K)))
+        bits[4] = 16  # a head of pivot rows only
+    oplan = make_plan(arch, bits, seed=4)
     pools = [PackedStatePool(device_plan(oplan), 12, V) for _ in range(2)]
-    assert pools[0]._desc.flags & N.POOL_FAST_GDN128
+    assert pools[0]._desc.flags & (N.POOL_FAST_GDN128 if arch == "gdn" else N.POOL_FAST_KDA128)
     pools[1]._desc.flags = 0  # the dense decode path
     g = torch.Generator().manual_seed(23)
     init = torch.tensor([3, 0, 5])
@@ -273,7 +281,8 @@ def test_prefill_reads_initial_pages_in_kernel():
     q = torch.randn(T, HK, K, generator=g).to(torch.bfloat16).to(dev())
     k = torch.randn(T, HK, K, generator=g).to(torch.bfloat16).to(dev())
     v = torch.randn(T, H, V, generator=g).to(torch.bfloat16).to(dev())
-    gate = (-torch.nn.functional.softplus(torch.randn(T, H, generator=g))).to(dev())
+    gshape = (T, H, K) if arch == "kda" else (T, H)
+    gate = (-torch.nn.functional.softplus(torch.randn(gshape, generator=g) * (.5 if arch == "kda" else 1.))).to(dev())
     beta = torch.sigmoid(torch.randn(T, H, generator=g)).to(dev())
     ck = torch.tensor([[64, 70], [1, 0], [100, 129]], dtype=torch.int32)
     ck_slots = torch.tensor([[6, 7], [8, 0], [9, 10]])
