@@ -258,7 +258,7 @@ class PackedStatePool:
         if slots.numel():
             self._writeback(state, slots)
 
-    def _writeback(self, state, slots, rows_ready=False, partial=None, row_tile=32):
+    def _writeback(self, state, slots):
         state = state.to(device=self.device, dtype=torch.float32).contiguous()
         idx = _indices(slots, self.device)
         N.check(N.lib().sq_encode(self._desc, N.ptr(state), N.ptr(idx), N.dtype_code(idx), idx.numel(),
