@@ -4394,67 +4394,70 @@ __global__ __launch_bounds__(NT) void kda_chunk_kernel(pf::PrefillDev D) {
   };
 
   Fetch F;
+  // ---- staging of the chunk whose inputs are in F (n tokens, flag word pa): v
+  // rows, raw k and q rows, norms, beta; cumulative decays per channel
+  auto stage_chunk = [&](int pa) {
+    const int n = F.n;
+    float kf[8], qf[8];
+    bf8(F.k, kf);
+    bf8(F.q, qf);
+    const bool live = tt < n;
+    const uint32_t mk = live ? 0xffffffffu : 0u;  // tokens past the chunk's: zero rows
+    *(uint4 *)(KB + (tt * RP + c8) * 2) = make_uint4(F.k.x & mk, F.k.y & mk, F.k.z & mk, F.k.w & mk);
+    *(uint4 *)(QB + (tt * RP + c8) * 2) = make_uint4(F.q.x & mk, F.q.y & mk, F.q.z & mk, F.q.w & mk);
+    *(uint4 *)(VR + (tt * RP + c8) * 2) = make_uint4(F.v.x & mk, F.v.y & mk, F.v.z & mk, F.v.w & mk);
+    float sk = 0.f, sq = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      sk = fmaf(kf[e], kf[e], sk);
+      sq = fmaf(qf[e], qf[e], sq);
+    }
+    sk = pf::row16_sum(sk);
+    sq = pf::row16_sum(sq);
+    if ((tid & 15) == 0) {
+      sm[SM_NK * C + tt] = live && D.normalize ? __builtin_amdgcn_rsqf(sk + 1e-6f) : (live ? 1.0f : 0.0f);
+      sm[SM_NQ * C + tt] = live ? (D.normalize ? __builtin_amdgcn_rsqf(sq + 1e-6f) : 1.0f) * D.scale : 0.0f;
+    }
+    if (w == 0 && l < C) {
+      float bt = F.beta;
+      if (D.beta_logits) bt = __builtin_amdgcn_rcpf(1.0f + __expf(-bt));
+      sm[SM_BETA * C + l] = l < n ? bt : 0.0f;
+    }
+    // log2 decays of tokens 8 gq .. 8 gq + 7 of channel gc (0 past the
+    // chunk's tokens), then the inclusive scan over the 32 tokens: within
+    // the thread, then across the quad (lanes gq = 0..3 of the channel)
+    float gl[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      float gv = F.g[i];
+      if (D.a_log) {
+        const float u = gv + dtb;
+        const float sp = u > 20.0f ? u : __logf(1.0f + __expf(u < 20.0f ? u : 20.0f));
+        gv = -ea * sp;
+      }
+      gl[i] = 8 * gq + i < n ? gv * LOG2E : 0.0f;
+    }
+#pragma unroll
+    for (int i = 1; i < 8; i++) gl[i] += gl[i - 1];
+    const float tot = gl[7];
+    const float t1 = pf::quad_bcast<0>(tot), t2 = pf::quad_bcast<1>(tot), t3 = pf::quad_bcast<2>(tot);
+    const float pre = gq == 0 ? 0.0f : gq == 1 ? t1 : gq == 2 ? t1 + t2 : (t1 + t2) + t3;
+#pragma unroll
+    for (int i = 0; i < 8; i++) G[(8 * gq + i) * GP + gc] = pre + gl[i];
+    // the chunk's decay of channel gc (log2): G_0 - G_C, read on lane gq = 0
+    const float gC = ((t1 + t2) + t3) + pf::quad_bcast<3>(tot);
+    if (gq == 0 && gl[0] - gC > GROW_MAX) sm[SM_FLAG * C + pa] = 1.0f;
+    return n;
+  };
+
   fetch(F, 0);
   int ci = 0;
   int par = 0;  // chunk parity: which flag word this chunk uses
+  int n = stage_chunk(par);
+  fetch(F, n);  // the next chunk's inputs are in flight while this one is computed
+  pf::lds_barrier();
   for (int c0 = 0; c0 < len; par ^= 1) {
-    const int n = F.n;
-    // ---- stage: v rows, raw k and q rows, norms, beta; cumulative decays per channel
-    {
-      float kf[8], qf[8];
-      bf8(F.k, kf);
-      bf8(F.q, qf);
-      const bool live = tt < n;
-      const uint32_t mk = live ? 0xffffffffu : 0u;  // tokens past the chunk's: zero rows
-      *(uint4 *)(KB + (tt * RP + c8) * 2) = make_uint4(F.k.x & mk, F.k.y & mk, F.k.z & mk, F.k.w & mk);
-      *(uint4 *)(QB + (tt * RP + c8) * 2) = make_uint4(F.q.x & mk, F.q.y & mk, F.q.z & mk, F.q.w & mk);
-      *(uint4 *)(VR + (tt * RP + c8) * 2) = make_uint4(F.v.x & mk, F.v.y & mk, F.v.z & mk, F.v.w & mk);
-      float sk = 0.f, sq = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; e++) {
-        sk = fmaf(kf[e], kf[e], sk);
-        sq = fmaf(qf[e], qf[e], sq);
-      }
-      sk = pf::row16_sum(sk);
-      sq = pf::row16_sum(sq);
-      if ((tid & 15) == 0) {
-        sm[SM_NK * C + tt] = live && D.normalize ? __builtin_amdgcn_rsqf(sk + 1e-6f) : (live ? 1.0f : 0.0f);
-        sm[SM_NQ * C + tt] = live ? (D.normalize ? __builtin_amdgcn_rsqf(sq + 1e-6f) : 1.0f) * D.scale : 0.0f;
-      }
-      if (w == 0 && l < C) {
-        float bt = F.beta;
-        if (D.beta_logits) bt = __builtin_amdgcn_rcpf(1.0f + __expf(-bt));
-        sm[SM_BETA * C + l] = l < n ? bt : 0.0f;
-      }
-      // log2 decays of tokens 8 gq .. 8 gq + 7 of channel gc (0 past the
-      // chunk's tokens), then the inclusive scan over the 32 tokens: within
-      // the thread, then across the quad (lanes gq = 0..3 of the channel)
-      float gl[8];
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        float gv = F.g[i];
-        if (D.a_log) {
-          const float u = gv + dtb;
-          const float sp = u > 20.0f ? u : __logf(1.0f + __expf(u < 20.0f ? u : 20.0f));
-          gv = -ea * sp;
-        }
-        gl[i] = 8 * gq + i < n ? gv * LOG2E : 0.0f;
-      }
-#pragma unroll
-      for (int i = 1; i < 8; i++) gl[i] += gl[i - 1];
-      const float tot = gl[7];
-      const float t1 = pf::quad_bcast<0>(tot), t2 = pf::quad_bcast<1>(tot), t3 = pf::quad_bcast<2>(tot);
-      const float pre = gq == 0 ? 0.0f : gq == 1 ? t1 : gq == 2 ? t1 + t2 : (t1 + t2) + t3;
-#pragma unroll
-      for (int i = 0; i < 8; i++) G[(8 * gq + i) * GP + gc] = pre + gl[i];
-      // the chunk's decay of channel gc (log2): G_0 - G_C, read on lane gq = 0
-      const float gC = ((t1 + t2) + t3) + pf::quad_bcast<3>(tot);
-      if (gq == 0 && gl[0] - gC > GROW_MAX) sm[SM_FLAG * C + par] = 1.0f;
-    }
-    // the next chunk's inputs are in flight while this one is computed
     const int c_next = c0 + n;
-    fetch(F, c_next);
-    pf::lds_barrier();
     const bool pairwise = sm[SM_FLAG * C + par] != 0.0f;  // workgroup-uniform
     // ---- operands of token tt, channels c8 .. c8 + 7: nk k e^G and nq q e^G
     // (hi/lo, pcol order), nk k e^{G_C - G} (hi/lo), e^{G_C}; for the MFMA path
@@ -4735,8 +4738,15 @@ __global__ __launch_bounds__(NT) void kda_chunk_kernel(pf::PrefillDev D) {
         for (int dt = d4; dt < d4 + 4; dt++) S[dt] = pf::mfma(kl[dt - d4], eh, S[dt]);
       }
     }
-    pf::lds_barrier();  // the next chunk's staging overwrites the shared tiles
+    // The next chunk's staging, issued behind the state update's products
+    // (its exponentials and scan run while they do): its rows, norms, beta
+    // and decays go to tiles that this chunk no longer reads (the update
+    // reads KE and EC only), and the barrier below orders them before use.
+    const int n_next = stage_chunk(par ^ 1);
+    fetch(F, c_next + n_next);
+    pf::lds_barrier();  // the next chunk's staging is complete, this chunk's tiles are read
     c0 = c_next;
+    n = n_next;
     for (; ci < D.NC; ci++) {
       const int p = __builtin_amdgcn_readlane(ckv, ci);
       if (p > c0 && p <= len) break;
