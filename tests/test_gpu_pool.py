@@ -140,6 +140,10 @@ STEP_CASES = {
     "gdn_two_bit_g64": ("gdn", lambda H, K: np.repeat(np.array([2, 4, 2, 6])[:, None], K, 1), 4, 128, 128, 64),
     "gdn_two_bit_g128": ("gdn", lambda H, K: np.repeat(np.array([8, 2, 2, 4])[:, None], K, 1), 4, 128, 128, 128),
     "gdn_small_v16": ("gdn", lambda H, K: np.repeat(np.array([2, 4, 6, 8, 16])[:, None], K, 1), 5, 8, 16, 4),
+    # the reference's small-dimension word-load cases (tests/test_kernel_edges.py:34-50): K = 4, every
+    # width, V = 8 (its byte-addressed path) and V = 32, group min(V, 32)
+    "gdn_small_v8_k4": ("gdn", lambda H, K: np.repeat(np.array([2, 4, 6, 8, 16])[:, None], K, 1), 5, 4, 8, 8),
+    "gdn_small_v32_k4": ("gdn", lambda H, K: np.repeat(np.array([2, 4, 6, 8, 16])[:, None], K, 1), 5, 4, 32, 32),
     "kda_mixed": ("kda", lambda H, K: np.where(np.random.default_rng(2).random((H, K)) < .03, 16,
                                                np.random.default_rng(3).choice([2, 4, 6, 8], (H, K))), 3, 128, 128, 32),
     "kda_edges_v4": ("kda", lambda H, K: np.array([[2, 4, 8, 16]]), 1, 4, 4, 32),
