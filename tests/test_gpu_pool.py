@@ -144,6 +144,13 @@ STEP_CASES = {
     # width, V = 8 (its byte-addressed path) and V = 32, group min(V, 32)
     "gdn_small_v8_k4": ("gdn", lambda H, K: np.repeat(np.array([2, 4, 6, 8, 16])[:, None], K, 1), 5, 4, 8, 8),
     "gdn_small_v32_k4": ("gdn", lambda H, K: np.repeat(np.array([2, 4, 6, 8, 16])[:, None], K, 1), 5, 4, 32, 32),
+    # one head per width at K = V = 32 (the reference's fused-decode sizes, tests/test_fused_cuda.py:13-20;
+    # KDA heads rolled so the pivot head comes first) and at K = V = 128 for KDA (a head of pivot rows
+    # only, which has no column-scale region, beside uniform integer heads)
+    "gdn_all_widths_32": ("gdn", lambda H, K: np.repeat(np.array([2, 4, 6, 8, 16])[:, None], K, 1), 5, 32, 32, 32),
+    "kda_all_widths_32": ("kda", lambda H, K: np.repeat(np.array([16, 2, 4, 6, 8])[:, None], K, 1), 5, 32, 32, 32),
+    "kda_all_widths_128": ("kda", lambda H, K: np.repeat(np.array([16, 2, 4, 6, 8])[:, None], K, 1), 5, 128, 128,
+                           32),
     "kda_mixed": ("kda", lambda H, K: np.where(np.random.default_rng(2).random((H, K)) < .03, 16,
                                                np.random.default_rng(3).choice([2, 4, 6, 8], (H, K))), 3, 128, 128, 32),
     "kda_edges_v4": ("kda", lambda H, K: np.array([[2, 4, 8, 16]]), 1, 4, 4, 32),
