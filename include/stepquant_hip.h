@@ -86,9 +86,10 @@ typedef struct sq_pool {
 
 /*
  * Inputs of one decode step (PackedStatePool.step, pool.py:200-282).
- *   q, k     [B, HK*K] rows with row strides q_stride/k_stride (elements);
+ *   q, k     [B, HK*K] rows with row strides q_stride/k_stride (elements,
+ *            non-negative: SQ_EINVAL otherwise);
  *            value head h reads key head h / (H/HK) (GQA).
- *   v        [B, H*V] rows with row stride v_stride.
+ *   v        [B, H*V] rows with row stride v_stride (non-negative).
  *   g        GDN: [B, H] log-decay (raw gate a when a_log != NULL);
  *            KDA: [B, H*K] per-channel values.
  *   beta     [B, H] (raw logits when a_log != NULL: beta = sigmoid(b)).

@@ -5370,6 +5370,8 @@ int fill_step(int heads, const sq_step_args *a, StepDev &sd) {
   if (!a || !a->q || !a->k || !a->v || !a->g || !a->beta || !a->out || !a->slots)
     return fail(SQ_EINVAL, "step: null input pointer");
   if (a->batch < 0) return fail(SQ_EINVAL, "step: negative batch");
+  if (a->q_stride < 0 || a->k_stride < 0 || a->v_stride < 0)
+    return fail(SQ_EINVAL, "step: negative q/k/v row stride");
   if (a->key_heads < 1 || heads % a->key_heads) return fail(SQ_EINVAL, "step: heads not divisible by key heads");
   if ((a->a_log == nullptr) != (a->dt_bias == nullptr)) return fail(SQ_EINVAL, "step: a_log and dt_bias go together");
   if (a->qkv_dtype < 0 || a->qkv_dtype > 2 || a->gate_dtype < 0 || a->gate_dtype > 2 || a->out_dtype < 0 ||

@@ -68,6 +68,13 @@ def test_invalid_arguments_are_reported_without_a_device():
     fmt = N.FormatPool(data=1, page_bytes=1024, num_slots=2, offsets=1, rows=1, columns=1, heads=1, keys=32,
                        values=256, kind=N.FMT_DSQ, bits=4, group=128, kda=0, flags=0)
     assert lib.sq_format_encode(fmt, None, None, 4, 0, None) == -23
+    # a negative row stride would address rows before q/k/v: refused before any launch
+    pool = N.Pool(data=1, page_bytes=1024, num_slots=2, bits=1, offsets=1, rows=1, columns=1, impact=1,
+                  head_meta=1, heads=1, keys=128, values=128, group=32)
+    args = N.StepArgs(q=1, k=1, v=1, g=1, beta=1, out=1, slots=1, batch=1, q_stride=-128, k_stride=128,
+                      v_stride=128, key_heads=1, slots_dtype=N.I32)
+    rc = lib.sq_decode_step(ctypes.byref(pool), ctypes.byref(args), None)
+    assert rc == -22 and b"stride" in lib.sq_last_error()
 
 
 @pytest.mark.parametrize("arch,bits,V,group", [
