@@ -2040,12 +2040,12 @@ __device__ __forceinline__ uint32_t pack_codes(const float v[4]) {
   return w;
 }
 
-// Wave priority of the fused step's short serial phases (row set-up, the
-// readout's reductions, the row-sum reduce-scatter and r' fit, the column
-// scales): one level above the long per-value passes, so a workgroup whose
-// waves wait at a barrier on such a phase gets it done before the SIMD's
-// other waves take their next pass instructions (G6 -0.7%, G4 -1.5%, K6
-// -0.9% in interleaved A/B runs).
+// Wave priority of the fused step's short serial phases (the page and input
+// loads with the set-up that follows them, the readout's reductions, the
+// row-sum reduce-scatter and r' fit, the column scales): one level above the
+// long per-value passes, so a tile's loads are issued, and a workgroup whose
+// waves wait at a barrier on such a phase gets it done, before the SIMD's
+// other waves take their next pass instructions.
 template <int MODE, bool ON>
 __device__ __forceinline__ void serial_phase() {
   if (MODE == MODE_FUSED) __builtin_amdgcn_s_setprio(ON ? 1 : 0);
@@ -2066,11 +2066,11 @@ __device__ __forceinline__ void int_body(const PoolDev &P, const StepDev &S, Ctx
   const int NG = W == 2 ? P.ng : 1;
   const int g = W == 2 ? (C.j0 * P.ng) >> 7 : 0;  // j0 / G with G = 128 / NG
   const uint16_t *c16 = (const uint16_t *)C.cst;
+  serial_phase<MODE, true>();  // the loads issue first, the set-up follows
   stage_async<W / 2>(C, 16 * NG, true);
   uint32_t vraw[4];
   prologue<MODE, QW4, MODE != MODE_WRITE>(P, S, C, vraw);
   __syncthreads();
-  serial_phase<MODE, true>();
   const float beta = C.misc[0];
   handoff<MODE>(P, S, C);
   row_setup_int<MODE>(S, C, NG, ZS);
@@ -3300,6 +3300,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KDA128_WAVE
   C.pmask = (uint32_t *)(C.rk + FK);
 
   // stage the head's code, row-scale and column-scale regions
+  serial_phase<MODE, true>();  // the loads issue first, the set-up follows
   const int pitch = block_pitch(C.stride);
   stage_blocks_async(C.page + C.code_start, C.stride, pitch, C.code, C.tid);
   C.lbase = C.cg * pitch + (int)((uintptr_t)(C.page + C.code_start + (int64_t)C.cg * C.stride) & 15);
@@ -3323,7 +3324,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KDA128_WAVE
     S.s_key[bh * FK + C.tid] = C.kraw[C.tid] * nk;
     S.s_decay[bh * FK + C.tid] = C.gv[C.tid];
   }
-  serial_phase<MODE, true>();
   row_setup<MODE>(S, C, rp);
   __syncthreads();
   serial_phase<MODE, false>();
