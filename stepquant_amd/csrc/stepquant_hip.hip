@@ -2040,7 +2040,7 @@ __device__ __forceinline__ uint32_t pack_codes(const float v[4]) {
   return w;
 }
 
-// Wave priority of the fused step's short serial phases (the page and input
+// Wave priority of a step's short serial phases (the page and input
 // loads with the set-up that follows them, the readout's reductions, the
 // row-sum reduce-scatter and r' fit, the column scales): one level above the
 // long per-value passes, so a tile's loads are issued, and a workgroup whose
@@ -2048,7 +2048,7 @@ __device__ __forceinline__ uint32_t pack_codes(const float v[4]) {
 // other waves take their next pass instructions.
 template <int MODE, bool ON>
 __device__ __forceinline__ void serial_phase() {
-  if (MODE == MODE_FUSED) __builtin_amdgcn_s_setprio(ON ? 1 : 0);
+  if (MODE != MODE_DECODE) __builtin_amdgcn_s_setprio(ON ? 1 : 0);
 }
 
 template <int W, int MODE, bool QW4>
